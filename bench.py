@@ -1,0 +1,307 @@
+"""Benchmark of the MI355X quantized linear path (BASELINE.json metric:
+"INT8/FP8 GEMM TOPS @M=4096 + HBM GB/s @M=32, % of MI355X roofline").
+
+One step = one decode step (M=32 tokens) through the INT8 quantized
+projections of a 16-layer 1B-class decoder (hidden 2048, QKV N=4096,
+o_proj N=2048, gate_up N=12288, down K=6144; BASELINE config 1 at M=32):
+per projection, dynamic per-token activation quantization of the bf16 input,
+then the INT8 GEMM with fused dequant to bf16. The 16 layers hold distinct
+weights (805 MB of int8), so HBM, not the 256 MB Infinity Cache, serves them.
+Inputs are resident in HBM before the timed region. The step is captured once
+as a HIP graph and replayed.
+
+value = algorithmic bytes per step / step time (GB/s), with per projection
+B = N*K + M*K + 4N + 4M + 2*M*N (GEMM) + 3*M*K + 4*M (quantizer).
+Also reported: per-projection decode GB/s, prefill (M=4096) INT8/FP8 TOPS,
+the roofline fraction of the dominant kernel and a CPU baseline (the oracle's
+multithreaded C restatement) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+I8_PEAK_TOPS = 5000.0
+FP8_PEAK_TFLOPS = 5000.0
+LAYERS = 16
+M_DECODE = 32
+M_PREFILL = 4096
+
+
+def gemm_bytes(M, N, K, group=0):
+    scales = 4 * N * K // group + 4 * M * K // group if group else 4 * N + 4 * M
+    return N * K + M * K + scales + 2 * M * N
+
+
+def quant_bytes(M, K, group=0):
+    return 3 * M * K + (4 * M * K // group if group else 4 * M)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the quantized linear path has no multi-GPU "
+              "component in this build (see DESIGN.md for how it would shard).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from breeze_tts_cpp_amd import qlinear, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    I8, FP8 = qlinear.I8, qlinear.FP8
+    projections = list(synthetic.PROJECTIONS.items())
+
+    def bf16_dev(bits):
+        return torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(dev)
+
+    # ---- operands: 16 layers of distinct int8 weights, quantized on the GPU
+    # (load-time weight quantization, io/weights.cpp:80-87).
+    layers = []
+    with torch.cuda.stream(stream):
+        for layer in range(LAYERS):
+            entry = {}
+            for name, (N, K) in projections:
+                wb = synthetic.weights(N, K, seed=1000 + layer) if layer < 2 else None
+                if wb is None:  # later layers: cheap distinct weights derived on device
+                    base = layers[layer % 2][name]["w_bf16"]
+                    w = (base * (1.0 + 0.001 * layer)).contiguous()
+                else:
+                    w = bf16_dev(wb)
+                wq, sw = qlinear.row_quantize(w, I8, stream=stream)
+                entry[name] = {"wq": wq, "sw": sw, "N": N, "K": K,
+                               "w_bf16": w if layer < 2 else None}
+            layers.append(entry)
+    torch.cuda.synchronize()
+    for entry in layers:
+        for v in entry.values():
+            v["w_bf16"] = None
+
+    inputs = {}
+    for name, (N, K) in projections:
+        x = bf16_dev(synthetic.activations(M_DECODE, K, seed=0))
+        inputs[name] = {"x": x,
+                        "xq": torch.empty((M_DECODE, K), dtype=torch.uint8, device=dev),
+                        "sx": torch.empty((M_DECODE,), dtype=torch.float32, device=dev),
+                        "y": torch.empty((M_DECODE, N), dtype=torch.bfloat16, device=dev),
+                        "path": qlinear.plan(M_DECODE, N, K, I8)}
+    for name in inputs:
+        p = inputs[name]["path"]
+        assert qlinear.workspace_bytes(p, M_DECODE, *synthetic.PROJECTIONS[name], I8) == 0
+
+    def step():
+        for entry in layers:
+            for name, _ in projections:
+                io, wt = inputs[name], entry[name]
+                qlinear.row_quantize(io["x"], I8, values=io["xq"], scales=io["sx"], stream=stream)
+                qlinear.gemm(io["xq"], io["sx"], wt["wq"], wt["sw"], I8, path=io["path"],
+                             out=io["y"], stream=stream)
+
+    # eager reference of one step, then capture the step as a graph
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    eager = {n: inputs[n]["y"].clone() for n in inputs}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    for n in inputs:
+        inputs[n]["y"].zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    for n in inputs:
+        assert torch.equal(inputs[n]["y"], eager[n]), f"graph replay differs from eager ({n})"
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    step_bytes = LAYERS * sum(gemm_bytes(M_DECODE, N, K) + quant_bytes(M_DECODE, K)
+                              for _, (N, K) in projections)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ---- per-projection decode GEMM: graph of the 16 layers' launches of one
+    # projection (distinct weights), timed with events on the launch stream.
+    per_proj = {}
+    reps = max(5, args.steps // 2)
+    for name, (N, K) in projections:
+        io = inputs[name]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for entry in layers:
+                qlinear.gemm(io["xq"], io["sx"], entry[name]["wq"], entry[name]["sw"], I8,
+                             path=io["path"], out=io["y"], stream=stream)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(reps):
+                g.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / (reps * LAYERS)
+        b = gemm_bytes(M_DECODE, N, K)
+        p = io["path"]
+        per_proj[name] = {"N": N, "K": K, "us_per_launch": round(us, 3), "bytes": b,
+                          "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                          "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "path": [p.kind, p.tokens, p.channels, p.splits, p.waves]}
+        del g
+    dominant = max(per_proj, key=lambda n: per_proj[n]["us_per_launch"])
+    d = per_proj[dominant]
+    roofline = {"bound": "hbm", "kernel": f"skinny_gemm INT8 {dominant} M={M_DECODE}",
+                "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": d["bytes"]}
+
+    result = {
+        "metric": "INT8/FP8 GEMM TOPS @M=4096 + HBM GB/s @M=32, % of MI355X roofline",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations with 0.5% x20 outlier channels, "
+                "N(0,0.02) weights; bf16)",
+        "config": {"workload": f"decode step M={M_DECODE}: {LAYERS} layers x "
+                               "(qkv 4096x2048, o_proj 2048x2048, gate_up 12288x2048, "
+                               "down 2048x6144), per-token INT8 quant + INT8 GEMM + bf16",
+                   "tokens": M_DECODE, "layers": LAYERS, "format": "int8",
+                   "step_bytes": step_bytes},
+        "decode_projections": per_proj,
+        "roofline": roofline,
+    }
+
+    if not args.no_prefill:
+        result["prefill"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args, value)
+
+    print(json.dumps(result), flush=True)
+
+
+def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
+    """M=4096 INT8 and FP8 GEMMs over the four projections (BASELINE configs 2
+    and 4): TOPS = 2*M*N*K / kernel time, averaged over graph replays."""
+    out = {}
+    M = M_PREFILL
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for fmt_name, fmt in (("int8", qlinear.I8), ("fp8", qlinear.FP8)):
+        rows = {}
+        total_ops, total_us = 0, 0.0
+        for name, (N, K) in synthetic.PROJECTIONS.items():
+            x = torch.from_numpy(synthetic.activations(M, K, seed=1).view(np.int16)).view(
+                torch.bfloat16).to(dev)
+            w = torch.from_numpy(synthetic.weights(N, K, seed=1).view(np.int16)).view(
+                torch.bfloat16).to(dev)
+            with torch.cuda.stream(stream):
+                xq, sx = qlinear.row_quantize(x, fmt, stream=stream)
+                wq, sw = qlinear.row_quantize(w, fmt, stream=stream)
+                y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+                path = qlinear.plan(M, N, K, fmt)
+                need = qlinear.workspace_bytes(path, M, N, K, fmt)
+                ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            reps = 10
+            with torch.cuda.graph(g, stream=stream):
+                for _ in range(reps):
+                    qlinear.gemm(xq, sx, wq, sw, fmt, path=path, out=y, workspace=ws,
+                                 stream=stream)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            n_rep = 5
+            with torch.cuda.stream(stream):
+                start.record(stream)
+                for _ in range(n_rep):
+                    g.replay()
+                end.record(stream)
+            torch.cuda.synchronize()
+            us = start.elapsed_time(end) * 1e3 / (n_rep * reps)
+            ops = 2 * M * N * K
+            total_ops += ops
+            total_us += us
+            rows[name] = {"N": N, "K": K, "us": round(us, 2),
+                          "TOPS": round(ops / (us * 1e-6) / 1e12, 1),
+                          "path": [path.kind, path.tokens, path.channels, path.splits,
+                                   path.waves]}
+            del g, x, w, xq, wq, y, ws
+        tops = total_ops / (total_us * 1e-6) / 1e12
+        peak = I8_PEAK_TOPS if fmt_name == "int8" else FP8_PEAK_TFLOPS
+        out[fmt_name] = {"TOPS": round(tops, 1), "frac_mfma": round(tops / peak, 4),
+                         "peak": peak, "projections": rows}
+    return out
+
+
+def cpu_baseline(args, gpu_value):
+    """The oracle's multithreaded C restatement of quant + INT8 GEMM + dequant
+    (oracle/qlinear_oracle.c, orc_cpu_qlinear) on one layer's four projections
+    at M=32: a bounded sample of the step (1 of 16 layers)."""
+    from breeze_tts_cpp_amd import synthetic
+    from oracle import oracle
+
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    jobs = []
+    total_bytes = 0
+    for name, (N, K) in synthetic.PROJECTIONS.items():
+        wq, sw = oracle.quantize_rows(synthetic.weights(N, K, seed=1000), oracle.I8)
+        xb = synthetic.activations(M_DECODE, K, seed=0)
+        jobs.append((xb, wq, sw))
+        total_bytes += gemm_bytes(M_DECODE, N, K) + quant_bytes(M_DECODE, K)
+    oracle.cpu_qlinear(*jobs[0], oracle.I8, threads=threads)  # warm-up
+    times = []
+    t_end = time.time() + 20.0
+    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        for xb, wq, sw in jobs:
+            oracle.cpu_qlinear(xb, wq, sw, oracle.I8, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    gbs = total_bytes / t / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"one layer (4 INT8 projections, M={M_DECODE}) of the {LAYERS}-layer "
+                      f"step, median of {len(times)} reps; GPU/CPU = "
+                      f"{round(gpu_value / gbs, 1)}x"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,218 @@
+// C ABI of libqlinear.so: argument validation, path planning and dispatch to
+// the gfx950 kernel launchers. No exceptions cross this boundary.
+#include "../../include/qlinear.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "qlin_internal.hpp"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int status, const char *fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, args);
+    va_end(args);
+    return status;
+}
+
+int ok() {
+    g_error[0] = '\0';
+    return QLIN_OK;
+}
+
+bool aligned(const void *p, size_t bytes) {
+    return reinterpret_cast<uintptr_t>(p) % bytes == 0;
+}
+
+bool valid_group(int g) { return g == 0 || g == 32 || g == 64 || g == 128; }
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(QLIN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+// Path selection for gfx950 (256 CUs, 8 XCDs). Decode shapes stream the
+// weights once through the skinny kernel; larger token counts use the
+// LDS-tiled MFMA GEMM.
+qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_group) {
+    (void)fmt;
+    (void)input_group;
+    (void)weight_group;
+    qlin_path p{};
+    if (rows <= 64) {
+        p.kind = QLIN_KIND_SKINNY;
+        p.tokens = (rows + 15) / 16 * 16;
+        p.channels = 16;
+        p.splits = 1;
+        const int blocks_k = (K + 255) / 256;
+        // Enough wave64s along K to keep loads in flight; ranges must divide
+        // the 256-wide K blocks evenly.
+        int waves = 8;
+        while (waves > 1 && blocks_k % waves) waves /= 2;
+        p.waves = waves;
+        return p;
+    }
+    p.kind = QLIN_KIND_SKINNY;
+    p.tokens = 64;
+    p.channels = 16;
+    p.splits = 1;
+    const int blocks_k = (K + 255) / 256;
+    int waves = 4;
+    while (waves > 1 && blocks_k % waves) waves /= 2;
+    p.waves = waves;
+    return p;
+}
+
+int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_group,
+               int weight_group) {
+    (void)rows;
+    (void)N;
+    (void)fmt;
+    if (p.kind == QLIN_KIND_SKINNY) {
+        if (p.tokens != 16 && p.tokens != 32 && p.tokens != 48 && p.tokens != 64)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny path tokens must be 16/32/48/64 (got %d)",
+                        p.tokens);
+        if (p.channels != 16 && p.channels != 32)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny path channels must be 16 or 32 (got %d)",
+                        p.channels);
+        if (p.waves != 1 && p.waves != 2 && p.waves != 4 && p.waves != 8)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny path waves must be 1/2/4/8 (got %d)",
+                        p.waves);
+        const int blocks_k = (K + 255) / 256;
+        if (p.splits < 1 || blocks_k % (p.splits * p.waves))
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "skinny path splits*waves (%d) must divide ceil(K/256) = %d",
+                        p.splits * p.waves, blocks_k);
+        if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
+        return ok();
+    }
+    return fail(QLIN_ERR_UNSUPPORTED, "unknown path kind %d", p.kind);
+}
+
+qlin::GemmPath to_internal(const qlin_path &p) {
+    return {p.kind, p.tokens, p.channels, p.splits, p.waves};
+}
+
+}  // namespace
+
+extern "C" {
+
+int qlin_version(void) { return 100; }
+
+const char *qlin_last_error(void) { return g_error; }
+
+int qlin_row_quantize(const void *src, int ld, int rows, int cols, int src_type, void *values,
+                      float *scales, int fmt, int group, int rotation, qlin_stream_t stream) {
+    // ops::quantize_rows (reference ops/basic.cpp:69-78) + RowScaledView::validate
+    // (core/quantization.h:39-48).
+    if (src_type != QLIN_BF16 && src_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "quantization source must be BF16 or F16");
+    if (fmt != QLIN_I8 && fmt != QLIN_FP8)
+        return fail(QLIN_ERR_INVALID, "quantized storage must be I8 or FP8");
+    if (rows < 1 || cols < 1 || ld < cols)
+        return fail(QLIN_ERR_INVALID, "quantization shape rows=%d cols=%d ld=%d", rows, cols, ld);
+    if (!src || !values || !scales)
+        return fail(QLIN_ERR_INVALID, "quantization source/destination pointer is null");
+    if (!valid_group(group))
+        return fail(QLIN_ERR_INVALID, "quantization group must be 0, 32, 64 or 128 (got %d)",
+                    group);
+    if (rotation && (rotation != 128 || cols % 128))
+        return fail(QLIN_ERR_INVALID, "rotation must be 128 with cols %% 128 == 0");
+    if (!aligned(src, 2)) return fail(QLIN_ERR_ALIGNMENT, "16-bit source must be 2-byte aligned");
+    if (!aligned(scales, 4)) return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
+    if (group && uint64_t(rows) * ((uint64_t(cols) + 2047) / 2048) > INT32_MAX)
+        return fail(QLIN_ERR_INVALID, "group quantization grid exceeds capacity");
+    qlin::RowQuantizeArgs a{src, src_type, ld, rows, cols, values, scales, fmt, group, rotation};
+    qlin::launch_row_quantize(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("row quantize launch");
+}
+
+int qlin_plan(int rows, int N, int K, int fmt, int input_group, int weight_group,
+              qlin_path *path) {
+    if (!path) return fail(QLIN_ERR_INVALID, "path is null");
+    if (rows < 1 || N < 1 || K < 1)
+        return fail(QLIN_ERR_INVALID, "invalid kernel problem rows=%d N=%d K=%d", rows, N, K);
+    *path = choose(rows, N, K, fmt, input_group, weight_group);
+    return ok();
+}
+
+size_t qlin_workspace_bytes(const qlin_path *path, int rows, int N, int K, int fmt,
+                            int input_group, int weight_group) {
+    qlin_path p = path && path->kind ? *path : choose(rows, N, K, fmt, input_group, weight_group);
+    qlin::GemmArgs a{};
+    a.M = rows;
+    a.N = N;
+    a.K = K;
+    a.fmt = fmt;
+    a.input_group = input_group;
+    a.weight_group = weight_group;
+    if (p.kind == QLIN_KIND_SKINNY) return qlin::skinny_workspace_bytes(a, to_internal(p));
+    return 0;
+}
+
+int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void *w,
+              const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
+              int input_group, int weight_group, void *workspace, size_t workspace_bytes,
+              qlin_stream_t stream) {
+    // check_linear + make_plan rules (reference ops/cuda/quantization.cpp:94-102,
+    // 206-222) and launch_quant_linear's type checks (quant_dispatch.cu:194-233).
+    if (fmt != QLIN_I8 && fmt != QLIN_FP8)
+        return fail(QLIN_ERR_INVALID, "unsupported quantized storage type");
+    if (out_type != QLIN_BF16 && out_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "quantized GEMM output must be F16 or BF16");
+    if (rows < 1 || N < 1 || K < 1 || K % 16 || N % 16)
+        return fail(QLIN_ERR_INVALID, "quantized GEMM unsupported shape rows=%d N=%d K=%d", rows,
+                    N, K);
+    if (fmt == QLIN_I8 && K > INT32_MAX / (128 * 128))
+        return fail(QLIN_ERR_INVALID, "INT8 reduction can overflow INT32");
+    if (!valid_group(input_group) || !valid_group(weight_group))
+        return fail(QLIN_ERR_INVALID, "group sizes must be 0, 32, 64 or 128");
+    if (!x || !sx || !w || !sw || !y)
+        return fail(QLIN_ERR_INVALID, "quantized GEMM operand pointer is null");
+    if (!aligned(x, 16) || !aligned(w, 16))
+        return fail(QLIN_ERR_ALIGNMENT, "quantized operands must be 16-byte aligned");
+    if (!aligned(y, 8)) return fail(QLIN_ERR_ALIGNMENT, "output must be 8-byte aligned");
+    if (!aligned(sx, 4) || !aligned(sw, 4))
+        return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
+    qlin_path p = path && path->kind ? *path : choose(rows, N, K, fmt, input_group, weight_group);
+    int status = check_path(p, rows, N, K, fmt, input_group, weight_group);
+    if (status) return status;
+    qlin::GemmArgs a{static_cast<const uint8_t *>(x),
+                     sx,
+                     static_cast<const uint8_t *>(w),
+                     sw,
+                     y,
+                     rows,
+                     N,
+                     K,
+                     fmt,
+                     out_type,
+                     input_group,
+                     weight_group,
+                     workspace,
+                     workspace_bytes};
+    const qlin::GemmPath ip = to_internal(p);
+    size_t need = 0;
+    if (p.kind == QLIN_KIND_SKINNY) need = qlin::skinny_workspace_bytes(a, ip);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(QLIN_ERR_WORKSPACE, "split-K partial workspace overflow: need %zu bytes, have %zu",
+                    need, workspace ? workspace_bytes : size_t(0));
+    if (need && !aligned(workspace, 16))
+        return fail(QLIN_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    int r = p.kind == QLIN_KIND_SKINNY ? qlin::launch_skinny(a, ip, s) : QLIN_ERR_UNSUPPORTED;
+    if (r) return fail(r, "no kernel variant for this path");
+    return check_launch("quantized GEMM launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,369 @@
+// Decode-regime quantized GEMM (M <= 64 tokens) for gfx950.
+//
+// y[M,N] = D(epilogue(x[M,K] . w[N,K]^T)), the work of the reference's small-M
+// path quant_gemv (ops/kernels/quant/quant_dispatch.cu:12-130), its split-K
+// reduction (quant_reduce.cuh:9-19) and, for K-group scales, grouped_gemm
+// (quant_grouped.cu:16-169).
+//
+// At these shapes the weight matrix is the only large operand: the kernel is
+// bound by streaming w from HBM exactly once. Each wave64 owns 16*NF weight
+// rows over a K range and issues 16-byte loads (64 lanes = 16 rows x 64
+// contiguous bytes per load) straight into MFMA A-fragment registers; the
+// tokens are the MFMA B side (zero-padded to 16*MT). INT8 uses
+// v_mfma_i32_16x16x64_i8 (exact int32), FP8 e4m3 uses
+// v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales. The waves of a
+// workgroup split K and reduce through LDS; optionally the grid splits K
+// further into workspace partials that a second kernel reduces in split order.
+//
+// Epilogues (all fp32, no contraction):
+//   per-channel : D((acc * sx[m]) * sw[n])      (quant_gemm_sm80.cu:24-29)
+//   K-group     : r = fmaf(p_g, sx_g*sw_g, r) per group, groups ascending
+//                 (quant_grouped.cu:135-144); ranges summed 0 + r_0 + r_1 ...
+#include "qlin_device.hpp"
+#include "qlin_internal.hpp"
+
+#include <type_traits>
+
+namespace qlin {
+namespace {
+
+constexpr int kBlockK = 256;  // K handled per main-loop iteration (4 pieces of 64)
+
+template <int Fmt> struct Mfma;
+template <> struct Mfma<I8> {
+    using Acc = i32x4;
+    using Scalar = int;
+    // Two 64-K pieces -> two MFMAs.
+    __device__ static void run(Acc &c, const i32x4 &a0, const i32x4 &a1, const i32x4 &b0,
+                               const i32x4 &b1) {
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma<FP8> {
+    using Acc = f32x4;
+    using Scalar = float;
+    // Two 64-K pieces -> one 128-K MFMA (format 0 = e4m3 for A and B, unit
+    // E8M0 scales 0x7f).
+    __device__ static void run(Acc &c, const i32x4 &a0, const i32x4 &a1, const i32x4 &b0,
+                               const i32x4 &b1) {
+        i32x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        i32x8 b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0,
+                                                             0x7f7f7f7f);
+    }
+};
+
+__device__ __forceinline__ i32x4 load16(const uint8_t *p) {
+    return *reinterpret_cast<const i32x4 *>(p);
+}
+
+template <class Out>
+__device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4]) {
+    uint2 packed;
+    packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
+    packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + index) = packed;
+}
+
+// One workgroup = WK waves over K, sharing 16*NF weight rows; tokens
+// [m0, m0 + 16*MT). Split: store raw (per-channel) or outer-scaled (grouped)
+// partials to workspace[blockIdx.y] instead of the output.
+template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out>
+__global__ __launch_bounds__(64 * WK) void skinny_gemm(
+    const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
+    const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
+    int K, int span, int input_group, int weight_group) {
+    using M_ = Mfma<Fmt>;
+    using Acc = typename M_::Acc;
+    using Scalar = typename M_::Scalar;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row16 = lane & 15, quad = lane >> 4;
+    const int n0 = blockIdx.x * 16 * NF;
+    const int m0 = blockIdx.z * 16 * MT;
+    const int range = blockIdx.y * WK + wave;
+    const int k_begin = range * span;
+    const int k_end = min(K, k_begin + span);
+
+    const uint8_t *wrow[NF];
+    bool wvalid[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        int n = n0 + f * 16 + row16;
+        wvalid[f] = n < N;
+        wrow[f] = w + size_t(wvalid[f] ? n : 0) * K + quad * 16;
+    }
+    const uint8_t *xrow[MT];
+    bool xvalid[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        int m = m0 + t * 16 + row16;
+        xvalid[t] = m < M;
+        xrow[t] = x + size_t(xvalid[t] ? m : 0) * K + quad * 16;
+    }
+
+    // Grouped: fp32 running sums; per-channel: the raw accumulator.
+    Acc acc[MT][NF];
+    float facc[MT][NF][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            acc[t][f] = Acc{0, 0, 0, 0};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) facc[t][f][r] = 0.f;
+        }
+
+    for (int kb = k_begin; kb < k_end; kb += kBlockK) {
+        i32x4 a[NF][4], b[MT][4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int k = kb + p * 64;
+            const bool in = k + quad * 16 < k_end;
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                a[f][p] = (in && wvalid[f]) ? load16(wrow[f] + k) : i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                b[t][p] = (in && xvalid[t]) ? load16(xrow[t] + k) : i32x4{0, 0, 0, 0};
+        }
+        if constexpr (!Grouped) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int f = 0; f < NF; ++f)
+                        M_::run(acc[t][f], a[f][2 * h], a[f][2 * h + 1], b[t][2 * h],
+                                b[t][2 * h + 1]);
+        } else {
+            // Two 128-K groups per block, each reduced natively then scaled.
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = kb + h * 128;
+                if (k >= k_end) break;
+                const int g_in = input_group ? k / input_group : 0;
+                const int g_w = weight_group ? k / weight_group : 0;
+                float swg[NF][4];
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        int n = n0 + f * 16 + quad * 4 + r;
+                        swg[f][r] = (weight_group && n < N) ? sw[size_t(g_w) * N + n] : 1.f;
+                    }
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    int m = m0 + t * 16 + row16;
+                    float sxg = (input_group && m < M) ? sx[size_t(g_in) * M + m] : 1.f;
+#pragma unroll
+                    for (int f = 0; f < NF; ++f) {
+                        Acc p = Acc{0, 0, 0, 0};
+                        M_::run(p, a[f][2 * h], a[f][2 * h + 1], b[t][2 * h], b[t][2 * h + 1]);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            facc[t][f][r] =
+                                __builtin_fmaf(float(p[r]), sxg * swg[f][r], facc[t][f][r]);
+                    }
+                }
+            }
+        }
+    }
+
+    // Cross-wave reduction in LDS, waves summed in ascending K order.
+    constexpr int kUnits = MT * NF * 64;  // (token tile, fragment, lane), 4 values each
+    using Red = std::conditional_t<Grouped, float, Scalar>;
+    __shared__ Red red[WK > 1 ? WK : 1][MT * NF][4][64];
+    if constexpr (WK > 1) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (Grouped) red[wave][t * NF + f][r][lane] = facc[t][f][r];
+                    else red[wave][t * NF + f][r][lane] = acc[t][f][r];
+                }
+        __syncthreads();
+    }
+    for (int u = threadIdx.x; u < kUnits; u += 64 * WK) {
+        const int tf = u >> 6, l = u & 63;
+        const int t = tf / NF, f = tf % NF;
+        const int m = m0 + t * 16 + (l & 15);
+        const int n = n0 + f * 16 + (l >> 4) * 4;
+        if (m >= M || n >= N) continue;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (Grouped) {
+                float s = 0.f;
+                if constexpr (WK > 1) {
+                    for (int q = 0; q < WK; ++q) s += red[q][tf][r][l];
+                } else {
+                    s += facc[t][f][r];
+                }
+                v[r] = s;
+            } else {
+                Scalar s = 0;
+                if constexpr (WK > 1) {
+                    for (int q = 0; q < WK; ++q) s += red[q][tf][r][l];
+                } else {
+                    s += acc[t][f][r];
+                }
+                v[r] = float(s);
+            }
+        }
+        if constexpr (Split) {
+            // Grouped partials carry their outer scales (quant_grouped.cu:161-165);
+            // per-channel partials stay raw for the reduce kernel.
+            if constexpr (Grouped) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float outer = input_group ? 1.f : sx[m];
+                    if (!weight_group) outer *= sw[n + r];
+                    v[r] = v[r] * outer;
+                }
+                float4 out = {v[0], v[1], v[2], v[3]};
+                *reinterpret_cast<float4 *>(static_cast<float *>(partial) +
+                                            (size_t(blockIdx.y) * M + m) * N + n) = out;
+            } else {
+                Scalar raw[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    Scalar s = 0;
+                    if constexpr (WK > 1) {
+                        for (int q = 0; q < WK; ++q) s += red[q][tf][r][l];
+                    } else {
+                        s += acc[t][f][r];
+                    }
+                    raw[r] = s;
+                }
+                *reinterpret_cast<uint4 *>(static_cast<Scalar *>(partial) +
+                                           (size_t(blockIdx.y) * M + m) * N + n) =
+                    *reinterpret_cast<uint4 *>(raw);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (Grouped) {
+                    float outer = input_group ? 1.f : sx[m];
+                    if (!weight_group) outer *= sw[n + r];
+                    v[r] = v[r] * outer;
+                } else {
+                    float s = v[r] * sx[m];
+                    v[r] = s * sw[n + r];
+                }
+            }
+            store4<Out>(y, size_t(m) * N + n, v);
+        }
+    }
+}
+
+// y = D((sum_s p_s) * sx * sw) or D(0 + sum_s p_s) for pre-scaled grouped
+// partials; splits summed in ascending order (reference quant_reduce.cuh:9-19).
+template <class Scalar, bool Scaled, class Out>
+__global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ partial,
+                                                    const float *__restrict__ sx,
+                                                    const float *__restrict__ sw,
+                                                    void *__restrict__ y, int M, int N,
+                                                    int splits) {
+    const size_t i4 = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    const size_t total = size_t(M) * N;
+    if (i4 >= total) return;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        Scalar s = 0;
+        for (int q = 0; q < splits; ++q) s += partial[size_t(q) * total + i4 + r];
+        if constexpr (Scaled) {
+            const size_t i = i4 + r;
+            float a = float(s) * sx[i / N];
+            v[r] = a * sw[i % N];
+        } else {
+            v[r] = float(s);
+        }
+    }
+    store4<Out>(y, i4, v);
+}
+
+template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out>
+int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
+    const int ranges = p.splits * WK;
+    const int span = blocks_k / ranges * kBlockK;
+    dim3 grid((a.N + 16 * NF - 1) / (16 * NF), p.splits, (a.M + 16 * MT - 1) / (16 * MT));
+    dim3 block(64 * WK);
+    if (p.splits == 1) {
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out>), grid, block, 0,
+                           stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span,
+                           a.input_group, a.weight_group);
+        return 0;
+    }
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
+                       a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
+                       a.input_group, a.weight_group);
+    const size_t quads = (size_t(a.M) * a.N) / 4;
+    dim3 rgrid(unsigned((quads + 255) / 256));
+    using Scalar = typename Mfma<Fmt>::Scalar;
+    if constexpr (Grouped)
+        hipLaunchKernelGGL((split_reduce<float, false, Out>), rgrid, dim3(256), 0, stream,
+                           static_cast<const float *>(a.workspace), a.sx, a.sw, a.y, a.M, a.N,
+                           p.splits);
+    else
+        hipLaunchKernelGGL((split_reduce<Scalar, true, Out>), rgrid, dim3(256), 0, stream,
+                           static_cast<const Scalar *>(a.workspace), a.sx, a.sw, a.y, a.M, a.N,
+                           p.splits);
+    return 0;
+}
+
+template <int Fmt, int MT, int NF, bool Grouped, class Out>
+int dispatch_wk(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    switch (p.waves) {
+    case 1: return launch_variant<Fmt, MT, NF, 1, Grouped, Out>(a, p, s);
+    case 2: return launch_variant<Fmt, MT, NF, 2, Grouped, Out>(a, p, s);
+    case 4: return launch_variant<Fmt, MT, NF, 4, Grouped, Out>(a, p, s);
+    case 8: return launch_variant<Fmt, MT, NF, 8, Grouped, Out>(a, p, s);
+    default: return -4;
+    }
+}
+
+template <int Fmt, int MT, bool Grouped, class Out>
+int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    if (p.channels == 16) return dispatch_wk<Fmt, MT, 1, Grouped, Out>(a, p, s);
+    if (p.channels == 32) return dispatch_wk<Fmt, MT, 2, Grouped, Out>(a, p, s);
+    return -4;
+}
+
+template <int Fmt, bool Grouped, class Out>
+int dispatch_mt(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    switch (p.tokens) {
+    case 16: return dispatch_nf<Fmt, 1, Grouped, Out>(a, p, s);
+    case 32: return dispatch_nf<Fmt, 2, Grouped, Out>(a, p, s);
+    case 48: return dispatch_nf<Fmt, 3, Grouped, Out>(a, p, s);
+    case 64: return dispatch_nf<Fmt, 4, Grouped, Out>(a, p, s);
+    default: return -4;
+    }
+}
+
+template <int Fmt, class Out>
+int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    if (a.input_group || a.weight_group) return dispatch_mt<Fmt, true, Out>(a, p, s);
+    return dispatch_mt<Fmt, false, Out>(a, p, s);
+}
+
+}  // namespace
+
+size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
+    return p.splits > 1 ? size_t(p.splits) * a.M * a.N * 4 : 0;
+}
+
+int launch_skinny(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    if (a.out_type == F16) {
+        if (a.fmt == I8) return dispatch_grouped<I8, f16_t>(a, p, stream);
+        return dispatch_grouped<FP8, f16_t>(a, p, stream);
+    }
+    if (a.fmt == I8) return dispatch_grouped<I8, bf16_t>(a, p, stream);
+    return dispatch_grouped<FP8, bf16_t>(a, p, stream);
+}
+
+}  // namespace qlin

@@ -1,0 +1,102 @@
+// Device helpers shared by the gfx950 quantized-linear kernels: 16-bit float
+// conversions, INT8 / OCP e4m3fn encoders, the H128 rotation sign and wave64
+// reductions. Every TU is compiled with -ffp-contract=off, so each a*b+c below
+// is two roundings unless written as __builtin_fmaf.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qlin {
+
+// Storage codes follow tts::Type (reference core/tensor.h:8).
+enum Type : int { BF16 = 0, F32 = 1, I32 = 2, FP8 = 3, I8 = 4, F16 = 5 };
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------- 16-bit floats
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__device__ __forceinline__ float to_float(uint16_t h, bf16_t) {
+    return __uint_as_float(uint32_t(h) << 16);
+}
+__device__ __forceinline__ float to_float(uint16_t h, f16_t) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return float(v);  // exact widening
+}
+// Round-to-nearest-even fp32 -> bf16 with quiet NaN.
+__device__ __forceinline__ uint16_t from_float(float f, bf16_t) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+__device__ __forceinline__ uint16_t from_float(float f, f16_t) {
+    _Float16 v = (_Float16)f;  // v_cvt_f16_f32, round-to-nearest-even
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+// ---------------------------------------------------------------- 8-bit encoders
+// INT8: clamp to +-127, then round half to even (reference
+// ops/kernels/quant/quant_format.cuh:37-47).
+__device__ __forceinline__ uint32_t encode_i8(float x) {
+    x = fminf(127.f, fmaxf(-127.f, x));
+    return uint32_t(int(__builtin_rintf(x))) & 0xffu;
+}
+
+// OCP e4m3fn, round-to-nearest-even, saturating to +-448 (the satfinite
+// conversion of reference quant_format.cuh:12-17). Integer rounding on the
+// fp32 bit pattern: exponent range [-6, 8] normal, 2^-9 subnormal step.
+__device__ __forceinline__ uint32_t encode_fp8(float x) {
+    uint32_t u = __float_as_uint(x);
+    uint32_t sign = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7fu;            // NaN
+    if (a >= 0x43e00000u) return sign | 0x7eu;    // >= 448 (incl. inf): max finite
+    if (a < 0x3c800000u) {                        // < 2^-6: subnormal, step 2^-9
+        float q = __builtin_rintf(__uint_as_float(a) * 512.f);  // exact scaling
+        return sign | uint32_t(q);
+    }
+    uint32_t exponent = (a >> 23) - 127u + 7u;    // biased e4m3 exponent, 1..15
+    uint32_t mantissa = a & 0x7fffffu;
+    uint32_t kept = mantissa >> 20, rest = mantissa & 0xfffffu;
+    uint32_t up = rest > 0x80000u || (rest == 0x80000u && (kept & 1u));
+    return sign | ((exponent << 3) + kept + up);  // carry moves into the exponent
+}
+
+template <int Fmt> __device__ __forceinline__ uint32_t encode(float x) {
+    if constexpr (Fmt == I8) return encode_i8(x);
+    else return encode_fp8(x);
+}
+
+// quant_device::scale (reference quant_format.cuh:62-64). Division is IEEE
+// correctly rounded (HIP default for fp32 '/').
+template <int Fmt> __device__ __forceinline__ float quant_scale(float amax) {
+    constexpr float range = Fmt == I8 ? 127.f : 448.f;
+    return amax == 0 ? 1.f : fmaxf(amax / range, 1.17549435e-38f);
+}
+
+// Rademacher sign of the H128 rotation for an absolute column (reference
+// quant_device.cuh:166-168).
+__device__ __forceinline__ float rotation_sign(int column) {
+    uint32_t h = uint32_t(column) * 0x45d9f3bu;
+    h = (h ^ (h >> 16)) * 0x45d9f3bu;
+    return ((h ^ (h >> 16)) & 1u) ? 1.f : -1.f;
+}
+
+// ---------------------------------------------------------------- wave64 reductions
+// Max over a power-of-two lane group of width W (aligned), via xor shuffles.
+template <int W> __device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int d = 1; d < W; d *= 2) v = fmaxf(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+}  // namespace qlin

@@ -1,0 +1,42 @@
+// Host-side contracts between the C-ABI layer (capi.cpp) and the kernel
+// launchers (*.hip). Launchers assume arguments were validated by the caller.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qlin {
+
+struct RowQuantizeArgs {
+    const void *src;  // bf16/f16 [rows, ld]
+    int src_type, ld, rows, cols;
+    void *values;     // int8/e4m3 [rows, cols]
+    float *scales;    // [rows] or [ceil(cols/group), rows]
+    int fmt, group, rotation;
+};
+void launch_row_quantize(const RowQuantizeArgs &, hipStream_t);
+
+// Kernel families; numbering is part of the C ABI (qlin_path.kind).
+enum Kind : int { KIND_AUTO = 0, KIND_SKINNY = 1, KIND_TILED = 2 };
+
+struct GemmArgs {
+    const uint8_t *x;  // [M, K]
+    const float *sx;   // [M] or [K/ig, M]
+    const uint8_t *w;  // [N, K]
+    const float *sw;   // [N] or [K/wg, N]
+    void *y;           // [M, N] bf16/f16
+    int M, N, K, fmt, out_type, input_group, weight_group;
+    void *workspace;
+    size_t workspace_bytes;
+};
+struct GemmPath {
+    int kind, tokens, channels, splits, waves;
+};
+// Skinny (decode) family: returns 0, or a negative status if the path's
+// parameters are not an instantiated variant.
+int launch_skinny(const GemmArgs &, const GemmPath &, hipStream_t);
+size_t skinny_workspace_bytes(const GemmArgs &, const GemmPath &);
+int launch_tiled(const GemmArgs &, const GemmPath &, hipStream_t);
+size_t tiled_workspace_bytes(const GemmArgs &, const GemmPath &);
+
+}  // namespace qlin

@@ -1,0 +1,150 @@
+"""Python host binding of libqlinear.so (ctypes over the C ABI in
+include/qlinear.h). Device memory and streams come from PyTorch; all compute
+is the HIP library. There is no fallback: if the library is missing or a
+call fails, this raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+BF16, F32, I32, FP8, I8, F16 = 0, 1, 2, 3, 4, 5
+KIND_AUTO, KIND_SKINNY, KIND_TILED = 0, 1, 2
+STATUS = {0: "ok", -1: "invalid", -2: "alignment", -3: "workspace", -4: "unsupported", -5: "hip"}
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqlinear.so")
+_lib = None
+
+
+class QLinearError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"qlinear error {status} ({STATUS.get(status, '?')}): {message}")
+        self.status = status
+
+
+class qlin_path(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("tokens", ctypes.c_int), ("channels", ctypes.c_int),
+                ("splits", ctypes.c_int), ("waves", ctypes.c_int)]
+
+
+@dataclass
+class Path:
+    kind: int = KIND_AUTO
+    tokens: int = 0
+    channels: int = 0
+    splits: int = 1
+    waves: int = 1
+
+    def to_c(self) -> qlin_path:
+        return qlin_path(self.kind, self.tokens, self.channels, self.splits, self.waves)
+
+
+EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
+           "qlin_workspace_bytes", "qlin_gemm")
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                           "(make -C breeze_tts_cpp_amd)")
+    L = ctypes.CDLL(LIB_PATH)
+    P, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    L.qlin_version.restype = i
+    L.qlin_version.argtypes = []
+    L.qlin_last_error.restype = ctypes.c_char_p
+    L.qlin_last_error.argtypes = []
+    L.qlin_row_quantize.restype = i
+    L.qlin_row_quantize.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
+    L.qlin_plan.restype = i
+    L.qlin_plan.argtypes = [i, i, i, i, i, i, ctypes.POINTER(qlin_path)]
+    L.qlin_workspace_bytes.restype = sz
+    L.qlin_workspace_bytes.argtypes = [ctypes.POINTER(qlin_path), i, i, i, i, i, i]
+    L.qlin_gemm.restype = i
+    L.qlin_gemm.argtypes = [ctypes.POINTER(qlin_path), P, P, P, P, P, i, i, i, i, i, i, i, P, sz, P]
+    _lib = L
+    return L
+
+
+def _check(status: int):
+    if status:
+        raise QLinearError(status, load().qlin_last_error().decode())
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+_TYPES = {torch.bfloat16: BF16, torch.float16: F16}
+
+
+def row_quantize(x: torch.Tensor, fmt: int, group: int = 0, rotation: int = 0,
+                 values: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                 stream=None):
+    """Quantize rows of a 2-D bf16/f16 tensor (row stride allowed).
+    Returns (values uint8 [rows, cols], scales f32 [rows] or [groups, rows])."""
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("row_quantize expects a 2-D tensor with unit column stride")
+    if x.dtype not in _TYPES:
+        raise ValueError("quantization source must be BF16 or F16")
+    rows, cols = x.shape
+    if values is None:
+        values = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    if scales is None:
+        shape = ((cols + group - 1) // group, rows) if group else (rows,)
+        scales = torch.empty(shape, dtype=torch.float32, device=x.device)
+    _check(load().qlin_row_quantize(x.data_ptr(), x.stride(0), rows, cols, _TYPES[x.dtype],
+                                    values.data_ptr(), scales.data_ptr(), fmt, group, rotation,
+                                    _stream(stream)))
+    return values, scales
+
+
+def plan(rows: int, N: int, K: int, fmt: int, input_group: int = 0, weight_group: int = 0) -> Path:
+    p = qlin_path()
+    _check(load().qlin_plan(rows, N, K, fmt, input_group, weight_group, ctypes.byref(p)))
+    return Path(p.kind, p.tokens, p.channels, p.splits, p.waves)
+
+
+def workspace_bytes(path: Path | None, rows: int, N: int, K: int, fmt: int,
+                    input_group: int = 0, weight_group: int = 0) -> int:
+    p = (path or Path()).to_c()
+    return int(load().qlin_workspace_bytes(ctypes.byref(p), rows, N, K, fmt, input_group,
+                                           weight_group))
+
+
+def gemm(xq: torch.Tensor, sx: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int,
+         out_dtype=torch.bfloat16, input_group: int = 0, weight_group: int = 0,
+         path: Path | None = None, workspace: torch.Tensor | None = None,
+         out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    M, K = xq.shape
+    N = wq.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=xq.device)
+    need = workspace_bytes(path, M, N, K, fmt, input_group, weight_group)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=xq.device)
+    p = (path or Path()).to_c()
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(load().qlin_gemm(ctypes.byref(p), xq.data_ptr(), sx.data_ptr(), wq.data_ptr(),
+                            sw.data_ptr(), out.data_ptr(), M, N, K, fmt,
+                            F16 if out.dtype == torch.float16 else BF16, input_group,
+                            weight_group, ws_ptr, ws_bytes, _stream(stream)))
+    return out
+
+
+def linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int, group: int = 0,
+           rotation: int = 0, out_dtype=torch.bfloat16, path: Path | None = None,
+           stream=None) -> torch.Tensor:
+    """Quantize activations then run the GEMM (the quantized branch of the
+    reference ops::linear, ops/linear.cpp:71-90)."""
+    xq, sx = row_quantize(x, fmt, group, rotation, stream=stream)
+    return gemm(xq, sx, wq, sw, fmt, out_dtype, group, group, path, stream=stream)

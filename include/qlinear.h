@@ -1,0 +1,112 @@
+/*
+ * qlinear.h — C ABI of the MI355X (gfx950) quantized linear library
+ * (libqlinear.so). Plain pointers and sizes only; every entry point returns
+ * an int status (0 = success, negative = error, message via
+ * qlin_last_error()) and never throws.
+ *
+ * It replaces, one for one, the kernel-launcher layer of TTS.cpp's quantized
+ * linear path (paths relative to the reference's src/):
+ *   qlin_row_quantize   <- launch_row_quantize     ops/kernels/quant/row_quantize.h:6
+ *                          (validation of ops::quantize_rows, ops/basic.cpp:69-78)
+ *   qlin_gemm           <- launch_quant_linear     ops/kernels/quant/quant_dispatch.h:11-15
+ *                          and grouped_quant_gemm  ops/kernels/quant/quant_dispatch.h:7-10
+ *   qlin_plan           <- select_linear / KernelSelector
+ *                          ops/cuda/quantization_policy.cpp:269-286, ops/cuda/quantization.cpp:27-64
+ *   qlin_workspace_bytes   (the split-K bound checks of quant_gemm_sm80.cu:45-46,
+ *                          quant_grouped.cu:232-233, made queryable)
+ *
+ * Operand layouts (reference core/quantization.h:24-49):
+ *   x  int8/e4m3 [rows, K] dense          sx f32 [rows] or [ceil(K/ig), rows]
+ *   w  int8/e4m3 [N, K]   dense (K fast)  sw f32 [N]    or [ceil(K/wg), N]
+ *   y  bf16/f16  [rows, N] dense
+ * All device pointers; the library never allocates, copies or repacks.
+ * Launches are asynchronous on `stream` and graph-capturable.
+ */
+#ifndef QLINEAR_H
+#define QLINEAR_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t; declared here so that bindings need no HIP headers. */
+typedef struct ihipStream_t *qlin_stream_t;
+
+/* Storage codes, numerically equal to tts::Type (reference core/tensor.h:8). */
+enum {
+    QLIN_BF16 = 0,
+    QLIN_F32 = 1,
+    QLIN_I32 = 2,
+    QLIN_FP8 = 3, /* OCP e4m3fn */
+    QLIN_I8 = 4,
+    QLIN_F16 = 5
+};
+
+/* Status codes. */
+enum {
+    QLIN_OK = 0,
+    QLIN_ERR_INVALID = -1,     /* shape/type/null pointer (reference: std::invalid_argument) */
+    QLIN_ERR_ALIGNMENT = -2,   /* pointer alignment the kernels require */
+    QLIN_ERR_WORKSPACE = -3,   /* workspace absent or too small */
+    QLIN_ERR_UNSUPPORTED = -4, /* valid request without a kernel variant (e.g. path params) */
+    QLIN_ERR_HIP = -5          /* HIP runtime error at launch */
+};
+
+/* Kernel families (qlin_path.kind). */
+enum {
+    QLIN_KIND_AUTO = 0,   /* qlin_gemm plans itself */
+    QLIN_KIND_SKINNY = 1, /* decode regime: weight-streaming MFMA GEMM, tokens <= 64 per tile */
+    QLIN_KIND_TILED = 2   /* prefill regime: LDS-tiled MFMA GEMM */
+};
+
+/* Execution path of one GEMM shape class; mirrors tts::LinearPath
+ * (reference ops/kernels/quant/kernel_config.h:5-9). */
+typedef struct qlin_path {
+    int kind;     /* QLIN_KIND_* */
+    int tokens;   /* token (M) tile */
+    int channels; /* output-channel (N) tile */
+    int splits;   /* grid-level K partitions (partials in workspace when > 1) */
+    int waves;    /* skinny: wave64s splitting K inside a workgroup */
+} qlin_path;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int qlin_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *qlin_last_error(void);
+
+/* Quantize rows of a bf16/f16 matrix (row stride `ld` elements) into
+ * int8/e4m3 values and f32 scales.
+ *   group    0 (per-token scale, scales [rows]) or 32/64/128 (scales
+ *            [ceil(cols/group), rows], rows contiguous)
+ *   rotation 0 or 128 (normalized Walsh-Hadamard H128 with the reference's
+ *            Rademacher signs; cols % 128 == 0)
+ * Used for activations per call and for weights once at load. */
+int qlin_row_quantize(const void *src, int ld, int rows, int cols, int src_type, void *values,
+                      float *scales, int fmt, int group, int rotation, qlin_stream_t stream);
+
+/* Choose a path for a shape (host only, no device calls). */
+int qlin_plan(int rows, int N, int K, int fmt, int input_group, int weight_group,
+              qlin_path *path);
+
+/* Workspace bytes `path` needs for this shape (0 when none). */
+size_t qlin_workspace_bytes(const qlin_path *path, int rows, int N, int K, int fmt,
+                            int input_group, int weight_group);
+
+/* y = D(dequant(x . w^T)). `path` may be NULL (planned internally, same as
+ * qlin_plan). input_group / weight_group: 0 = per-row scales, 128 = K-group
+ * scales (group_int8 / group_fp8). Shape rules of the reference make_plan
+ * (ops/cuda/quantization.cpp:210-222): K % 16 == 0, N % 16 == 0, and for
+ * INT8 K <= 131071. */
+int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void *w,
+              const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
+              int input_group, int weight_group, void *workspace, size_t workspace_bytes,
+              qlin_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLINEAR_H */

@@ -1,0 +1,224 @@
+"""ctypes front end of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker. The product path
+(breeze_tts_cpp_amd) never imports it.
+
+All arrays are numpy; 16-bit floats travel as uint16 bit patterns.
+Reference citations for each function are in qlinear_oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+BF16, F32, I32, FP8, I8, F16 = 0, 1, 2, 3, 4, 5
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-C", _HERE, "-B" if force else "all"], check=True,
+                       stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i = ctypes.c_int
+        L.orc_bf16_to_f32.restype = ctypes.c_float
+        L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f32_to_bf16.restype = ctypes.c_uint16
+        L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_fp8_decode.restype = ctypes.c_float
+        L.orc_fp8_decode.argtypes = [ctypes.c_uint8]
+        L.orc_fp8_encode.restype = ctypes.c_uint8
+        L.orc_fp8_encode.argtypes = [ctypes.c_float]
+        L.orc_i8_round.restype = i
+        L.orc_i8_round.argtypes = [ctypes.c_float]
+        L.orc_scale.restype = ctypes.c_float
+        L.orc_scale.argtypes = [ctypes.c_float, i]
+        L.orc_rotation_sign.restype = ctypes.c_float
+        L.orc_rotation_sign.argtypes = [i]
+        L.orc_rotate128.restype = None
+        L.orc_rotate128.argtypes = [P, i]
+        L.orc_quantize_rows.restype = i
+        L.orc_quantize_rows.argtypes = [P, i, i, i, i, i, i, i, P, P]
+        L.orc_gemm_i8_acc.restype = None
+        L.orc_gemm_i8_acc.argtypes = [P, P, i, i, i, P]
+        L.orc_epilogue_i8.restype = None
+        L.orc_epilogue_i8.argtypes = [P, P, P, i, i, i, i, P]
+        L.orc_gemm_fp8_ideal.restype = None
+        L.orc_gemm_fp8_ideal.argtypes = [P, P, P, P, i, i, i, P]
+        L.orc_gemm_grouped.restype = i
+        L.orc_gemm_grouped.argtypes = [P, P, P, P, i, i, i, i, i, i, i, i, i, i, P, P]
+        L.orc_gemm_grouped_ideal.restype = None
+        L.orc_gemm_grouped_ideal.argtypes = [P, P, P, P, i, i, i, i, i, i, P]
+        L.orc_cpu_qlinear.restype = i
+        L.orc_cpu_qlinear.argtypes = [P, i, i, i, i, P, P, i, i, i, i, P, P, P, i]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- scalar codecs
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    f = lib().orc_f32_to_bf16
+    flat = np.asarray(x, np.float32).ravel()
+    return np.fromiter((f(float(v)) for v in flat), np.uint16, flat.size).reshape(np.shape(x))
+
+
+def fp8_decode_table() -> np.ndarray:
+    f = lib().orc_fp8_decode
+    return np.array([f(c) for c in range(256)], np.float32)
+
+
+def fp8_encode(x) -> np.ndarray:
+    f = lib().orc_fp8_encode
+    flat = np.asarray(x, np.float32).ravel()
+    return np.fromiter((f(float(v)) for v in flat), np.uint8, flat.size).reshape(np.shape(x))
+
+
+def i8_round(x) -> np.ndarray:
+    f = lib().orc_i8_round
+    flat = np.asarray(x, np.float32).ravel()
+    return np.fromiter((f(float(v)) for v in flat), np.int32, flat.size).reshape(np.shape(x))
+
+
+def quant_scale(amax: float, fmt: int) -> float:
+    return lib().orc_scale(float(amax), fmt)
+
+
+def rotation_signs(columns: int) -> np.ndarray:
+    f = lib().orc_rotation_sign
+    return np.array([f(c) for c in range(columns)], np.float32)
+
+
+def rotate128(v: np.ndarray, c0: int) -> np.ndarray:
+    out = np.ascontiguousarray(v, np.float32).copy()
+    assert out.size == 128
+    lib().orc_rotate128(_p(out), c0)
+    return out
+
+
+# ---------------------------------------------------------------- quantizer / GEMMs
+def quantize_rows(src_bits: np.ndarray, fmt: int, group: int = 0, rotation: int = 0,
+                  src_type: int = BF16, ld: int | None = None, cols: int | None = None):
+    """Returns (values uint8 [rows, cols], scales f32 [rows] or [G, rows])."""
+    src_bits = np.ascontiguousarray(src_bits, np.uint16)
+    rows = src_bits.shape[0]
+    ld = src_bits.shape[1] if ld is None else ld
+    cols = src_bits.shape[1] if cols is None else cols
+    q = np.zeros((rows, cols), np.uint8)
+    groups = (cols + group - 1) // group if group else 1
+    scales = np.zeros((groups, rows) if group else (rows,), np.float32)
+    rc = lib().orc_quantize_rows(_p(src_bits), src_type, ld, rows, cols, fmt, group, rotation,
+                                 _p(q), _p(scales))
+    if rc:
+        raise ValueError("oracle: unsupported quantization layout")
+    return q, scales
+
+
+def gemm_i8_acc(xq: np.ndarray, wq: np.ndarray) -> np.ndarray:
+    xq = np.ascontiguousarray(xq).view(np.int8)
+    wq = np.ascontiguousarray(wq).view(np.int8)
+    M, K = xq.shape
+    N = wq.shape[0]
+    acc = np.zeros((M, N), np.int32)
+    lib().orc_gemm_i8_acc(_p(xq), _p(wq), M, N, K, _p(acc))
+    return acc
+
+
+def epilogue_i8(acc, sx, sw, order: int = 0, out_type: int = BF16) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, np.int32)
+    sx = np.ascontiguousarray(sx, np.float32)
+    sw = np.ascontiguousarray(sw, np.float32)
+    M, N = acc.shape
+    y = np.zeros((M, N), np.uint16)
+    lib().orc_epilogue_i8(_p(acc), _p(sx), _p(sw), M, N, order, out_type, _p(y))
+    return y
+
+
+def gemm_fp8_ideal(xq, sx, wq, sw) -> np.ndarray:
+    xq = np.ascontiguousarray(xq, np.uint8)
+    wq = np.ascontiguousarray(wq, np.uint8)
+    sx = np.ascontiguousarray(sx, np.float32)
+    sw = np.ascontiguousarray(sw, np.float32)
+    M, K = xq.shape
+    N = wq.shape[0]
+    y = np.zeros((M, N), np.float32)
+    lib().orc_gemm_fp8_ideal(_p(xq), _p(sx), _p(wq), _p(sw), M, N, K, _p(y))
+    return y
+
+
+def gemm_grouped(xq, sx, wq, sw, fmt: int, input_group: int, weight_group: int,
+                 splits: int = 1, waves: int = 1, span: int | None = None,
+                 out_type: int = BF16):
+    """Returns (y 16-bit bits [M,N], y fp32 before the final rounding)."""
+    xq = np.ascontiguousarray(xq, np.uint8)
+    wq = np.ascontiguousarray(wq, np.uint8)
+    sx = np.ascontiguousarray(sx, np.float32)
+    sw = np.ascontiguousarray(sw, np.float32)
+    M, K = xq.shape
+    N = wq.shape[0]
+    if span is None:
+        span = -(-K // (splits * waves))
+    y = np.zeros((M, N), np.uint16)
+    yf = np.zeros((M, N), np.float32)
+    rc = lib().orc_gemm_grouped(_p(xq), _p(sx), _p(wq), _p(sw), M, N, K, fmt, input_group,
+                                weight_group, splits, waves, span, out_type, _p(y), _p(yf))
+    if rc:
+        raise ValueError("oracle: unsupported grouped GEMM layout")
+    return y, yf
+
+
+def gemm_grouped_ideal(xq, sx, wq, sw, fmt: int, input_group: int, weight_group: int):
+    xq = np.ascontiguousarray(xq, np.uint8)
+    wq = np.ascontiguousarray(wq, np.uint8)
+    sx = np.ascontiguousarray(sx, np.float32)
+    sw = np.ascontiguousarray(sw, np.float32)
+    M, K = xq.shape
+    N = wq.shape[0]
+    y = np.zeros((M, N), np.float32)
+    lib().orc_gemm_grouped_ideal(_p(xq), _p(sx), _p(wq), _p(sw), M, N, K, fmt, input_group,
+                                 weight_group, _p(y))
+    return y
+
+
+def cpu_qlinear(x_bits, wq, sw, fmt: int, group: int = 0, rotation: int = 0,
+                threads: int = 1, out_type: int = BF16):
+    """The whole per-call path on the CPU (quantize X, GEMM, dequant)."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint16)
+    wq = np.ascontiguousarray(wq, np.uint8)
+    sw = np.ascontiguousarray(sw, np.float32)
+    M, K = x_bits.shape
+    N = wq.shape[0]
+    y = np.zeros((M, N), np.uint16)
+    xq = np.zeros((M, K), np.uint8)
+    groups = (K + group - 1) // group if group else 1
+    sx = np.zeros((groups * M,), np.float32)
+    lib().orc_cpu_qlinear(_p(x_bits), BF16, M, N, K, _p(wq), _p(sw), fmt, group, rotation,
+                          out_type, _p(y), _p(xq), _p(sx), threads)
+    return y

@@ -1,0 +1,442 @@
+/*
+ * qlinear_oracle.c — CPU restatement of TTS.cpp's quantized linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the parity checker for the HIP
+ * library in breeze_tts_cpp_amd/. Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it; the product path never does.
+ *
+ * Every function names the reference file:line whose arithmetic it restates
+ * (paths relative to the reference's src/). Build flags (oracle/Makefile):
+ * -O3 -ffp-contract=off -fno-fast-math, so that every a*b+c here is two
+ * IEEE fp32 roundings, matching the reference's `--fmad=false` translation
+ * units (CMakeLists.txt:93-104). Where the reference leaves fusion to nvcc
+ * (quant_grouped.cu:144) the contraction is written explicitly with fmaf().
+ *
+ * Pinning (tests/test_oracle.py): FP8 codec exhaustively against its closed
+ * form and torch.float8_e4m3fn; INT8 quant against the closed form and
+ * special cases; rotation against an explicit Sylvester-matrix product and
+ * orthogonality; GEMMs against brute force, linearity and fp64 products.
+ * NaN propagation through the quantizers is "parity unpinned": the reference
+ * mixes fmaxf (NaN-dropping) with integer max over float bits, and no test of
+ * the reference fixes which one a NaN meets first.
+ */
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* Storage codes follow tts::Type (core/tensor.h:8). */
+enum { T_BF16 = 0, T_F32 = 1, T_I32 = 2, T_FP8 = 3, T_I8 = 4, T_F16 = 5 };
+
+/* ---------------------------------------------------------------- 16-bit floats */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* Round-to-nearest-even fp32 -> bf16 (__float2bfloat16_rn semantics). */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    int exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0x1f) return u2f(sign | 0x7f800000u | (man << 13));
+    if (exp == 0) { /* subnormal: man * 2^-24, exact in fp32 */
+        float v = (float)man * 5.9604644775390625e-8f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((uint32_t)(exp - 15 + 127) << 23) | (man << 13));
+}
+
+/* Round-to-nearest-even fp32 -> IEEE half (__float2half_rn semantics). */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t u = f2u(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    float a = fabsf(f);
+    if (a != a) return (uint16_t)(sign | 0x7e00u);
+    if (a >= 65520.f) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
+    if (a < 6.103515625e-05f) { /* half subnormal range: step 2^-24 */
+        float q = nearbyintf(a * 16777216.f);           /* exact scale, RNE */
+        return (uint16_t)(sign | (uint16_t)q);           /* q == 1024 is min normal */
+    }
+    int e;
+    float m = frexpf(a, &e); /* a = m * 2^e, m in [0.5,1) */
+    float q = nearbyintf(m * 2048.f); /* 11 significant bits, RNE */
+    if (q >= 2048.f) { q = 1024.f; ++e; }
+    int biased = e - 1 + 15;
+    if (biased >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | (uint16_t)(biased << 10) | (uint16_t)((int)q - 1024));
+}
+
+static inline float load_src(const void *p, int type, size_t i) {
+    const uint16_t *h = (const uint16_t *)p;
+    return type == T_F16 ? orc_f16_to_f32(h[i]) : orc_bf16_to_f32(h[i]);
+}
+static inline uint16_t store_out(float v, int type) {
+    return type == T_F16 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+}
+
+/* ---------------------------------------------------------------- 8-bit codecs */
+/* Format<FP8>::decode (ops/kernels/quant/quant_format.cuh:18-22): OCP e4m3fn,
+ * bias 7, 3 mantissa bits, 0x7f/0xff NaN, max finite 448. */
+float orc_fp8_decode(uint8_t c) {
+    int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+    float v;
+    if (e == 15 && m == 7) return s ? -NAN : NAN;
+    if (e == 0) v = (float)m * 0.001953125f; /* m * 2^-9 */
+    else v = ldexpf(1.f + (float)m / 8.f, e - 7);
+    return s ? -v : v;
+}
+
+/* Format<FP8>::encode (quant_format.cuh:12-14): __nv_fp8_e4m3(x), i.e.
+ * round-to-nearest-even with saturation to +-448 (satfinite). */
+uint8_t orc_fp8_encode(float x) {
+    uint8_t sign = (f2u(x) >> 31) ? 0x80 : 0;
+    float a = fabsf(x);
+    if (a != a) return 0x7f;
+    if (a >= 448.f) return sign | 0x7e; /* satfinite: 448 and above -> max finite */
+    if (a < 0.015625f) {                /* below 2^-6: subnormal step 2^-9 */
+        float q = nearbyintf(a * 512.f); /* q in [0, 8]; 8 encodes 2^-6 (0x08) */
+        return sign | (uint8_t)q;
+    }
+    int e;
+    float m = frexpf(a, &e);            /* a = m * 2^e, m in [0.5, 1) */
+    float q = nearbyintf(m * 16.f);     /* 4 significant bits, RNE, q in [8, 16] */
+    if (q >= 16.f) { q = 8.f; ++e; }
+    int biased = e - 1 + 7;             /* >= 1 here; a < 448 keeps it <= 15 */
+    return sign | (uint8_t)(biased << 3) | (uint8_t)((int)q - 8);
+}
+
+/* Format<I8>::rounded (quant_format.cuh:37-44): clamp to +-127, then RNE. */
+int orc_i8_round(float x) {
+    x = fminf(127.f, fmaxf(-127.f, x));
+    return (int)nearbyintf(x);
+}
+
+static inline uint8_t encode(float x, int fmt) {
+    return fmt == T_I8 ? (uint8_t)(int8_t)orc_i8_round(x) : orc_fp8_encode(x);
+}
+
+/* quant_device::scale (quant_format.cuh:62-64). */
+float orc_scale(float amax, int fmt) {
+    float range = fmt == T_I8 ? 127.f : 448.f;
+    return amax == 0 ? 1.f : fmaxf(amax / range, FLT_MIN);
+}
+
+/* ---------------------------------------------------------------- H128 rotation */
+/* Rademacher sign of rotate_pack (quant_device.cuh:162-169), absolute column. */
+float orc_rotation_sign(int column) {
+    uint32_t h = (uint32_t)column * 0x45d9f3bu;
+    h = (h ^ (h >> 16)) * 0x45d9f3bu;
+    return ((h ^ (h >> 16)) & 1u) ? 1.f : -1.f;
+}
+
+/* rotate_pack (quant_device.cuh:161-190) over one 128-column block starting at
+ * absolute column c0: sign, Sylvester butterflies with ascending stride
+ * (lower index gets a+b, upper gets a-b), then a separate multiply by
+ * 0.08838834764831845f. */
+void orc_rotate128(float *v, int c0) {
+    for (int i = 0; i < 128; ++i) v[i] = v[i] * orc_rotation_sign(c0 + i);
+    for (int span = 1; span < 128; span *= 2)
+        for (int i = 0; i < 128; ++i)
+            if (!(i & span)) {
+                float a = v[i], b = v[i | span];
+                v[i] = a + b;
+                v[i | span] = a - b;
+            }
+    for (int i = 0; i < 128; ++i) v[i] *= 0.08838834764831845f;
+}
+
+/* ---------------------------------------------------------------- row quantizer */
+/* launch_row_quantize (ops/kernels/quant/row_quantize.cu:167-193) and its
+ * kernels: dynamic/cached_token_quantize (:24-87, same arithmetic),
+ * rotated_token_quantize (:90-115), group_token_quantize + encode_group
+ * (:145-165, quant_device.cuh:63-88). Scales: [rows] for per-token,
+ * [ceil(K/group), rows] group-major otherwise (core/quantization.h:24-32).
+ * Returns 0, or -1 on an unsupported layout. */
+int orc_quantize_rows(const void *src, int src_type, int ld, int rows, int cols, int fmt,
+                      int group, int rotation, uint8_t *q, float *scales) {
+    if (rotation && (rotation != 128 || cols % 128)) return -1;
+    if (group && group != 32 && group != 64 && group != 128) return -1;
+    float *row = (float *)malloc(sizeof(float) * (size_t)cols);
+    if (!row) return -1;
+    int groups = group ? (cols + group - 1) / group : 1;
+    for (int r = 0; r < rows; ++r) {
+        for (int c = 0; c < cols; ++c) row[c] = load_src(src, src_type, (size_t)r * ld + c);
+        if (rotation)
+            for (int c0 = 0; c0 < cols; c0 += 128) orc_rotate128(row + c0, c0);
+        if (group) {
+            for (int g = 0; g < groups; ++g) {
+                int c0 = g * group, c1 = c0 + group < cols ? c0 + group : cols;
+                float amax = 0;
+                for (int c = c0; c < c1; ++c) amax = fmaxf(amax, fabsf(row[c]));
+                float step = orc_scale(amax, fmt), inverse = 1.f / step;
+                scales[(size_t)g * rows + r] = step;
+                for (int c = c0; c < c1; ++c) q[(size_t)r * cols + c] = encode(row[c] * inverse, fmt);
+            }
+        } else {
+            float amax = 0;
+            for (int c = 0; c < cols; ++c) amax = fmaxf(amax, fabsf(row[c]));
+            float step = orc_scale(amax, fmt), inverse = 1.f / step;
+            scales[r] = step;
+            for (int c = 0; c < cols; ++c) q[(size_t)r * cols + c] = encode(row[c] * inverse, fmt);
+        }
+    }
+    free(row);
+    return 0;
+}
+
+/* ---------------------------------------------------------------- GEMMs */
+/* Exact INT8 GEMM: acc[m][n] = sum_k x[m][k]*w[n][k] in int32. Any tiling or
+ * split of the reference (quant_dispatch.cu:58-61 dp4a, quant_gemm_sm80.cu
+ * mma.16x8x32, split-K partials) produces exactly this value. */
+void orc_gemm_i8_acc(const int8_t *x, const int8_t *w, int M, int N, int K, int32_t *acc) {
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            int32_t s = 0;
+            const int8_t *a = x + (size_t)m * K, *b = w + (size_t)n * K;
+            for (int k = 0; k < K; ++k) s += (int32_t)a[k] * (int32_t)b[k];
+            acc[(size_t)m * N + n] = s;
+        }
+}
+
+/* INT8 per-channel epilogue. order 0: D((acc*sx)*sw) — the CUTLASS EVT tree of
+ * quant_gemm_sm80.cu:24-29 (and sm90 :131-132); order 1: D((acc*sw)*sx) — the
+ * GEMV store of quant_dispatch.cu:125. */
+void orc_epilogue_i8(const int32_t *acc, const float *sx, const float *sw, int M, int N,
+                     int order, int out_type, uint16_t *y) {
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            float a = (float)acc[(size_t)m * N + n], v;
+            if (order == 0) { v = a * sx[m]; v = v * sw[n]; }
+            else { v = a * sw[n]; v = v * sx[m]; }
+            y[(size_t)m * N + n] = store_out(v, out_type);
+        }
+}
+
+/* FP8 per-channel ideal: exact products of e4m3 pairs summed in fp64, scaled
+ * by sx*sw in fp64. The reference accumulates in fp32 in a hardware order
+ * (sm90 WGMMA promotion, cuBLASLt) that no CPU can restate; FP8 parity is
+ * therefore a tolerance against this value (rel-L2). */
+void orc_gemm_fp8_ideal(const uint8_t *x, const float *sx, const uint8_t *w, const float *sw,
+                        int M, int N, int K, float *y) {
+    float lut[256];
+    for (int i = 0; i < 256; ++i) lut[i] = orc_fp8_decode((uint8_t)i);
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double s = 0;
+            const uint8_t *a = x + (size_t)m * K, *b = w + (size_t)n * K;
+            for (int k = 0; k < K; ++k) s += (double)lut[a[k]] * (double)lut[b[k]];
+            y[(size_t)m * N + n] = (float)(s * (double)sx[m] * (double)sw[n]);
+        }
+}
+
+/* K-group GEMM of grouped_gemm (quant_grouped.cu:79-166) and its split-K
+ * reduction (quant_grouped.cu:221-239, quant_reduce.cuh:9-19).
+ * K is cut into splits*waves ranges of `span` columns (range r = s*waves+w
+ * covers [r*span, min(K, (r+1)*span))). Inside a range, groups ascending:
+ *   p_g   = sum_{k in g} x*w              (int32 exact for INT8;
+ *                                           fp64-then-fp32 for FP8)
+ *   scale = sxg * swg                      (quant_grouped.cu:135)
+ *   r     = fmaf(p_g, scale, r)            (quant_grouped.cu:144, FMA-contracted)
+ * A split's ranges are summed R_s = 0 + r_0 + r_1 + ..., then R_s *= the
+ * outer scale of a side without groups (quant_grouped.cu:161-163), and
+ * y = D(0 + R_0 + R_1 + ...) (quant_reduce.cuh:14-17). With splits = waves =
+ * 1 and span >= K this is the reference's single-partition kernel (up to the
+ * sign of an exact zero). The loop group is the smaller nonzero group
+ * (quant_grouped.cu:185-187). Returns -1 on an unsupported layout. */
+int orc_gemm_grouped(const uint8_t *x, const float *sx, const uint8_t *w, const float *sw,
+                     int M, int N, int K, int fmt, int input_group, int weight_group, int splits,
+                     int waves, int span, int out_type, uint16_t *y, float *y_f32) {
+    int g = input_group ? input_group : weight_group;
+    if (weight_group && weight_group < g) g = weight_group;
+    if (!g || splits < 1 || waves < 1 || span < 1 || span % g) return -1;
+    if ((long long)splits * waves * span < K) return -1;
+    float lut[256];
+    for (int i = 0; i < 256; ++i) lut[i] = orc_fp8_decode((uint8_t)i);
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            float total = 0;
+            for (int s = 0; s < splits; ++s) {
+                float R = 0;
+                for (int wv = 0; wv < waves; ++wv) {
+                    int r0 = (s * waves + wv) * span;
+                    int r1 = r0 + span < K ? r0 + span : K;
+                    float r = 0;
+                    for (int k0 = r0; k0 < r1; k0 += g) {
+                        int k1 = k0 + g < K ? k0 + g : K;
+                        float p;
+                        if (fmt == T_I8) {
+                            int32_t acc = 0;
+                            for (int k = k0; k < k1; ++k)
+                                acc += (int32_t)(int8_t)x[(size_t)m * K + k] *
+                                       (int32_t)(int8_t)w[(size_t)n * K + k];
+                            p = (float)acc;
+                        } else {
+                            double acc = 0;
+                            for (int k = k0; k < k1; ++k)
+                                acc += (double)lut[x[(size_t)m * K + k]] *
+                                       (double)lut[w[(size_t)n * K + k]];
+                            p = (float)acc;
+                        }
+                        float sa = input_group ? sx[(size_t)(k0 / input_group) * M + m] : 1.f;
+                        float sb = weight_group ? sw[(size_t)(k0 / weight_group) * N + n] : 1.f;
+                        r = fmaf(p, sa * sb, r);
+                    }
+                    R = R + r;
+                }
+                float outer = input_group ? 1.f : sx[m];
+                if (!weight_group) outer *= sw[n];
+                R = R * outer;
+                total = total + R;
+            }
+            if (y) y[(size_t)m * N + n] = store_out(total, out_type);
+            if (y_f32) y_f32[(size_t)m * N + n] = total;
+        }
+    return 0;
+}
+
+/* fp64 ideal of the grouped GEMM for tolerance checks: sum_g p_g*sxg*swg. */
+void orc_gemm_grouped_ideal(const uint8_t *x, const float *sx, const uint8_t *w, const float *sw,
+                            int M, int N, int K, int fmt, int input_group, int weight_group,
+                            float *y) {
+    float lut[256];
+    for (int i = 0; i < 256; ++i)
+        lut[i] = fmt == T_I8 ? (float)(int8_t)i : orc_fp8_decode((uint8_t)i);
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double s = 0;
+            for (int k = 0; k < K; ++k) {
+                double a = lut[x[(size_t)m * K + k]], b = lut[w[(size_t)n * K + k]];
+                a *= input_group ? sx[(size_t)(k / input_group) * M + m] : sx[m];
+                b *= weight_group ? sw[(size_t)(k / weight_group) * N + n] : sw[n];
+                s += a * b;
+            }
+            y[(size_t)m * N + n] = (float)s;
+        }
+}
+
+/* ---------------------------------------------------------------- CPU baseline */
+/* Multithreaded quant -> GEMM -> dequant of the whole path (the same work the
+ * GPU does per call), used as the reported CPU baseline. INT8 per-channel:
+ * int32 dot products vectorised by the compiler; epilogue order 0. FP8:
+ * 256-entry decode table, fp32 accumulation. Grouped modes: per-K-group
+ * partials as orc_gemm_grouped with one split. */
+typedef struct {
+    const uint8_t *xq, *wq;
+    const float *sx, *sw;
+    uint16_t *y;
+    int M, N, K, fmt, group, n0, n1, out_type;
+    const float *lut;
+} job_t;
+
+static void *gemm_job(void *arg) {
+    job_t *j = (job_t *)arg;
+    int M = j->M, N = j->N, K = j->K, G = j->group;
+    for (int n = j->n0; n < j->n1; ++n) {
+        const uint8_t *b = j->wq + (size_t)n * K;
+        for (int m = 0; m < M; ++m) {
+            const uint8_t *a = j->xq + (size_t)m * K;
+            float v;
+            if (j->fmt == T_I8 && !G) {
+                const int8_t *ai = (const int8_t *)a, *bi = (const int8_t *)b;
+                int32_t s = 0;
+                for (int k = 0; k < K; ++k) s += (int32_t)ai[k] * (int32_t)bi[k];
+                v = (float)s * j->sx[m];
+                v = v * j->sw[n];
+            } else if (!G) {
+                float s = 0;
+                for (int k = 0; k < K; ++k) s += j->lut[a[k]] * j->lut[b[k]];
+                v = s * j->sx[m];
+                v = v * j->sw[n];
+            } else {
+                float r = 0;
+                for (int k0 = 0; k0 < K; k0 += G) {
+                    float p;
+                    if (j->fmt == T_I8) {
+                        const int8_t *ai = (const int8_t *)a, *bi = (const int8_t *)b;
+                        int32_t s = 0;
+                        for (int k = k0; k < k0 + G; ++k) s += (int32_t)ai[k] * (int32_t)bi[k];
+                        p = (float)s;
+                    } else {
+                        float s = 0;
+                        for (int k = k0; k < k0 + G; ++k) s += j->lut[a[k]] * j->lut[b[k]];
+                        p = s;
+                    }
+                    r = fmaf(p, j->sx[(size_t)(k0 / G) * M + m] * j->sw[(size_t)(k0 / G) * N + n], r);
+                }
+                v = r;
+            }
+            j->y[(size_t)m * N + n] = store_out(v, j->out_type);
+        }
+    }
+    return NULL;
+}
+
+typedef struct {
+    const void *src;
+    int src_type, ld, r0, r1, rows, cols, fmt, group, rotation;
+    uint8_t *q;
+    float *scales;
+} qjob_t;
+
+static void *quant_job(void *arg) {
+    qjob_t *j = (qjob_t *)arg;
+    int n = j->r1 - j->r0;
+    if (n <= 0) return NULL;
+    /* quantize a row slice into a private scale buffer, then scatter */
+    int groups = j->group ? (j->cols + j->group - 1) / j->group : 1;
+    float *sc = (float *)malloc(sizeof(float) * (size_t)n * groups);
+    const uint16_t *s = (const uint16_t *)j->src + (size_t)j->r0 * j->ld;
+    orc_quantize_rows(s, j->src_type, j->ld, n, j->cols, j->fmt, j->group, j->rotation,
+                      j->q + (size_t)j->r0 * j->cols, sc);
+    for (int g = 0; g < groups; ++g)
+        for (int r = 0; r < n; ++r)
+            j->scales[(size_t)g * (j->group ? j->rows : 0) + j->r0 + r] = sc[(size_t)g * n + r];
+    free(sc);
+    return NULL;
+}
+
+/* One quantized linear call on the CPU: quantize X (bf16 [M,K]) with the
+ * mode's activation layout, then GEMM against pre-quantized weights and
+ * store bf16/f16. Weight quantization happens at load time in the reference
+ * (io/weights.cpp:80-87) and is not part of a call. */
+int orc_cpu_qlinear(const void *x, int x_type, int M, int N, int K, const uint8_t *wq,
+                    const float *sw, int fmt, int group, int rotation, int out_type,
+                    uint16_t *y, uint8_t *xq_scratch, float *sx_scratch, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    qjob_t qj[256];
+    int rows_per = (M + threads - 1) / threads;
+    int qt = 0;
+    for (int t = 0; t < threads; ++t) {
+        int r0 = t * rows_per, r1 = r0 + rows_per < M ? r0 + rows_per : M;
+        if (r0 >= r1) break;
+        qj[t] = (qjob_t){x, x_type, K, r0, r1, M, K, fmt, group, rotation, xq_scratch, sx_scratch};
+        pthread_create(&tid[t], NULL, quant_job, &qj[t]);
+        ++qt;
+    }
+    for (int t = 0; t < qt; ++t) pthread_join(tid[t], NULL);
+    float lut[256];
+    for (int i = 0; i < 256; ++i) lut[i] = orc_fp8_decode((uint8_t)i);
+    job_t jobs[256];
+    int per = (N + threads - 1) / threads, started = 0;
+    for (int t = 0; t < threads; ++t) {
+        int n0 = t * per, n1 = n0 + per < N ? n0 + per : N;
+        if (n0 >= n1) break;
+        jobs[t] = (job_t){xq_scratch, wq, sx_scratch, sw, y, M, N, K, fmt, group, n0, n1, out_type, lut};
+        pthread_create(&tid[t], NULL, gemm_job, &jobs[t]);
+        ++started;
+    }
+    for (int t = 0; t < started; ++t) pthread_join(tid[t], NULL);
+    return 0;
+}

@@ -1,0 +1,202 @@
+"""Parity of the HIP quantized GEMM (qlin_gemm through the C ABI) against the
+oracle.
+
+INT8 per-channel: bf16 output bit-exact against D((acc*sx)*sw) with exact
+int32 acc (the CUTLASS EVT order, quant_gemm_sm80.cu:24-29), hence within one
+bf16 ulp of the GEMV order (acc*sw)*sx (quant_dispatch.cu:125).
+INT8 K-group: bit-exact against the oracle's grouped accumulation with the
+same K partition (quant_grouped.cu:112-166).
+FP8: rel-L2 <= 1e-2 against the fp64 product of the quantized operands
+(tolerance of the task contract; the reference's fp32 accumulation order is
+hardware-defined)."""
+import numpy as np
+import pytest
+import torch
+
+from breeze_tts_cpp_amd import synthetic
+
+BF16, F32, I32, FP8, I8, F16 = 0, 1, 2, 3, 4, 5
+pytestmark = pytest.mark.gpu
+FP8_REL_L2 = 1e-2
+
+
+def dev_u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint8)).to(dev)
+
+
+def dev_f32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+
+
+def out_bits(y: torch.Tensor) -> np.ndarray:
+    return y.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def bits_to_f32(bits, out_type=BF16):
+    if out_type == F16:
+        return bits.view(np.float16).astype(np.float32)
+    return synthetic.bf16_bits_to_f32(bits)
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / np.linalg.norm(b))
+
+
+_cache = {}
+
+
+def operands(orc, M, N, K, fmt, group=0, rotation=0, seed=0):
+    key = (M, N, K, fmt, group, rotation, seed)
+    if key not in _cache:
+        xb = synthetic.activations(M, K, seed=seed)
+        wb = synthetic.weights(N, K, seed=seed)
+        xq, sx = orc.quantize_rows(xb, fmt, group=group, rotation=rotation)
+        wq, sw = orc.quantize_rows(wb, fmt, group=group, rotation=rotation)
+        _cache.clear()
+        _cache[key] = (xq, sx, wq, sw)
+    return _cache[key]
+
+
+def gpu_gemm(dev, xq, sx, wq, sw, fmt, group=0, path=None, out_dtype=torch.bfloat16):
+    from breeze_tts_cpp_amd import qlinear
+    y = qlinear.gemm(dev_u8(xq, dev), dev_f32(sx, dev), dev_u8(wq, dev), dev_f32(sw, dev), fmt,
+                     out_dtype=out_dtype, input_group=group, weight_group=group, path=path)
+    torch.cuda.synchronize()
+    return out_bits(y)
+
+
+def check_i8(orc, y, xq, sx, wq, sw, out_type=BF16):
+    acc = orc.gemm_i8_acc(xq, wq)
+    ref = orc.epilogue_i8(acc, sx, sw, order=0, out_type=out_type)
+    alt = orc.epilogue_i8(acc, sx, sw, order=1, out_type=out_type)
+    assert np.array_equal(y, ref), f"{np.count_nonzero(y != ref)} mismatches of {y.size}"
+    assert np.abs(y.astype(np.int32) - alt.astype(np.int32)).max() <= 1
+
+
+PROJ = [(4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144)]
+
+
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 64])
+@pytest.mark.parametrize("N,K", PROJ)
+def test_i8_decode_projections(dev, orc, M, N, K):
+    print(f"i8 decode M={M} N={N} K={K}", flush=True)
+    xq, sx, wq, sw = operands(orc, M, N, K, I8, seed=M + N)
+    y = gpu_gemm(dev, xq, sx, wq, sw, I8)
+    check_i8(orc, y, xq, sx, wq, sw)
+
+
+def test_i8_config0(dev, orc):
+    """M=16, N=K=2048, seed 0."""
+    xq, sx, wq, sw = operands(orc, 16, 2048, 2048, I8, seed=0)
+    y = gpu_gemm(dev, xq, sx, wq, sw, I8)
+    check_i8(orc, y, xq, sx, wq, sw)
+
+
+def _skinny_paths(K):
+    from breeze_tts_cpp_amd.qlinear import Path, KIND_SKINNY
+    blocks = -(-K // 256)
+    for tokens in (16, 32, 64):
+        for channels in (16, 32):
+            for waves in (1, 2, 4, 8):
+                for splits in (1, 2, 3):
+                    if blocks % (waves * splits) == 0:
+                        yield Path(KIND_SKINNY, tokens, channels, splits, waves)
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+def test_skinny_path_variants(dev, orc, fmt):
+    """Every skinny variant (token tile, channel tile, in-workgroup and grid
+    K splits) gives the same bits for INT8 and agrees within tolerance for FP8."""
+    M, N, K = 40, 96, 1536
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=21)
+    for p in _skinny_paths(K):
+        print(f"skinny path {p}", flush=True)
+        y = gpu_gemm(dev, xq, sx, wq, sw, fmt, path=p)
+        if fmt == I8:
+            check_i8(orc, y, xq, sx, wq, sw)
+        else:
+            ideal = orc.gemm_fp8_ideal(xq, sx, wq, sw)
+            assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
+
+
+@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("N,K", PROJ)
+def test_fp8_decode_projections(dev, orc, M, N, K):
+    print(f"fp8 decode M={M} N={N} K={K}", flush=True)
+    xq, sx, wq, sw = operands(orc, M, N, K, FP8, seed=M + 3)
+    y = gpu_gemm(dev, xq, sx, wq, sw, FP8)
+    ideal = orc.gemm_fp8_ideal(xq, sx, wq, sw)
+    err = rel_l2(bits_to_f32(y), ideal)
+    print(f"  rel_l2={err:.3e}")
+    assert err <= FP8_REL_L2
+    # much tighter in practice: bf16 output rounding dominates
+    assert err <= 4e-3
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 6144)])
+def test_grouped_decode(dev, orc, fmt, M, N, K):
+    from breeze_tts_cpp_amd import qlinear
+    print(f"grouped decode fmt={fmt} M={M} N={N} K={K}", flush=True)
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=128, rotation=128, seed=M + 5)
+    p = qlinear.plan(M, N, K, fmt, 128, 128)
+    y = gpu_gemm(dev, xq, sx, wq, sw, fmt, group=128, path=p)
+    span = -(-K // 256) * 256 // (p.splits * p.waves)
+    ref, ref_f = orc.gemm_grouped(xq, sx, wq, sw, fmt, 128, 128, p.splits, p.waves, span)
+    if fmt == I8:
+        assert np.array_equal(y, ref), f"{np.count_nonzero(y != ref)} mismatches"
+    else:
+        ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, 128, 128)
+        assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
+
+
+def test_grouped_path_variants(dev, orc):
+    M, N, K = 24, 64, 1536
+    xq, sx, wq, sw = operands(orc, M, N, K, I8, group=128, rotation=128, seed=31)
+    for p in _skinny_paths(K):
+        y = gpu_gemm(dev, xq, sx, wq, sw, I8, group=128, path=p)
+        span = -(-K // 256) * 256 // (p.splits * p.waves)
+        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, I8, 128, 128, p.splits, p.waves, span)
+        assert np.array_equal(y, ref), p
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+def test_f16_output(dev, orc, fmt):
+    M, N, K = 32, 256, 2048
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=41)
+    y = gpu_gemm(dev, xq, sx, wq, sw, fmt, out_dtype=torch.float16)
+    if fmt == I8:
+        check_i8(orc, y, xq, sx, wq, sw, out_type=F16)
+    else:
+        ideal = orc.gemm_fp8_ideal(xq, sx, wq, sw)
+        assert rel_l2(bits_to_f32(y, F16), ideal) <= FP8_REL_L2
+
+
+def test_ragged_k(dev, orc):
+    """K a multiple of 16 but not of 64/256 (masked tail pieces)."""
+    for K in (16, 80, 272, 2064):
+        xq, sx, wq, sw = operands(orc, 9, 48, K, I8, seed=K)
+        y = gpu_gemm(dev, xq, sx, wq, sw, I8)
+        check_i8(orc, y, xq, sx, wq, sw)
+
+
+def test_end_to_end_linear(dev, orc):
+    """quantize -> GEMM -> bf16 through the library equals the CPU pipeline."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N, K = 16, 2048, 2048
+    xb = synthetic.activations(M, K, seed=0)
+    wb = synthetic.weights(N, K, seed=0)
+    for fmt, group, rot in ((I8, 0, 0), (I8, 128, 128)):
+        wq, sw = orc.quantize_rows(wb, fmt, group=group, rotation=rot)
+        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+        p = qlinear.plan(M, N, K, fmt, group, group)
+        y = qlinear.linear(x, dev_u8(wq, dev), dev_f32(sw, dev), fmt, group, rot, path=p)
+        torch.cuda.synchronize()
+        xq, sx = orc.quantize_rows(xb, fmt, group=group, rotation=rot)
+        if group:
+            span = -(-K // 256) * 256 // (p.splits * p.waves)
+            ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, 128, 128, p.splits, p.waves, span)
+        else:
+            ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw)
+        assert np.array_equal(out_bits(y), ref)
