@@ -61,14 +61,17 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         p.waves = waves;
         return p;
     }
-    p.kind = QLIN_KIND_SKINNY;
-    p.tokens = 64;
-    p.channels = 16;
+    // Prefill: the largest macro tile that still gives every CU a tile.
+    p.kind = QLIN_KIND_TILED;
     p.splits = 1;
-    const int blocks_k = (K + 255) / 256;
-    int waves = 4;
-    while (waves > 1 && blocks_k % waves) waves /= 2;
-    p.waves = waves;
+    p.waves = 1;
+    static const int shapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+    for (const auto &s : shapes) {
+        long tiles = long((N + s[0] - 1) / s[0]) * ((rows + s[1] - 1) / s[1]);
+        p.channels = s[0];
+        p.tokens = s[1];
+        if (tiles >= 256) break;
+    }
     return p;
 }
 
@@ -92,6 +95,17 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED,
                         "skinny path splits*waves (%d) must divide ceil(K/256) = %d",
                         p.splits * p.waves, blocks_k);
+        if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
+        return ok();
+    }
+    if (p.kind == QLIN_KIND_TILED) {
+        if ((p.channels != 128 && p.channels != 256) || (p.tokens != 128 && p.tokens != 256))
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "tiled path channels/tokens must be 128 or 256 (got %d/%d)", p.channels,
+                        p.tokens);
+        if (p.splits != 1)
+            return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no split-K variant");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
         return ok();
@@ -210,7 +224,7 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
     if (need && !aligned(workspace, 16))
         return fail(QLIN_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    int r = p.kind == QLIN_KIND_SKINNY ? qlin::launch_skinny(a, ip, s) : QLIN_ERR_UNSUPPORTED;
+    int r = p.kind == QLIN_KIND_SKINNY ? qlin::launch_skinny(a, ip, s) : qlin::launch_tiled(a, ip, s);
     if (r) return fail(r, "no kernel variant for this path");
     return check_launch("quantized GEMM launch");
 }

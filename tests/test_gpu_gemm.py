@@ -200,3 +200,66 @@ def test_end_to_end_linear(dev, orc):
         else:
             ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw)
         assert np.array_equal(out_bits(y), ref)
+
+
+# ---------------------------------------------------------------- prefill (tiled) GEMM
+def _tiled_paths():
+    from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
+    for channels in (128, 256):
+        for tokens in (128, 256):
+            yield Path(KIND_TILED, tokens, channels, 1, 1)
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("M,N,K", [(200, 144, 336), (300, 272, 1024), (130, 512, 2048)])
+def test_tiled_variants_ragged(dev, orc, fmt, M, N, K):
+    """Every macro-tile shape on ragged M/N edges and K not a multiple of 128."""
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=M + N + K)
+    ideal = None if fmt == I8 else orc.gemm_fp8_ideal(xq, sx, wq, sw)
+    for p in _tiled_paths():
+        print(f"tiled path {p} M={M} N={N} K={K}", flush=True)
+        y = gpu_gemm(dev, xq, sx, wq, sw, fmt, path=p)
+        if fmt == I8:
+            check_i8(orc, y, xq, sx, wq, sw)
+        else:
+            assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("M", [1024, 4096])
+@pytest.mark.parametrize("N,K", PROJ)
+def test_prefill_projections(dev, orc, fmt, M, N, K):
+    """Full prefill shapes (BASELINE configs 2 and 4) through the planned path.
+    Rows are independent, so the oracle checks a sample of 48 token rows
+    (including the first and last tile) against the full GPU output."""
+    print(f"prefill fmt={fmt} M={M} N={N} K={K}", flush=True)
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=M + N)
+    y = gpu_gemm(dev, xq, sx, wq, sw, fmt)
+    rng = np.random.default_rng(M + N + K)
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, M - 1], rng.choice(M, 43, replace=False)]))
+    xs, sxs = xq[rows], sx[rows]
+    if fmt == I8:
+        check_i8(orc, y[rows], xs, sxs, wq, sw)
+    else:
+        ideal = orc.gemm_fp8_ideal(xs, sxs, wq, sw)
+        assert rel_l2(bits_to_f32(y[rows]), ideal) <= FP8_REL_L2
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 1024), (320, 400, 2048), (4096, 2048, 6144)])
+def test_tiled_grouped(dev, orc, fmt, M, N, K):
+    from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
+    print(f"tiled grouped fmt={fmt} M={M} N={N} K={K}", flush=True)
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=128, rotation=128, seed=M + 9)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 30)]))
+    paths = list(_tiled_paths()) if M * N <= 320 * 400 else [None]
+    for p in paths:
+        y = gpu_gemm(dev, xq, sx, wq, sw, fmt, group=128, path=p)
+        xs = xq[rows]
+        sxs = np.ascontiguousarray(sx[:, rows])
+        if fmt == I8:
+            ref, _ = orc.gemm_grouped(xs, sxs, wq, sw, fmt, 128, 128)
+            assert np.array_equal(y[rows], ref), p
+        else:
+            ideal = orc.gemm_grouped_ideal(xs, sxs, wq, sw, fmt, 128, 128)
+            assert rel_l2(bits_to_f32(y[rows]), ideal) <= FP8_REL_L2
