@@ -54,6 +54,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--profile", action="store_true",
+                    help="short run for rocprofv3 counter passes: a 64 MiB device copy "
+                         "(calibrates FETCH_SIZE/WRITE_SIZE), then the decode GEMM graphs "
+                         "and one prefill GEMM per format; prints no JSON")
     return ap.parse_args()
 
 
@@ -117,6 +121,10 @@ def main():
                 qlinear.row_quantize(io["x"], I8, values=io["xq"], scales=io["sx"], stream=stream)
                 qlinear.gemm(io["xq"], io["sx"], wt["wq"], wt["sw"], I8, path=io["path"],
                              out=io["y"], stream=stream)
+
+    if args.profile:
+        profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections)
+        return
 
     # eager reference of one step, then capture the step as a graph
     with torch.cuda.stream(stream):
@@ -183,7 +191,8 @@ def main():
     d = per_proj[dominant]
     roofline = {"bound": "hbm", "kernel": f"skinny_gemm INT8 {dominant} M={M_DECODE}",
                 "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(d["GBps"] / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(dominant),
                 "bytes_per_launch": d["bytes"]}
 
     result = {
@@ -216,6 +225,56 @@ def main():
         result["cpu_baseline"] = cpu_baseline(args, value)
 
     print(json.dumps(result), flush=True)
+
+
+# Decode GEMM grid sizes (threads) per projection at M=32 with the planned path,
+# used to find the kernel's row in the committed counter summary.
+_DECODE_GRID = {"qkv": "131072", "gate_up": "393216"}
+
+
+def measured_traffic(name):
+    """HBM bytes per launch of the decode GEMM for `name`, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/hbm_traffic_decode_prefill.md,
+    copy-kernel calibrated); None when that summary has no row for it."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_prefill.md")
+    grid = _DECODE_GRID.get(name)
+    if not grid or not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.split("|")]
+        if len(cells) > 6 and cells[1].startswith("`skinny_gemm") and cells[2] == grid:
+            return int(cells[6].replace(",", ""))
+    return None
+
+
+def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections):
+    """Kernels for counter passes, in this order: one 64 MiB copy (known
+    traffic: 64 MiB read + 64 MiB written), 5 replays of each projection's
+    16-layer decode GEMM graph, then one M=4096 INT8 and FP8 GEMM per
+    projection."""
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for name, (N, K) in projections:
+        io = inputs[name]
+        for _ in range(5):
+            for entry in layers:
+                qlinear.gemm(io["xq"], io["sx"], entry[name]["wq"], entry[name]["sw"], qlinear.I8,
+                             path=io["path"], out=io["y"], stream=stream)
+    torch.cuda.synchronize()
+    M = M_PREFILL
+    for fmt in (qlinear.I8, qlinear.FP8):
+        for name, (N, K) in projections:
+            x = torch.from_numpy(synthetic.activations(M, K, seed=1).view(np.int16)).view(
+                torch.bfloat16).to(dev)
+            w = torch.from_numpy(synthetic.weights(N, K, seed=1).view(np.int16)).view(
+                torch.bfloat16).to(dev)
+            xq, sx = qlinear.row_quantize(x, fmt, stream=stream)
+            wq, sw = qlinear.row_quantize(w, fmt, stream=stream)
+            qlinear.gemm(xq, sx, wq, sw, fmt, stream=stream)
+            torch.cuda.synchronize()
 
 
 def bench_prefill(torch, qlinear, synthetic, dev, stream, args):

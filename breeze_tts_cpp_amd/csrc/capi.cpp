@@ -44,9 +44,6 @@ int check_launch(const char *what) {
 // weights once through the skinny kernel; larger token counts use the
 // LDS-tiled MFMA GEMM.
 qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_group) {
-    (void)fmt;
-    (void)input_group;
-    (void)weight_group;
     qlin_path p{};
     if (rows <= 64) {
         p.kind = QLIN_KIND_SKINNY;
@@ -62,16 +59,22 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         return p;
     }
     // Prefill: the largest macro tile that still gives every CU a tile.
+    // INT8 256x256 runs eight waves of 128x64; FP8 keeps 128x128 tiles, whose
+    // 32-byte operand fragments still fit a double-buffered register set.
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;
-    static const int shapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+    static const int shapes[3][2] = {{256, 256}, {256, 128}, {128, 128}};
+    const bool grouped = input_group || weight_group;
     for (const auto &s : shapes) {
+        if (grouped && s[1] == 256) continue;
+        if (fmt == QLIN_FP8 && !grouped && s[0] == 256) continue;
         long tiles = long((N + s[0] - 1) / s[0]) * ((rows + s[1] - 1) / s[1]);
         p.channels = s[0];
         p.tokens = s[1];
         if (tiles >= 256) break;
     }
+    if (p.channels == 256 && p.tokens == 256) p.waves = 8;
     return p;
 }
 
@@ -100,12 +103,19 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         return ok();
     }
     if (p.kind == QLIN_KIND_TILED) {
-        if ((p.channels != 128 && p.channels != 256) || (p.tokens != 128 && p.tokens != 256))
+        if (!((p.channels == 256 && (p.tokens == 256 || p.tokens == 128)) ||
+              (p.channels == 128 && p.tokens == 128)))
             return fail(QLIN_ERR_UNSUPPORTED,
-                        "tiled path channels/tokens must be 128 or 256 (got %d/%d)", p.channels,
+                        "tiled path channels x tokens must be 256x256, 256x128 or 128x128 (got %dx%d)", p.channels,
                         p.tokens);
         if (p.splits != 1)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no split-K variant");
+        if (p.waves != 1 && p.waves != 8)
+            return fail(QLIN_ERR_UNSUPPORTED, "tiled path waves must be 1 or 8");
+        if (p.waves == 8 && !(p.channels == 256 && p.tokens == 256))
+            return fail(QLIN_ERR_UNSUPPORTED, "eight-wave tiled path is 256x256 only");
+        if ((input_group || weight_group) && p.tokens == 256)
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
         return ok();

@@ -6,75 +6,92 @@
 // FP8 WGMMA kernels (quant_gemm_sm90.cu:16-283) and the K-group GEMM
 // (quant_grouped.cu:16-169, quant_gemm_sm90.cu:289-372).
 //
-// Work decomposition: one workgroup per (BN weight rows) x (BM token rows)
-// macro tile; 64*WN*WM threads; each wave64 owns a 128 (weight rows) x 64
-// (tokens) sub-tile = 8 x 4 MFMA 16x16 tiles, 128 accumulator registers.
-// K advances in 128-byte stages through a double-buffered LDS ring: global
-// loads for stage s+1 are in flight while stage s feeds the MFMAs. LDS rows
-// are 128 bytes; the 16-byte chunk c of row r lives at chunk c ^ ((r>>1)&7),
-// which makes both the 16-byte stores and the MFMA fragment reads
-// bank-conflict free (16 lanes of a phase hit 16 distinct 16-byte slots).
-// The weight tile is the MFMA A operand, so each lane's accumulator holds
-// four consecutive output channels of one token: 8-byte output stores.
+// Work decomposition: one workgroup per macro tile of BN weight rows x BM
+// tokens; WN x WM wave64s, each owning a (16*WTN) x (16*WTM) sub-tile of
+// 16x16 MFMA tiles (INT8: v_mfma_i32_16x16x64_i8, exact int32; FP8:
+// v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales).
+//
+// Operand staging: K advances in BK-byte stages through a STAGES-deep LDS
+// ring filled by buffer_load ... lds (global -> LDS without registers), so
+// STAGES-1 stages are in flight while one feeds the MFMAs. Each wave's load
+// instruction writes 1 KB of LDS contiguously in lane order; the swizzle is
+// applied by choosing each lane's global source chunk, so that 16-byte chunk
+// c of stage row r sits at chunk c ^ ((r >> 1) & (CPR - 1)). With it the MFMA
+// fragment reads (16 rows, same logical chunk) measured free of LDS bank
+// conflicts on gfx950 (SQ_LDS_BANK_CONFLICT = 0), where the unswizzled
+// layout takes 12 conflict cycles per ds_read_b128. Buffer descriptors cover exactly the tile's valid rows, so rows
+// past the matrix edge and chunks past K read as zero (out-of-range offset).
+// The weight tile is the MFMA A operand: a lane's accumulator holds four
+// consecutive output channels of one token -> 8-byte output stores.
 // Tiles are numbered XCD-major (consecutive tiles on one XCD share its L2).
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 
+#include <algorithm>
+#include <type_traits>
+
 namespace qlin {
 namespace {
 
-constexpr int kBK = 128;          // bytes of K per stage (= one K group of 128)
-constexpr int kWaveN = 128;       // weight rows per wave
-constexpr int kWaveM = 64;        // tokens per wave
-
-// A 128-byte K slice of one MFMA operand row group: 32 bytes per lane, the two
-// 16-byte halves covering K [0,64) and [64,128) of the stage.
 template <int Fmt> struct TileMma;
 template <> struct TileMma<I8> {
     using Acc = i32x4;
-    // 128 K = two v_mfma_i32_16x16x64_i8.
-    __device__ static void run(Acc &c, const i32x8 &a, const i32x8 &b) {
-        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(a, a, 0, 1, 2, 3),
-                                                  __builtin_shufflevector(b, b, 0, 1, 2, 3), c, 0,
-                                                  0, 0);
-        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(a, a, 4, 5, 6, 7),
-                                                  __builtin_shufflevector(b, b, 4, 5, 6, 7), c, 0,
-                                                  0, 0);
+    __device__ static void run(Acc &c, const i32x4 &a, const i32x4 &b) {
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
     }
 };
 template <> struct TileMma<FP8> {
     using Acc = f32x4;
-    // 128 K = one v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 x e4m3, unit scales).
     __device__ static void run(Acc &c, const i32x8 &a, const i32x8 &b) {
         c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0,
                                                              0x7f7f7f7f);
     }
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
-
-template <class Out>
-__device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4]) {
-    uint2 packed;
-    packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
-    packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
-    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + index) = packed;
+// Physical 16-byte chunk of logical chunk c in stage row r is c ^ swizzle(r).
+template <int BK> __device__ __forceinline__ int swizzle(int r) {
+    if constexpr (BK == 128) return (r >> 1) & 7;
+    else return (r >> 1) & 3;
 }
 
-template <int Fmt, int WN, int WM, bool Grouped, bool KFull, class Out>
+// s_waitcnt vmcnt(n) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for the LDS ring: this wave's LDS reads are complete
+// (lgkmcnt(0)) before any wave passes, so a buffer read before the barrier
+// may be refilled after it. No memory fence: the global->LDS loads are waited
+// for explicitly with wait_vmcnt.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, bool KFull,
+          class Out>
 __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
     int tiles_n, int input_group, int weight_group) {
-    constexpr int BN = kWaveN * WN, BM = kWaveM * WM, T = 64 * WN * WM;
-    constexpr int kChunks = (BN + BM) * (kBK / 16);    // 16-byte chunks per stage
-    constexpr int kPerThread = kChunks / T;
-    static_assert(kChunks % T == 0, "stage chunks must divide evenly");
+    constexpr int NW = WN * WM;
+    constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
+    constexpr int CPR = BK / 16;          // 16-byte chunks per stage row
+    constexpr int RPI = 64 / CPR;         // stage rows written by one wave instruction
+    constexpr int ROWS = BN + BM;
+    constexpr int INSTS = ROWS / (RPI * NW);
+    constexpr int W_INSTS = BN / (RPI * NW);
+    constexpr int STAGE_BYTES = ROWS * BK;
+    static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
+    static_assert(Fmt == I8 || BK == 128, "FP8 MFMA consumes 128 bytes of K");
+    static_assert(!Grouped || BK == 128, "one K group of 128 per stage");
     using MMA = TileMma<Fmt>;
     using Acc = typename MMA::Acc;
 
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int kStageBytes = (BN + BM) * kBK;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
     // XCD-major tile numbering: hardware places workgroup b on XCD b % 8.
     const int tiles = tiles_m * tiles_n;
@@ -83,138 +100,209 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const int tn = b / tiles_m, tm = b % tiles_m;
     const int n_base = tn * BN, m_base = tm * BM;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wave_n = wave % WN, wave_m = wave / WN;
     const int row16 = lane & 15, quad = lane >> 4;
 
-    // Chunk i of this thread: stage row row0 + i*(T/8), 16-byte column tid&7.
-    // Rows [0, BN) are weight rows, [BN, BN+BM) token rows; rows past the
-    // matrix edge are clamped to a valid row (their outputs are not stored).
-    constexpr int kRowStep = T / 8;
-    constexpr int kWeightChunks = BN / kRowStep;
-    const int row0 = tid >> 3, chunk0 = tid & 7;
-    uint32_t src_off[kPerThread];
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-        const int row = row0 + i * kRowStep;
-        if (i < kWeightChunks)
-            src_off[i] = uint32_t(min(n_base + row, N - 1)) * uint32_t(K) + chunk0 * 16;
-        else
-            src_off[i] = uint32_t(min(m_base + row - BN, M - 1)) * uint32_t(K) + chunk0 * 16;
-    }
-    const int lds_off0 = row0 * kBK + swz(row0, chunk0) * 16;
+    const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w + size_t(n_base) * K), 0, min(BN, N - n_base) * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_x = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(x + size_t(m_base) * K), 0, min(BM, M - m_base) * K, 0x00020000);
 
-    Acc acc[Grouped ? 1 : 8][4];
-    float facc[Grouped ? 8 : 1][Grouped ? 4 : 1][4];
+    // Load instruction i of this wave fills stage rows [(i*NW + wave)*RPI, +RPI),
+    // 1 KB of LDS in lane order: lane -> row += lane / CPR, physical chunk
+    // lane % CPR. Every instruction's first row is a multiple of RPI, so the
+    // swizzle (row bits 1..) and thus the lane's source column are the same
+    // for all i: a per-lane voffset plus a wave-uniform soffset per i.
+    const int lane_row = lane / CPR;
+    const int lane_chunk = (lane % CPR) ^ swizzle<BK>(wave * RPI + lane_row);
+    const uint32_t lane_voff = uint32_t(lane_row) * uint32_t(K) + uint32_t(lane_chunk * 16);
+    auto issue = [&](int stage, int k0) {
+        uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
+        const uint32_t voff =
+            (KFull || k0 + lane_chunk * 16 < K) ? lane_voff + uint32_t(k0) : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < INSTS; ++i) {
+            const int row = (i * NW + wave) * RPI;
+            const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
+            lds_ptr_t dst = (lds_ptr_t)(base + (i * NW + wave) * 1024);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rsrc_w : rsrc_x, dst, 16, voff,
+                                                     soff, 0, 0);
+        }
+    };
+
+    Acc acc[Grouped ? 1 : WTN][WTM];
+    float facc[Grouped ? WTN : 1][Grouped ? WTM : 1][4];
     if constexpr (!Grouped) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < WTN; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+            for (int j = 0; j < WTM; ++j) acc[i][j] = Acc{0, 0, 0, 0};
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < WTN; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < WTM; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) facc[i][j][r] = 0.f;
     }
 
-    i32x4 staged[kPerThread];
-    auto load_stage = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const uint8_t *base = i < kWeightChunks ? w : x;
-            if (KFull || k0 + chunk0 * 16 < K)
-                staged[i] = *reinterpret_cast<const i32x4 *>(base + src_off[i] + uint32_t(k0));
-            else
-                staged[i] = i32x4{0, 0, 0, 0};
-        }
+    // Fragment of stage row `row`, 64-K sub-step h: lane quad q holds K bytes
+    // [64h + 16q, +16). Rows row0 + 16i share row bits 1..3, hence the chunk.
+    auto frag16 = [&](const uint8_t *base, int row, int h) {
+        const int chunk = (h * 4 + quad) ^ swizzle<BK>(row);
+        return *reinterpret_cast<const i32x4 *>(base + row * BK + chunk * 16);
     };
-    auto store_stage = [&](uint8_t *base) {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i)
-            *reinterpret_cast<i32x4 *>(base + lds_off0 + i * kRowStep * kBK) = staged[i];
-    };
-    // 32-byte operand fragment of stage row `row`: K [16*quad, +16) and
-    // [64 + 16*quad, +16).
-    auto fragment = [&](const uint8_t *base, int row) {
-        i32x4 lo = *reinterpret_cast<const i32x4 *>(base + row * kBK + swz(row, quad) * 16);
-        i32x4 hi = *reinterpret_cast<const i32x4 *>(base + row * kBK + swz(row, 4 + quad) * 16);
+    auto frag32 = [&](const uint8_t *base, int row) {
+        const i32x4 lo = frag16(base, row, 0), hi = frag16(base, row, 1);
         return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
-    const int stages = (K + kBK - 1) / kBK;
-    load_stage(0);
-    store_stage(lds);
-    __syncthreads();
-
-    // Fragment rows within the stage: weight rows for A, token rows for B.
-    const int a_row0 = wave_n * kWaveN + row16;
-    const int b_row0 = BN + wave_m * kWaveM + row16;
-
-    for (int s = 0; s < stages; ++s) {
-        const uint8_t *cur = lds + (s & 1) * kStageBytes;
-        if (s + 1 < stages) load_stage((s + 1) * kBK);
-
-        i32x8 bf[4];
+    const int stages = (K + BK - 1) / BK;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[j] = fragment(cur, b_row0 + j * 16);
-        if constexpr (!Grouped) {
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < stages) issue(s, s * BK);
+
+    const int a_row0 = wave_n * 16 * WTN + row16;
+    const int b_row0 = BN + wave_m * 16 * WTM + row16;
+
+    if constexpr (!Grouped) {
+        // Software pipeline, one MFMA sub-step per stage (INT8: BK = 64,
+        // FP8: BK = 128). Iteration s: issue the global loads of stage
+        // s+STAGES-1; run the first MFMA rows of stage s; wait for stage s+1
+        // and barrier; read stage s+1 fragments into the other register set
+        // while the remaining MFMAs of stage s run. The barrier also retires
+        // every wave's reads of buffer s % STAGES, which iteration s+1 refills.
+        static_assert(Fmt == FP8 || BK == 64, "INT8 pipeline uses 64-byte stages");
+        using Frag = std::conditional_t<Fmt == I8, i32x4, i32x8>;
+        const int a_off = a_row0 * BK, b_off = b_row0 * BK;
+        const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
+        const int a_c1 = ((4 + quad) ^ swizzle<BK>(a_row0)) * 16;
+        const int b_c1 = ((4 + quad) ^ swizzle<BK>(b_row0)) * 16;
+        auto read = [&](int st, Frag (&a)[WTN], Frag (&bb)[WTM]) {
+            const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
+            const uint8_t *pa = cur + a_off, *pb = cur + b_off;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const i32x8 af = fragment(cur, a_row0 + i * 16);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) MMA::run(acc[i][j], af, bf[j]);
+            for (int j = 0; j < WTM; ++j) {
+                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c0);
+                if constexpr (Fmt == I8) {
+                    bb[j] = lo;
+                } else {
+                    const i32x4 hi = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c1);
+                    bb[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
             }
-        } else {
+#pragma unroll
+            for (int i = 0; i < WTN; ++i) {
+                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c0);
+                if constexpr (Fmt == I8) {
+                    a[i] = lo;
+                } else {
+                    const i32x4 hi = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c1);
+                    a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+        };
+        auto mma = [&](const Frag (&a)[WTN], const Frag (&bb)[WTM], int i0, int i1) {
+#pragma unroll
+            for (int i = i0; i < i1; ++i)
+#pragma unroll
+                for (int j = 0; j < WTM; ++j) MMA::run(acc[i][j], a[i], bb[j]);
+        };
+        constexpr int kEarly = WTN / 4;  // MFMA rows issued before the barrier
+        auto step = [&](int s, const Frag (&a)[WTN], const Frag (&bb)[WTM], Frag (&na)[WTN],
+                        Frag (&nb)[WTM]) {
+            if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
+            mma(a, bb, 0, kEarly);
+            if (s + 1 < stages) {
+                if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+                else wait_vmcnt<0>();
+                lds_barrier();
+                read(s + 1, na, nb);
+            }
+            mma(a, bb, kEarly, WTN);
+        };
+        Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
+        wait_vmcnt<INSTS * (STAGES - 2)>();
+        lds_barrier();
+        read(0, a0, b0);
+        int s = 0;
+        for (; s + 1 < stages; s += 2) {
+            step(s, a0, b0, a1, b1);
+            step(s + 1, a1, b1, a0, b0);
+        }
+        if (s < stages) step(s, a0, b0, a1, b1);
+    } else {
+        for (int s = 0; s < stages; ++s) {
+            // Stage s has landed once at most the newer stages are outstanding.
+            if (s + STAGES - 2 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
+            const uint8_t *cur = lds + (s % STAGES) * STAGE_BYTES;
             // One 128-wide K group per stage: r = fmaf(p, sxg*swg, r).
-            const int k = s * kBK;
+            const int k = s * BK;
             const int g_in = input_group ? k / input_group : 0;
             const int g_w = weight_group ? k / weight_group : 0;
-            float sxg[4];
+            float sxg[WTM];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int m = min(m_base + wave_m * kWaveM + j * 16 + row16, M - 1);
+            for (int j = 0; j < WTM; ++j) {
+                int m = min(m_base + wave_m * 16 * WTM + j * 16 + row16, M - 1);
                 sxg[j] = input_group ? sx[size_t(g_in) * M + m] : 1.f;
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const i32x8 af = fragment(cur, a_row0 + i * 16);
-                Acc part[4];
+            for (int i = 0; i < WTN; ++i) {
+                Acc part[WTM];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    part[j] = Acc{0, 0, 0, 0};
-                    MMA::run(part[j], af, bf[j]);
+                for (int j = 0; j < WTM; ++j) part[j] = Acc{0, 0, 0, 0};
+                if constexpr (Fmt == I8) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const i32x4 af = frag16(cur, a_row0 + i * 16, h);
+#pragma unroll
+                        for (int j = 0; j < WTM; ++j)
+                            MMA::run(part[j], af, frag16(cur, b_row0 + j * 16, h));
+                    }
+                } else {
+                    const i32x8 af = frag32(cur, a_row0 + i * 16);
+#pragma unroll
+                    for (int j = 0; j < WTM; ++j)
+                        MMA::run(part[j], af, frag32(cur, b_row0 + j * 16));
                 }
                 float swg[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    int n = min(n_base + wave_n * kWaveN + i * 16 + quad * 4 + r, N - 1);
+                    int n = min(n_base + wave_n * 16 * WTN + i * 16 + quad * 4 + r, N - 1);
                     swg[r] = weight_group ? sw[size_t(g_w) * N + n] : 1.f;
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < WTM; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         facc[i][j][r] =
                             __builtin_fmaf(float(part[j][r]), sxg[j] * swg[r], facc[i][j][r]);
             }
         }
-        if (s + 1 < stages) store_stage(lds + ((s + 1) & 1) * kStageBytes);
-        __syncthreads();
     }
 
-    // Epilogue: lane holds C[n = 4*quad + r][m = row16] of each 16x16 tile.
+    // Epilogue. A lane holds C[n = 4*quad + r][m = row16] of each 16x16 tile:
+    // scale, round to 16-bit, and transpose through LDS (the stage ring is
+    // free now) so that each token row of the wave's sub-tile leaves as
+    // contiguous 16-byte stores. Row m_l of the wave's [16*WTM][16*WTN]
+    // buffer keeps 16-byte chunk c at c ^ (m_l % CH): conflict-free both for
+    // the 8-byte column writes and the row reads.
+    constexpr int TM = 16 * WTM, TN = 16 * WTN, ROWB = TN * 2, CH = ROWB / 16;
+    lds_barrier();
+    uint8_t *wbuf = lds + wave * TM * ROWB;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = m_base + wave_m * kWaveM + j * 16 + row16;
-        if (m >= M) continue;
+    for (int j = 0; j < WTM; ++j) {
+        const int m_l = j * 16 + row16;
+        const int m = min(m_base + wave_m * TM + m_l, M - 1);
         const float sxm = sx[m];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int n = n_base + wave_n * kWaveN + i * 16 + quad * 4;
-            if (n >= N) continue;
+        for (int i = 0; i < WTN; ++i) {
+            const int n = min(n_base + wave_n * TN + i * 16 + quad * 4, N - 4);
             float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -227,36 +315,82 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                     v[r] = t * sw[n + r];
                 }
             }
-            store4<Out>(y, size_t(m) * N + n, v);
+            uint2 packed;
+            packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
+            packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
+            const int byte = i * 32 + quad * 8;
+            *reinterpret_cast<uint2 *>(wbuf + m_l * ROWB + (((byte >> 4) ^ (m_l % CH)) << 4) +
+                                       (byte & 15)) = packed;
+        }
+    }
+    const bool vec16 = (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+    for (int r0 = 0; r0 < TM; r0 += 64 / CH) {
+        const int m_l = r0 + lane / CH, c = lane % CH;
+        const uint4 val =
+            *reinterpret_cast<const uint4 *>(wbuf + m_l * ROWB + ((c ^ (m_l % CH)) << 4));
+        const int m = m_base + wave_m * TM + m_l, n = n_base + wave_n * TN + c * 8;
+        if (m >= M || n >= N) continue;
+        uint16_t *dst = static_cast<uint16_t *>(y) + size_t(m) * N + n;
+        if (vec16) {
+            *reinterpret_cast<uint4 *>(dst) = val;
+        } else {
+            reinterpret_cast<uint2 *>(dst)[0] = make_uint2(val.x, val.y);
+            reinterpret_cast<uint2 *>(dst)[1] = make_uint2(val.z, val.w);
         }
     }
 }
 
-template <int Fmt, int WN, int WM, bool Grouped, class Out>
+template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, class Out>
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
-    constexpr int BN = kWaveN * WN, BM = kWaveM * WM;
+    constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
     const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
-    const size_t lds = size_t(2) * (BN + BM) * kBK;
+    const size_t lds = std::max(size_t(STAGES) * (BN + BM) * BK, size_t(BN) * BM * 2);
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
-    if (a.K % kBK == 0)
-        hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, Grouped, true, Out>), grid, block, lds, stream,
-                           a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n,
-                           a.input_group, a.weight_group);
+    if (a.K % BK == 0)
+        hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, true, Out>),
+                           grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,
+                           tiles_m, tiles_n, a.input_group, a.weight_group);
     else
-        hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, Grouped, false, Out>), grid, block, lds,
-                           stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n,
-                           a.input_group, a.weight_group);
+        hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, false, Out>),
+                           grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,
+                           tiles_m, tiles_n, a.input_group, a.weight_group);
     return 0;
 }
 
+// Macro tiles (weight rows x tokens), all with four waves: 256x256 (waves of
+// 128x128), 256x128 (128x64) and 128x128 (64x64).
 template <int Fmt, bool Grouped, class Out>
 int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    // channels x tokens macro tile
-    if (p.channels == 256 && p.tokens == 256) return launch_shape<Fmt, 2, 4, Grouped, Out>(a, s);
-    if (p.channels == 256 && p.tokens == 128) return launch_shape<Fmt, 2, 2, Grouped, Out>(a, s);
-    if (p.channels == 128 && p.tokens == 256) return launch_shape<Fmt, 1, 4, Grouped, Out>(a, s);
-    if (p.channels == 128 && p.tokens == 128) return launch_shape<Fmt, 1, 2, Grouped, Out>(a, s);
-    return -4;
+    if constexpr (Grouped) {
+        // No 256x256: the fp32 group accumulators would double the 128x128
+        // register tile per wave and spill.
+        if (p.channels == 256 && p.tokens == 128)
+            return launch_shape<Fmt, 2, 2, 8, 4, 128, 3, true, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 128)
+            return launch_shape<Fmt, 2, 2, 4, 4, 128, 4, true, Out>(a, s);
+        return -4;
+    } else if constexpr (Fmt == I8) {
+        if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
+        if (p.channels == 256 && p.tokens == 256)
+            return launch_shape<Fmt, 2, 2, 8, 8, 64, 4, false, Out>(a, s);
+        if (p.channels == 256 && p.tokens == 128)
+            return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 128)
+            return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
+        return -4;
+    } else {
+        if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
+        if (p.channels == 256 && p.tokens == 256)
+            return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
+        if (p.channels == 256 && p.tokens == 128)
+            return launch_shape<Fmt, 2, 2, 8, 4, 128, 3, false, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 128)
+            return launch_shape<Fmt, 2, 2, 4, 4, 128, 4, false, Out>(a, s);
+        return -4;
+    }
 }
 
 template <int Fmt, class Out>

@@ -16,7 +16,7 @@ KIND_AUTO, KIND_SKINNY, KIND_TILED = 0, 1, 2
 STATUS = {0: "ok", -1: "invalid", -2: "alignment", -3: "workspace", -4: "unsupported", -5: "hip"}
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libqlinear.so")
+LIB_PATH = os.environ.get("QLINEAR_LIB") or os.path.join(_HERE, "libqlinear.so")
 _lib = None
 
 

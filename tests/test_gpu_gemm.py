@@ -203,10 +203,10 @@ def test_end_to_end_linear(dev, orc):
 
 
 # ---------------------------------------------------------------- prefill (tiled) GEMM
-def _tiled_paths():
+def _tiled_paths(grouped=False):
     from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
-    for channels in (128, 256):
-        for tokens in (128, 256):
+    for channels, tokens in ((256, 256), (256, 128), (128, 128)):
+        if not (grouped and tokens == 256):
             yield Path(KIND_TILED, tokens, channels, 1, 1)
 
 
@@ -252,7 +252,7 @@ def test_tiled_grouped(dev, orc, fmt, M, N, K):
     print(f"tiled grouped fmt={fmt} M={M} N={N} K={K}", flush=True)
     xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=128, rotation=128, seed=M + 9)
     rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 30)]))
-    paths = list(_tiled_paths()) if M * N <= 320 * 400 else [None]
+    paths = list(_tiled_paths(grouped=True)) if M * N <= 320 * 400 else [None]
     for p in paths:
         y = gpu_gemm(dev, xq, sx, wq, sw, fmt, group=128, path=p)
         xs = xq[rows]
