@@ -87,8 +87,8 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         if (p.tokens != 16 && p.tokens != 32 && p.tokens != 48 && p.tokens != 64)
             return fail(QLIN_ERR_UNSUPPORTED, "skinny path tokens must be 16/32/48/64 (got %d)",
                         p.tokens);
-        if (p.channels != 16 && p.channels != 32)
-            return fail(QLIN_ERR_UNSUPPORTED, "skinny path channels must be 16 or 32 (got %d)",
+        if (p.channels != 16 && p.channels != 32 && p.channels != 64)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny path channels must be 16, 32 or 64 (got %d)",
                         p.channels);
         if (p.waves != 1 && p.waves != 2 && p.waves != 4 && p.waves != 8)
             return fail(QLIN_ERR_UNSUPPORTED, "skinny path waves must be 1/2/4/8 (got %d)",

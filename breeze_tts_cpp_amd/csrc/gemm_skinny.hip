@@ -331,6 +331,7 @@ template <int Fmt, int MT, bool Grouped, class Out>
 int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if (p.channels == 16) return dispatch_wk<Fmt, MT, 1, Grouped, Out>(a, p, s);
     if (p.channels == 32) return dispatch_wk<Fmt, MT, 2, Grouped, Out>(a, p, s);
+    if (p.channels == 64) return dispatch_wk<Fmt, MT, 4, Grouped, Out>(a, p, s);
     return -4;
 }
 

@@ -1,0 +1,293 @@
+// C++ host interface (include/tts_qlinear.hpp) over the C ABI: the reference's
+// layer/op names and exceptions, implemented by calls into qlin_* entry points.
+#include "../../include/tts_qlinear.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <limits>
+#include <mutex>
+
+namespace tts {
+namespace {
+
+// Status -> exception of the reference's kind.
+void check(int status, const char *what) {
+    if (!status) return;
+    std::string message = std::string(what) + ": " + qlin_last_error();
+    switch (status) {
+    case QLIN_ERR_INVALID:
+    case QLIN_ERR_ALIGNMENT:
+    case QLIN_ERR_WORKSPACE: throw std::invalid_argument(message);
+    default: throw std::runtime_error(message);
+    }
+}
+
+int code(Type type) { return static_cast<int>(type); }
+
+}  // namespace
+
+// ---------------------------------------------------------------- metadata
+// include/tts/quantization.h:8-29
+const char *quantization_name(Quantization quantization) {
+    switch (quantization) {
+    case Quantization::None: return "none";
+    case Quantization::FP8: return "fp8";
+    case Quantization::INT8: return "int8";
+    case Quantization::GroupINT8: return "group_int8";
+    case Quantization::GroupFP8: return "group_fp8";
+    }
+    throw std::invalid_argument("invalid quantization mode");
+}
+
+Quantization quantization_from_string(const std::string &name) {
+    if (name.empty()) return Quantization::None;
+    if (name == "fp8") return Quantization::FP8;
+    if (name == "int8") return Quantization::INT8;
+    if (name == "group_int8") return Quantization::GroupINT8;
+    if (name == "group_fp8") return Quantization::GroupFP8;
+    throw std::invalid_argument("quantization must be int8, fp8, group_int8 or group_fp8");
+}
+
+// core/quantization.h:6-23
+Type quantized_type(Quantization quantization) {
+    if (quantization == Quantization::FP8 || quantization == Quantization::GroupFP8)
+        return Type::FP8;
+    if (quantization == Quantization::INT8 || quantization == Quantization::GroupINT8)
+        return Type::I8;
+    throw std::invalid_argument("BF16 has no quantized storage type");
+}
+
+QuantizationGroups quantization_groups(Quantization quantization) {
+    if (quantization == Quantization::GroupINT8 || quantization == Quantization::GroupFP8)
+        return {128, 128, 128};
+    return {};
+}
+
+// core/quantization.h:39-48
+void RowScaledView::validate() const {
+    const bool groups_ok =
+        !group_size || group_size == 32 || group_size == 64 || group_size == 128;
+    if ((values.type != Type::FP8 && values.type != Type::I8) || !values.dense() ||
+        (rotation_size && (rotation_size != 128 || values.cols % 128)) || !groups_ok ||
+        scales.type != Type::F32 || !scales.dense() ||
+        scales.numel() != size_t(values.rows) * size_t(groups()) ||
+        (group_size && (scales.rows != groups() || scales.cols != values.rows)) ||
+        values.device != scales.device)
+        throw std::invalid_argument("invalid row-scaled quantized tensor");
+}
+
+// core/row_capacity.h:10-19
+int row_capacity(int rows, unsigned bins_per_octave) {
+    if (rows < 1 || !bins_per_octave) throw std::invalid_argument("invalid row capacity class");
+    int64_t upper = 1;
+    while (upper < rows) upper *= 2;
+    int64_t step = std::max<int64_t>(1, upper / (2ll * bins_per_octave));
+    int64_t capacity = (int64_t(rows) + step - 1) / step * step;
+    return int(std::min<int64_t>(capacity, std::numeric_limits<int>::max()));
+}
+
+// ---------------------------------------------------------------- launchers
+void launch_row_quantize(TensorView source, RowScaledView destination, qlin_stream_t stream) {
+    check(qlin_row_quantize(source.data, source.ld(), source.rows, source.cols, code(source.type),
+                            destination.values.data, destination.scales.ptr<float>(),
+                            code(destination.values.type), destination.group_size,
+                            destination.rotation_size, stream),
+          "row quantization");
+}
+
+void launch_quant_linear(LinearPath config, KernelProblem shape, const void *input,
+                         const float *input_scales, const void *weights,
+                         const float *weight_scales, void *output, void *workspace,
+                         size_t workspace_bytes, qlin_stream_t stream, Type format,
+                         Type output_type) {
+    qlin_path path{static_cast<int>(config.kind), config.tokens, config.channels, config.splits,
+                   config.waves};
+    check(qlin_gemm(&path, input, input_scales, weights, weight_scales, output, shape.rows,
+                    shape.channels, shape.reduction, code(format), code(output_type),
+                    shape.input_group, shape.weight_group, workspace, workspace_bytes, stream),
+          "quantized GEMM");
+}
+
+// quant_grouped.cu:221-239: the token tile and split count select the variant;
+// splits > 1 need a workspace of rows*channels*splits floats.
+void grouped_quant_gemm(KernelProblem problem, const void *input, const float *input_scales,
+                        const void *weights, const float *weight_scales, void *output,
+                        qlin_stream_t stream, Type format, Type output_type, int tokens,
+                        int splits, void *workspace, size_t workspace_bytes) {
+    if (!problem.input_group && !problem.weight_group)
+        throw std::invalid_argument("grouped GEMM requires K-group scales");
+    qlin_path planned{};
+    check(qlin_plan(problem.rows, problem.channels, problem.reduction, code(format),
+                    problem.input_group, problem.weight_group, &planned),
+          "grouped GEMM plan");
+    LinearPath path{static_cast<LinearKind>(planned.kind), planned.tokens, planned.channels,
+                    planned.splits, planned.waves};
+    if (path.kind == LinearKind::Skinny) {
+        path.tokens = std::max(16, std::min(64, tokens));
+        if (splits > 1) path.splits = splits;
+    }
+    launch_quant_linear(path, problem, input, input_scales, weights, weight_scales, output,
+                        workspace, workspace_bytes, stream, format, output_type);
+}
+
+// ---------------------------------------------------------------- QuantizedGemm
+QuantizedGemm::QuantizedGemm(qlin_stream_t stream, void *workspace, size_t workspace_bytes,
+                             Type format)
+    : stream_(stream), workspace_(workspace), workspace_bytes_(workspace_bytes), format_(format) {
+    if (format != Type::FP8 && format != Type::I8)
+        throw std::invalid_argument("unsupported quantized storage type");
+}
+
+void QuantizedGemm::seal() { sealed_ = true; }
+
+QuantCacheStats QuantizedGemm::cache_stats() const {
+    QuantCacheStats result{};
+    result.selection = stats_;
+    result.selection.entries = plans_.size();
+    result.prepared_plans = plans_.size();
+    return result;
+}
+
+LinearPath QuantizedGemm::planned(int rows, int channels, int reduction, Type output_type,
+                                  QuantizationGroups groups) const {
+    auto it = plans_.find(Key{row_capacity(rows), channels, reduction, output_type,
+                              groups.activation, groups.weight});
+    if (it == plans_.end())
+        throw std::logic_error("quantized GEMM shape was not prepared before execution");
+    return it->second;
+}
+
+// ops/cuda/quantization.cpp:366-393 and the shape rules of make_plan (:206-222).
+void QuantizedGemm::prepare(int rows, int channels, int reduction, Type output_type,
+                            QuantizationGroups groups) {
+    if (output_type != Type::BF16 && output_type != Type::F16)
+        throw std::invalid_argument("quantized GEMM output must be F16 or BF16");
+    rows = row_capacity(rows);
+    Key key{rows, channels, reduction, output_type, groups.activation, groups.weight};
+    if (plans_.count(key)) {
+        ++stats_.hits;
+        return;
+    }
+    if (sealed_) throw std::logic_error("prepared resource missing after initialization");
+    if (rows < 1 || channels < 1 || reduction < 1 || reduction % 16 || channels % 16)
+        throw std::invalid_argument("quantized GEMM unsupported shape");
+    if (format_ == Type::I8 && reduction > INT32_MAX / (128 * 128))
+        throw std::invalid_argument("INT8 reduction can overflow INT32");
+    qlin_path p{};
+    check(qlin_plan(rows, channels, reduction, code(format_), groups.activation, groups.weight,
+                    &p),
+          "quantized GEMM plan");
+    if (qlin_workspace_bytes(&p, rows, channels, reduction, code(format_), groups.activation,
+                             groups.weight) > workspace_bytes_)
+        throw std::invalid_argument("quantized GEMM workspace overflow");
+    plans_.emplace(key, LinearPath{static_cast<LinearKind>(p.kind), p.tokens, p.channels,
+                                   p.splits, p.waves});
+    ++stats_.searches;
+}
+
+// ops/cuda/quantization.cpp:94-102 (check_linear) and :455-464.
+void QuantizedGemm::linear(RowScaledView input, RowScaledView weight, TensorView output) {
+    input.validate();
+    weight.validate();
+    if (input.values.type != format_ || weight.values.type != format_ ||
+        input.rotation_size != weight.rotation_size || input.values.cols != weight.values.cols ||
+        input.values.rows != output.rows || weight.values.rows != output.cols ||
+        (output.type != Type::BF16 && output.type != Type::F16) || !output.dense())
+        throw std::invalid_argument("quantized linear dimensions/type mismatch");
+    const QuantizationGroups groups{input.group_size, weight.group_size, input.rotation_size};
+    LinearPath path = planned(output.rows, output.cols, input.values.cols, output.type, groups);
+    launch_quant_linear(path,
+                        {output.rows, output.cols, input.values.cols, input.group_size,
+                         weight.group_size},
+                        input.values.data, input.scales.ptr<float>(), weight.values.data,
+                        weight.scales.ptr<float>(), output.data, workspace_, workspace_bytes_,
+                        stream_, format_, output.type);
+}
+
+// ---------------------------------------------------------------- workspace
+QuantizationWorkspace::QuantizationWorkspace(int rows, Capacity capacity)
+    : rows_(rows), capacity_(capacity) {
+    if (rows < 1 || capacity.columns < 0 || capacity.scales_per_row < 0 ||
+        bool(capacity.columns) != bool(capacity.scales_per_row))
+        throw std::invalid_argument("invalid quantization workspace capacity");
+    const size_t values = size_t(rows) * size_t(std::max(1, capacity.columns));
+    const size_t scales = size_t(rows) * size_t(std::max(1, capacity.scales_per_row)) * 4;
+    if (hipMalloc(&values_, values) != hipSuccess || hipMalloc(&scales_, scales) != hipSuccess)
+        throw std::runtime_error("quantization workspace allocation failed");
+}
+
+QuantizationWorkspace::~QuantizationWorkspace() {
+    if (values_) (void)hipFree(values_);
+    if (scales_) (void)hipFree(scales_);
+}
+
+// layers/quantization.h:39-48
+RowScaledView QuantizationWorkspace::view(int rows, int columns, Type format,
+                                          QuantizationGroups layout) const {
+    const auto required = Capacity::matrix(columns, layout.activation);
+    if (rows < 1 || rows > rows_ || columns < 1 || columns > capacity_.columns ||
+        required.scales_per_row > capacity_.scales_per_row ||
+        (format != Type::FP8 && format != Type::I8))
+        throw std::invalid_argument("projection exceeds initialized quantization workspace");
+    const int scale_rows = layout.activation ? required.scales_per_row : rows;
+    const int scale_cols = layout.activation ? rows : 1;
+    return {TensorView(values_, rows, columns, format), TensorView(scales_, scale_rows, scale_cols,
+                                                                   Type::F32),
+            layout.activation, layout.rotation};
+}
+
+// ---------------------------------------------------------------- ops
+namespace ops {
+namespace {
+std::mutex g_mutex;
+std::map<int, QuantizedGemm *> g_contexts;
+}  // namespace
+
+void bind(int device, QuantizedGemm *gemm) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (gemm) g_contexts[device] = gemm;
+    else g_contexts.erase(device);
+}
+
+QuantizedGemm &context(int device) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    auto it = g_contexts.find(device);
+    if (it == g_contexts.end()) throw std::logic_error("no execution context bound for device");
+    return *it->second;
+}
+
+// ops/basic.cpp:69-78
+void quantize_rows(TensorView input, RowScaledView output) {
+    output.validate();
+    if ((input.type != Type::BF16 && input.type != Type::F16) || input.rows < 1 ||
+        input.cols < 1 || !input.data || !output.values.data || !output.scales.data ||
+        input.rows != output.values.rows || input.cols != output.values.cols)
+        throw std::invalid_argument("quantization source/destination shape/type mismatch");
+    launch_row_quantize(input, output, context(input.device).stream());
+}
+
+// ops/basic.cpp:64-67
+void matmul(RowScaledView input, RowScaledView weight, TensorView output) {
+    context(output.device).linear(input, weight, output);
+}
+
+// ops/basic.cpp:48-53 (the finish-epilogue plan of the reference is not part
+// of this library).
+void prepare_quantized(TensorView weight, int rows, int output_channels, int input_channels,
+                       Type type, QuantizationGroups groups) {
+    context(weight.device).prepare(rows, output_channels, input_channels, type, groups);
+}
+
+// ops/linear.cpp:71-90 (quantized weight, dense activation, no epilogue).
+void linear(TensorView input, RowScaledView weight, TensorView output, RowScaledView scratch) {
+    weight.validate();
+    quantize_rows(input, scratch);
+    if (scratch.values.cols != weight.values.cols || output.rows != scratch.values.rows ||
+        output.cols != weight.values.rows || !output.dense())
+        throw std::invalid_argument("quantized linear dimensions/layout mismatch");
+    matmul(scratch, weight, output);
+}
+}  // namespace ops
+
+}  // namespace tts

@@ -1,0 +1,197 @@
+// tts_qlinear.hpp — C++ host interface of the quantized linear path, with the
+// names, argument meaning and error behaviour of TTS.cpp's layers/ops API, on
+// top of the C ABI in qlinear.h (libqlinear.so). Callers written against the
+// reference's src/ops and src/layers link against this unchanged:
+//
+//   tts::Type, TensorView                    <- core/tensor.h:8-114 (subset)
+//   tts::Quantization, quantization_*        <- include/tts/quantization.h:6-29,
+//                                               core/quantization.h:6-27
+//   tts::RowScaledView                       <- core/quantization.h:33-49
+//   tts::KernelProblem                       <- core/kernel_problem.h:4-7
+//   tts::row_capacity                        <- core/row_capacity.h:10-19
+//   tts::LinearPath                          <- ops/kernels/quant/kernel_config.h:5-9
+//   tts::launch_row_quantize                 <- ops/kernels/quant/row_quantize.h:6
+//   tts::launch_quant_linear                 <- ops/kernels/quant/quant_dispatch.h:11-15
+//   tts::grouped_quant_gemm                  <- ops/kernels/quant/quant_dispatch.h:7-10
+//   tts::QuantizedGemm                       <- ops/cuda/quantization.h:15-42
+//   tts::QuantizationWorkspace               <- layers/quantization.h:9-49
+//   tts::ops::quantize_rows / matmul /
+//     prepare_quantized / linear             <- ops/storage.h:12, ops/basic.h:11,25-26,
+//                                               ops/linear.h:11-13 (quantized branch)
+//
+// Errors: std::invalid_argument for shape/type/alignment/workspace problems,
+// std::runtime_error for device errors and missing kernel variants,
+// std::logic_error for unprepared shapes — as the reference throws.
+// Device pointers only; nothing here allocates device memory except
+// QuantizationWorkspace, which owns its buffers like the reference's.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+
+#include "qlinear.h"
+
+namespace tts {
+
+// ---------------------------------------------------------------- tensors
+enum class Type { BF16, F32, I32, FP8, I8, F16, I16, I64, F64 };
+
+inline size_t bytes(Type type) {
+    if (type == Type::I64 || type == Type::F64) return 8;
+    return (type == Type::FP8 || type == Type::I8)                                   ? 1
+           : (type == Type::BF16 || type == Type::F16 || type == Type::I16) ? 2
+                                                                                      : 4;
+}
+
+struct TensorView {
+    void *data = nullptr;
+    int rows = 0, cols = 0;
+    Type type = Type::BF16;
+    int stride = 0;  // row stride in elements; zero means dense
+    int device = -1;
+    TensorView() = default;
+    TensorView(void *pointer, int row_count, int column_count, Type data_type = Type::BF16,
+               int leading_dimension = 0, int ordinal = -1)
+        : data(pointer), rows(row_count), cols(column_count), type(data_type),
+          stride(leading_dimension), device(ordinal) {
+        if (rows < 0 || cols < 0) throw std::invalid_argument("negative tensor dimension");
+        if (stride < 0 || (stride && stride < cols))
+            throw std::invalid_argument("invalid tensor stride");
+        if (size_t(rows) * size_t(cols) && !pointer)
+            throw std::invalid_argument("invalid tensor pointer/stride");
+    }
+    int ld() const { return stride ? stride : cols; }
+    bool dense() const { return rows <= 1 || ld() == cols; }
+    size_t numel() const { return size_t(rows) * size_t(cols); }
+    size_t size() const { return numel() * bytes(type); }
+    template <typename T> T *ptr() const { return static_cast<T *>(data); }
+};
+
+// ---------------------------------------------------------------- quantization metadata
+enum class Quantization { None, FP8, INT8, GroupINT8, GroupFP8 };
+
+const char *quantization_name(Quantization quantization);
+Quantization quantization_from_string(const std::string &name);
+Type quantized_type(Quantization quantization);
+
+struct QuantizationGroups {
+    int activation = 0, weight = 0, rotation = 0;
+};
+QuantizationGroups quantization_groups(Quantization quantization);
+
+// Values row-major; scales [rows] (group 0) or [ceil(cols/group), rows].
+struct RowScaledView {
+    TensorView values, scales;
+    int group_size = 0, rotation_size = 0;
+    int groups() const { return group_size ? (values.cols + group_size - 1) / group_size : 1; }
+    void validate() const;
+};
+
+struct KernelProblem {
+    int rows, channels, reduction;
+    int input_group = 0, weight_group = 0;
+};
+
+int row_capacity(int rows, unsigned bins_per_octave = 8);
+
+// ---------------------------------------------------------------- kernel launchers
+enum class LinearKind { Auto = QLIN_KIND_AUTO, Skinny = QLIN_KIND_SKINNY, Tiled = QLIN_KIND_TILED };
+struct LinearPath {
+    LinearKind kind = LinearKind::Auto;
+    int tokens = 0, channels = 0, splits = 1, waves = 1;
+};
+
+void launch_row_quantize(TensorView source, RowScaledView destination, qlin_stream_t stream);
+void launch_quant_linear(LinearPath config, KernelProblem shape, const void *input,
+                         const float *input_scales, const void *weights,
+                         const float *weight_scales, void *output, void *workspace,
+                         size_t workspace_bytes, qlin_stream_t stream, Type format = Type::FP8,
+                         Type output_type = Type::BF16);
+void grouped_quant_gemm(KernelProblem, const void *input, const float *input_scales,
+                        const void *weights, const float *weight_scales, void *output,
+                        qlin_stream_t, Type format, Type output_type, int tokens = 16,
+                        int splits = 1, void *workspace = nullptr, size_t workspace_bytes = 0);
+
+// ---------------------------------------------------------------- QuantizedGemm
+struct SelectionStats {
+    size_t entries = 0, hits = 0, searches = 0;
+};
+struct QuantCacheStats {
+    SelectionStats selection;
+    size_t prepared_plans = 0;
+};
+
+// Plans are prepared per row-capacity class at initialization and sealed;
+// linear() only looks them up. `workspace` is caller-owned device memory
+// (split-K partials), as the reference's CudaContext::gemm_workspace.
+class QuantizedGemm {
+  public:
+    QuantizedGemm(qlin_stream_t stream, void *workspace, size_t workspace_bytes,
+                  Type format = Type::FP8);
+    QuantizedGemm(const QuantizedGemm &) = delete;
+    void seal();
+    QuantCacheStats cache_stats() const;
+    void prepare(int rows, int output_channels, int input_channels, Type output_type = Type::BF16,
+                 QuantizationGroups groups = {});
+    void linear(RowScaledView input, RowScaledView weight, TensorView output);
+    LinearPath planned(int rows, int output_channels, int input_channels,
+                       Type output_type = Type::BF16, QuantizationGroups groups = {}) const;
+    Type format() const { return format_; }
+    qlin_stream_t stream() const { return stream_; }
+
+  private:
+    using Key = std::tuple<int, int, int, Type, int, int>;
+    qlin_stream_t stream_;
+    void *workspace_;
+    size_t workspace_bytes_;
+    Type format_;
+    bool sealed_ = false;
+    std::map<Key, LinearPath> plans_;
+    SelectionStats stats_;
+};
+
+// ---------------------------------------------------------------- activation workspace
+// Reusable activation storage (reference layers/quantization.h:9-49); owns
+// device buffers allocated with hipMalloc.
+class QuantizationWorkspace {
+  public:
+    struct Capacity {
+        int columns = 0, scales_per_row = 0;
+        static Capacity matrix(int columns, int group_size) {
+            return {columns, group_size ? (columns + group_size - 1) / group_size : 1};
+        }
+    };
+    QuantizationWorkspace() = default;
+    QuantizationWorkspace(int rows, Capacity capacity);
+    ~QuantizationWorkspace();
+    QuantizationWorkspace(const QuantizationWorkspace &) = delete;
+    QuantizationWorkspace &operator=(const QuantizationWorkspace &) = delete;
+    RowScaledView view(int rows, int columns, Type format, QuantizationGroups layout) const;
+
+  private:
+    void *values_ = nullptr, *scales_ = nullptr;
+    int rows_ = 0;
+    Capacity capacity_;
+};
+
+// ---------------------------------------------------------------- semantic ops
+namespace ops {
+// The execution context the reference resolves per device
+// (execution_context(device)); here bound once per device by the host.
+void bind(int device, QuantizedGemm *gemm);
+QuantizedGemm &context(int device);
+
+void quantize_rows(TensorView input, RowScaledView output);
+void matmul(RowScaledView input, RowScaledView weight, TensorView output);
+void prepare_quantized(TensorView weight, int rows, int output_channels, int input_channels,
+                       Type type, QuantizationGroups groups = {});
+// Quantized branch of ops::linear: quantize `input` into `scratch`, then GEMM.
+void linear(TensorView input, RowScaledView weight, TensorView output, RowScaledView scratch);
+}  // namespace ops
+
+}  // namespace tts

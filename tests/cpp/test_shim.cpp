@@ -1,0 +1,186 @@
+// Tests of the C++ host interface (include/tts_qlinear.hpp).
+//   test_shim host      : metadata and validation paths (no device needed)
+//   test_shim gpu DIR   : end to end on the GPU: reads DIR/{x,w}.bf16 and
+//                         DIR/shape.txt (M N K mode), quantizes W with
+//                         launch_row_quantize (load-time path), runs
+//                         ops::linear and writes DIR/y.bf16 plus the
+//                         quantized weights DIR/{wq.u8,sw.f32}.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "../../include/tts_qlinear.hpp"
+
+using namespace tts;
+
+static int failures = 0;
+#define EXPECT(cond)                                                        \
+    do {                                                                    \
+        if (!(cond)) {                                                      \
+            std::fprintf(stderr, "FAIL %s:%d %s\n", __FILE__, __LINE__, #cond); \
+            ++failures;                                                     \
+        }                                                                   \
+    } while (0)
+
+template <class E> static bool throws(const std::function<void()> &f) {
+    try {
+        f();
+    } catch (const E &) {
+        return true;
+    } catch (...) {
+        return false;
+    }
+    return false;
+}
+
+static int host_tests() {
+    // quantization names (include/tts/quantization.h)
+    EXPECT(quantization_from_string("group_int8") == Quantization::GroupINT8);
+    EXPECT(std::string(quantization_name(Quantization::FP8)) == "fp8");
+    EXPECT(throws<std::invalid_argument>([] { quantization_from_string("int4"); }));
+    EXPECT(quantized_type(Quantization::GroupFP8) == Type::FP8);
+    EXPECT(quantization_groups(Quantization::GroupINT8).rotation == 128);
+    EXPECT(quantization_groups(Quantization::INT8).activation == 0);
+    // row capacity classes (core/row_capacity.h)
+    EXPECT(row_capacity(1) == 1 && row_capacity(17) == 18 && row_capacity(32) == 32);
+    EXPECT(row_capacity(4096) == 4096 && row_capacity(4097) == 4608);
+    EXPECT(throws<std::invalid_argument>([] { row_capacity(0); }));
+    // RowScaledView::validate
+    char dummy[64];
+    RowScaledView ok{TensorView(dummy, 4, 256, Type::I8), TensorView(dummy, 4, 1, Type::F32), 0, 0};
+    ok.validate();
+    RowScaledView grouped{TensorView(dummy, 4, 256, Type::I8), TensorView(dummy, 2, 4, Type::F32),
+                          128, 128};
+    grouped.validate();
+    RowScaledView bad = grouped;
+    bad.scales = TensorView(dummy, 4, 2, Type::F32);
+    EXPECT(throws<std::invalid_argument>([&] { bad.validate(); }));
+    bad = ok;
+    bad.values.type = Type::BF16;
+    EXPECT(throws<std::invalid_argument>([&] { bad.validate(); }));
+    bad = grouped;
+    bad.rotation_size = 64;
+    EXPECT(throws<std::invalid_argument>([&] { bad.validate(); }));
+    // QuantizedGemm planning: prepare, seal, lookup by capacity class
+    QuantizedGemm gemm(nullptr, nullptr, 0, Type::I8);
+    gemm.prepare(30, 4096, 2048);
+    EXPECT(gemm.planned(29, 4096, 2048).kind == LinearKind::Skinny);  // same class as 30
+    gemm.prepare(4096, 4096, 2048);
+    EXPECT(gemm.planned(4096, 4096, 2048).kind == LinearKind::Tiled);
+    EXPECT(throws<std::logic_error>([&] { gemm.planned(7, 4096, 2048); }));
+    EXPECT(throws<std::invalid_argument>([&] { gemm.prepare(8, 4096, 2040); }));  // K % 16
+    EXPECT(throws<std::invalid_argument>([&] { gemm.prepare(8, 4096, 131072); }));
+    gemm.seal();
+    EXPECT(throws<std::logic_error>([&] { gemm.prepare(8, 512, 512); }));
+    gemm.prepare(30, 4096, 2048);  // already prepared: allowed after seal
+    EXPECT(gemm.cache_stats().prepared_plans == 2);
+    // check_linear: mismatched shapes throw before any launch
+    RowScaledView x{TensorView(dummy, 30, 2048, Type::I8), TensorView(dummy, 30, 1, Type::F32), 0,
+                    0};
+    RowScaledView w{TensorView(dummy, 4096, 2048, Type::I8),
+                    TensorView(dummy, 4096, 1, Type::F32), 0, 0};
+    EXPECT(throws<std::invalid_argument>(
+        [&] { gemm.linear(x, w, TensorView(dummy, 30, 4000, Type::BF16)); }));
+    RowScaledView xf = x;
+    xf.values.type = Type::FP8;
+    EXPECT(throws<std::invalid_argument>(
+        [&] { gemm.linear(xf, w, TensorView(dummy, 30, 4096, Type::BF16)); }));
+    // launcher status -> exception mapping
+    EXPECT(throws<std::invalid_argument>([&] {
+        launch_row_quantize(TensorView(dummy, 2, 64, Type::F32), ok, nullptr);
+    }));
+    EXPECT(throws<std::invalid_argument>([&] {
+        launch_quant_linear({}, {16, 40, 256}, dummy, nullptr, dummy, nullptr, dummy, nullptr, 0,
+                            nullptr, Type::I8, Type::BF16);
+    }));
+    // ops without a bound context
+    EXPECT(throws<std::logic_error>([&] { ops::matmul(x, w, TensorView(dummy, 30, 4096)); }));
+    std::printf("host tests: %s\n", failures ? "FAILED" : "ok");
+    return failures ? 1 : 0;
+}
+
+template <class T> static std::vector<T> read_file(const std::string &path, size_t count) {
+    std::vector<T> v(count);
+    std::ifstream f(path, std::ios::binary);
+    f.read(reinterpret_cast<char *>(v.data()), count * sizeof(T));
+    if (!f) throw std::runtime_error("cannot read " + path);
+    return v;
+}
+template <class T> static void write_file(const std::string &path, const std::vector<T> &v) {
+    std::ofstream f(path, std::ios::binary);
+    f.write(reinterpret_cast<const char *>(v.data()), v.size() * sizeof(T));
+}
+#define HIP(x)                                                               \
+    do {                                                                     \
+        if ((x) != hipSuccess) throw std::runtime_error("HIP error: " #x);  \
+    } while (0)
+
+static int gpu_test(const std::string &dir) {
+    int M, N, K;
+    std::string mode;
+    std::ifstream(dir + "/shape.txt") >> M >> N >> K >> mode;
+    const Quantization q = quantization_from_string(mode);
+    const Type fmt = quantized_type(q);
+    const QuantizationGroups groups = quantization_groups(q);
+    auto x = read_file<uint16_t>(dir + "/x.bf16", size_t(M) * K);
+    auto w = read_file<uint16_t>(dir + "/w.bf16", size_t(N) * K);
+    void *dx, *dw, *dwq, *dsw, *dy, *dws;
+    const int wgroups = groups.weight ? (K + groups.weight - 1) / groups.weight : 1;
+    HIP(hipMalloc(&dx, x.size() * 2));
+    HIP(hipMalloc(&dw, w.size() * 2));
+    HIP(hipMalloc(&dwq, size_t(N) * K));
+    HIP(hipMalloc(&dsw, size_t(N) * wgroups * 4));
+    HIP(hipMalloc(&dy, size_t(M) * N * 2));
+    const size_t ws_bytes = 8 << 20;  // the reference's gemm_workspace size
+    HIP(hipMalloc(&dws, ws_bytes));
+    HIP(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(dw, w.data(), w.size() * 2, hipMemcpyHostToDevice));
+    hipStream_t stream;
+    HIP(hipStreamCreate(&stream));
+    {
+        QuantizedGemm gemm(reinterpret_cast<qlin_stream_t>(stream), dws, ws_bytes, fmt);
+        ops::bind(0, &gemm);
+        // Load time: weight quantization with the activation quantizer
+        // (io/weights.cpp:80-87), plan preparation, seal.
+        RowScaledView wq{TensorView(dwq, N, K, fmt, 0, 0),
+                         groups.weight ? TensorView(dsw, wgroups, N, Type::F32, 0, 0)
+                                       : TensorView(dsw, N, 1, Type::F32, 0, 0),
+                         groups.weight, groups.rotation};
+        ops::quantize_rows(TensorView(dw, N, K, Type::BF16, 0, 0), wq);
+        ops::prepare_quantized(TensorView(dwq, N, K, fmt, 0, 0), M, N, K, Type::BF16, groups);
+        gemm.seal();
+        // Serving: dense bf16 activations through ops::linear.
+        QuantizationWorkspace workspace(M, QuantizationWorkspace::Capacity::matrix(K, groups.activation));
+        RowScaledView scratch = workspace.view(M, K, fmt, groups);
+        scratch.values.device = scratch.scales.device = 0;
+        ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq, TensorView(dy, M, N, Type::BF16, 0, 0),
+                    scratch);
+        HIP(hipStreamSynchronize(stream));
+        std::vector<uint16_t> y(size_t(M) * N);
+        std::vector<uint8_t> wqh(size_t(N) * K);
+        std::vector<float> swh(size_t(N) * wgroups);
+        HIP(hipMemcpy(y.data(), dy, y.size() * 2, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(wqh.data(), dwq, wqh.size(), hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(swh.data(), dsw, swh.size() * 4, hipMemcpyDeviceToHost));
+        write_file(dir + "/y.bf16", y);
+        write_file(dir + "/wq.u8", wqh);
+        write_file(dir + "/sw.f32", swh);
+        ops::bind(0, nullptr);
+    }
+    for (void *p : {dx, dw, dwq, dsw, dy, dws}) (void)hipFree(p);
+    (void)hipStreamDestroy(stream);
+    std::printf("gpu test %s M=%d N=%d K=%d: done\n", mode.c_str(), M, N, K);
+    return 0;
+}
+
+int main(int argc, char **argv) {
+    if (argc >= 2 && std::string(argv[1]) == "host") return host_tests();
+    if (argc >= 3 && std::string(argv[1]) == "gpu") return gpu_test(argv[2]);
+    std::fprintf(stderr, "usage: test_shim host | gpu DIR\n");
+    return 2;
+}

@@ -1,0 +1,65 @@
+"""The C++ host interface (include/tts_qlinear.hpp), exercised by the compiled
+tests/cpp/test_shim program: host-side metadata and validation on the CPU,
+and the reference's load-then-serve sequence (weight quantization,
+prepare/seal, ops::linear) on the GPU, checked against the oracle."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from breeze_tts_cpp_amd import synthetic
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "tests", "cpp", "bin", "test_shim")
+BF16, F32, I32, FP8, I8, F16 = 0, 1, 2, 3, 4, 5
+
+
+def _binary():
+    if not os.path.exists(BIN):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True,
+                       stdout=subprocess.DEVNULL)
+    return BIN
+
+
+def test_host_interface():
+    r = subprocess.run([_binary(), "host"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    assert "host tests: ok" in r.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,M,N,K", [("int8", 16, 2048, 2048), ("group_int8", 32, 512, 1024),
+                                        ("int8", 300, 384, 512), ("fp8", 8, 256, 2048)])
+def test_linear_end_to_end(dev, orc, tmp_path, mode, M, N, K):
+    xb = synthetic.activations(M, K, seed=M)
+    wb = synthetic.weights(N, K, seed=N)
+    xb.tofile(tmp_path / "x.bf16")
+    wb.tofile(tmp_path / "w.bf16")
+    (tmp_path / "shape.txt").write_text(f"{M} {N} {K} {mode}\n")
+    print(f"test_shim gpu {mode} M={M} N={N} K={K}", flush=True)
+    r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    fmt = FP8 if "fp8" in mode else I8
+    group = 128 if mode.startswith("group") else 0
+    y = np.fromfile(tmp_path / "y.bf16", np.uint16).reshape(M, N)
+    wq = np.fromfile(tmp_path / "wq.u8", np.uint8).reshape(N, K)
+    wq_ref, sw_ref = orc.quantize_rows(wb, fmt, group=group, rotation=group)
+    assert np.array_equal(wq, wq_ref)
+    assert np.array_equal(np.fromfile(tmp_path / "sw.f32", np.float32), sw_ref.ravel())
+    xq, sx = orc.quantize_rows(xb, fmt, group=group, rotation=group)
+    if fmt == FP8:
+        ideal = orc.gemm_fp8_ideal(xq, sx, wq_ref, sw_ref)
+        got = synthetic.bf16_bits_to_f32(y).astype(np.float64)
+        assert np.linalg.norm(got - ideal) / np.linalg.norm(ideal) <= 1e-2
+    elif group:
+        from breeze_tts_cpp_amd import qlinear
+        p = qlinear.plan(M, N, K, fmt, group, group)
+        span = -(-K // 256) * 256 // (p.splits * p.waves) if p.kind == qlinear.KIND_SKINNY else K
+        splits, waves = (p.splits, p.waves) if p.kind == qlinear.KIND_SKINNY else (1, 1)
+        ref, _ = orc.gemm_grouped(xq, sx, wq_ref, sw_ref, fmt, group, group, splits, waves, span)
+        assert np.array_equal(y, ref)
+    else:
+        ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq_ref), sx, sw_ref)
+        assert np.array_equal(y, ref)
