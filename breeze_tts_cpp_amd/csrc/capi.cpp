@@ -46,16 +46,22 @@ int check_launch(const char *what) {
 qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_group) {
     qlin_path p{};
     if (rows <= 64) {
+        // Decode: wave64s split K eight ways; weight slabs are staged through
+        // LDS when they fit (whole-row runs per load instruction). Wide
+        // projections take 32 weight rows per workgroup (half the activation
+        // re-reads per weight byte). Chosen from a sweep of the four BASELINE
+        // projections at M=32 on MI355X.
         p.kind = QLIN_KIND_SKINNY;
         p.tokens = (rows + 15) / 16 * 16;
-        p.channels = 16;
+        p.channels = N >= 8192 ? 32 : 16;
         p.splits = 1;
         const int blocks_k = (K + 255) / 256;
-        // Enough wave64s along K to keep loads in flight; ranges must divide
-        // the 256-wide K blocks evenly.
         int waves = 8;
         while (waves > 1 && blocks_k % waves) waves /= 2;
         p.waves = waves;
+        const bool slab_fits = waves == 8 && blocks_k / 8 <= 3 &&
+                               long(p.channels) * blocks_k * 256 <= 160 * 1024;
+        p.staged = slab_fits ? (p.channels == 32 ? 1 : 2) : 0;
         return p;
     }
     // Prefill: the largest macro tile that still gives every CU a tile.
@@ -100,6 +106,13 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
                         p.splits * p.waves, blocks_k);
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
+        if (p.staged < 0 || p.staged > 2)
+            return fail(QLIN_ERR_UNSUPPORTED, "staged must be 0, 1 or 2");
+        if (p.staged && (p.waves != 8 || p.channels > 32 || p.splits != 1 ||
+                         blocks_k / p.waves > 3 || p.channels * blocks_k * 256 > 160 * 1024))
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "staged skinny path needs waves 8, channels 16/32, no split, "
+                        "ceil(K/256) <= 24 and a weight slab within 160 KiB of LDS");
         return ok();
     }
     if (p.kind == QLIN_KIND_TILED) {
@@ -124,14 +137,14 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
 }
 
 qlin::GemmPath to_internal(const qlin_path &p) {
-    return {p.kind, p.tokens, p.channels, p.splits, p.waves};
+    return {p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged};
 }
 
 }  // namespace
 
 extern "C" {
 
-int qlin_version(void) { return 100; }
+int qlin_version(void) { return 101; }
 
 const char *qlin_last_error(void) { return g_error; }
 

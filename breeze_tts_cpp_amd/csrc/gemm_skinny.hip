@@ -69,7 +69,22 @@ __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4
 // One workgroup = WK waves over K, sharing 16*NF weight rows; tokens
 // [m0, m0 + 16*MT). Split: store raw (per-channel) or outer-scaled (grouped)
 // partials to workspace[blockIdx.y] instead of the output.
-template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out>
+// NB > 0: each wave's weight slab (16*NF rows x NB*256 bytes of K) is first
+// copied global -> LDS with buffer_load ... lds in one shot. Each load
+// instruction moves 1 KB of consecutive (row, 16-byte granule) positions of
+// the slab, so every instruction reads whole 256-byte (or longer) runs of a
+// weight row instead of 64-byte pieces of 16 rows. Granule g of slab row r
+// is stored at slot g ^ (r & 15) (the lane's global source is permuted, the
+// LDS write stays linear), which keeps the MFMA fragment reads (16 rows, one
+// granule) on distinct banks. Each wave reads back only what it loaded, so
+// no workgroup barrier is needed. NB == 0: weights load straight to registers.
+//
+// SL == 2 (with NB > 0): the workgroup's slab (16*NF rows x WK*NB*256 bytes)
+// is loaded cooperatively, wave w moving a contiguous run of whole rows, and
+// a workgroup barrier precedes the fragment reads (each wave then reads its
+// K range of every row).
+template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out, int NB = 0,
+          int SL = 1>
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
@@ -102,6 +117,43 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         xrow[t] = x + size_t(xvalid[t] ? m : 0) * K + quad * 16;
     }
 
+    extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
+    constexpr int kSlabBytes = 16 * NF * NB * kBlockK;          // per wave
+    constexpr int kRowBytes = SL == 2 ? WK * NB * kBlockK : NB * kBlockK;
+    constexpr int kRowGranules = kRowBytes / 16;
+    uint8_t *slab = SL == 2 ? wlds : wlds + wave * kSlabBytes;
+    const int slab_k0 = SL == 2 ? blockIdx.y * WK * span : k_begin;
+    if constexpr (NB > 0) {
+        typedef __attribute__((address_space(3))) void *lds_ptr_t;
+        const int rows_valid = max(0, min(16 * NF, N - n0));
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(w + size_t(n0) * K), 0, rows_valid * K, 0x00020000);
+        const int k_stop = SL == 2 ? min(K, slab_k0 + WK * span) : k_end;
+#pragma unroll
+        for (int i = 0; i < kSlabBytes / 1024; ++i) {
+            // SL 2: this wave's contiguous share of the workgroup slab.
+            const int q = (SL == 2 ? wave * (kSlabBytes / 16) : 0) + i * 64 + lane;
+            const int r = q / kRowGranules, slot = q % kRowGranules;
+            const int g = slot ^ (r & 15);
+            const int k = slab_k0 + g * 16;
+            const uint32_t off = k < k_stop ? uint32_t(r) * uint32_t(K) + uint32_t(k) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (lds_ptr_t)(slab + (SL == 2 ? wave * kSlabBytes : 0) + i * 1024), 16, off,
+                0, 0, 0);
+        }
+    }
+
+    // Cross-wave reduction buffer. INT8 per-channel sums are exact in int32,
+    // so waves add into one slot with LDS atomics (ds_add_u32); fp32 sums keep
+    // one slot per wave and are added in ascending K order.
+    constexpr bool kAtomic = (Fmt == I8) && !Grouped && WK > 1;
+    constexpr int kSlots = kAtomic ? 1 : (WK > 1 ? WK : 1);
+    using Red = std::conditional_t<Grouped, float, Scalar>;
+    __shared__ Red red[kSlots][MT * NF][4][64];
+    if constexpr (kAtomic) {
+        for (int i = threadIdx.x; i < MT * NF * 4 * 64; i += 64 * WK) (&red[0][0][0][0])[i] = 0;
+    }
+
     // Grouped: fp32 running sums; per-channel: the raw accumulator.
     Acc acc[MT][NF];
     float facc[MT][NF][4];
@@ -121,11 +173,34 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             const int k = kb + p * 64;
             const bool in = k + quad * 16 < k_end;
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
-                a[f][p] = (in && wvalid[f]) ? load16(wrow[f] + k) : i32x4{0, 0, 0, 0};
-#pragma unroll
             for (int t = 0; t < MT; ++t)
                 b[t][p] = (in && xvalid[t]) ? load16(xrow[t] + k) : i32x4{0, 0, 0, 0};
+        }
+        if constexpr (NB > 0) {
+            // The slab DMA was issued before these MT*4 activation loads: once
+            // at most they are outstanding, this wave's slab is in LDS.
+            if (kb == k_begin) {
+                constexpr int n = MT * 4;
+                __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+                if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int k = kb + p * 64;
+            const bool in = k + quad * 16 < k_end;
+            (void)in;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                if constexpr (NB > 0) {
+                    const int r = f * 16 + row16;
+                    const int g = ((kb - slab_k0) + p * 64) / 16 + quad;
+                    a[f][p] = *reinterpret_cast<const i32x4 *>(slab + r * kRowBytes +
+                                                               ((g ^ row16) << 4));
+                } else {
+                    a[f][p] = (in && wvalid[f]) ? load16(wrow[f] + k) : i32x4{0, 0, 0, 0};
+                }
+            }
         }
         if constexpr (!Grouped) {
 #pragma unroll
@@ -170,11 +245,17 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         }
     }
 
-    // Cross-wave reduction in LDS, waves summed in ascending K order.
     constexpr int kUnits = MT * NF * 64;  // (token tile, fragment, lane), 4 values each
-    using Red = std::conditional_t<Grouped, float, Scalar>;
-    __shared__ Red red[WK > 1 ? WK : 1][MT * NF][4][64];
-    if constexpr (WK > 1) {
+    if constexpr (kAtomic) {
+        __syncthreads();  // the zeroed slot is visible to every wave
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) atomicAdd(&red[0][t * NF + f][r][lane], acc[t][f][r]);
+        __syncthreads();
+    } else if constexpr (WK > 1) {
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -186,6 +267,19 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 }
         __syncthreads();
     }
+    // Sum over the waves of value r of unit (tf, l): ascending wave order.
+    auto total = [&](int tf, int r, int l, int t, int f) -> Red {
+        Red v = 0;
+        if constexpr (kAtomic) {
+            v += red[0][tf][r][l];
+        } else if constexpr (WK > 1) {
+            for (int q = 0; q < WK; ++q) v += red[q][tf][r][l];
+        } else {
+            if constexpr (Grouped) v += facc[t][f][r];
+            else v += acc[t][f][r];
+        }
+        return v;
+    };
     for (int u = threadIdx.x; u < kUnits; u += 64 * WK) {
         const int tf = u >> 6, l = u & 63;
         const int t = tf / NF, f = tf % NF;
@@ -194,25 +288,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         if (m >= M || n >= N) continue;
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if constexpr (Grouped) {
-                float s = 0.f;
-                if constexpr (WK > 1) {
-                    for (int q = 0; q < WK; ++q) s += red[q][tf][r][l];
-                } else {
-                    s += facc[t][f][r];
-                }
-                v[r] = s;
-            } else {
-                Scalar s = 0;
-                if constexpr (WK > 1) {
-                    for (int q = 0; q < WK; ++q) s += red[q][tf][r][l];
-                } else {
-                    s += acc[t][f][r];
-                }
-                v[r] = float(s);
-            }
-        }
+        for (int r = 0; r < 4; ++r) v[r] = float(total(tf, r, l, t, f));
         if constexpr (Split) {
             // Grouped partials carry their outer scales (quant_grouped.cu:161-165);
             // per-channel partials stay raw for the reduce kernel.
@@ -229,15 +305,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             } else {
                 Scalar raw[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    Scalar s = 0;
-                    if constexpr (WK > 1) {
-                        for (int q = 0; q < WK; ++q) s += red[q][tf][r][l];
-                    } else {
-                        s += acc[t][f][r];
-                    }
-                    raw[r] = s;
-                }
+                for (int r = 0; r < 4; ++r) raw[r] = Scalar(total(tf, r, l, t, f));
                 *reinterpret_cast<uint4 *>(static_cast<Scalar *>(partial) +
                                            (size_t(blockIdx.y) * M + m) * N + n) =
                     *reinterpret_cast<uint4 *>(raw);
@@ -286,6 +354,19 @@ __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ p
     store4<Out>(y, i4, v);
 }
 
+template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
+void launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t stream) {
+    const size_t lds = size_t(WK) * 16 * NF * NB * kBlockK;
+    if (layout == 2)
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2>), grid,
+                           dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
+                           a.N, a.K, span, a.input_group, a.weight_group);
+    else
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1>), grid,
+                           dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
+                           a.N, a.K, span, a.input_group, a.weight_group);
+}
+
 template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
@@ -294,11 +375,25 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     dim3 grid((a.N + 16 * NF - 1) / (16 * NF), p.splits, (a.M + 16 * MT - 1) / (16 * MT));
     dim3 block(64 * WK);
     if (p.splits == 1) {
+        // LDS-staged weight slabs (path.kind flag bit): one-shot streaming of
+        // whole weight rows; slab LDS per workgroup = WK * 16*NF * span bytes.
+        if constexpr (WK == 8 && NF <= 2) {
+            if (p.staged) {
+                switch (span / kBlockK) {
+                case 1: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, p.staged, stream); return 0;
+                case 2: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 2>(a, grid, span, p.staged, stream); return 0;
+                case 3: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 3>(a, grid, span, p.staged, stream); return 0;
+                default: return -4;
+                }
+            }
+        }
+        if (p.staged) return -4;
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out>), grid, block, 0,
                            stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span,
                            a.input_group, a.weight_group);
         return 0;
     }
+    if (p.staged) return -4;
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
                        a.input_group, a.weight_group);

@@ -30,7 +30,7 @@ struct GemmArgs {
     size_t workspace_bytes;
 };
 struct GemmPath {
-    int kind, tokens, channels, splits, waves;
+    int kind, tokens, channels, splits, waves, staged;
 };
 // Skinny (decode) family: returns 0, or a negative status if the path's
 // parameters are not an instantiated variant.

@@ -102,7 +102,7 @@ void launch_quant_linear(LinearPath config, KernelProblem shape, const void *inp
                          size_t workspace_bytes, qlin_stream_t stream, Type format,
                          Type output_type) {
     qlin_path path{static_cast<int>(config.kind), config.tokens, config.channels, config.splits,
-                   config.waves};
+                   config.waves, config.staged};
     check(qlin_gemm(&path, input, input_scales, weights, weight_scales, output, shape.rows,
                     shape.channels, shape.reduction, code(format), code(output_type),
                     shape.input_group, shape.weight_group, workspace, workspace_bytes, stream),
@@ -122,7 +122,7 @@ void grouped_quant_gemm(KernelProblem problem, const void *input, const float *i
                     problem.input_group, problem.weight_group, &planned),
           "grouped GEMM plan");
     LinearPath path{static_cast<LinearKind>(planned.kind), planned.tokens, planned.channels,
-                    planned.splits, planned.waves};
+                    planned.splits, planned.waves, planned.staged};
     if (path.kind == LinearKind::Skinny) {
         path.tokens = std::max(16, std::min(64, tokens));
         if (splits > 1) path.splits = splits;
@@ -182,7 +182,7 @@ void QuantizedGemm::prepare(int rows, int channels, int reduction, Type output_t
                              groups.weight) > workspace_bytes_)
         throw std::invalid_argument("quantized GEMM workspace overflow");
     plans_.emplace(key, LinearPath{static_cast<LinearKind>(p.kind), p.tokens, p.channels,
-                                   p.splits, p.waves});
+                                   p.splits, p.waves, p.staged});
     ++stats_.searches;
 }
 

@@ -28,7 +28,7 @@ class QLinearError(RuntimeError):
 
 class qlin_path(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int), ("tokens", ctypes.c_int), ("channels", ctypes.c_int),
-                ("splits", ctypes.c_int), ("waves", ctypes.c_int)]
+                ("splits", ctypes.c_int), ("waves", ctypes.c_int), ("staged", ctypes.c_int)]
 
 
 @dataclass
@@ -38,9 +38,11 @@ class Path:
     channels: int = 0
     splits: int = 1
     waves: int = 1
+    staged: int = 0
 
     def to_c(self) -> qlin_path:
-        return qlin_path(self.kind, self.tokens, self.channels, self.splits, self.waves)
+        return qlin_path(self.kind, self.tokens, self.channels, self.splits, self.waves,
+                         self.staged)
 
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
@@ -110,7 +112,7 @@ def row_quantize(x: torch.Tensor, fmt: int, group: int = 0, rotation: int = 0,
 def plan(rows: int, N: int, K: int, fmt: int, input_group: int = 0, weight_group: int = 0) -> Path:
     p = qlin_path()
     _check(load().qlin_plan(rows, N, K, fmt, input_group, weight_group, ctypes.byref(p)))
-    return Path(p.kind, p.tokens, p.channels, p.splits, p.waves)
+    return Path(p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged)
 
 
 def workspace_bytes(path: Path | None, rows: int, N: int, K: int, fmt: int,

@@ -68,7 +68,10 @@ typedef struct qlin_path {
     int tokens;   /* token (M) tile */
     int channels; /* output-channel (N) tile */
     int splits;   /* grid-level K partitions (partials in workspace when > 1) */
-    int waves;    /* skinny: wave64s splitting K inside a workgroup */
+    int waves;    /* skinny: wave64s splitting K inside a workgroup;
+                     tiled: 1, or 8 for the eight-wave 256x256 INT8 tile */
+    int staged;   /* skinny: weight slabs staged global->LDS; 1 = per wave,
+                     2 = per workgroup (contiguous row runs per wave, one barrier) */
 } qlin_path;
 
 /* Library version (major*10000 + minor*100 + patch). */

@@ -103,7 +103,7 @@ int row_capacity(int rows, unsigned bins_per_octave = 8);
 enum class LinearKind { Auto = QLIN_KIND_AUTO, Skinny = QLIN_KIND_SKINNY, Tiled = QLIN_KIND_TILED };
 struct LinearPath {
     LinearKind kind = LinearKind::Auto;
-    int tokens = 0, channels = 0, splits = 1, waves = 1;
+    int tokens = 0, channels = 0, splits = 1, waves = 1, staged = 0;
 };
 
 void launch_row_quantize(TensorView source, RowScaledView destination, qlin_stream_t stream);

@@ -263,3 +263,32 @@ def test_tiled_grouped(dev, orc, fmt, M, N, K):
         else:
             ideal = orc.gemm_grouped_ideal(xs, sxs, wq, sw, fmt, 128, 128)
             assert rel_l2(bits_to_f32(y[rows]), ideal) <= FP8_REL_L2
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("grouped", [False, True])
+def test_staged_skinny_variants(dev, orc, fmt, grouped):
+    """Weight slabs staged through LDS: same results as the register path."""
+    from breeze_tts_cpp_amd.qlinear import Path, KIND_SKINNY
+    g = 128 if grouped else 0
+    for M, N, K in ((32, 96, 2048), (5, 48, 4096), (64, 64, 6144), (17, 32, 2064)):
+        rot = g if K % 128 == 0 else 0
+        xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=g, rotation=rot, seed=N + K)
+        blocks = -(-K // 256)
+        for channels, staged in ((16, 1), (32, 1), (16, 2), (32, 2)):
+            if blocks % 8 or blocks // 8 > 3 or channels * blocks * 256 > 160 * 1024:
+                continue
+            p = Path(KIND_SKINNY, -(-M // 16) * 16, channels, 1, 8, staged)
+            print(f"staged {p} M={M} N={N} K={K}", flush=True)
+            y = gpu_gemm(dev, xq, sx, wq, sw, fmt, group=g, path=p)
+            if grouped and fmt == I8:
+                ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, 128, 128, 1, 8, blocks * 256 // 8)
+                assert np.array_equal(y, ref)
+            elif grouped:
+                ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, 128, 128)
+                assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
+            elif fmt == I8:
+                check_i8(orc, y, xq, sx, wq, sw)
+            else:
+                ideal = orc.gemm_fp8_ideal(xq, sx, wq, sw)
+                assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
