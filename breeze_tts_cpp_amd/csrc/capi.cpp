@@ -65,8 +65,8 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         return p;
     }
     // Prefill: the largest macro tile that still gives every CU a tile.
-    // INT8 256x256 runs eight waves of 128x64; FP8 keeps 128x128 tiles, whose
-    // 32-byte operand fragments still fit a double-buffered register set.
+    // INT8 256x256 runs eight waves of 128x64; FP8 (32x32x64 MFMA tiles) uses
+    // 128x128, the fastest shape whose double-buffered fragments fit in registers.
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;

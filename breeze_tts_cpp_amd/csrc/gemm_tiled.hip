@@ -86,7 +86,10 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     constexpr int W_INSTS = BN / (RPI * NW);
     constexpr int STAGE_BYTES = ROWS * BK;
     static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
-    static_assert(Fmt == I8 || BK == 128, "FP8 MFMA consumes 128 bytes of K");
+    // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
+    // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
+    constexpr bool kMF32 = Fmt == FP8 && !Grouped;
+    static_assert(Fmt == I8 || BK == 128 || (kMF32 && BK == 64), "FP8 K per stage");
     static_assert(!Grouped || BK == 128, "one K group of 128 per stage");
     using MMA = TileMma<Fmt>;
     using Acc = typename MMA::Acc;
@@ -132,14 +135,23 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         }
     };
 
-    Acc acc[Grouped ? 1 : WTN][WTM];
+    Acc acc[(Grouped || kMF32) ? 1 : WTN][(Grouped || kMF32) ? 1 : WTM];
+    f32x16 acc32[kMF32 ? WTN / 2 : 1][kMF32 ? WTM / 2 : 1];
+    if constexpr (kMF32) {
+#pragma unroll
+        for (int i = 0; i < WTN / 2; ++i)
+#pragma unroll
+            for (int j = 0; j < WTM / 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc32[i][j][e] = 0.f;
+    }
     float facc[Grouped ? WTN : 1][Grouped ? WTM : 1][4];
-    if constexpr (!Grouped) {
+    if constexpr (!Grouped && !kMF32) {
 #pragma unroll
         for (int i = 0; i < WTN; ++i)
 #pragma unroll
             for (int j = 0; j < WTM; ++j) acc[i][j] = Acc{0, 0, 0, 0};
-    } else {
+    } else if constexpr (Grouped) {
 #pragma unroll
         for (int i = 0; i < WTN; ++i)
 #pragma unroll
@@ -167,7 +179,63 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const int a_row0 = wave_n * 16 * WTN + row16;
     const int b_row0 = BN + wave_m * 16 * WTM + row16;
 
-    if constexpr (!Grouped) {
+    if constexpr (kMF32) {
+        // Same pipeline as below with 32x32x64 FP8 tiles: lane l holds row
+        // l % 32 of a fragment and K bytes [32*(l/32), +32) of the stage.
+        const int r32 = lane & 31, g32 = lane >> 5;
+        const int a_r0 = wave_n * 16 * WTN + r32, b_r0 = BN + wave_m * 16 * WTM + r32;
+        const int a_c0 = ((2 * g32) ^ swizzle<BK>(a_r0)) * 16, a_c1 = ((2 * g32 + 1) ^ swizzle<BK>(a_r0)) * 16;
+        const int b_c0 = ((2 * g32) ^ swizzle<BK>(b_r0)) * 16, b_c1 = ((2 * g32 + 1) ^ swizzle<BK>(b_r0)) * 16;
+        const int a_off = a_r0 * BK, b_off = b_r0 * BK;
+        constexpr int NA = WTN / 2, NBF = WTM / 2;
+        auto read = [&](int st, i32x8 (&a)[NA], i32x8 (&bb)[NBF]) {
+            const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
+            const uint8_t *pa = cur + a_off, *pb = cur + b_off;
+#pragma unroll
+            for (int j = 0; j < NBF; ++j) {
+                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pb + j * 32 * BK + b_c0);
+                const i32x4 hi = *reinterpret_cast<const i32x4 *>(pb + j * 32 * BK + b_c1);
+                bb[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pa + i * 32 * BK + a_c0);
+                const i32x4 hi = *reinterpret_cast<const i32x4 *>(pa + i * 32 * BK + a_c1);
+                a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+        };
+        auto mma = [&](const i32x8 (&a)[NA], const i32x8 (&bb)[NBF], int i0, int i1) {
+#pragma unroll
+            for (int i = i0; i < i1; ++i)
+#pragma unroll
+                for (int j = 0; j < NBF; ++j)
+                    acc32[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        a[i], bb[j], acc32[i][j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        };
+        constexpr int kEarly = NA / 4 > 0 ? NA / 4 : 1;
+        auto step = [&](int s, const i32x8 (&a)[NA], const i32x8 (&bb)[NBF], i32x8 (&na)[NA],
+                        i32x8 (&nb)[NBF]) {
+            if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
+            mma(a, bb, 0, kEarly);
+            if (s + 1 < stages) {
+                if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+                else wait_vmcnt<0>();
+                lds_barrier();
+                read(s + 1, na, nb);
+            }
+            mma(a, bb, kEarly, NA);
+        };
+        i32x8 a0[NA], b0[NBF], a1[NA], b1[NBF];
+        wait_vmcnt<INSTS * (STAGES - 2)>();
+        lds_barrier();
+        read(0, a0, b0);
+        int s = 0;
+        for (; s + 1 < stages; s += 2) {
+            step(s, a0, b0, a1, b1);
+            step(s + 1, a1, b1, a0, b0);
+        }
+        if (s < stages) step(s, a0, b0, a1, b1);
+    } else if constexpr (!Grouped) {
         // Software pipeline, one MFMA sub-step per stage (INT8: BK = 64,
         // FP8: BK = 128). Iteration s: issue the global loads of stage
         // s+STAGES-1; run the first MFMA rows of stage s; wait for stage s+1
@@ -295,32 +363,59 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     constexpr int TM = 16 * WTM, TN = 16 * WTN, ROWB = TN * 2, CH = ROWB / 16;
     lds_barrier();
     uint8_t *wbuf = lds + wave * TM * ROWB;
+    auto emit = [&](int m_l, int n_l, const float (&v)[4]) {
+        uint2 packed;
+        packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
+        packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
+        const int byte = n_l * 2;
+        *reinterpret_cast<uint2 *>(wbuf + m_l * ROWB + (((byte >> 4) ^ (m_l % CH)) << 4) +
+                                   (byte & 15)) = packed;
+    };
+    if constexpr (kMF32) {
+        // 32x32 tile: lane l, register 4b+e holds C[n = 8b + 4*(l/32) + e][m = l % 32].
 #pragma unroll
-    for (int j = 0; j < WTM; ++j) {
-        const int m_l = j * 16 + row16;
-        const int m = min(m_base + wave_m * TM + m_l, M - 1);
-        const float sxm = sx[m];
+        for (int j = 0; j < WTM / 2; ++j) {
+            const int m_l = j * 32 + (lane & 31);
+            const int m = min(m_base + wave_m * TM + m_l, M - 1);
+            const float sxm = sx[m];
 #pragma unroll
-        for (int i = 0; i < WTN; ++i) {
-            const int n = min(n_base + wave_n * TN + i * 16 + quad * 4, N - 4);
-            float v[4];
+            for (int i = 0; i < WTN / 2; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (Grouped) {
-                    float outer = input_group ? 1.f : sxm;
-                    if (!weight_group) outer *= sw[n + r];
-                    v[r] = (0.f + facc[i][j][r]) * outer;
-                } else {
-                    float t = float(acc[i][j][r]) * sxm;
-                    v[r] = t * sw[n + r];
+                for (int blk = 0; blk < 4; ++blk) {
+                    const int n_l = i * 32 + blk * 8 + (lane >> 5) * 4;
+                    const int n = min(n_base + wave_n * TN + n_l, N - 4);
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float t = acc32[i][j][blk * 4 + e] * sxm;
+                        v[e] = t * sw[n + e];
+                    }
+                    emit(m_l, n_l, v);
                 }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < WTM; ++j) {
+            const int m_l = j * 16 + row16;
+            const int m = min(m_base + wave_m * TM + m_l, M - 1);
+            const float sxm = sx[m];
+#pragma unroll
+            for (int i = 0; i < WTN; ++i) {
+                const int n = min(n_base + wave_n * TN + i * 16 + quad * 4, N - 4);
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (Grouped) {
+                        float outer = input_group ? 1.f : sxm;
+                        if (!weight_group) outer *= sw[n + r];
+                        v[r] = (0.f + facc[i][j][r]) * outer;
+                    } else {
+                        float t = float(acc[i][j][r]) * sxm;
+                        v[r] = t * sw[n + r];
+                    }
+                }
+                emit(m_l, i * 16 + quad * 4, v);
             }
-            uint2 packed;
-            packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
-            packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
-            const int byte = i * 32 + quad * 8;
-            *reinterpret_cast<uint2 *>(wbuf + m_l * ROWB + (((byte >> 4) ^ (m_l % CH)) << 4) +
-                                       (byte & 15)) = packed;
         }
     }
     const bool vec16 = (reinterpret_cast<uintptr_t>(y) & 15) == 0;
@@ -382,13 +477,11 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
         return -4;
     } else {
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
-        if (p.channels == 256 && p.tokens == 256)
-            return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
-            return launch_shape<Fmt, 2, 2, 8, 4, 128, 3, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
-            return launch_shape<Fmt, 2, 2, 4, 4, 128, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         return -4;
     }
 }

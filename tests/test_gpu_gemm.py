@@ -203,11 +203,14 @@ def test_end_to_end_linear(dev, orc):
 
 
 # ---------------------------------------------------------------- prefill (tiled) GEMM
-def _tiled_paths(grouped=False):
+def _tiled_paths(grouped=False, fmt=I8):
+    """Every instantiated macro tile (channels x tokens, waves) for the mode."""
     from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
-    for channels, tokens in ((256, 256), (256, 128), (128, 128)):
-        if not (grouped and tokens == 256):
-            yield Path(KIND_TILED, tokens, channels, 1, 1)
+    shapes = [(256, 128, 1), (128, 128, 1)]
+    if not grouped and fmt == I8:
+        shapes = [(256, 256, 8), (256, 256, 1)] + shapes
+    for channels, tokens, waves in shapes:
+        yield Path(KIND_TILED, tokens, channels, 1, waves)
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])
@@ -216,7 +219,7 @@ def test_tiled_variants_ragged(dev, orc, fmt, M, N, K):
     """Every macro-tile shape on ragged M/N edges and K not a multiple of 128."""
     xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=M + N + K)
     ideal = None if fmt == I8 else orc.gemm_fp8_ideal(xq, sx, wq, sw)
-    for p in _tiled_paths():
+    for p in _tiled_paths(fmt=fmt):
         print(f"tiled path {p} M={M} N={N} K={K}", flush=True)
         y = gpu_gemm(dev, xq, sx, wq, sw, fmt, path=p)
         if fmt == I8:
@@ -252,7 +255,7 @@ def test_tiled_grouped(dev, orc, fmt, M, N, K):
     print(f"tiled grouped fmt={fmt} M={M} N={N} K={K}", flush=True)
     xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=128, rotation=128, seed=M + 9)
     rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 30)]))
-    paths = list(_tiled_paths(grouped=True)) if M * N <= 320 * 400 else [None]
+    paths = list(_tiled_paths(grouped=True, fmt=fmt)) if M * N <= 320 * 400 else [None]
     for p in paths:
         y = gpu_gemm(dev, xq, sx, wq, sw, fmt, group=128, path=p)
         xs = xq[rows]
