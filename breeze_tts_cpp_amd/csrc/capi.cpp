@@ -129,6 +129,8 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED, "eight-wave tiled path is 256x256 only");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
+        if (p.staged)
+            return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no staged variant");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
         return ok();

@@ -61,8 +61,8 @@ __device__ __forceinline__ i32x4 load16(const uint8_t *p) {
 template <class Out>
 __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4]) {
     uint2 packed;
-    packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
-    packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
+    packed.x = pack2(v[0], v[1], Out{});
+    packed.y = pack2(v[2], v[3], Out{});
     *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + index) = packed;
 }
 

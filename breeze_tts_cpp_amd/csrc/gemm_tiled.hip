@@ -100,7 +100,12 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const int tiles = tiles_m * tiles_n;
     int b = blockIdx.x;
     if (tiles % 8 == 0) b = (b % 8) * (tiles / 8) + b / 8;
-    const int tn = b / tiles_m, tm = b % tiles_m;
+    // Column groups of kGroupN weight tiles: consecutive tiles (one XCD's
+    // share) cover a kGroupN x (tiles/8/kGroupN) block, not one tall column.
+    constexpr int kGroupN = 4;
+    const int group = b / (kGroupN * tiles_m), in_group = b % (kGroupN * tiles_m);
+    const int group_w = min(kGroupN, tiles_n - group * kGroupN);
+    const int tn = group * kGroupN + in_group % group_w, tm = in_group / group_w;
     const int n_base = tn * BN, m_base = tm * BM;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -171,10 +176,32 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
+    // Per-channel and per-token scales of the tile go to LDS past the ring
+    // (weight scales [BN], then token scales [BM]; 1.0 where the scales are
+    // per K group): the loads are issued ahead of the stage prologue and the
+    // epilogue reads them from LDS instead of waiting on global loads.
+    constexpr int kRingBytes = STAGES * STAGE_BYTES > BN * BM * 2 ? STAGES * STAGE_BYTES : BN * BM * 2;
+    float *scl = reinterpret_cast<float *>(lds + kRingBytes);
+    constexpr int kScaleLoads = (BN + BM + 64 * NW - 1) / (64 * NW);
+    float scale_v[kScaleLoads];
+#pragma unroll
+    for (int l = 0; l < kScaleLoads; ++l) {
+        const int i = tid + l * 64 * NW;
+        float v = 1.f;
+        if (i < BN) {
+            if (!Grouped || !weight_group) v = sw[min(n_base + i, N - 1)];
+        } else if (i < BN + BM) {
+            if (!Grouped || !input_group) v = sx[min(m_base + i - BN, M - 1)];
+        }
+        scale_v[l] = v;
+    }
     const int stages = (K + BK - 1) / BK;
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < stages) issue(s, s * BK);
+#pragma unroll
+    for (int l = 0; l < kScaleLoads; ++l)
+        if (tid + l * 64 * NW < BN + BM) scl[tid + l * 64 * NW] = scale_v[l];
 
     const int a_row0 = wave_n * 16 * WTN + row16;
     const int b_row0 = BN + wave_m * 16 * WTM + row16;
@@ -365,8 +392,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     uint8_t *wbuf = lds + wave * TM * ROWB;
     auto emit = [&](int m_l, int n_l, const float (&v)[4]) {
         uint2 packed;
-        packed.x = uint32_t(from_float(v[0], Out{})) | (uint32_t(from_float(v[1], Out{})) << 16);
-        packed.y = uint32_t(from_float(v[2], Out{})) | (uint32_t(from_float(v[3], Out{})) << 16);
+        packed.x = pack2(v[0], v[1], Out{});
+        packed.y = pack2(v[2], v[3], Out{});
         const int byte = n_l * 2;
         *reinterpret_cast<uint2 *>(wbuf + m_l * ROWB + (((byte >> 4) ^ (m_l % CH)) << 4) +
                                    (byte & 15)) = packed;
@@ -376,19 +403,18 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 #pragma unroll
         for (int j = 0; j < WTM / 2; ++j) {
             const int m_l = j * 32 + (lane & 31);
-            const int m = min(m_base + wave_m * TM + m_l, M - 1);
-            const float sxm = sx[m];
+            const float sxm = scl[BN + wave_m * TM + m_l];
 #pragma unroll
             for (int i = 0; i < WTN / 2; ++i)
 #pragma unroll
                 for (int blk = 0; blk < 4; ++blk) {
                     const int n_l = i * 32 + blk * 8 + (lane >> 5) * 4;
-                    const int n = min(n_base + wave_n * TN + n_l, N - 4);
+                    const f32x4 swv = *reinterpret_cast<const f32x4 *>(scl + wave_n * TN + n_l);
                     float v[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         float t = acc32[i][j][blk * 4 + e] * sxm;
-                        v[e] = t * sw[n + e];
+                        v[e] = t * swv[e];
                     }
                     emit(m_l, n_l, v);
                 }
@@ -397,21 +423,22 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 #pragma unroll
         for (int j = 0; j < WTM; ++j) {
             const int m_l = j * 16 + row16;
-            const int m = min(m_base + wave_m * TM + m_l, M - 1);
-            const float sxm = sx[m];
+            const float sxm = scl[BN + wave_m * TM + m_l];
 #pragma unroll
             for (int i = 0; i < WTN; ++i) {
-                const int n = min(n_base + wave_n * TN + i * 16 + quad * 4, N - 4);
+                const f32x4 swv =
+                    *reinterpret_cast<const f32x4 *>(scl + wave_n * TN + i * 16 + quad * 4);
                 float v[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if constexpr (Grouped) {
-                        float outer = input_group ? 1.f : sxm;
-                        if (!weight_group) outer *= sw[n + r];
+                        // Unit scales stand in for per-K-group ones: 1*s and
+                        // s*1 are exact, so this is (sx or 1) * (sw or 1).
+                        const float outer = sxm * swv[r];
                         v[r] = (0.f + facc[i][j][r]) * outer;
                     } else {
                         float t = float(acc[i][j][r]) * sxm;
-                        v[r] = t * sw[n + r];
+                        v[r] = t * swv[r];
                     }
                 }
                 emit(m_l, i * 16 + quad * 4, v);
@@ -440,7 +467,8 @@ template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Gr
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
     const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
-    const size_t lds = std::max(size_t(STAGES) * (BN + BM) * BK, size_t(BN) * BM * 2);
+    const size_t lds = std::max(size_t(STAGES) * (BN + BM) * BK, size_t(BN) * BM * 2) +
+                       size_t(BN + BM) * 4;
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
     if (a.K % BK == 0)
         hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, true, Out>),

@@ -43,6 +43,21 @@ __device__ __forceinline__ uint16_t from_float(float f, f16_t) {
     return h;
 }
 
+// Two values rounded to nearest even and packed low|high<<16. bf16 uses
+// gfx950's v_cvt_pk_bf16_f32 (IEEE RNE, subnormals kept): the same bits as
+// the integer rounding above for every non-NaN input, one instruction per pair.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, bf16_t) {
+    const bf16x2_t h = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, f16_t) {
+    return uint32_t(from_float(lo, f16_t{})) | (uint32_t(from_float(hi, f16_t{})) << 16);
+}
+
 // ---------------------------------------------------------------- 8-bit encoders
 // INT8: clamp to +-127, then round half to even (reference
 // ops/kernels/quant/quant_format.cuh:37-47).

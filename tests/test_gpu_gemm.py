@@ -173,6 +173,26 @@ def test_f16_output(dev, orc, fmt):
         assert rel_l2(bits_to_f32(y, F16), ideal) <= FP8_REL_L2
 
 
+@pytest.mark.parametrize("M", [16, 300])
+@pytest.mark.parametrize("exp_x,exp_w", [(-110, -30), (95, 20)])
+def test_i8_extreme_scales(dev, orc, M, exp_x, exp_w):
+    """Scales that push the epilogue into fp32/bf16 subnormals (products down
+    to 2^-150) or past the bf16 range (to inf): the output rounding keeps
+    subnormals and overflows like the oracle, on the skinny and tiled paths."""
+    N, K = 272, 512
+    xq, sx, wq, sw = operands(orc, M, N, K, I8, seed=M + abs(exp_x))
+    rng = np.random.default_rng(abs(exp_w) + M)
+    sx = (np.ldexp(1.0, exp_x) * rng.uniform(0.5, 2.0, M)).astype(np.float32)
+    sw = (np.ldexp(1.0, exp_w) * rng.uniform(0.5, 2.0, N)).astype(np.float32)
+    y = gpu_gemm(dev, xq, sx, wq, sw, I8)
+    ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw, order=0, out_type=BF16)
+    if exp_x < 0:
+        assert np.count_nonzero((ref & 0x7f80) == 0) > 0  # subnormal outputs occur
+    else:
+        assert np.count_nonzero((ref & 0x7fff) == 0x7f80) > 0  # infinities occur
+    check_i8(orc, y, xq, sx, wq, sw)
+
+
 def test_ragged_k(dev, orc):
     """K a multiple of 16 but not of 64/256 (masked tail pieces)."""
     for K in (16, 80, 272, 2064):
@@ -226,6 +246,24 @@ def test_tiled_variants_ragged(dev, orc, fmt, M, N, K):
             check_i8(orc, y, xq, sx, wq, sw)
         else:
             assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("M,N,K", [(2100, 4112, 320), (4096, 6144, 256)])
+def test_tiled_many_tiles(dev, orc, fmt, M, N, K):
+    """More tiles than CUs, ragged last tiles, every tile shape: sampled rows
+    against the oracle (tile order and per-tile scale staging)."""
+    xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=M + K)
+    rng = np.random.default_rng(M)
+    rows = np.unique(np.concatenate([[0, 127, 128, M - 1], rng.choice(M, 60, replace=False)]))
+    for p in _tiled_paths(fmt=fmt):
+        print(f"tiled path {p} M={M} N={N} K={K}", flush=True)
+        y = gpu_gemm(dev, xq, sx, wq, sw, fmt, path=p)
+        if fmt == I8:
+            check_i8(orc, y[rows], xq[rows], sx[rows], wq, sw)
+        else:
+            ideal = orc.gemm_fp8_ideal(xq[rows], sx[rows], wq, sw)
+            assert rel_l2(bits_to_f32(y[rows]), ideal) <= FP8_REL_L2
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])
