@@ -125,8 +125,8 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no split-K variant");
         if (p.waves != 1 && p.waves != 8)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled path waves must be 1 or 8");
-        if (p.waves == 8 && !(p.channels == 256 && p.tokens == 256))
-            return fail(QLIN_ERR_UNSUPPORTED, "eight-wave tiled path is 256x256 only");
+        if ((p.waves == 8) != (p.channels == 256 && p.tokens == 256))
+            return fail(QLIN_ERR_UNSUPPORTED, "tiled 256x256 runs eight waves; other tiles run one");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
         if (p.staged)

@@ -244,16 +244,15 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                         i32x8 (&nb)[NBF]) {
             if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
             mma(a, bb, 0, kEarly);
-            if (s + 1 < stages) {
-                if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
-                else wait_vmcnt<0>();
-                lds_barrier();
-                read(s + 1, na, nb);
-            }
+            if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+            else if (s + 1 < stages) wait_vmcnt<0>();
+            lds_barrier();
+            if (s + 1 < stages) read(s + 1, na, nb);
             mma(a, bb, kEarly, NA);
         };
         i32x8 a0[NA], b0[NBF], a1[NA], b1[NBF];
-        wait_vmcnt<INSTS * (STAGES - 2)>();
+        if (stages >= STAGES - 1) wait_vmcnt<INSTS * (STAGES - 2)>();
+        else wait_vmcnt<0>();
         lds_barrier();
         read(0, a0, b0);
         int s = 0;
@@ -306,20 +305,22 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                 for (int j = 0; j < WTM; ++j) MMA::run(acc[i][j], a[i], bb[j]);
         };
         constexpr int kEarly = WTN / 4;  // MFMA rows issued before the barrier
+        // The barrier (and its lgkmcnt(0)) runs on every step, also the last:
+        // with no control-flow path around it, the compiler's LDS wait
+        // counting never makes a stage's MFMAs wait on the next stage's reads.
         auto step = [&](int s, const Frag (&a)[WTN], const Frag (&bb)[WTM], Frag (&na)[WTN],
                         Frag (&nb)[WTM]) {
             if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
             mma(a, bb, 0, kEarly);
-            if (s + 1 < stages) {
-                if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
-                else wait_vmcnt<0>();
-                lds_barrier();
-                read(s + 1, na, nb);
-            }
+            if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+            else if (s + 1 < stages) wait_vmcnt<0>();
+            lds_barrier();
+            if (s + 1 < stages) read(s + 1, na, nb);
             mma(a, bb, kEarly, WTN);
         };
         Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
-        wait_vmcnt<INSTS * (STAGES - 2)>();
+        if (stages >= STAGES - 1) wait_vmcnt<INSTS * (STAGES - 2)>();
+        else wait_vmcnt<0>();
         lds_barrier();
         read(0, a0, b0);
         int s = 0;
@@ -481,8 +482,8 @@ int launch_shape(const GemmArgs &a, hipStream_t stream) {
     return 0;
 }
 
-// Macro tiles (weight rows x tokens), all with four waves: 256x256 (waves of
-// 128x128), 256x128 (128x64) and 128x128 (64x64).
+// Macro tiles (weight rows x tokens): 256x256 with eight waves of 128x64;
+// 256x128 (waves of 128x64) and 128x128 (64x64) with four.
 template <int Fmt, bool Grouped, class Out>
 int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if constexpr (Grouped) {
@@ -496,8 +497,6 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     } else if constexpr (Fmt == I8) {
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
-        if (p.channels == 256 && p.tokens == 256)
-            return launch_shape<Fmt, 2, 2, 8, 8, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)

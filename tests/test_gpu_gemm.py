@@ -228,7 +228,7 @@ def _tiled_paths(grouped=False, fmt=I8):
     from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
     shapes = [(256, 128, 1), (128, 128, 1)]
     if not grouped and fmt == I8:
-        shapes = [(256, 256, 8), (256, 256, 1)] + shapes
+        shapes = [(256, 256, 8)] + shapes
     for channels, tokens, waves in shapes:
         yield Path(KIND_TILED, tokens, channels, 1, waves)
 
