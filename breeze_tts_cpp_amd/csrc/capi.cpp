@@ -40,28 +40,56 @@ int check_launch(const char *what) {
     return ok();
 }
 
+qlin::GemmPath to_internal(const qlin_path &p) {
+    return {p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged};
+}
+
 // Path selection for gfx950 (256 CUs, 8 XCDs). Decode shapes stream the
 // weights once through the skinny kernel; larger token counts use the
 // LDS-tiled MFMA GEMM.
 qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_group) {
     qlin_path p{};
     if (rows <= 64) {
-        // Decode: wave64s split K eight ways; weight slabs are staged through
-        // LDS when they fit (whole-row runs per load instruction). Wide
-        // projections take 32 weight rows per workgroup (half the activation
-        // re-reads per weight byte). Chosen from a sweep of the four BASELINE
-        // projections at M=32 on MI355X.
+        // Decode: the weights are streamed once and each CU's share of them
+        // bounds the time, so the grid is sized to one workgroup per CU
+        // (256 on MI355X): the token tile and the weight rows per workgroup
+        // are chosen so that ceil(N/channels) * ceil(rows/tokens) is the
+        // largest count not above 256 (a second workgroup on some CUs would
+        // double their share). Wave64s split K eight ways; weight slabs are
+        // staged through LDS when they fit (whole-row runs per load).
         p.kind = QLIN_KIND_SKINNY;
-        p.tokens = (rows + 15) / 16 * 16;
-        p.channels = N >= 8192 ? 32 : 16;
         p.splits = 1;
+        const int full_tokens = (rows + 15) / 16 * 16;
+        long best = -1;
+        for (int channels : {16, 32, 48}) {
+            for (int tokens = full_tokens; tokens >= 16; tokens -= 16) {
+                if (full_tokens % tokens && tokens != 16) continue;
+                const long wgs = long((N + channels - 1) / channels) * ((rows + tokens - 1) / tokens);
+                // Prefer more workgroups up to 256, then wider token tiles
+                // (fewer activation re-reads), then fewer weight rows.
+                const long score = (wgs <= 256 ? wgs : 256 - (wgs - 256)) * 4096 + tokens * 64 - channels;
+                if (score > best) {
+                    best = score;
+                    p.tokens = tokens;
+                    p.channels = channels;
+                }
+            }
+        }
         const int blocks_k = (K + 255) / 256;
         int waves = 8;
         while (waves > 1 && blocks_k % waves) waves /= 2;
         p.waves = waves;
         const bool slab_fits = waves == 8 && blocks_k / 8 <= 3 &&
                                long(p.channels) * blocks_k * 256 <= 160 * 1024;
-        p.staged = slab_fits ? (p.channels == 32 ? 1 : 2) : 0;
+        p.staged = slab_fits ? (p.channels >= 32 ? 1 : 2) : 0;
+        qlin::GemmArgs a{};
+        a.M = rows;
+        a.N = N;
+        a.K = K;
+        a.fmt = fmt;
+        a.input_group = input_group;
+        a.weight_group = weight_group;
+        if (p.staged && qlin::skinny_lds_bytes(a, to_internal(p)) > qlin::kLdsBytes) p.staged = 0;
         return p;
     }
     // Prefill: the largest macro tile that still gives every CU a tile.
@@ -93,9 +121,9 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         if (p.tokens != 16 && p.tokens != 32 && p.tokens != 48 && p.tokens != 64)
             return fail(QLIN_ERR_UNSUPPORTED, "skinny path tokens must be 16/32/48/64 (got %d)",
                         p.tokens);
-        if (p.channels != 16 && p.channels != 32 && p.channels != 64)
-            return fail(QLIN_ERR_UNSUPPORTED, "skinny path channels must be 16, 32 or 64 (got %d)",
-                        p.channels);
+        if (p.channels != 16 && p.channels != 32 && p.channels != 48 && p.channels != 64)
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "skinny path channels must be 16, 32, 48 or 64 (got %d)", p.channels);
         if (p.waves != 1 && p.waves != 2 && p.waves != 4 && p.waves != 8)
             return fail(QLIN_ERR_UNSUPPORTED, "skinny path waves must be 1/2/4/8 (got %d)",
                         p.waves);
@@ -108,11 +136,23 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
         if (p.staged < 0 || p.staged > 2)
             return fail(QLIN_ERR_UNSUPPORTED, "staged must be 0, 1 or 2");
-        if (p.staged && (p.waves != 8 || p.channels > 32 || p.splits != 1 ||
+        if (p.staged && (p.waves != 8 || p.channels > 48 || p.splits != 1 ||
                          blocks_k / p.waves > 3 || p.channels * blocks_k * 256 > 160 * 1024))
             return fail(QLIN_ERR_UNSUPPORTED,
-                        "staged skinny path needs waves 8, channels 16/32, no split, "
+                        "staged skinny path needs waves 8, channels 16/32/48, no split, "
                         "ceil(K/256) <= 24 and a weight slab within 160 KiB of LDS");
+        qlin::GemmArgs a{};
+        a.M = rows;
+        a.N = N;
+        a.K = K;
+        a.fmt = fmt;
+        a.input_group = input_group;
+        a.weight_group = weight_group;
+        const size_t lds = qlin::skinny_lds_bytes(a, to_internal(p));
+        if (lds > qlin::kLdsBytes)
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "skinny path needs %zu bytes of LDS (slab + reduction), limit %zu", lds,
+                        qlin::kLdsBytes);
         return ok();
     }
     if (p.kind == QLIN_KIND_TILED) {
@@ -136,10 +176,6 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         return ok();
     }
     return fail(QLIN_ERR_UNSUPPORTED, "unknown path kind %d", p.kind);
-}
-
-qlin::GemmPath to_internal(const qlin_path &p) {
-    return {p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged};
 }
 
 }  // namespace

@@ -117,6 +117,28 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         xrow[t] = x + size_t(xvalid[t] ? m : 0) * K + quad * 16;
     }
 
+    // Epilogue scales, loaded before anything else so that their latency hides
+    // under the weight stream instead of following the reduction. Thread
+    // unit u = threadIdx.x + k*64*WK covers (token tile, fragment, lane) with
+    // four output channels; the factors are the ones the epilogue applies
+    // (K-group scales enter per group instead, leaving a factor of 1).
+    constexpr int kUnits = MT * NF * 64;  // (token tile, fragment, lane), 4 values each
+    constexpr int kMaxU = (kUnits + 64 * WK - 1) / (64 * WK);
+    float pre_x[kMaxU];
+    f32x4 pre_w[kMaxU];
+#pragma unroll
+    for (int k = 0; k < kMaxU; ++k) {
+        const int u = threadIdx.x + k * 64 * WK;
+        const int tf = u >> 6, l = u & 63;
+        const int m = m0 + (tf / NF) * 16 + (l & 15);
+        const int n = n0 + (tf % NF) * 16 + (l >> 4) * 4;
+        const bool live = u < kUnits && m < M && n < N;
+        pre_x[k] = (live && !(Grouped && input_group)) ? sx[m] : 1.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            pre_w[k][r] = (live && !(Grouped && weight_group)) ? sw[n + r] : 1.f;
+    }
+
     extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
     constexpr int kSlabBytes = 16 * NF * NB * kBlockK;          // per wave
     constexpr int kRowBytes = SL == 2 ? WK * NB * kBlockK : NB * kBlockK;
@@ -245,7 +267,6 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         }
     }
 
-    constexpr int kUnits = MT * NF * 64;  // (token tile, fragment, lane), 4 values each
     if constexpr (kAtomic) {
         __syncthreads();  // the zeroed slot is visible to every wave
 #pragma unroll
@@ -280,7 +301,10 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         }
         return v;
     };
-    for (int u = threadIdx.x; u < kUnits; u += 64 * WK) {
+#pragma unroll
+    for (int k = 0; k < kMaxU; ++k) {
+        const int u = threadIdx.x + k * 64 * WK;
+        if (u >= kUnits) break;
         const int tf = u >> 6, l = u & 63;
         const int t = tf / NF, f = tf % NF;
         const int m = m0 + t * 16 + (l & 15);
@@ -293,12 +317,9 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             // Grouped partials carry their outer scales (quant_grouped.cu:161-165);
             // per-channel partials stay raw for the reduce kernel.
             if constexpr (Grouped) {
+                // (sx or 1) * (sw or 1): a unit factor is exact.
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float outer = input_group ? 1.f : sx[m];
-                    if (!weight_group) outer *= sw[n + r];
-                    v[r] = v[r] * outer;
-                }
+                for (int r = 0; r < 4; ++r) v[r] = v[r] * (pre_x[k] * pre_w[k][r]);
                 float4 out = {v[0], v[1], v[2], v[3]};
                 *reinterpret_cast<float4 *>(static_cast<float *>(partial) +
                                             (size_t(blockIdx.y) * M + m) * N + n) = out;
@@ -314,12 +335,10 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if constexpr (Grouped) {
-                    float outer = input_group ? 1.f : sx[m];
-                    if (!weight_group) outer *= sw[n + r];
-                    v[r] = v[r] * outer;
+                    v[r] = v[r] * (pre_x[k] * pre_w[k][r]);
                 } else {
-                    float s = v[r] * sx[m];
-                    v[r] = s * sw[n + r];
+                    float s = v[r] * pre_x[k];
+                    v[r] = s * pre_w[k][r];
                 }
             }
             store4<Out>(y, size_t(m) * N + n, v);
@@ -369,6 +388,7 @@ void launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t
 
 template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    if (skinny_lds_bytes(a, p) > kLdsBytes) return -4;  // would not launch
     const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
     const int ranges = p.splits * WK;
     const int span = blocks_k / ranges * kBlockK;
@@ -377,7 +397,7 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (p.splits == 1) {
         // LDS-staged weight slabs (path.kind flag bit): one-shot streaming of
         // whole weight rows; slab LDS per workgroup = WK * 16*NF * span bytes.
-        if constexpr (WK == 8 && NF <= 2) {
+        if constexpr (WK == 8 && NF <= 3) {
             if (p.staged) {
                 switch (span / kBlockK) {
                 case 1: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, p.staged, stream); return 0;
@@ -426,6 +446,7 @@ template <int Fmt, int MT, bool Grouped, class Out>
 int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if (p.channels == 16) return dispatch_wk<Fmt, MT, 1, Grouped, Out>(a, p, s);
     if (p.channels == 32) return dispatch_wk<Fmt, MT, 2, Grouped, Out>(a, p, s);
+    if (p.channels == 48) return dispatch_wk<Fmt, MT, 3, Grouped, Out>(a, p, s);
     if (p.channels == 64) return dispatch_wk<Fmt, MT, 4, Grouped, Out>(a, p, s);
     return -4;
 }
@@ -448,6 +469,18 @@ int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 }
 
 }  // namespace
+
+size_t skinny_lds_bytes(const GemmArgs &a, const GemmPath &p) {
+    const int mt = p.tokens / 16, nf = p.channels / 16, wk = p.waves;
+    const bool grouped = a.input_group || a.weight_group;
+    const bool atomic = a.fmt == I8 && !grouped && wk > 1;   // kAtomic in skinny_gemm
+    const size_t slots = atomic ? 1 : size_t(wk > 1 ? wk : 1);
+    const size_t red = slots * mt * nf * 4 * 64 * 4;         // red[kSlots][MT*NF][4][64]
+    const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
+    const int nb = blocks_k / (p.splits * wk);
+    const size_t slab = p.staged ? size_t(wk) * 16 * nf * nb * kBlockK : 0;
+    return red + slab;
+}
 
 size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
     return p.splits > 1 ? size_t(p.splits) * a.M * a.N * 4 : 0;

@@ -36,6 +36,10 @@ struct GemmPath {
 // parameters are not an instantiated variant.
 int launch_skinny(const GemmArgs &, const GemmPath &, hipStream_t);
 size_t skinny_workspace_bytes(const GemmArgs &, const GemmPath &);
+// LDS of a skinny launch (weight slab + cross-wave reduction buffer); a path
+// above kLdsBytes must not be launched.
+size_t skinny_lds_bytes(const GemmArgs &, const GemmPath &);
+constexpr size_t kLdsBytes = 160 * 1024;  // per workgroup on gfx950
 int launch_tiled(const GemmArgs &, const GemmPath &, hipStream_t);
 size_t tiled_workspace_bytes(const GemmArgs &, const GemmPath &);
 

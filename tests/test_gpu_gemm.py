@@ -95,8 +95,8 @@ def test_i8_config0(dev, orc):
 def _skinny_paths(K):
     from breeze_tts_cpp_amd.qlinear import Path, KIND_SKINNY
     blocks = -(-K // 256)
-    for tokens in (16, 32, 64):
-        for channels in (16, 32):
+    for tokens in (16, 32, 48, 64):
+        for channels in (16, 32, 48, 64):
             for waves in (1, 2, 4, 8):
                 for splits in (1, 2, 3):
                     if blocks % (waves * splits) == 0:
@@ -316,7 +316,7 @@ def test_staged_skinny_variants(dev, orc, fmt, grouped):
         rot = g if K % 128 == 0 else 0
         xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=g, rotation=rot, seed=N + K)
         blocks = -(-K // 256)
-        for channels, staged in ((16, 1), (32, 1), (16, 2), (32, 2)):
+        for channels, staged in ((16, 1), (32, 1), (48, 1), (16, 2), (32, 2), (48, 2)):
             if blocks % 8 or blocks // 8 > 3 or channels * blocks * 256 > 160 * 1024:
                 continue
             p = Path(KIND_SKINNY, -(-M // 16) * 16, channels, 1, 8, staged)
