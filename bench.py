@@ -4,9 +4,11 @@
 One step = one decode step (M=32 tokens) through the INT8 quantized
 projections of a 16-layer 1B-class decoder (hidden 2048, QKV N=4096,
 o_proj N=2048, gate_up N=12288, down K=6144; BASELINE config 1 at M=32):
-per projection, dynamic per-token activation quantization of the bf16 input,
-then the INT8 GEMM with fused dequant to bf16. The 16 layers hold distinct
-weights (805 MB of int8), so HBM, not the 256 MB Infinity Cache, serves them.
+per projection, the quantized branch of ops::linear (qlin_linear): dynamic
+per-token activation quantization of the bf16 input into the scratch
+activation, then the INT8 GEMM with fused dequant to bf16. The 16 layers hold
+distinct weights
+(805 MB of int8), so HBM, not the 256 MB Infinity Cache, serves them.
 Inputs are resident in HBM before the timed region. The step is captured once
 as a HIP graph and replayed.
 
@@ -44,6 +46,7 @@ def gemm_bytes(M, N, K, group=0):
 
 def quant_bytes(M, K, group=0):
     return 3 * M * K + (4 * M * K // group if group else 4 * M)
+
 
 
 def parse():
@@ -114,13 +117,14 @@ def main():
         p = inputs[name]["path"]
         assert qlinear.workspace_bytes(p, M_DECODE, *synthetic.PROJECTIONS[name], I8) == 0
 
+    def linear(io, wt):
+        qlinear.linear(io["x"], wt["wq"], wt["sw"], I8, path=io["path"],
+                       scratch=(io["xq"], io["sx"]), out=io["y"], stream=stream)
+
     def step():
         for entry in layers:
             for name, _ in projections:
-                io, wt = inputs[name], entry[name]
-                qlinear.row_quantize(io["x"], I8, values=io["xq"], scales=io["sx"], stream=stream)
-                qlinear.gemm(io["xq"], io["sx"], wt["wq"], wt["sw"], I8, path=io["path"],
-                             out=io["y"], stream=stream)
+                linear(inputs[name], entry[name])
 
     if args.profile:
         profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections)
@@ -158,35 +162,41 @@ def main():
                               for _, (N, K) in projections)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # ---- per-projection decode GEMM: graph of the 16 layers' launches of one
-    # projection (distinct weights), timed with events on the launch stream.
-    per_proj = {}
-    reps = max(5, args.steps // 2)
-    for name, (N, K) in projections:
-        io = inputs[name]
+    # ---- per projection: graph of the 16 layers' launches of one projection
+    # (distinct weights), timed with events on the launch stream: the GEMM on
+    # the quantized activations (the dominant kernel), and the whole linear.
+    def time_graph(launch):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            for entry in layers:
-                qlinear.gemm(io["xq"], io["sx"], entry[name]["wq"], entry[name]["sw"], I8,
-                             path=io["path"], out=io["y"], stream=stream)
+            launch()
         torch.cuda.synchronize()
         for _ in range(3):
             g.replay()
         torch.cuda.synchronize()
+        reps = max(5, args.steps // 2)
         with torch.cuda.stream(stream):
             start.record(stream)
             for _ in range(reps):
                 g.replay()
             end.record(stream)
         torch.cuda.synchronize()
-        us = start.elapsed_time(end) * 1e3 / (reps * LAYERS)
+        return start.elapsed_time(end) * 1e3 / (reps * LAYERS)
+
+    per_proj = {}
+    for name, (N, K) in projections:
+        io = inputs[name]
+        us = time_graph(lambda: [qlinear.gemm(io["xq"], io["sx"], entry[name]["wq"],
+                                              entry[name]["sw"], I8, path=io["path"],
+                                              out=io["y"], stream=stream)
+                                 for entry in layers])
+        us_linear = time_graph(lambda: [linear(io, entry[name]) for entry in layers])
         b = gemm_bytes(M_DECODE, N, K)
         p = io["path"]
         per_proj[name] = {"N": N, "K": K, "us_per_launch": round(us, 3), "bytes": b,
                           "GBps": round(b / (us * 1e-6) / 1e9, 1),
                           "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                          "path": [p.kind, p.tokens, p.channels, p.splits, p.waves]}
-        del g
+                          "path": [p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged],
+                          "linear_us": round(us_linear, 3)}
     dominant = max(per_proj, key=lambda n: per_proj[n]["us_per_launch"])
     d = per_proj[dominant]
     roofline = {"bound": "hbm", "kernel": f"skinny_gemm INT8 {dominant} M={M_DECODE}",
@@ -211,7 +221,8 @@ def main():
                 "N(0,0.02) weights; bf16)",
         "config": {"workload": f"decode step M={M_DECODE}: {LAYERS} layers x "
                                "(qkv 4096x2048, o_proj 2048x2048, gate_up 12288x2048, "
-                               "down 2048x6144), per-token INT8 quant + INT8 GEMM + bf16",
+                               "down 2048x6144), per-token INT8 quant + INT8 GEMM + bf16 "
+                               "(qlin_linear)",
                    "tokens": M_DECODE, "layers": LAYERS, "format": "int8",
                    "step_bytes": step_bytes},
         "decode_projections": per_proj,
@@ -227,31 +238,30 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-# Decode GEMM grid sizes (threads) per projection at M=32 with the planned path,
-# used to find the kernel's row in the committed counter summary.
-_DECODE_GRID = {"qkv": "131072", "gate_up": "393216"}
-
-
 def measured_traffic(name):
-    """HBM bytes per launch of the decode GEMM for `name`, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/hbm_traffic_decode_prefill.md,
-    copy-kernel calibrated); None when that summary has no row for it."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_prefill.md")
-    grid = _DECODE_GRID.get(name)
-    if not grid or not os.path.exists(path):
+    """HBM bytes per launch of the decode linear for projection `name`, from the
+    committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (profiles/hbm_traffic_decode_linear.md, copy-kernel calibrated: a row per
+    projection, the last column the scaled bytes per dispatch); None when that
+    summary has no row for it."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_linear.md")
+    if not os.path.exists(path):
         return None
     for line in open(path):
-        cells = [c.strip() for c in line.split("|")]
-        if len(cells) > 6 and cells[1].startswith("`skinny_gemm") and cells[2] == grid:
-            return int(cells[6].replace(",", ""))
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0] == name:
+            try:
+                return int(cells[-1].replace(",", ""))
+            except ValueError:
+                return None
     return None
 
 
 def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections):
     """Kernels for counter passes, in this order: one 64 MiB copy (known
-    traffic: 64 MiB read + 64 MiB written), 5 replays of each projection's
-    16-layer decode GEMM graph, then one M=4096 INT8 and FP8 GEMM per
-    projection."""
+    traffic: 64 MiB read + 64 MiB written), 5 rounds of each projection's
+    16-layer decode linear (qlin_linear, fused at M=32), then one M=4096 INT8
+    and FP8 GEMM per projection."""
     src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -261,8 +271,9 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
         io = inputs[name]
         for _ in range(5):
             for entry in layers:
-                qlinear.gemm(io["xq"], io["sx"], entry[name]["wq"], entry[name]["sw"], qlinear.I8,
-                             path=io["path"], out=io["y"], stream=stream)
+                qlinear.linear(io["x"], entry[name]["wq"], entry[name]["sw"], qlinear.I8,
+                               path=io["path"], scratch=(io["xq"], io["sx"]), out=io["y"],
+                               stream=stream)
     torch.cuda.synchronize()
     M = M_PREFILL
     for fmt in (qlinear.I8, qlinear.FP8):

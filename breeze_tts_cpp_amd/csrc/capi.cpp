@@ -290,4 +290,18 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
     return check_launch("quantized GEMM launch");
 }
 
+int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void *xq, float *sx,
+                const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,
+                int out_type, int input_group, int weight_group, int rotation, void *workspace,
+                size_t workspace_bytes, qlin_stream_t stream) {
+    // ops::linear, quantized branch (reference ops/linear.cpp:51-71):
+    // quantize_rows into the scratch activation, then the GEMM.
+    if (!xq || !sx) return fail(QLIN_ERR_INVALID, "linear needs the scratch activation (xq, sx)");
+    int status = qlin_row_quantize(x, ld, rows, K, src_type, xq, sx, fmt, input_group, rotation,
+                                   stream);
+    if (status) return status;
+    return qlin_gemm(path, xq, sx, w, sw, y, rows, N, K, fmt, out_type, input_group, weight_group,
+                     workspace, workspace_bytes, stream);
+}
+
 }  // extern "C"

@@ -165,16 +165,19 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         }
     }
 
-    // Cross-wave reduction buffer. INT8 per-channel sums are exact in int32,
-    // so waves add into one slot with LDS atomics (ds_add_u32); fp32 sums keep
-    // one slot per wave and are added in ascending K order.
-    constexpr bool kAtomic = (Fmt == I8) && !Grouped && WK > 1;
-    constexpr int kSlots = kAtomic ? 1 : (WK > 1 ? WK : 1);
+    // Cross-wave reduction: each wave stores its partial sums of unit (tf, l)
+    // as four consecutive values, and the epilogue adds the slots in ascending
+    // wave (= K) order. With a staged slab the slots reuse it: a slot is
+    // MT*NF KB, never more than a wave's slab (16*NF*NB*256 bytes, MT <= 4 <=
+    // 4*NB); with no slab they live in a static buffer.
     using Red = std::conditional_t<Grouped, float, Scalar>;
-    __shared__ Red red[kSlots][MT * NF][4][64];
-    if constexpr (kAtomic) {
-        for (int i = threadIdx.x; i < MT * NF * 4 * 64; i += 64 * WK) (&red[0][0][0][0])[i] = 0;
-    }
+    typedef Red Red4 __attribute__((ext_vector_type(4)));
+    constexpr int kSlotVals = MT * NF * 64 * 4;
+    constexpr int kSlotStride = NB > 0 ? (SL == 2 ? kSlotVals : kSlabBytes / int(sizeof(Red)))
+                                       : kSlotVals;
+    static_assert(NB == 0 || kSlotVals * int(sizeof(Red)) <= kSlabBytes, "slot fits the slab");
+    __shared__ Red4 red_static[NB > 0 || WK == 1 ? 1 : WK * kSlotVals / 4];
+    Red *red = NB > 0 ? reinterpret_cast<Red *>(wlds) : reinterpret_cast<Red *>(red_static);
 
     // Grouped: fp32 running sums; per-channel: the raw accumulator.
     Acc acc[MT][NF];
@@ -188,8 +191,8 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             for (int r = 0; r < 4; ++r) facc[t][f][r] = 0.f;
         }
 
-    for (int kb = k_begin; kb < k_end; kb += kBlockK) {
-        i32x4 a[NF][4], b[MT][4];
+    // Activation fragments of block kb: lane quad q holds K bytes [kb + 64p + 16q, +16).
+    auto load_x = [&](int kb, i32x4 (&b)[MT][4]) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int k = kb + p * 64;
@@ -198,15 +201,24 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             for (int t = 0; t < MT; ++t)
                 b[t][p] = (in && xvalid[t]) ? load16(xrow[t] + k) : i32x4{0, 0, 0, 0};
         }
-        if constexpr (NB > 0) {
-            // The slab DMA was issued before these MT*4 activation loads: once
-            // at most they are outstanding, this wave's slab is in LDS.
-            if (kb == k_begin) {
-                constexpr int n = MT * 4;
-                __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-                if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
-            }
-        }
+    };
+    // With a staged slab of NB blocks, all of the wave's activation blocks are
+    // requested right behind the slab DMA (when they fit in registers), so no
+    // block waits for its own L2 round trip inside the loop.
+    constexpr bool kPreX = NB > 0 && NB * MT <= 6;
+    i32x4 xpre[kPreX ? NB : 1][MT][4];
+    if constexpr (kPreX) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
+        // The slab DMA was issued before these loads: once at most they are
+        // outstanding, this wave's slab is in LDS.
+        constexpr int n = NB * MT * 4;
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+        if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
+    }
+
+    auto block = [&](int kb, const i32x4 (&b)[MT][4]) {
+        i32x4 a[NF][4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int k = kb + p * 64;
@@ -265,41 +277,67 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 }
             }
         }
+    };
+    if constexpr (kPreX) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk) {
+            const int kb = k_begin + blk * kBlockK;
+            if (kb < k_end) block(kb, xpre[blk]);
+        }
+    } else {
+        for (int kb = k_begin; kb < k_end; kb += kBlockK) {
+            i32x4 b[MT][4];
+            load_x(kb, b);
+            if constexpr (NB > 0) {
+                // The slab DMA was issued before these MT*4 activation loads:
+                // once at most they are outstanding, this wave's slab is in LDS.
+                if (kb == k_begin) {
+                    constexpr int n = MT * 4;
+                    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+                    if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
+                }
+            }
+            block(kb, b);
+        }
     }
 
-    if constexpr (kAtomic) {
-        __syncthreads();  // the zeroed slot is visible to every wave
+
+    if constexpr (WK > 1) {
+        // A shared slab is read by every wave: all reads finish first.
+        if constexpr (NB > 0 && SL == 2) __syncthreads();
+        Red *slot = red + wave * kSlotStride;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) atomicAdd(&red[0][t * NF + f][r][lane], acc[t][f][r]);
-        __syncthreads();
-    } else if constexpr (WK > 1) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int f = 0; f < NF; ++f)
+            for (int f = 0; f < NF; ++f) {
+                Red4 v;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if constexpr (Grouped) red[wave][t * NF + f][r][lane] = facc[t][f][r];
-                    else red[wave][t * NF + f][r][lane] = acc[t][f][r];
+                    if constexpr (Grouped) v[r] = facc[t][f][r];
+                    else v[r] = acc[t][f][r];
                 }
+                *reinterpret_cast<Red4 *>(slot + ((t * NF + f) * 64 + lane) * 4) = v;
+            }
         __syncthreads();
     }
-    // Sum over the waves of value r of unit (tf, l): ascending wave order.
-    auto total = [&](int tf, int r, int l, int t, int f) -> Red {
-        Red v = 0;
-        if constexpr (kAtomic) {
-            v += red[0][tf][r][l];
-        } else if constexpr (WK > 1) {
-            for (int q = 0; q < WK; ++q) v += red[q][tf][r][l];
+    // Sum over the waves of the four values of unit (tf, l): ascending wave order.
+    auto total = [&](int tf, int l, int t, int f, Red (&v)[4]) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = 0;
+        if constexpr (WK > 1) {
+#pragma unroll
+            for (int q = 0; q < WK; ++q) {
+                const Red4 s4 = *reinterpret_cast<const Red4 *>(red + q * kSlotStride + (tf * 64 + l) * 4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] += s4[r];
+            }
         } else {
-            if constexpr (Grouped) v += facc[t][f][r];
-            else v += acc[t][f][r];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (Grouped) v[r] += facc[t][f][r];
+                else v[r] += acc[t][f][r];
+            }
         }
-        return v;
     };
 #pragma unroll
     for (int k = 0; k < kMaxU; ++k) {
@@ -310,9 +348,11 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         const int m = m0 + t * 16 + (l & 15);
         const int n = n0 + f * 16 + (l >> 4) * 4;
         if (m >= M || n >= N) continue;
+        Red sum[4];
+        total(tf, l, t, f, sum);
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = float(total(tf, r, l, t, f));
+        for (int r = 0; r < 4; ++r) v[r] = float(sum[r]);
         if constexpr (Split) {
             // Grouped partials carry their outer scales (quant_grouped.cu:161-165);
             // per-channel partials stay raw for the reduce kernel.
@@ -326,7 +366,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             } else {
                 Scalar raw[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) raw[r] = Scalar(total(tf, r, l, t, f));
+                for (int r = 0; r < 4; ++r) raw[r] = Scalar(sum[r]);
                 *reinterpret_cast<uint4 *>(static_cast<Scalar *>(partial) +
                                            (size_t(blockIdx.y) * M + m) * N + n) =
                     *reinterpret_cast<uint4 *>(raw);
@@ -374,7 +414,7 @@ __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ p
 }
 
 template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
-void launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t stream) {
+int launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t stream) {
     const size_t lds = size_t(WK) * 16 * NF * NB * kBlockK;
     if (layout == 2)
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2>), grid,
@@ -384,6 +424,7 @@ void launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
                            a.N, a.K, span, a.input_group, a.weight_group);
+    return 0;
 }
 
 template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out>
@@ -400,9 +441,9 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         if constexpr (WK == 8 && NF <= 3) {
             if (p.staged) {
                 switch (span / kBlockK) {
-                case 1: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, p.staged, stream); return 0;
-                case 2: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 2>(a, grid, span, p.staged, stream); return 0;
-                case 3: launch_slab<Fmt, MT, NF, WK, Grouped, Out, 3>(a, grid, span, p.staged, stream); return 0;
+                case 1: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, p.staged, stream);
+                case 2: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 2>(a, grid, span, p.staged, stream);
+                case 3: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 3>(a, grid, span, p.staged, stream);
                 default: return -4;
                 }
             }
@@ -472,13 +513,11 @@ int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 
 size_t skinny_lds_bytes(const GemmArgs &a, const GemmPath &p) {
     const int mt = p.tokens / 16, nf = p.channels / 16, wk = p.waves;
-    const bool grouped = a.input_group || a.weight_group;
-    const bool atomic = a.fmt == I8 && !grouped && wk > 1;   // kAtomic in skinny_gemm
-    const size_t slots = atomic ? 1 : size_t(wk > 1 ? wk : 1);
-    const size_t red = slots * mt * nf * 4 * 64 * 4;         // red[kSlots][MT*NF][4][64]
     const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
     const int nb = blocks_k / (p.splits * wk);
     const size_t slab = p.staged ? size_t(wk) * 16 * nf * nb * kBlockK : 0;
+    // Reduction slots reuse a staged slab; otherwise one static slot per wave.
+    const size_t red = p.staged || wk == 1 ? 16 : size_t(wk) * mt * nf * 64 * 4 * 4;
     return red + slab;
 }
 

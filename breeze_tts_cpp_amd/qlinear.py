@@ -46,7 +46,7 @@ class Path:
 
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
-           "qlin_workspace_bytes", "qlin_gemm")
+           "qlin_workspace_bytes", "qlin_gemm", "qlin_linear")
 
 
 def load():
@@ -70,6 +70,9 @@ def load():
     L.qlin_workspace_bytes.argtypes = [ctypes.POINTER(qlin_path), i, i, i, i, i, i]
     L.qlin_gemm.restype = i
     L.qlin_gemm.argtypes = [ctypes.POINTER(qlin_path), P, P, P, P, P, i, i, i, i, i, i, i, P, sz, P]
+    L.qlin_linear.restype = i
+    L.qlin_linear.argtypes = [ctypes.POINTER(qlin_path), P, i, i, P, P, P, P, P, i, i, i, i, i,
+                              i, i, i, P, sz, P]
     _lib = L
     return L
 
@@ -145,8 +148,31 @@ def gemm(xq: torch.Tensor, sx: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor,
 
 def linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int, group: int = 0,
            rotation: int = 0, out_dtype=torch.bfloat16, path: Path | None = None,
+           scratch: tuple[torch.Tensor, torch.Tensor] | None = None,
+           out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
            stream=None) -> torch.Tensor:
-    """Quantize activations then run the GEMM (the quantized branch of the
-    reference ops::linear, ops/linear.cpp:71-90)."""
-    xq, sx = row_quantize(x, fmt, group, rotation, stream=stream)
-    return gemm(xq, sx, wq, sw, fmt, out_dtype, group, group, path, stream=stream)
+    """Quantize the 16-bit activations into the scratch activation (xq, sx) and
+    run the GEMM: the quantized branch of the reference ops::linear
+    (ops/linear.cpp:51-71) through qlin_linear. `scratch` is allocated when
+    not given."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.dtype not in _TYPES:
+        raise ValueError("linear expects a 2-D bf16/f16 tensor with unit column stride")
+    rows, K = x.shape
+    N = wq.shape[0]
+    if out is None:
+        out = torch.empty((rows, N), dtype=out_dtype, device=x.device)
+    if scratch is None:
+        shape = ((K + group - 1) // group, rows) if group else (rows,)
+        scratch = (torch.empty((rows, K), dtype=torch.uint8, device=x.device),
+                   torch.empty(shape, dtype=torch.float32, device=x.device))
+    need = workspace_bytes(path, rows, N, K, fmt, group, group)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    p = (path or Path()).to_c()
+    _check(load().qlin_linear(ctypes.byref(p), x.data_ptr(), x.stride(0), _TYPES[x.dtype],
+                              scratch[0].data_ptr(), scratch[1].data_ptr(), wq.data_ptr(),
+                              sw.data_ptr(), out.data_ptr(), rows, N, K, fmt, _TYPES[out.dtype],
+                              group, group, rotation, ws_ptr, ws_bytes, _stream(stream)))
+    return out

@@ -14,6 +14,8 @@
  *                          ops/cuda/quantization_policy.cpp:269-286, ops/cuda/quantization.cpp:27-64
  *   qlin_workspace_bytes   (the split-K bound checks of quant_gemm_sm80.cu:45-46,
  *                          quant_grouped.cu:232-233, made queryable)
+ *   qlin_linear         <- the quantized branch of ops::linear  ops/linear.cpp:51-71
+ *                          (quantize_rows into scratch, then QuantizedGemm::linear)
  *
  * Operand layouts (reference core/quantization.h:24-49):
  *   x  int8/e4m3 [rows, K] dense          sx f32 [rows] or [ceil(K/ig), rows]
@@ -107,6 +109,17 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
               const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
               int input_group, int weight_group, void *workspace, size_t workspace_bytes,
               qlin_stream_t stream);
+
+/* Quantized branch of the reference ops::linear (ops/linear.cpp:51-71): the
+ * 16-bit activations x [rows, ld] are quantized with (fmt, input_group,
+ * rotation) into the scratch activation (xq [rows, K], sx), as
+ * qlin_row_quantize, then y = D(xq . w^T) as qlin_gemm with `path` (NULL =
+ * planned). Two launches on `stream`; the first failing check's status is
+ * returned. */
+int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void *xq, float *sx,
+                const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,
+                int out_type, int input_group, int weight_group, int rotation, void *workspace,
+                size_t workspace_bytes, qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -89,3 +89,31 @@ def test_plan_and_workspace():
     assert qlinear.workspace_bytes(split, 32, 4096, 2048, I8) == 4 * 32 * 4096 * 4
     with pytest.raises(qlinear.QLinearError):
         qlinear.plan(0, 16, 16, I8)
+
+
+def test_decode_grid_plans():
+    """Decode planning puts one workgroup on each of the 256 CUs at the
+    BASELINE projections (M=32): tiles x token tiles == 256, slab within LDS."""
+    for N, K in ((4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144)):
+        p = qlinear.plan(32, N, K, I8)
+        assert p.kind == qlinear.KIND_SKINNY
+        assert (N // p.channels) * (-(-32 // p.tokens)) == 256, (N, K, p)
+        assert p.staged
+
+
+def test_linear_validation():
+    """qlin_linear checks its quantize half, then its GEMM half."""
+    L = qlinear.load()
+
+    def call(x=FAKE, ld=2048, st=BF16, xq=FAKE, sx=FAKE, M=32, N=4096, K=2048, fmt=I8,
+             out=BF16, ig=0, wg=0, rot=0):
+        return L.qlin_linear(None, x, ld, st, xq, sx, FAKE, FAKE, FAKE, M, N, K, fmt, out, ig,
+                             wg, rot, None, 0, None)
+
+    assert call(xq=None) == -1                 # scratch activation required
+    assert b"scratch" in L.qlin_last_error()
+    assert call(st=F32) == -1
+    assert call(ld=1024) == -1
+    assert call(x=None) == -1
+    assert call(rot=64) == -1
+    assert call(x=FAKE + 1) == -2
