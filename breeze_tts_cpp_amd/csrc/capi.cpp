@@ -93,8 +93,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         return p;
     }
     // Prefill: the largest macro tile that still gives every CU a tile.
-    // INT8 256x256 runs eight waves of 128x64; FP8 (32x32x64 MFMA tiles) uses
-    // 128x128, the fastest shape whose double-buffered fragments fit in registers.
+    // 256x256 runs eight waves of 128x64 for INT8 (16x16x64 MFMA) and four
+    // waves of 128x128 for FP8 (32x32x64 MFMA), the faster shape of each
+    // format on MI355X at M=4096; 256x128 and 128x128 run four waves.
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;
@@ -102,13 +103,12 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     const bool grouped = input_group || weight_group;
     for (const auto &s : shapes) {
         if (grouped && s[1] == 256) continue;
-        if (fmt == QLIN_FP8 && !grouped && s[0] == 256) continue;
         long tiles = long((N + s[0] - 1) / s[0]) * ((rows + s[1] - 1) / s[1]);
         p.channels = s[0];
         p.tokens = s[1];
         if (tiles >= 256) break;
     }
-    if (p.channels == 256 && p.tokens == 256) p.waves = 8;
+    if (p.channels == 256 && p.tokens == 256) p.waves = fmt == QLIN_FP8 ? 4 : 8;
     return p;
 }
 
@@ -163,10 +163,17 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
                         p.tokens);
         if (p.splits != 1)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no split-K variant");
-        if (p.waves != 1 && p.waves != 8)
-            return fail(QLIN_ERR_UNSUPPORTED, "tiled path waves must be 1 or 8");
-        if ((p.waves == 8) != (p.channels == 256 && p.tokens == 256))
-            return fail(QLIN_ERR_UNSUPPORTED, "tiled 256x256 runs eight waves; other tiles run one");
+        // 256x256: eight waves of 128x64 (16x16 MFMA) or four of 128x128
+        // (32x32 MFMA); 256x128: one workgroup of 128x64 waves, or two waves
+        // of 128x128; 128x128: four waves of 64x64.
+        const bool wave_ok = (p.channels == 256 && p.tokens == 256) ? (p.waves == 8 || p.waves == 4)
+                             : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2)
+                                                                       : p.waves == 1;
+        if (!wave_ok)
+            return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,
+                        p.tokens, p.waves);
+        if ((p.waves == 2 || p.waves == 4) && (input_group || weight_group))
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
         if (p.staged)

@@ -464,6 +464,252 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     }
 }
 
+// Per-channel GEMM on 32x32 MFMA tiles with 128x128 wave tiles
+// (INT8: v_mfma_i32_32x32x32_i8; FP8: v_mfma_scale_f32_32x32x64_f8f6f4),
+// WN x WM wave64s, one wave per SIMD. LDS traffic per MFMA op is what bounds
+// the 128x64-wave kernel above on gfx950 (~128 B/clk per CU for ds_read_b128
+// plus the global->LDS writes): a 128x128 wave tile reads (128+128)*64 bytes
+// of fragments per 128*128*64 MACs, 2/3 of the 128x64 tile's bytes per MAC.
+// The K ring is the same: 64-byte stages filled by buffer_load ... lds, 16-byte
+// chunk c of stage row r at c ^ ((r >> 2) & 3) (conflict-free for 32-row
+// fragment reads, where lanes l and l+32 read chunks 2h and 2h+1).
+template <int Fmt, int WN, int WM, int STAGES, bool KFull, class Out>
+__global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
+    const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
+    const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+    constexpr int NW = WN * WM, BN = 128 * WN, BM = 128 * WM, BK = 64, RPI = 16;
+    constexpr int ROWS = BN + BM, INSTS = ROWS / (RPI * NW), W_INSTS = BN / (RPI * NW);
+    constexpr int STAGE_BYTES = ROWS * BK;
+    static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+
+    const int tiles = tiles_m * tiles_n;
+    int b = blockIdx.x;
+    if (tiles % 8 == 0) b = (b % 8) * (tiles / 8) + b / 8;
+    constexpr int kGroupN = 4;
+    const int group = b / (kGroupN * tiles_m), in_group = b % (kGroupN * tiles_m);
+    const int group_w = min(kGroupN, tiles_n - group * kGroupN);
+    const int tn = group * kGroupN + in_group % group_w, tm = in_group / group_w;
+    const int n_base = tn * BN, m_base = tm * BM;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_n = wave % WN, wave_m = wave / WN;
+
+    const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w + size_t(n_base) * K), 0, min(BN, N - n_base) * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_x = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(x + size_t(m_base) * K), 0, min(BM, M - m_base) * K, 0x00020000);
+
+    // Load instruction i of this wave writes stage rows [(i*NW + wave)*16, +16)
+    // in lane order (row += lane / 4, physical chunk lane % 4); the first row
+    // is a multiple of 16, so the lane's logical source chunk is fixed.
+    const int lane_row = lane >> 2;
+    const int lane_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const uint32_t lane_voff = uint32_t(lane_row) * uint32_t(K) + uint32_t(lane_chunk * 16);
+    constexpr int kRingBytes = STAGES * STAGE_BYTES > NW * 128 * 256 ? STAGES * STAGE_BYTES
+                                                                      : NW * 128 * 256;
+    float *scl = reinterpret_cast<float *>(lds + kRingBytes);
+    const int stages = (K + BK - 1) / BK;
+    auto issue = [&](int stage, int k0) {
+        uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
+        const uint32_t voff =
+            (KFull || k0 + lane_chunk * 16 < K) ? lane_voff + uint32_t(k0) : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < INSTS; ++i) {
+            const int row = (i * NW + wave) * RPI;
+            const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
+            lds_ptr_t dst = (lds_ptr_t)(base + (i * NW + wave) * 1024);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rsrc_w : rsrc_x, dst, 16, voff,
+                                                     soff, 0, 0);
+        }
+    };
+
+    // Tile scales to LDS past the ring (read by the epilogue).
+
+    // Tile scales to LDS past the ring (read by the epilogue).
+    constexpr int kScaleLoads = (BN + BM + 64 * NW - 1) / (64 * NW);
+    float scale_v[kScaleLoads];
+#pragma unroll
+    for (int l = 0; l < kScaleLoads; ++l) {
+        const int i = tid + l * 64 * NW;
+        float v = 1.f;
+        if (i < BN) v = sw[min(n_base + i, N - 1)];
+        else if (i < BN + BM) v = sx[min(m_base + i - BN, M - 1)];
+        scale_v[l] = v;
+    }
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+        if (s < stages) issue(s, s * BK);
+#pragma unroll
+    for (int l = 0; l < kScaleLoads; ++l)
+        if (tid + l * 64 * NW < BN + BM) scl[tid + l * 64 * NW] = scale_v[l];
+
+    // Fragment reads: lane l covers row l % 32 of a 32-row tile; tiles t of
+    // the wave's A (weights) and B (tokens) rows are 32*64 bytes apart.
+    const int swz = (lane >> 2) & 3, g = lane >> 5;
+    const int a_off = (wave_n * 128 + (lane & 31)) * BK;
+    const int b_off = (BN + wave_m * 128 + (lane & 31)) * BK;
+    const int c0 = ((2 * 0 + g) ^ swz) * 16, c1 = ((2 * 1 + g) ^ swz) * 16;  // INT8 sub-steps
+    const int f0 = ((2 * g) ^ swz) * 16, f1 = ((2 * g + 1) ^ swz) * 16;      // FP8 halves
+
+    using Acc = std::conditional_t<Fmt == I8, i32x16, f32x16>;
+    Acc acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    if constexpr (Fmt == I8) {
+        // Iteration s: read sub-step 1 of stage s while sub-step 0's MFMAs
+        // run; barrier (stage s fully read by every wave, stage s+1 landed);
+        // refill stage s's buffer with stage s+STAGES; read sub-step 0 of
+        // stage s+1 while sub-step 1's MFMAs run.
+        auto read = [&](int st, int h, i32x4 (&fa)[4], i32x4 (&fb)[4]) {
+            const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
+            const int c = h ? c1 : c0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                fa[t] = *reinterpret_cast<const i32x4 *>(cur + a_off + t * 32 * BK + c);
+                fb[t] = *reinterpret_cast<const i32x4 *>(cur + b_off + t * 32 * BK + c);
+            }
+        };
+        auto mma = [&](const i32x4 (&fa)[4], const i32x4 (&fb)[4]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        };
+        i32x4 a0[4], b0[4], a1[4], b1[4];
+        if (stages >= STAGES) wait_vmcnt<INSTS * (STAGES - 1)>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        read(0, 0, a0, b0);
+        for (int s = 0; s < stages; ++s) {
+            read(s, 1, a1, b1);
+            mma(a0, b0);
+            if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+            else wait_vmcnt<0>();
+            lds_barrier();
+            if (s + STAGES < stages) issue(s + STAGES, (s + STAGES) * BK);
+            if (s + 1 < stages) read(s + 1, 0, a0, b0);
+            mma(a1, b1);
+        }
+    } else {
+        // FP8: one 32x32x64 MFMA per tile pair per stage. Sub-step 0 = A
+        // fragments + token tiles 0-1, sub-step 1 = token tiles 2-3.
+        auto frag = [&](const uint8_t *p) {
+            const i32x4 lo = *reinterpret_cast<const i32x4 *>(p + f0);
+            const i32x4 hi = *reinterpret_cast<const i32x4 *>(p + f1);
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        auto read0 = [&](int st, i32x8 (&fa)[4], i32x8 (&fb)[2]) {
+            const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) fa[t] = frag(cur + a_off + t * 32 * BK);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) fb[t] = frag(cur + b_off + t * 32 * BK);
+        };
+        auto read1 = [&](int st, i32x8 (&fb)[2]) {
+            const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) fb[t] = frag(cur + b_off + (t + 2) * 32 * BK);
+        };
+        auto mma = [&](const i32x8 (&fa)[4], const i32x8 (&fb)[2], int j0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j0 + j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        fa[i], fb[j], acc[i][j0 + j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        };
+        i32x8 fa[4], fb0[2], fb1[2];
+        if (stages >= STAGES) wait_vmcnt<INSTS * (STAGES - 1)>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        read0(0, fa, fb0);
+        for (int s = 0; s < stages; ++s) {
+            read1(s, fb1);
+            mma(fa, fb0, 0);
+            // fa is still needed by the second half: the next stage's A
+            // fragments are read after it.
+            if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+            else wait_vmcnt<0>();
+            lds_barrier();
+            if (s + STAGES < stages) issue(s + STAGES, (s + STAGES) * BK);
+            mma(fa, fb1, 2);
+            if (s + 1 < stages) read0(s + 1, fa, fb0);
+        }
+    }
+
+    // Epilogue: scale, round, transpose through LDS (the ring is free after
+    // the barrier), 16-byte row stores. Lane l, register 4b+e of tile (i, j)
+    // holds C[n = 32i + 8b + 4*(l/32) + e][m = 32j + l % 32].
+    constexpr int TM = 128, TN = 128, ROWB = TN * 2, CH = ROWB / 16;
+    lds_barrier();
+    uint8_t *wbuf = lds + wave * TM * ROWB;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m_l = j * 32 + (lane & 31);
+        const float sxm = scl[BN + wave_m * TM + m_l];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int blk = 0; blk < 4; ++blk) {
+                const int n_l = i * 32 + blk * 8 + g * 4;
+                const f32x4 swv = *reinterpret_cast<const f32x4 *>(scl + wave_n * TN + n_l);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float t = float(acc[i][j][blk * 4 + e]) * sxm;
+                    v[e] = t * swv[e];
+                }
+                uint2 packed;
+                packed.x = pack2(v[0], v[1], Out{});
+                packed.y = pack2(v[2], v[3], Out{});
+                const int byte = n_l * 2;
+                *reinterpret_cast<uint2 *>(wbuf + m_l * ROWB + (((byte >> 4) ^ (m_l % CH)) << 4) +
+                                           (byte & 15)) = packed;
+            }
+    }
+    const bool vec16 = (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll 4
+    for (int r0 = 0; r0 < TM; r0 += 64 / CH) {
+        const int m_l = r0 + lane / CH, c = lane % CH;
+        const uint4 val =
+            *reinterpret_cast<const uint4 *>(wbuf + m_l * ROWB + ((c ^ (m_l % CH)) << 4));
+        const int m = m_base + wave_m * TM + m_l, n = n_base + wave_n * TN + c * 8;
+        if (m >= M || n >= N) continue;
+        uint16_t *dst = static_cast<uint16_t *>(y) + size_t(m) * N + n;
+        if (vec16) {
+            *reinterpret_cast<uint4 *>(dst) = val;
+        } else {
+            reinterpret_cast<uint2 *>(dst)[0] = make_uint2(val.x, val.y);
+            reinterpret_cast<uint2 *>(dst)[1] = make_uint2(val.z, val.w);
+        }
+    }
+}
+
+template <int Fmt, int WN, int WM, int STAGES, class Out>
+int launch_wide(const GemmArgs &a, hipStream_t stream) {
+    constexpr int BN = 128 * WN, BM = 128 * WM;
+    const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
+    const size_t lds = std::max(size_t(STAGES) * (BN + BM) * 64, size_t(WN * WM) * 128 * 256) +
+                       size_t(BN + BM) * 4;
+    dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
+    if (a.K % 64 == 0)
+        hipLaunchKernelGGL((wide_gemm<Fmt, WN, WM, STAGES, true, Out>), grid, block, lds, stream,
+                           a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((wide_gemm<Fmt, WN, WM, STAGES, false, Out>), grid, block, lds, stream,
+                           a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n);
+    return 0;
+}
+
 template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, class Out>
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
@@ -495,6 +741,10 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 4, 4, 128, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
+        if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
+            return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
+        if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
+            return launch_wide<Fmt, 2, 1, 3, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
@@ -503,6 +753,10 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         return -4;
     } else {
+        if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
+            return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
+        if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
+            return launch_wide<Fmt, 2, 1, 3, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)

@@ -227,8 +227,11 @@ def _tiled_paths(grouped=False, fmt=I8):
     """Every instantiated macro tile (channels x tokens, waves) for the mode."""
     from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
     shapes = [(256, 128, 1), (128, 128, 1)]
-    if not grouped and fmt == I8:
-        shapes = [(256, 256, 8)] + shapes
+    if not grouped:
+        # 32x32-MFMA kernels: four waves of 128x128, two waves of 128x128
+        shapes = [(256, 256, 4), (256, 128, 2)] + shapes
+        if fmt == I8:
+            shapes = [(256, 256, 8)] + shapes
     for channels, tokens, waves in shapes:
         yield Path(KIND_TILED, tokens, channels, 1, waves)
 
