@@ -311,4 +311,60 @@ int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void
                      workspace, workspace_bytes, stream);
 }
 
+int qlin_quantized_norm(void *residual, const void *update, const void *update_scale,
+                        const void *weight, int src_type, int rows, int cols, float eps, int gemma,
+                        void *values, float *scales, int fmt, int group, int rotation,
+                        qlin_stream_t stream) {
+    // launch_quantized_norm's checks (reference quant_norm.cu:166-180) plus
+    // RowScaledView::validate (core/quantization.h:39-48).
+    if (src_type != QLIN_BF16 && src_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "quantized RMS input must be BF16 or F16");
+    if (fmt != QLIN_I8 && fmt != QLIN_FP8)
+        return fail(QLIN_ERR_INVALID, "quantized storage must be I8 or FP8");
+    if (rows < 1 || cols < 1 || cols > 2048)
+        return fail(QLIN_ERR_INVALID, "quantized RMS shape rows=%d cols=%d (1 <= cols <= 2048)",
+                    rows, cols);
+    if (!residual || !weight || !values || !scales)
+        return fail(QLIN_ERR_INVALID, "quantized RMS pointer is null");
+    if (update_scale && !update)
+        return fail(QLIN_ERR_INVALID, "update_scale without update");
+    if (!valid_group(group))
+        return fail(QLIN_ERR_INVALID, "quantization group must be 0, 32, 64 or 128 (got %d)", group);
+    if (rotation && (rotation != 128 || cols % 128))
+        return fail(QLIN_ERR_INVALID, "rotation must be 128 with cols %% 128 == 0");
+    if (!aligned(residual, 2) || !aligned(weight, 2) || (update && !aligned(update, 2)) ||
+        (update_scale && !aligned(update_scale, 2)))
+        return fail(QLIN_ERR_ALIGNMENT, "16-bit tensors must be 2-byte aligned");
+    if (!aligned(scales, 4)) return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
+    qlin::NormQuantizeArgs a{residual, update, update_scale, weight, src_type, rows, cols,
+                             values, scales, fmt, group, rotation, gemma ? 1 : 0, eps};
+    qlin::launch_quantized_norm(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("quantized norm launch");
+}
+
+int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,
+                         void *values, float *scales, int fmt, int group, int rotation,
+                         qlin_stream_t stream) {
+    // launch_quantized_gated's checks (reference quant_gated.cu:182-191).
+    if (src_type != QLIN_BF16 && src_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "quantized gated input must be BF16 or F16");
+    if (fmt != QLIN_I8 && fmt != QLIN_FP8)
+        return fail(QLIN_ERR_INVALID, "quantized storage must be I8 or FP8");
+    if (rows < 1 || width < 1 || width > 8192 || kind < 0 || kind > 1)
+        return fail(QLIN_ERR_INVALID, "quantized gated shape/kind rows=%d width=%d kind=%d", rows,
+                    width, kind);
+    if (!input || !values || !scales)
+        return fail(QLIN_ERR_INVALID, "quantized gated pointer is null");
+    if (!valid_group(group))
+        return fail(QLIN_ERR_INVALID, "quantization group must be 0, 32, 64 or 128 (got %d)", group);
+    if (rotation && (rotation != 128 || width % 128))
+        return fail(QLIN_ERR_INVALID, "rotation must be 128 with width %% 128 == 0");
+    if (!aligned(input, 2)) return fail(QLIN_ERR_ALIGNMENT, "16-bit input must be 2-byte aligned");
+    if (!aligned(scales, 4)) return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
+    qlin::GatedQuantizeArgs a{input, src_type, rows, width, values, scales, fmt, group, rotation,
+                              kind};
+    qlin::launch_quantized_gated(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("quantized gated launch");
+}
+
 }  // extern "C"

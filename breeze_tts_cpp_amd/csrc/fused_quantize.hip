@@ -1,0 +1,250 @@
+// Fused quantizing producers for gfx950: the kernels that write the quantized
+// activation of the next projection directly, without a 16-bit round trip
+// through HBM.
+//
+//   residual_rms_quantize: optional residual update x += u (* s), RMSNorm
+//     (plain or Gemma weight+1) in 16-bit storage precision, then row
+//     quantization (reference launch_quantized_norm,
+//     ops/kernels/quant/quant_norm.cu:14-123,166-188; cols <= 2048).
+//   gated_quantize: act(gate) * up of a [rows, 2*width] gate|up matrix,
+//     act = SiLU (kind 0) or tanh-GeLU (kind 1), then row quantization
+//     (reference launch_quantized_gated, quant_gated.cu:18-85,179-198;
+//     width <= 8192).
+//
+// Both hand the normalized / activated 16-bit row, held in registers, to the
+// same row encoder as the row quantizer (per token, H128-rotated, K groups).
+//
+// Arithmetic contract (every TU builds with -ffp-contract=off):
+//  - 16-bit pair arithmetic (the reference's __hadd2 / __hmul2 and packing)
+//    is the fp32 result rounded to the storage type, to nearest even; for
+//    bf16/f16 operands that equals the singly rounded 16-bit operation.
+//  - The squared sum follows the reference's order: lane t of 256 sums its 8
+//    columns as sum += x0*x0 + x1*x1 pairwise, a 32-lane shuffle-down tree
+//    (strides 16..1) reduces each 32-lane group, and the 8 group partials are
+//    added in order. The mean is total / cols (IEEE).
+//  - 1/sqrt(mean + eps) is the correctly rounded fp32 value (evaluated in
+//    fp64); the reference's rsqrtf is an approximation within 2 ulp of it.
+//  - SiLU is (x*2^-16) / ((1 + e^-x) * 2^-16) and tanh-GeLU is
+//    (0.5x)(1 + tanh(0.7978845608028654 (x + ((0.044715x)x)x))) in fp32, with
+//    e^-x and tanh evaluated in fp64 and rounded to fp32 (the reference's
+//    __expf / __fdividef / tanhf are approximations of the same values).
+#include "qlin_device.hpp"
+#include "qlin_internal.hpp"
+#include "row_encode.hpp"
+
+namespace qlin {
+namespace {
+
+template <class T> __device__ __forceinline__ float round16(float x) {
+    return to_float(from_float(x, T{}), T{});
+}
+
+template <class T, bool Vec>
+__device__ __forceinline__ void store16x8(uint16_t *row, int column, int cols, const float (&v)[8]) {
+    if constexpr (Vec) {
+        if (column < cols) {
+            uint4 packed;
+            packed.x = pack2(v[0], v[1], T{});
+            packed.y = pack2(v[2], v[3], T{});
+            packed.z = pack2(v[4], v[5], T{});
+            packed.w = pack2(v[6], v[7], T{});
+            *reinterpret_cast<uint4 *>(row + column) = packed;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (column + i < cols) row[column + i] = from_float(v[i], T{});
+    }
+}
+
+// Correctly rounded 1/sqrt(a) in fp32.
+__device__ __forceinline__ float rsqrt_rn(float a) {
+    return float(1.0 / sqrt(double(a)));
+}
+
+// One 256-thread workgroup per row; lane t holds columns [8t, 8t+8).
+template <int Fmt, class T, bool Add, bool Scaled, bool Gemma, bool Rot, int G, bool Vec>
+__global__ __launch_bounds__(kThreads) void residual_rms_quantize(
+    uint16_t *__restrict__ x, const uint16_t *__restrict__ update,
+    const uint16_t *__restrict__ update_scale, const uint16_t *__restrict__ weight,
+    uint8_t *__restrict__ q, float *__restrict__ scales, int rows, int cols, float eps) {
+    const int row = blockIdx.x, column = threadIdx.x * 8;
+    uint16_t *xr = x + size_t(row) * cols;
+    float v[1][8], w[8];
+    load8<T, Vec>(xr, column, cols, v[0]);
+    load8<T, Vec>(weight, column, cols, w);
+    if constexpr (Add) {
+        float u[8];
+        load8<T, Vec>(update + size_t(row) * cols, column, cols, u);
+        if constexpr (Scaled) {
+            float s[8];
+            load8<T, Vec>(update_scale, column, cols, s);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) u[i] = round16<T>(u[i] * s[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[0][i] = round16<T>(v[0][i] + u[i]);
+        store16x8<T, Vec>(xr, column, cols, v[0]);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) sum += v[0][2 * p] * v[0][2 * p] + v[0][2 * p + 1] * v[0][2 * p + 1];
+#pragma unroll
+    for (int d = 16; d; d /= 2) sum += __shfl_down(sum, d, 32);
+    __shared__ float partial[kThreads / 32];
+    if ((threadIdx.x & 31) == 0) partial[threadIdx.x / 32] = sum;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int p = 0; p < kThreads / 32; ++p) total += partial[p];
+    const float inv_norm = rsqrt_rn(total / float(cols) + eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if constexpr (Gemma) v[0][i] = round16<T>((v[0][i] * inv_norm) * (w[i] + 1.f));
+        else v[0][i] = round16<T>(round16<T>(v[0][i] * inv_norm) * w[i]);
+    }
+    encode_row<Fmt, 1, Rot, G, Vec>(v, q, scales, row, rows, cols);
+}
+
+template <int Kind> __device__ __forceinline__ float activate(float x) {
+    if constexpr (Kind == 0) {
+        const float e = float(exp(-double(x)));
+        return (x * 0x1p-16f) / ((1.f + e) * 0x1p-16f);
+    } else {
+        const float inner = x + ((0.044715f * x) * x) * x;
+        const float t = float(tanh(double(0.7978845608028654f * inner)));
+        return (0.5f * x) * (1.f + t);
+    }
+}
+
+// One 256-thread workgroup per row; chunk `it` of lane t covers output
+// columns (it*256 + t)*8 .. +8 (gate at that column, up at width + column).
+template <int Fmt, class T, int Kind, int Items, bool Rot, int G, bool Vec>
+__global__ __launch_bounds__(kThreads) void gated_quantize(const uint16_t *__restrict__ input,
+                                                           uint8_t *__restrict__ q,
+                                                           float *__restrict__ scales, int rows,
+                                                           int width) {
+    const int row = blockIdx.x;
+    const uint16_t *gate = input + size_t(row) * width * 2, *up = gate + width;
+    float v[Items][8];
+#pragma unroll
+    for (int it = 0; it < Items; ++it) {
+        const int column = (it * kThreads + threadIdx.x) * 8;
+        float g[8], u[8];
+        load8<T, Vec>(gate, column, width, g);
+        load8<T, Vec>(up, column, width, u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(round16<T>(activate<Kind>(g[i])) * u[i]);
+    }
+    encode_row<Fmt, Items, Rot, G, Vec>(v, q, scales, row, rows, width);
+}
+
+// ---------------------------------------------------------------- launchers
+template <int Fmt, class T, bool Add, bool Scaled, bool Gemma, bool Vec>
+void launch_norm_enc(const NormQuantizeArgs &a, hipStream_t s) {
+    auto *x = static_cast<uint16_t *>(a.residual);
+    auto *u = static_cast<const uint16_t *>(a.update);
+    auto *us = static_cast<const uint16_t *>(a.update_scale);
+    auto *w = static_cast<const uint16_t *>(a.weight);
+    auto *q = static_cast<uint8_t *>(a.values);
+#define QLIN_NORM(R, G)                                                                        \
+    hipLaunchKernelGGL((residual_rms_quantize<Fmt, T, Add, Scaled, Gemma, R, G, Vec>),         \
+                       dim3(a.rows), dim3(kThreads), 0, s, x, u, us, w, q, a.scales, a.rows,  \
+                       a.cols, a.eps)
+    if (a.group == 32) { if (a.rotation) QLIN_NORM(true, 32); else QLIN_NORM(false, 32); }
+    else if (a.group == 64) { if (a.rotation) QLIN_NORM(true, 64); else QLIN_NORM(false, 64); }
+    else if (a.group == 128) { if (a.rotation) QLIN_NORM(true, 128); else QLIN_NORM(false, 128); }
+    else if (a.rotation) QLIN_NORM(true, 0);
+    else QLIN_NORM(false, 0);
+#undef QLIN_NORM
+}
+
+template <int Fmt, class T, bool Vec>
+void launch_norm_t(const NormQuantizeArgs &a, hipStream_t s) {
+    if (!a.update) {
+        if (a.gemma) launch_norm_enc<Fmt, T, false, false, true, Vec>(a, s);
+        else launch_norm_enc<Fmt, T, false, false, false, Vec>(a, s);
+    } else if (!a.update_scale) {
+        if (a.gemma) launch_norm_enc<Fmt, T, true, false, true, Vec>(a, s);
+        else launch_norm_enc<Fmt, T, true, false, false, Vec>(a, s);
+    } else {
+        if (a.gemma) launch_norm_enc<Fmt, T, true, true, true, Vec>(a, s);
+        else launch_norm_enc<Fmt, T, true, true, false, Vec>(a, s);
+    }
+}
+
+template <int Fmt, class T, int Kind, int Items, bool Vec>
+void launch_gated_enc(const GatedQuantizeArgs &a, hipStream_t s) {
+    auto *in = static_cast<const uint16_t *>(a.input);
+    auto *q = static_cast<uint8_t *>(a.values);
+#define QLIN_GATED(R, G)                                                                       \
+    hipLaunchKernelGGL((gated_quantize<Fmt, T, Kind, Items, R, G, Vec>), dim3(a.rows),         \
+                       dim3(kThreads), 0, s, in, q, a.scales, a.rows, a.width)
+    if (a.group == 32) { if (a.rotation) QLIN_GATED(true, 32); else QLIN_GATED(false, 32); }
+    else if (a.group == 64) { if (a.rotation) QLIN_GATED(true, 64); else QLIN_GATED(false, 64); }
+    else if (a.group == 128) { if (a.rotation) QLIN_GATED(true, 128); else QLIN_GATED(false, 128); }
+    else if (a.rotation) QLIN_GATED(true, 0);
+    else QLIN_GATED(false, 0);
+#undef QLIN_GATED
+}
+
+template <int Fmt, class T, int Kind, bool Vec>
+void launch_gated_items(const GatedQuantizeArgs &a, hipStream_t s) {
+    switch ((a.width + kChunk - 1) / kChunk) {
+    case 1: launch_gated_enc<Fmt, T, Kind, 1, Vec>(a, s); break;
+    case 2: launch_gated_enc<Fmt, T, Kind, 2, Vec>(a, s); break;
+    case 3: launch_gated_enc<Fmt, T, Kind, 3, Vec>(a, s); break;
+    default: launch_gated_enc<Fmt, T, Kind, 4, Vec>(a, s); break;
+    }
+}
+
+template <int Fmt, class T, bool Vec>
+void launch_gated_t(const GatedQuantizeArgs &a, hipStream_t s) {
+    if (a.kind == 0) launch_gated_items<Fmt, T, 0, Vec>(a, s);
+    else launch_gated_items<Fmt, T, 1, Vec>(a, s);
+}
+
+template <int Fmt, bool Vec>
+void launch_norm_f(const NormQuantizeArgs &a, hipStream_t s) {
+    if (a.src_type == F16) launch_norm_t<Fmt, f16_t, Vec>(a, s);
+    else launch_norm_t<Fmt, bf16_t, Vec>(a, s);
+}
+
+template <int Fmt, bool Vec>
+void launch_gated_f(const GatedQuantizeArgs &a, hipStream_t s) {
+    if (a.src_type == F16) launch_gated_t<Fmt, f16_t, Vec>(a, s);
+    else launch_gated_t<Fmt, bf16_t, Vec>(a, s);
+}
+
+bool aligned_to(const void *p, uintptr_t bytes) {
+    return !p || reinterpret_cast<uintptr_t>(p) % bytes == 0;
+}
+
+}  // namespace
+
+void launch_quantized_norm(const NormQuantizeArgs &a, hipStream_t stream) {
+    // 16-byte row loads/stores and 8-byte code stores need 8-column rows.
+    const bool vec = a.cols % 8 == 0 && aligned_to(a.residual, 16) && aligned_to(a.update, 16) &&
+                     aligned_to(a.update_scale, 16) && aligned_to(a.weight, 16) &&
+                     aligned_to(a.values, 8);
+    if (a.fmt == I8) {
+        if (vec) launch_norm_f<I8, true>(a, stream);
+        else launch_norm_f<I8, false>(a, stream);
+    } else {
+        if (vec) launch_norm_f<FP8, true>(a, stream);
+        else launch_norm_f<FP8, false>(a, stream);
+    }
+}
+
+void launch_quantized_gated(const GatedQuantizeArgs &a, hipStream_t stream) {
+    const bool vec = a.width % 8 == 0 && aligned_to(a.input, 16) && aligned_to(a.values, 8);
+    if (a.fmt == I8) {
+        if (vec) launch_gated_f<I8, true>(a, stream);
+        else launch_gated_f<I8, false>(a, stream);
+    } else {
+        if (vec) launch_gated_f<FP8, true>(a, stream);
+        else launch_gated_f<FP8, false>(a, stream);
+    }
+}
+
+}  // namespace qlin

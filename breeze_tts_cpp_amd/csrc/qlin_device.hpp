@@ -36,7 +36,12 @@ __device__ __forceinline__ uint16_t from_float(float f, bf16_t) {
     u += 0x7fffu + ((u >> 16) & 1u);
     return uint16_t(u >> 16);
 }
+// The empty asm keeps `f` a materialized fp32 value: without it the compiler
+// may fold the fp32 operation producing `f` and this conversion into one
+// mixed-precision instruction (v_mad_mixlo_f16) that rounds the exact result
+// once, where the reference rounds to fp32 first and then to f16.
 __device__ __forceinline__ uint16_t from_float(float f, f16_t) {
+    asm volatile("" : "+v"(f));
     _Float16 v = (_Float16)f;  // v_cvt_f16_f32, round-to-nearest-even
     uint16_t h;
     __builtin_memcpy(&h, &v, 2);

@@ -16,6 +16,28 @@ struct RowQuantizeArgs {
 };
 void launch_row_quantize(const RowQuantizeArgs &, hipStream_t);
 
+// Fused producers (fused_quantize.hip). Dense rows; 16-bit tensors share src_type.
+struct NormQuantizeArgs {
+    void *residual;              // [rows, cols], updated in place when update != null
+    const void *update;          // [rows, cols] or null
+    const void *update_scale;    // [cols] or null
+    const void *weight;          // [cols]
+    int src_type, rows, cols;    // cols <= 2048
+    void *values;                // int8/e4m3 [rows, cols]
+    float *scales;
+    int fmt, group, rotation, gemma;
+    float eps;
+};
+void launch_quantized_norm(const NormQuantizeArgs &, hipStream_t);
+struct GatedQuantizeArgs {
+    const void *input;           // [rows, 2*width]: gate | up
+    int src_type, rows, width;   // width <= 8192
+    void *values;                // int8/e4m3 [rows, width]
+    float *scales;
+    int fmt, group, rotation, kind;  // kind 0 = SiLU, 1 = tanh-GeLU
+};
+void launch_quantized_gated(const GatedQuantizeArgs &, hipStream_t);
+
 // Kernel families; numbering is part of the C ABI (qlin_path.kind).
 enum Kind : int { KIND_AUTO = 0, KIND_SKINNY = 1, KIND_TILED = 2 };
 

@@ -1,0 +1,140 @@
+// Row encoders shared by the row quantizer and the fused quantizing producers
+// (residual + RMSNorm -> quant, gated activation -> quant): a 256-thread
+// workgroup holds a row in registers, lane t owning the 8 columns
+// (it * 256 + t) * 8 .. +8 of each 2048-column chunk `it`, and encodes it per
+// token, per token after the H128 rotation, or per K group (optionally
+// rotated) exactly as the reference quant_device helpers do
+// (ops/kernels/quant/quant_device.cuh:63-195).
+#pragma once
+#include "qlin_device.hpp"
+
+namespace qlin {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = kThreads * 8;  // columns covered by one pass of the block
+
+template <class Tin, bool Vec>
+__device__ __forceinline__ void load8(const uint16_t *row, int column, int cols, float (&v)[8]) {
+    if constexpr (Vec) {
+        if (column < cols) {
+            uint4 raw = *reinterpret_cast<const uint4 *>(row + column);
+            uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = to_float(uint16_t(words[i] & 0xffffu), Tin{});
+                v[2 * i + 1] = to_float(uint16_t(words[i] >> 16), Tin{});
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = column + i < cols ? to_float(row[column + i], Tin{}) : 0.f;
+    }
+}
+
+template <int Fmt, bool Vec>
+__device__ __forceinline__ void store8(uint8_t *row, int column, int cols, const float (&v)[8],
+                                       float inverse) {
+    uint32_t code[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) code[i] = encode<Fmt>(v[i] * inverse);
+    if constexpr (Vec) {
+        if (column < cols) {
+            uint2 packed;
+            packed.x = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+            packed.y = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+            *reinterpret_cast<uint2 *>(row + column) = packed;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (column + i < cols) row[column + i] = uint8_t(code[i]);
+    }
+}
+
+// H128 rotation of the 8 columns [column, column+8) held by this lane; the 16
+// lanes sharing (lane >> 4) hold one aligned 128-column block.
+__device__ __forceinline__ void rotate8(float (&v)[8], int column) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * rotation_sign(column + i);
+#pragma unroll
+    for (int span = 1; span < 8; span *= 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & span)) {
+                float a = v[i], b = v[i | span];
+                v[i] = a + b;
+                v[i | span] = a - b;
+            }
+    }
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int span = 1; span < 16; span *= 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float other = __shfl_xor(v[i], span, 64);
+            v[i] = (lane & span) ? other - v[i] : v[i] + other;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] *= 0.08838834764831845f;
+}
+
+__device__ __forceinline__ float block_max(float v) {
+    __shared__ float partial[kThreads / 64];
+    v = group_max<64>(v);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = partial[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, partial[w]);
+    return r;
+}
+
+// Encode a row held in registers (v[it][i] = column (it*kThreads + t)*8 + i;
+// columns past `cols` hold 0): optional H128 rotation, then per-(row, G) scales
+// ([ceil(cols/G), rows]) when G > 0, else one per-token scale ([rows]).
+// The reference's rotated_quantize / encode_group / token paths
+// (quant_device.cuh:63-88,145-195, row_quantize.cu:24-165).
+template <int Fmt, int Items, bool Rot, int G, bool Vec>
+__device__ __forceinline__ void encode_row(float (&v)[Items][8], uint8_t *__restrict__ q,
+                                           float *__restrict__ scales, int row, int rows,
+                                           int cols) {
+    uint8_t *dst = q + size_t(row) * cols;
+    if constexpr (Rot) {
+#pragma unroll
+        for (int it = 0; it < Items; ++it) rotate8(v[it], (it * kThreads + threadIdx.x) * 8);
+    }
+    if constexpr (G > 0) {
+#pragma unroll
+        for (int it = 0; it < Items; ++it) {
+            const int column = (it * kThreads + threadIdx.x) * 8;
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[it][i]));
+            amax = group_max<G / 8>(amax);
+            const float step = quant_scale<Fmt>(amax);
+            if (column < cols && (column % G) == 0) scales[size_t(column / G) * rows + row] = step;
+            store8<Fmt, Vec>(dst, column, cols, v[it], 1.f / step);
+        }
+    } else {
+        float amax = 0.f;
+#pragma unroll
+        for (int it = 0; it < Items; ++it)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[it][i]));
+        const float step = quant_scale<Fmt>(block_max(amax));
+        const float inverse = 1.f / step;
+        if (threadIdx.x == 0) scales[row] = step;
+#pragma unroll
+        for (int it = 0; it < Items; ++it)
+            store8<Fmt, Vec>(dst, (it * kThreads + threadIdx.x) * 8, cols, v[it], inverse);
+    }
+}
+
+}  // namespace
+}  // namespace qlin

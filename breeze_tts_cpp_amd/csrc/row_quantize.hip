@@ -17,93 +17,10 @@
 // shuffles (stride 8..64), the ascending-stride order the reference uses.
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
+#include "row_encode.hpp"
 
 namespace qlin {
 namespace {
-
-constexpr int kThreads = 256;
-constexpr int kChunk = kThreads * 8;  // columns covered by one pass of the block
-
-template <class Tin, bool Vec>
-__device__ __forceinline__ void load8(const uint16_t *row, int column, int cols, float (&v)[8]) {
-    if constexpr (Vec) {
-        if (column < cols) {
-            uint4 raw = *reinterpret_cast<const uint4 *>(row + column);
-            uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[2 * i] = to_float(uint16_t(words[i] & 0xffffu), Tin{});
-                v[2 * i + 1] = to_float(uint16_t(words[i] >> 16), Tin{});
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.f;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            v[i] = column + i < cols ? to_float(row[column + i], Tin{}) : 0.f;
-    }
-}
-
-template <int Fmt, bool Vec>
-__device__ __forceinline__ void store8(uint8_t *row, int column, int cols, const float (&v)[8],
-                                       float inverse) {
-    uint32_t code[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = encode<Fmt>(v[i] * inverse);
-    if constexpr (Vec) {
-        if (column < cols) {
-            uint2 packed;
-            packed.x = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
-            packed.y = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
-            *reinterpret_cast<uint2 *>(row + column) = packed;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (column + i < cols) row[column + i] = uint8_t(code[i]);
-    }
-}
-
-// H128 rotation of the 8 columns [column, column+8) held by this lane; the 16
-// lanes sharing (lane >> 4) hold one aligned 128-column block.
-__device__ __forceinline__ void rotate8(float (&v)[8], int column) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = v[i] * rotation_sign(column + i);
-#pragma unroll
-    for (int span = 1; span < 8; span *= 2) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (!(i & span)) {
-                float a = v[i], b = v[i | span];
-                v[i] = a + b;
-                v[i | span] = a - b;
-            }
-    }
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int span = 1; span < 16; span *= 2) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float other = __shfl_xor(v[i], span, 64);
-            v[i] = (lane & span) ? other - v[i] : v[i] + other;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] *= 0.08838834764831845f;
-}
-
-__device__ __forceinline__ float block_max(float v) {
-    __shared__ float partial[kThreads / 64];
-    v = group_max<64>(v);
-    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = partial[0];
-#pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, partial[w]);
-    return r;
-}
 
 // Per-token (optionally rotated) quantization. Items > 0 keeps the row in
 // registers (cols <= Items * 2048); Items == 0 streams the row twice.

@@ -46,7 +46,8 @@ class Path:
 
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
-           "qlin_workspace_bytes", "qlin_gemm", "qlin_linear")
+           "qlin_workspace_bytes", "qlin_gemm", "qlin_linear", "qlin_quantized_norm",
+           "qlin_quantized_gated")
 
 
 def load():
@@ -73,6 +74,10 @@ def load():
     L.qlin_linear.restype = i
     L.qlin_linear.argtypes = [ctypes.POINTER(qlin_path), P, i, i, P, P, P, P, P, i, i, i, i, i,
                               i, i, i, P, sz, P]
+    L.qlin_quantized_norm.restype = i
+    L.qlin_quantized_norm.argtypes = [P, P, P, P, i, i, i, ctypes.c_float, i, P, P, i, i, i, P]
+    L.qlin_quantized_gated.restype = i
+    L.qlin_quantized_gated.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
     _lib = L
     return L
 
@@ -109,6 +114,53 @@ def row_quantize(x: torch.Tensor, fmt: int, group: int = 0, rotation: int = 0,
     _check(load().qlin_row_quantize(x.data_ptr(), x.stride(0), rows, cols, _TYPES[x.dtype],
                                     values.data_ptr(), scales.data_ptr(), fmt, group, rotation,
                                     _stream(stream)))
+    return values, scales
+
+
+def _outputs(rows, cols, group, device, values, scales):
+    if values is None:
+        values = torch.empty((rows, cols), dtype=torch.uint8, device=device)
+    if scales is None:
+        shape = ((cols + group - 1) // group, rows) if group else (rows,)
+        scales = torch.empty(shape, dtype=torch.float32, device=device)
+    return values, scales
+
+
+def quantized_norm(residual: torch.Tensor, weight: torch.Tensor, fmt: int,
+                   update: torch.Tensor | None = None, update_scale: torch.Tensor | None = None,
+                   eps: float = 1e-6, gemma: bool = False, group: int = 0, rotation: int = 0,
+                   values: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                   stream=None):
+    """Residual update (in place, when `update` is given) + RMSNorm + row
+    quantization of a dense [rows, cols] bf16/f16 tensor (cols <= 2048).
+    Returns (values, scales)."""
+    if residual.dim() != 2 or not residual.is_contiguous() or residual.dtype not in _TYPES:
+        raise ValueError("quantized_norm expects a dense 2-D bf16/f16 residual")
+    for t in (weight, update, update_scale):
+        if t is not None and (t.dtype != residual.dtype or not t.is_contiguous()):
+            raise ValueError("quantized_norm tensors must share the residual dtype and be dense")
+    rows, cols = residual.shape
+    values, scales = _outputs(rows, cols, group, residual.device, values, scales)
+    _check(load().qlin_quantized_norm(
+        residual.data_ptr(), None if update is None else update.data_ptr(),
+        None if update_scale is None else update_scale.data_ptr(), weight.data_ptr(),
+        _TYPES[residual.dtype], rows, cols, float(eps), int(gemma), values.data_ptr(),
+        scales.data_ptr(), fmt, group, rotation, _stream(stream)))
+    return values, scales
+
+
+def quantized_gated(x: torch.Tensor, fmt: int, kind: int = 0, group: int = 0, rotation: int = 0,
+                    values: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                    stream=None):
+    """act(gate) * up of a dense [rows, 2*width] gate|up tensor (kind 0 =
+    SiLU, 1 = tanh-GeLU), then row quantization. Returns (values, scales)."""
+    if x.dim() != 2 or not x.is_contiguous() or x.dtype not in _TYPES or x.shape[1] % 2:
+        raise ValueError("quantized_gated expects a dense [rows, 2*width] bf16/f16 tensor")
+    rows, width = x.shape[0], x.shape[1] // 2
+    values, scales = _outputs(rows, width, group, x.device, values, scales)
+    _check(load().qlin_quantized_gated(x.data_ptr(), _TYPES[x.dtype], rows, width, kind,
+                                       values.data_ptr(), scales.data_ptr(), fmt, group,
+                                       rotation, _stream(stream)))
     return values, scales
 
 

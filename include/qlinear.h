@@ -16,6 +16,10 @@
  *                          quant_grouped.cu:232-233, made queryable)
  *   qlin_linear         <- the quantized branch of ops::linear  ops/linear.cpp:51-71
  *                          (quantize_rows into scratch, then QuantizedGemm::linear)
+ *   qlin_quantized_norm <- launch_quantized_norm   ops/kernels/quant/quant_norm.h:5-7
+ *                          (ops::quantized_norm, ops/basic.h:33-34, ops/basic.cpp:54-58)
+ *   qlin_quantized_gated<- launch_quantized_gated  ops/kernels/quant/quant_gated.h:7-8
+ *                          (ops::quantized_gated, ops/basic.h:35, ops/basic.cpp:59-63)
  *
  * Operand layouts (reference core/quantization.h:24-49):
  *   x  int8/e4m3 [rows, K] dense          sx f32 [rows] or [ceil(K/ig), rows]
@@ -120,6 +124,30 @@ int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void
                 const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,
                 int out_type, int input_group, int weight_group, int rotation, void *workspace,
                 size_t workspace_bytes, qlin_stream_t stream);
+
+/* Residual update + RMSNorm + row quantization in one pass (the reference's
+ * quantized_norm producer, ops/kernels/quant/quant_norm.cu:14-123,166-188):
+ *   if update:  residual[r,c] = s16(residual[r,c] + s16(update[r,c] * update_scale[c]))
+ *               (update_scale optional), stored back into `residual`;
+ *   n[r,c] = gemma ? s16((v*inv) * (weight[c] + 1)) : s16(s16(v*inv) * weight[c]),
+ *               inv = 1/sqrt(mean_c(v^2) + eps);
+ *   then n is quantized as qlin_row_quantize (fmt, group, rotation).
+ * s16 = round to the 16-bit src_type. Dense rows, 1 <= cols <= 2048; residual,
+ * update, update_scale and weight share src_type (BF16 or F16). */
+int qlin_quantized_norm(void *residual, const void *update, const void *update_scale,
+                        const void *weight, int src_type, int rows, int cols, float eps, int gemma,
+                        void *values, float *scales, int fmt, int group, int rotation,
+                        qlin_stream_t stream);
+
+/* Gated activation + row quantization (the reference's quantized_gated
+ * producer, ops/kernels/quant/quant_gated.cu:18-85,179-198): input is
+ * [rows, 2*width] with the gate in columns [0, width) and up in [width, 2*width);
+ *   a[r,c] = s16(s16(act(gate[r,c])) * up[r,c]),  act = SiLU (kind 0) or
+ *   tanh-GeLU (kind 1), then a is quantized as qlin_row_quantize.
+ * Dense rows, 1 <= width <= 8192. */
+int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,
+                         void *values, float *scales, int fmt, int group, int rotation,
+                         qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,16 @@ def lib():
         L.orc_gemm_grouped.argtypes = [P, P, P, P, i, i, i, i, i, i, i, i, i, i, P, P]
         L.orc_gemm_grouped_ideal.restype = None
         L.orc_gemm_grouped_ideal.argtypes = [P, P, P, P, i, i, i, i, i, i, P]
+        L.orc_rsqrt_rn.restype = ctypes.c_float
+        L.orc_rsqrt_rn.argtypes = [ctypes.c_float]
+        L.orc_norm_sumsq.restype = ctypes.c_float
+        L.orc_norm_sumsq.argtypes = [P, i]
+        L.orc_quantized_norm.restype = i
+        L.orc_quantized_norm.argtypes = [P, P, P, P, i, i, i, ctypes.c_float, i, i, i, i, P, P, P]
+        L.orc_activate.restype = ctypes.c_float
+        L.orc_activate.argtypes = [ctypes.c_float, i]
+        L.orc_quantized_gated.restype = i
+        L.orc_quantized_gated.argtypes = [P, i, i, i, i, i, i, i, P, P, P]
         L.orc_cpu_qlinear.restype = i
         L.orc_cpu_qlinear.argtypes = [P, i, i, i, i, P, P, i, i, i, i, P, P, P, i]
         _lib = L
@@ -222,3 +232,57 @@ def cpu_qlinear(x_bits, wq, sw, fmt: int, group: int = 0, rotation: int = 0,
     lib().orc_cpu_qlinear(_p(x_bits), BF16, M, N, K, _p(wq), _p(sw), fmt, group, rotation,
                           out_type, _p(y), _p(xq), _p(sx), threads)
     return y
+
+
+# ---------------------------------------------------------------- fused producers
+def rsqrt_rn(a: float) -> float:
+    return lib().orc_rsqrt_rn(float(a))
+
+
+def norm_sumsq(v: np.ndarray) -> float:
+    v = np.ascontiguousarray(v, np.float32)
+    return lib().orc_norm_sumsq(_p(v), v.size)
+
+
+def activate(x: float, kind: int) -> float:
+    return lib().orc_activate(float(x), kind)
+
+
+def quantized_norm(residual_bits, weight_bits, fmt: int, update_bits=None, scale_bits=None,
+                   eps: float = 1e-6, gemma: bool = False, group: int = 0, rotation: int = 0,
+                   src_type: int = BF16):
+    """Returns (updated residual bits, values uint8 [rows, cols], scales,
+    normalized 16-bit rows)."""
+    res = np.ascontiguousarray(residual_bits, np.uint16).copy()
+    rows, cols = res.shape
+    w = np.ascontiguousarray(weight_bits, np.uint16)
+    u = None if update_bits is None else np.ascontiguousarray(update_bits, np.uint16)
+    s = None if scale_bits is None else np.ascontiguousarray(scale_bits, np.uint16)
+    q = np.zeros((rows, cols), np.uint8)
+    n = np.zeros((rows, cols), np.uint16)
+    groups = (cols + group - 1) // group if group else 1
+    scales = np.zeros((groups, rows) if group else (rows,), np.float32)
+    rc = lib().orc_quantized_norm(_p(res), None if u is None else _p(u),
+                                  None if s is None else _p(s), _p(w), src_type, rows, cols,
+                                  float(eps), int(gemma), fmt, group, rotation, _p(q), _p(scales),
+                                  _p(n))
+    if rc:
+        raise ValueError("oracle: unsupported quantized norm layout")
+    return res, q, scales, n
+
+
+def quantized_gated(input_bits, kind: int, fmt: int, group: int = 0, rotation: int = 0,
+                    src_type: int = BF16):
+    """input [rows, 2*width] (gate | up). Returns (values [rows, width], scales,
+    activated 16-bit rows)."""
+    x = np.ascontiguousarray(input_bits, np.uint16)
+    rows, width = x.shape[0], x.shape[1] // 2
+    q = np.zeros((rows, width), np.uint8)
+    a = np.zeros((rows, width), np.uint16)
+    groups = (width + group - 1) // group if group else 1
+    scales = np.zeros((groups, rows) if group else (rows,), np.float32)
+    rc = lib().orc_quantized_gated(_p(x), src_type, rows, width, kind, fmt, group, rotation,
+                                   _p(q), _p(scales), _p(a))
+    if rc:
+        raise ValueError("oracle: unsupported quantized gated layout")
+    return q, scales, a

@@ -194,6 +194,125 @@ int orc_quantize_rows(const void *src, int src_type, int ld, int rows, int cols,
     return 0;
 }
 
+/* ---------------------------------------------------------------- fused producers */
+/* 1/sqrt(a) rounded once to fp32 (via fp64). The reference's rsqrtf
+ * (quant_norm.cu:75) is an approximation within 2 ulp of this value, so the
+ * normalized rows agree with the reference except where that error crosses a
+ * 16-bit rounding boundary ("parity bounded" for this step). */
+float orc_rsqrt_rn(float a) { return (float)(1.0 / sqrt((double)a)); }
+
+/* Squared-sum reduction of residual_rms_quantize (quant_norm.cu:30-73) over
+ * one row of 16-bit-rounded values v[0..cols): 256 threads, thread t owning
+ * columns [8t, 8t+8) (cols <= 2048), sum += x0*x0 + x1*x1 per pair; per
+ * 32-thread warp a __shfl_down_sync tree with strides 16..1 (a lane whose
+ * source is out of range adds its own value); warp partials summed in order. */
+float orc_norm_sumsq(const float *v, int cols) {
+    float warp[32], next[32], total = 0.f;
+    for (int w = 0; w < 8; ++w) {
+        for (int i = 0; i < 32; ++i) {
+            int t = w * 32 + i;
+            float sum = 0.f;
+            for (int p = 0; p < 4; ++p) {
+                int c = 8 * t + 2 * p;
+                float a = c < cols ? v[c] : 0.f, b = c + 1 < cols ? v[c + 1] : 0.f;
+                sum += a * a + b * b;
+            }
+            warp[i] = sum;
+        }
+        for (int d = 16; d; d /= 2) {
+            for (int i = 0; i < 32; ++i) next[i] = warp[i] + (i + d < 32 ? warp[i + d] : warp[i]);
+            memcpy(warp, next, sizeof(warp));
+        }
+        total += warp[0];
+    }
+    return total;
+}
+
+/* launch_quantized_norm / residual_rms_quantize (quant_norm.cu:14-123,
+ * 166-188): optional residual update (stored back), RMSNorm with 16-bit
+ * rounding points (__hadd2/__hmul2/pack), then the row quantizer on the
+ * normalized 16-bit row (its transformed branch calls the same encode_group /
+ * rotated_quantize as launch_row_quantize). `normalized` (optional) receives
+ * the normalized 16-bit rows. Returns 0, or -1 on bad layout. */
+int orc_quantized_norm(uint16_t *residual, const uint16_t *update, const uint16_t *update_scale,
+                       const uint16_t *weight, int src_type, int rows, int cols, float eps,
+                       int gemma, int fmt, int group, int rotation, uint8_t *q, float *scales,
+                       uint16_t *normalized) {
+    if (cols < 1 || cols > 2048) return -1;
+    float *v = (float *)malloc(sizeof(float) * 2048);
+    uint16_t *n = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)rows * cols);
+    if (!v || !n) { free(v); free(n); return -1; }
+    for (int r = 0; r < rows; ++r) {
+        uint16_t *x = residual + (size_t)r * cols;
+        for (int c = 0; c < cols; ++c) {
+            float a = load_src(x, src_type, c);
+            if (update) {
+                float b = load_src(update, src_type, (size_t)r * cols + c);
+                if (update_scale)
+                    b = load_src(&(uint16_t){store_out(b * load_src(update_scale, src_type, c),
+                                                       src_type)}, src_type, 0);
+                uint16_t sum = store_out(a + b, src_type);
+                x[c] = sum;
+                a = load_src(&sum, src_type, 0);
+            }
+            v[c] = a;
+        }
+        float inv = orc_rsqrt_rn(orc_norm_sumsq(v, cols) / (float)cols + eps);
+        for (int c = 0; c < cols; ++c) {
+            float w = load_src(weight, src_type, c);
+            if (gemma) {
+                n[(size_t)r * cols + c] = store_out((v[c] * inv) * (w + 1.f), src_type);
+            } else {
+                uint16_t h = store_out(v[c] * inv, src_type);
+                n[(size_t)r * cols + c] = store_out(load_src(&h, src_type, 0) * w, src_type);
+            }
+        }
+    }
+    int status = orc_quantize_rows(n, src_type, cols, rows, cols, fmt, group, rotation, q, scales);
+    if (normalized) memcpy(normalized, n, sizeof(uint16_t) * (size_t)rows * cols);
+    free(v);
+    free(n);
+    return status;
+}
+
+/* activate<Kind> (quant_gated.cu:9-16): SiLU (kind 0) as
+ * (x*2^-16) / ((1 + e^-x) * 2^-16), tanh-GeLU (kind 1) as
+ * (0.5x)(1 + tanh(0.7978845608028654f * (x + ((0.044715f*x)*x)*x))), fp32
+ * arithmetic with e^-x and tanh rounded once from fp64 (the reference's
+ * __expf, __fdividef and tanhf approximate these within a few ulp). */
+float orc_activate(float x, int kind) {
+    if (kind == 0) {
+        float e = (float)exp(-(double)x);
+        return (x * 0x1p-16f) / ((1.f + e) * 0x1p-16f);
+    }
+    float inner = x + ((0.044715f * x) * x) * x;
+    float t = (float)tanh((double)(0.7978845608028654f * inner));
+    return (0.5f * x) * (1.f + t);
+}
+
+/* launch_quantized_gated / vector_gated_quantize (quant_gated.cu:18-85,
+ * 179-198): a = s16(s16(act(gate)) * up) over input [rows, 2*width]
+ * (gate | up), then the row quantizer. `activated` (optional) receives the
+ * 16-bit activated rows. Returns 0, or -1 on bad layout. */
+int orc_quantized_gated(const uint16_t *input, int src_type, int rows, int width, int kind,
+                        int fmt, int group, int rotation, uint8_t *q, float *scales,
+                        uint16_t *activated) {
+    if (width < 1 || width > 8192 || kind < 0 || kind > 1) return -1;
+    uint16_t *a = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)rows * width);
+    if (!a) return -1;
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < width; ++c) {
+            float g = load_src(input, src_type, (size_t)r * 2 * width + c);
+            float u = load_src(input, src_type, (size_t)r * 2 * width + width + c);
+            uint16_t h = store_out(orc_activate(g, kind), src_type);
+            a[(size_t)r * width + c] = store_out(load_src(&h, src_type, 0) * u, src_type);
+        }
+    int status = orc_quantize_rows(a, src_type, width, rows, width, fmt, group, rotation, q, scales);
+    if (activated) memcpy(activated, a, sizeof(uint16_t) * (size_t)rows * width);
+    free(a);
+    return status;
+}
+
 /* ---------------------------------------------------------------- GEMMs */
 /* Exact INT8 GEMM: acc[m][n] = sum_k x[m][k]*w[n][k] in int32. Any tiling or
  * split of the reference (quant_dispatch.cu:58-61 dp4a, quant_gemm_sm80.cu

@@ -117,3 +117,44 @@ def test_linear_validation():
     assert call(x=None) == -1
     assert call(rot=64) == -1
     assert call(x=FAKE + 1) == -2
+
+
+def test_quantized_norm_validation():
+    """launch_quantized_norm's checks (reference quant_norm.cu:166-180)."""
+    L = qlinear.load()
+
+    def call(res=FAKE, upd=None, scl=None, w=FAKE, st=BF16, rows=4, cols=2048, fmt=I8, g=0, r=0,
+             v=FAKE, s=FAKE):
+        return L.qlin_quantized_norm(res, upd, scl, w, st, rows, cols, 1e-6, 0, v, s, fmt, g, r,
+                                     None)
+
+    assert call(st=F32) == -1
+    assert call(fmt=BF16) == -1
+    assert call(cols=2049) == -1          # the reference's single-CTA row bound
+    assert call(cols=0) == -1
+    assert call(rows=0) == -1
+    assert call(res=None) == -1
+    assert call(w=None) == -1
+    assert call(scl=FAKE) == -1           # a scale without an update
+    assert call(g=48) == -1
+    assert call(cols=200, r=128) == -1
+    assert call(res=FAKE + 1) == -2
+    assert call(s=FAKE + 2) == -2
+
+
+def test_quantized_gated_validation():
+    """launch_quantized_gated's checks (reference quant_gated.cu:182-191)."""
+    L = qlinear.load()
+
+    def call(x=FAKE, st=BF16, rows=4, width=6144, kind=0, v=FAKE, s=FAKE, fmt=I8, g=0, r=0):
+        return L.qlin_quantized_gated(x, st, rows, width, kind, v, s, fmt, g, r, None)
+
+    assert call(st=F32) == -1
+    assert call(fmt=F16) == -1
+    assert call(width=8193) == -1
+    assert call(width=0) == -1
+    assert call(kind=2) == -1
+    assert call(x=None) == -1
+    assert call(g=16) == -1
+    assert call(width=200, r=128) == -1
+    assert call(x=FAKE + 1) == -2

@@ -1,0 +1,170 @@
+"""Pins the oracle's fused producers (residual + RMSNorm -> quant and gated
+activation -> quant; reference ops/kernels/quant/quant_norm.cu:14-123 and
+quant_gated.cu:9-85) by routes independent of its C code: exact decimal
+arithmetic for the reciprocal square root, exact sums for the reduction,
+torch's bf16/f16 arithmetic and fp64 activations for the element-wise steps,
+and the already pinned row quantizer for the encoding step."""
+import decimal
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from breeze_tts_cpp_amd import synthetic
+
+
+def bits_to_torch(bits, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(dtype)
+
+
+def torch_to_bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_rsqrt_rn_is_correctly_rounded(orc):
+    """1/sqrt(a) is the fp32 value nearest the exact result (decimal, 60 digits)."""
+    decimal.getcontext().prec = 60
+    rng = np.random.default_rng(5)
+    cases = np.concatenate([rng.uniform(1e-3, 1e3, 400), 2.0 ** rng.integers(-120, 120, 60),
+                            [1.0, 2.0, 3.0, 1e-30, 1e30, 1.17549435e-38, 0.5000001]])
+    for a in cases.astype(np.float32):
+        r = np.float32(orc.rsqrt_rn(float(a)))
+        exact = decimal.Decimal(1) / decimal.Decimal(float(a)).sqrt()
+        err = abs(decimal.Decimal(float(r)) - exact)
+        for nb in (np.nextafter(r, np.float32(0)), np.nextafter(r, np.float32(np.inf))):
+            assert err <= abs(decimal.Decimal(float(nb)) - exact), (a, r)
+
+
+def test_norm_sumsq_exact_cases(orc):
+    """Every column enters the squared sum exactly once, for every row length
+    up to 2048 (one-hot rows), and small-integer rows sum exactly."""
+    for cols in (1, 7, 8, 9, 255, 256, 1000, 2047, 2048):
+        for c in sorted({0, cols // 2, cols - 1}):
+            v = np.zeros(cols, np.float32)
+            v[c] = 3.0
+            assert orc.norm_sumsq(v) == 9.0
+    rng = np.random.default_rng(1)
+    v = rng.integers(-8, 9, 2048).astype(np.float32)
+    assert orc.norm_sumsq(v) == float(np.sum(v.astype(np.int64) ** 2))
+    w = rng.standard_normal(1536).astype(np.float32)
+    ref = float(np.sum(w.astype(np.float64) ** 2))
+    assert abs(orc.norm_sumsq(w) - ref) <= 1e-6 * ref
+
+
+def _torch_norm(x, w, inv, gemma):
+    """Element-wise normalization with torch's 16-bit rounding (fp32 compute,
+    round to the storage dtype after each reference rounding point)."""
+    xf = x.float()
+    if gemma:
+        return ((xf * inv) * (w.float() + 1.0)).to(x.dtype)
+    return ((xf * inv).to(x.dtype).float() * w.float()).to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, 0), (torch.float16, 5)])
+@pytest.mark.parametrize("gemma", [False, True])
+@pytest.mark.parametrize("update", ["none", "add", "scaled"])
+def test_quantized_norm_matches_torch(orc, dtype, src_type, gemma, update):
+    rows, cols, eps = 6, 2000, 1e-6
+    g = torch.Generator().manual_seed(rows + cols + int(gemma))
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    w = (1.0 + 0.1 * torch.randn(cols, generator=g)).to(dtype)
+    u = torch.randn(rows, cols, generator=g).to(dtype) if update != "none" else None
+    s = (0.5 + torch.rand(cols, generator=g)).to(dtype) if update == "scaled" else None
+    res, q, scales, n = orc.quantized_norm(
+        torch_to_bits(x), torch_to_bits(w), orc.I8,
+        update_bits=None if u is None else torch_to_bits(u),
+        scale_bits=None if s is None else torch_to_bits(s), eps=eps, gemma=gemma,
+        src_type=src_type)
+    # residual update: x + u (* s) with 16-bit rounding of each operation
+    v = x if u is None else (x.float() + (u if s is None else (u.float() * s.float()).to(dtype)).float()).to(dtype)
+    assert np.array_equal(res, torch_to_bits(v))
+    nt = bits_to_torch(n, dtype)
+    for r in range(rows):
+        vr = v[r].double()
+        inv64 = 1.0 / math.sqrt(float((vr * vr).sum()) / cols + eps)
+        # with the fp64 normalizer: within one 16-bit ulp everywhere
+        near = _torch_norm(v[r], w, inv64, gemma).float()
+        ulp = (near.abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10)).clamp_min(1e-30)
+        assert torch.all((nt[r].float() - near).abs() <= ulp + 1e-30)
+        # with the oracle's own fp32 normalizer: bit-exact element-wise steps
+        inv32 = orc.rsqrt_rn(orc.norm_sumsq(v[r].float().numpy()) / np.float32(cols) + np.float32(eps))
+        assert abs(inv32 - inv64) <= 2e-7 * inv64
+        assert torch.equal(torch_to_bits_t(nt[r]), torch_to_bits_t(_torch_norm(v[r], w, inv32, gemma)))
+    # the normalized rows go through the (separately pinned) row quantizer
+    q2, s2 = orc.quantize_rows(n, orc.I8, src_type=src_type)
+    assert np.array_equal(q, q2) and np.array_equal(scales, s2)
+
+
+def torch_to_bits_t(t):
+    return t.contiguous().view(torch.int16)
+
+
+def test_quantized_norm_rms_and_modes(orc):
+    """Unit weights: the normalized row has RMS 1 (to bf16 precision); group
+    and rotated modes equal the row quantizer applied to the normalized row."""
+    x = synthetic.activations(4, 2048, seed=3)
+    w = synthetic.f32_to_bf16_bits(np.ones(2048, np.float32))
+    _, _, _, n = orc.quantized_norm(x, w, orc.I8)
+    nf = synthetic.bf16_bits_to_f32(n).astype(np.float64)
+    assert np.allclose(np.sqrt((nf ** 2).mean(axis=1)), 1.0, atol=5e-3)
+    for fmt in (orc.I8, orc.FP8):
+        for group, rot in ((0, 128), (128, 0), (64, 128), (32, 0)):
+            _, q, s, n2 = orc.quantized_norm(x, w, fmt, group=group, rotation=rot)
+            q2, s2 = orc.quantize_rows(n2, fmt, group=group, rotation=rot)
+            assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_activation_matches_fp64(orc, kind):
+    """SiLU / tanh-GeLU against torch's fp64 functions: the fp32 result is
+    within 3 ulp of the fp64 value, and special values are exact."""
+    xs = np.concatenate([np.linspace(-20, 20, 4001), [-100.0, -88.0, 0.0, 1e-30, 50.0]])
+    xs = xs.astype(np.float32)
+    t = torch.from_numpy(xs.astype(np.float64))
+    ref = (torch.nn.functional.silu(t) if kind == 0
+           else torch.nn.functional.gelu(t, approximate="tanh")).numpy()
+    got = np.array([orc.activate(float(v), kind) for v in xs], np.float64)
+    # three fp32 roundings (exp, 1 + e, the quotient) bound the error to 3 ulp
+    tol = 3 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) + 1e-40
+    # tanh-GeLU's fp32 form (0.5x)(1 + tanh(.)) cancels for negative x: its
+    # absolute error is a few ulp of 1 times |0.5x|, plus the fp32 argument
+    if kind == 1:
+        tol = tol * 4 + 1e-7 * np.abs(ref) + np.abs(xs.astype(np.float64)) * 2.0 ** -22
+    assert np.all(np.abs(got - ref) <= tol)
+    assert orc.activate(0.0, kind) == 0.0
+    if kind == 0:
+        assert orc.activate(-100.0, 0) == 0.0 and math.copysign(1, orc.activate(-100.0, 0)) < 0
+        assert orc.activate(50.0, 0) == 50.0
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("fmt", [3, 4])
+def test_quantized_gated_matches_torch(orc, kind, fmt):
+    """act(gate) rounded to bf16 equals torch's fp64 activation rounded to bf16
+    except on rare rounding boundaries (never by more than one ulp); the
+    product with `up` is torch's bf16 multiply; the encoding is the row
+    quantizer of the activated rows."""
+    rows, width = 4, 3000
+    g = torch.Generator().manual_seed(11 + kind)
+    inp = (2.0 * torch.randn(rows, 2 * width, generator=g)).to(torch.bfloat16)
+    q, s, a = orc.quantized_gated(torch_to_bits(inp), kind, fmt)
+    gate, up = inp[:, :width], inp[:, width:]
+    t64 = gate.double()
+    act64 = torch.nn.functional.silu(t64) if kind == 0 else torch.nn.functional.gelu(
+        t64, approximate="tanh")
+    act_bits = np.array([[orc.f32_to_bf16_bits(np.float32(orc.activate(float(v), kind)))
+                          for v in row] for row in gate.float().numpy()], np.uint16)
+    ref_bits = torch_to_bits(act64.float().to(torch.bfloat16))
+    if kind == 0:
+        diff = np.abs(act_bits.astype(np.int32) - ref_bits.astype(np.int32))
+        assert diff.max() <= 1 and (diff > 0).mean() < 1e-3
+    else:
+        # fp32 cancellation of (0.5x)(1 + tanh) for negative x (the reference's form)
+        got = bits_to_torch(act_bits).double()
+        tol = act64.abs() * 2.0 ** -8 + gate.double().abs() * 2.0 ** -22 + 1e-38
+        assert torch.all((got - act64).abs() <= tol)
+    prod = (bits_to_torch(act_bits).float() * up.float()).to(torch.bfloat16)
+    assert np.array_equal(a, torch_to_bits(prod))
+    q2, s2 = orc.quantize_rows(a, fmt)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
