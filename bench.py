@@ -231,6 +231,7 @@ def main():
 
     if not args.no_prefill:
         result["prefill"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args)
+        result["producers"] = bench_producers(torch, qlinear, synthetic, dev, stream, args)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args, value)
@@ -339,6 +340,58 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
         peak = I8_PEAK_TOPS if fmt_name == "int8" else FP8_PEAK_TFLOPS
         out[fmt_name] = {"TOPS": round(tops, 1), "frac_mfma": round(tops / peak, 4),
                          "peak": peak, "projections": rows}
+    return out
+
+
+def bench_producers(torch, qlinear, synthetic, dev, stream, args):
+    """The fused quantizing producers at the decoder's shapes (hidden 2048,
+    FFN 6144; INT8 per-token): residual update + RMSNorm -> quant, and
+    SiLU(gate) * up -> quant, at M=32 and M=4096. Algorithmic bytes: norm
+    reads x, update (2MK each) and weight (2K), writes the residual (2MK),
+    codes (MK) and scales (4M); gated reads gate|up (4MW), writes codes (MW)
+    and scales (4M)."""
+    out = {}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    H, W = 2048, 6144
+
+    def timed(launch, reps=20, n_rep=5):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(reps):
+                launch()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(n_rep):
+                g.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / (n_rep * reps)
+
+    for M in (M_DECODE, M_PREFILL):
+        def bf(shape, seed):
+            return torch.from_numpy(synthetic.activations(shape[0], shape[1], seed=seed).view(
+                np.int16)).view(torch.bfloat16).to(dev)
+        x, u, gu = bf((M, H), 1), bf((M, H), 2), bf((M, 2 * W), 3)
+        w = torch.ones(H, dtype=torch.bfloat16, device=dev)
+        nq = torch.empty((M, H), dtype=torch.uint8, device=dev)
+        gq = torch.empty((M, W), dtype=torch.uint8, device=dev)
+        ns = torch.empty((M,), dtype=torch.float32, device=dev)
+        gs = torch.empty((M,), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        us_n = timed(lambda: qlinear.quantized_norm(x, w, qlinear.I8, update=u, values=nq,
+                                                    scales=ns, stream=stream))
+        us_g = timed(lambda: qlinear.quantized_gated(gu, qlinear.I8, kind=0, values=gq,
+                                                     scales=gs, stream=stream))
+        b_n = 7 * M * H + 2 * H + 4 * M
+        b_g = 5 * M * W + 4 * M
+        out[f"M={M}"] = {
+            "quantized_norm": {"us": round(us_n, 2), "bytes": b_n,
+                               "GBps": round(b_n / (us_n * 1e-6) / 1e9, 1)},
+            "quantized_gated": {"us": round(us_g, 2), "bytes": b_g,
+                                "GBps": round(b_g / (us_g * 1e-6) / 1e9, 1)}}
     return out
 
 

@@ -96,6 +96,49 @@ void launch_row_quantize(TensorView source, RowScaledView destination, qlin_stre
           "row quantization");
 }
 
+// quant_norm.cu:166-188: the reference's shape/type checks, then the kernel.
+void launch_quantized_norm(TensorView residual, TensorView update, TensorView weight,
+                           RowScaledView output, float epsilon, bool gemma,
+                           TensorView update_scale, qlin_stream_t stream) {
+    output.validate();
+    if ((residual.type != Type::BF16 && residual.type != Type::F16) || !residual.data ||
+        !weight.data || !output.values.data || !output.scales.data || !residual.dense() ||
+        residual.cols < 1 || residual.cols > 2048 || residual.rows < 1 ||
+        residual.cols != output.values.cols || residual.rows != output.values.rows ||
+        weight.type != residual.type || !weight.dense() ||
+        weight.numel() != size_t(residual.cols) ||
+        (update.data && (update.type != residual.type || update.rows != residual.rows ||
+                         update.cols != residual.cols || !update.dense())) ||
+        (update_scale.data && (update_scale.type != residual.type || !update_scale.dense() ||
+                               update_scale.numel() != size_t(residual.cols))))
+        throw std::invalid_argument("quantized RMS shape/type mismatch");
+    check(qlin_quantized_norm(residual.data, update.data, update.data ? update_scale.data : nullptr,
+                              weight.data, code(residual.type), residual.rows, residual.cols,
+                              epsilon, gemma ? 1 : 0, output.values.data,
+                              output.scales.ptr<float>(), code(output.values.type),
+                              output.group_size, output.rotation_size, stream),
+          "quantized norm");
+}
+
+bool quant_gated_supports_clusters(int) { return false; }
+
+// quant_gated.cu:182-198: the reference's checks; one workgroup per row on gfx950.
+void launch_quantized_gated(TensorView input, RowScaledView output, int kind,
+                            qlin_stream_t stream, int, bool) {
+    output.validate();
+    const int width = output.values.cols;
+    if ((input.type != Type::BF16 && input.type != Type::F16) || !input.data ||
+        !output.values.data || !output.scales.data || !input.dense() ||
+        input.rows != output.values.rows || input.cols != int64_t(2) * width || kind < 0 ||
+        kind > 1 || width < 1 || width > 8192 || input.rows < 1)
+        throw std::invalid_argument("quantized gated shape/type mismatch");
+    check(qlin_quantized_gated(input.data, code(input.type), input.rows, width, kind,
+                               output.values.data, output.scales.ptr<float>(),
+                               code(output.values.type), output.group_size, output.rotation_size,
+                               stream),
+          "quantized gated");
+}
+
 void launch_quant_linear(LinearPath config, KernelProblem shape, const void *input,
                          const float *input_scales, const void *weights,
                          const float *weight_scales, void *output, void *workspace,
@@ -287,6 +330,17 @@ void linear(TensorView input, RowScaledView weight, TensorView output, RowScaled
         output.cols != weight.values.rows || !output.dense())
         throw std::invalid_argument("quantized linear dimensions/layout mismatch");
     matmul(scratch, weight, output);
+}
+// ops/basic.cpp:54-58
+void quantized_norm(TensorView input, TensorView update, TensorView weight, RowScaledView output,
+                    float epsilon, bool gemma, TensorView scale) {
+    launch_quantized_norm(input, update, weight, output, epsilon, gemma, scale,
+                          context(input.device).stream());
+}
+
+// ops/basic.cpp:59-63
+void quantized_gated(TensorView input, RowScaledView output, int kind) {
+    launch_quantized_gated(input, output, kind, context(input.device).stream());
 }
 }  // namespace ops
 

@@ -13,11 +13,15 @@
 //   tts::launch_row_quantize                 <- ops/kernels/quant/row_quantize.h:6
 //   tts::launch_quant_linear                 <- ops/kernels/quant/quant_dispatch.h:11-15
 //   tts::grouped_quant_gemm                  <- ops/kernels/quant/quant_dispatch.h:7-10
+//   tts::launch_quantized_norm               <- ops/kernels/quant/quant_norm.h:5-7
+//   tts::launch_quantized_gated,
+//     quant_gated_supports_clusters          <- ops/kernels/quant/quant_gated.h:5-8
 //   tts::QuantizedGemm                       <- ops/cuda/quantization.h:15-42
 //   tts::QuantizationWorkspace               <- layers/quantization.h:9-49
 //   tts::ops::quantize_rows / matmul /
 //     prepare_quantized / linear             <- ops/storage.h:12, ops/basic.h:11,25-26,
 //                                               ops/linear.h:11-13 (quantized branch)
+//   tts::ops::quantized_norm / quantized_gated <- ops/basic.h:33-35
 //
 // Errors: std::invalid_argument for shape/type/alignment/workspace problems,
 // std::runtime_error for device errors and missing kernel variants,
@@ -117,6 +121,18 @@ void grouped_quant_gemm(KernelProblem, const void *input, const float *input_sca
                         qlin_stream_t, Type format, Type output_type, int tokens = 16,
                         int splits = 1, void *workspace = nullptr, size_t workspace_bytes = 0);
 
+// Fused quantizing producers. `residual` is updated in place when `update` is
+// given; `update_scale` may be empty. The gated input is [rows, 2*width]
+// (gate | up); kind 0 = SiLU, 1 = tanh-GeLU. Workgroup clusters do not exist
+// on gfx950: `multiprocessors` and `clusters` are accepted and unused, and
+// quant_gated_supports_clusters() is false.
+void launch_quantized_norm(TensorView residual, TensorView update, TensorView weight,
+                           RowScaledView output, float epsilon, bool gemma,
+                           TensorView update_scale, qlin_stream_t stream);
+bool quant_gated_supports_clusters(int device);
+void launch_quantized_gated(TensorView input, RowScaledView output, int kind,
+                            qlin_stream_t stream, int multiprocessors = 0, bool clusters = false);
+
 // ---------------------------------------------------------------- QuantizedGemm
 struct SelectionStats {
     size_t entries = 0, hits = 0, searches = 0;
@@ -192,6 +208,9 @@ void prepare_quantized(TensorView weight, int rows, int output_channels, int inp
                        Type type, QuantizationGroups groups = {});
 // Quantized branch of ops::linear: quantize `input` into `scratch`, then GEMM.
 void linear(TensorView input, RowScaledView weight, TensorView output, RowScaledView scratch);
+void quantized_norm(TensorView input, TensorView update, TensorView weight, RowScaledView output,
+                    float epsilon, bool gemma = false, TensorView scale = {});
+void quantized_gated(TensorView input, RowScaledView output, int kind);
 }  // namespace ops
 
 }  // namespace tts

@@ -5,6 +5,10 @@
 //                         launch_row_quantize (load-time path), runs
 //                         ops::linear and writes DIR/y.bf16 plus the
 //                         quantized weights DIR/{wq.u8,sw.f32}.
+//   test_shim producers DIR : ops::quantized_norm (residual update, RMSNorm)
+//                         on DIR/{x,u,w}.bf16 and ops::quantized_gated (SiLU)
+//                         on DIR/g.bf16 (shape.txt: M WIDTH GROUP), writing
+//                         DIR/{res.bf16,nq.u8,ns.f32,gq.u8,gs.f32}.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -98,6 +102,24 @@ static int host_tests() {
         launch_quant_linear({}, {16, 40, 256}, dummy, nullptr, dummy, nullptr, dummy, nullptr, 0,
                             nullptr, Type::I8, Type::BF16);
     }));
+    // fused producers: the reference's shape checks throw before any launch
+    RowScaledView nq{TensorView(dummy, 4, 2048, Type::I8), TensorView(dummy, 4, 1, Type::F32), 0, 0};
+    EXPECT(throws<std::invalid_argument>([&] {  // weight length != cols
+        launch_quantized_norm(TensorView(dummy, 4, 2048), {}, TensorView(dummy, 1, 1024), nq, 1e-6f,
+                              false, {}, nullptr);
+    }));
+    RowScaledView wide{TensorView(dummy, 4, 4096, Type::I8), TensorView(dummy, 4, 1, Type::F32), 0, 0};
+    EXPECT(throws<std::invalid_argument>([&] {  // cols > 2048
+        launch_quantized_norm(TensorView(dummy, 4, 4096), {}, TensorView(dummy, 1, 4096), wide,
+                              1e-6f, false, {}, nullptr);
+    }));
+    EXPECT(throws<std::invalid_argument>([&] {  // input is not [rows, 2*width]
+        launch_quantized_gated(TensorView(dummy, 4, 4000), nq, 0, nullptr);
+    }));
+    EXPECT(throws<std::invalid_argument>([&] {  // kind
+        launch_quantized_gated(TensorView(dummy, 4, 4096), nq, 2, nullptr);
+    }));
+    EXPECT(!quant_gated_supports_clusters(0));
     // ops without a bound context
     EXPECT(throws<std::logic_error>([&] { ops::matmul(x, w, TensorView(dummy, 30, 4096)); }));
     std::printf("host tests: %s\n", failures ? "FAILED" : "ok");
@@ -178,9 +200,71 @@ static int gpu_test(const std::string &dir) {
     return 0;
 }
 
+static int producers_test(const std::string &dir) {
+    int M, width, group;
+    std::ifstream(dir + "/shape.txt") >> M >> width >> group;
+    const int H = 2048, rot = group ? 128 : 0;
+    auto x = read_file<uint16_t>(dir + "/x.bf16", size_t(M) * H);
+    auto u = read_file<uint16_t>(dir + "/u.bf16", size_t(M) * H);
+    auto w = read_file<uint16_t>(dir + "/w.bf16", size_t(H));
+    auto g = read_file<uint16_t>(dir + "/g.bf16", size_t(M) * 2 * width);
+    const int ng = group ? H / group : 1, gg = group ? (width + group - 1) / group : 1;
+    void *dx, *du, *dw, *dg, *dnq, *dns, *dgq, *dgs, *dws;
+    HIP(hipMalloc(&dx, x.size() * 2));
+    HIP(hipMalloc(&du, u.size() * 2));
+    HIP(hipMalloc(&dw, w.size() * 2));
+    HIP(hipMalloc(&dg, g.size() * 2));
+    HIP(hipMalloc(&dnq, size_t(M) * H));
+    HIP(hipMalloc(&dns, size_t(M) * ng * 4));
+    HIP(hipMalloc(&dgq, size_t(M) * width));
+    HIP(hipMalloc(&dgs, size_t(M) * gg * 4));
+    HIP(hipMalloc(&dws, 1 << 20));
+    HIP(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(du, u.data(), u.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(dw, w.data(), w.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(dg, g.data(), g.size() * 2, hipMemcpyHostToDevice));
+    hipStream_t stream;
+    HIP(hipStreamCreate(&stream));
+    {
+        QuantizedGemm gemm(reinterpret_cast<qlin_stream_t>(stream), dws, 1 << 20, Type::I8);
+        ops::bind(0, &gemm);
+        RowScaledView nq{TensorView(dnq, M, H, Type::I8, 0, 0),
+                         group ? TensorView(dns, ng, M, Type::F32, 0, 0)
+                               : TensorView(dns, M, 1, Type::F32, 0, 0),
+                         group, rot};
+        ops::quantized_norm(TensorView(dx, M, H, Type::BF16, 0, 0),
+                            TensorView(du, M, H, Type::BF16, 0, 0), TensorView(dw, 1, H), nq, 1e-6f);
+        RowScaledView gq{TensorView(dgq, M, width, Type::I8, 0, 0),
+                         group ? TensorView(dgs, gg, M, Type::F32, 0, 0)
+                               : TensorView(dgs, M, 1, Type::F32, 0, 0),
+                         group, rot};
+        ops::quantized_gated(TensorView(dg, M, 2 * width, Type::BF16, 0, 0), gq, 0);
+        HIP(hipStreamSynchronize(stream));
+        std::vector<uint16_t> res(x.size());
+        std::vector<uint8_t> nqh(size_t(M) * H), gqh(size_t(M) * width);
+        std::vector<float> nsh(size_t(M) * ng), gsh(size_t(M) * gg);
+        HIP(hipMemcpy(res.data(), dx, res.size() * 2, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(nqh.data(), dnq, nqh.size(), hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(nsh.data(), dns, nsh.size() * 4, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(gqh.data(), dgq, gqh.size(), hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(gsh.data(), dgs, gsh.size() * 4, hipMemcpyDeviceToHost));
+        write_file(dir + "/res.bf16", res);
+        write_file(dir + "/nq.u8", nqh);
+        write_file(dir + "/ns.f32", nsh);
+        write_file(dir + "/gq.u8", gqh);
+        write_file(dir + "/gs.f32", gsh);
+        ops::bind(0, nullptr);
+    }
+    for (void *p : {dx, du, dw, dg, dnq, dns, dgq, dgs, dws}) (void)hipFree(p);
+    (void)hipStreamDestroy(stream);
+    std::printf("producers test M=%d width=%d group=%d: done\n", M, width, group);
+    return 0;
+}
+
 int main(int argc, char **argv) {
     if (argc >= 2 && std::string(argv[1]) == "host") return host_tests();
     if (argc >= 3 && std::string(argv[1]) == "gpu") return gpu_test(argv[2]);
-    std::fprintf(stderr, "usage: test_shim host | gpu DIR\n");
+    if (argc >= 3 && std::string(argv[1]) == "producers") return producers_test(argv[2]);
+    std::fprintf(stderr, "usage: test_shim host | gpu DIR | producers DIR\n");
     return 2;
 }

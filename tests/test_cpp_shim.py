@@ -63,3 +63,31 @@ def test_linear_end_to_end(dev, orc, tmp_path, mode, M, N, K):
     else:
         ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq_ref), sx, sw_ref)
         assert np.array_equal(y, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,width,group", [(32, 6144, 0), (5, 6144, 128), (64, 2048, 0)])
+def test_producers_end_to_end(dev, orc, tmp_path, M, width, group):
+    """ops::quantized_norm (residual update + RMSNorm, hidden 2048) and
+    ops::quantized_gated (SiLU over the gate|up output) through the C++
+    interface, against the oracle."""
+    x = synthetic.activations(M, 2048, seed=M)
+    u = synthetic.activations(M, 2048, seed=M + 1)
+    w = synthetic.f32_to_bf16_bits(1.0 + 0.05 * np.random.default_rng(M).standard_normal(2048))
+    g = synthetic.activations(M, 2 * width, seed=M + 2)
+    for name, a in (("x", x), ("u", u), ("w", w), ("g", g)):
+        a.tofile(tmp_path / f"{name}.bf16")
+    (tmp_path / "shape.txt").write_text(f"{M} {width} {group}\n")
+    print(f"test_shim producers M={M} width={width} group={group}", flush=True)
+    r = subprocess.run([_binary(), "producers", str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    rot = 128 if group else 0
+    res, nq, ns, _ = orc.quantized_norm(x, w, I8, update_bits=u, eps=1e-6, group=group,
+                                        rotation=rot)
+    assert np.array_equal(np.fromfile(tmp_path / "res.bf16", np.uint16).reshape(M, 2048), res)
+    assert np.array_equal(np.fromfile(tmp_path / "nq.u8", np.uint8).reshape(M, 2048), nq)
+    assert np.array_equal(np.fromfile(tmp_path / "ns.f32", np.float32), ns.ravel())
+    gq, gs, _ = orc.quantized_gated(g, 0, I8, group=group, rotation=rot)
+    assert np.array_equal(np.fromfile(tmp_path / "gq.u8", np.uint8).reshape(M, width), gq)
+    assert np.array_equal(np.fromfile(tmp_path / "gs.f32", np.float32), gs.ravel())
