@@ -242,10 +242,13 @@ size_t qlin_workspace_bytes(const qlin_path *path, int rows, int N, int K, int f
     return 0;
 }
 
-int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void *w,
+}  // extern "C"
+
+namespace {
+int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void *w,
               const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
               int input_group, int weight_group, void *workspace, size_t workspace_bytes,
-              qlin_stream_t stream) {
+              qlin_stream_t stream, bool packed) {
     // check_linear + make_plan rules (reference ops/cuda/quantization.cpp:94-102,
     // 206-222) and launch_quant_linear's type checks (quant_dispatch.cu:194-233).
     if (fmt != QLIN_I8 && fmt != QLIN_FP8)
@@ -267,6 +270,8 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
     if (!aligned(sx, 4) || !aligned(sw, 4))
         return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
     qlin_path p = path && path->kind ? *path : choose(rows, N, K, fmt, input_group, weight_group);
+    // Packed weights stream straight into registers: no LDS slab staging.
+    if (packed && !(path && path->kind)) p.staged = 0;
     int status = check_path(p, rows, N, K, fmt, input_group, weight_group);
     if (status) return status;
     qlin::GemmArgs a{static_cast<const uint8_t *>(x),
@@ -282,7 +287,8 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
                      input_group,
                      weight_group,
                      workspace,
-                     workspace_bytes};
+                     workspace_bytes,
+                     packed ? 1 : 0};
     const qlin::GemmPath ip = to_internal(p);
     size_t need = 0;
     if (p.kind == QLIN_KIND_SKINNY) need = qlin::skinny_workspace_bytes(a, ip);
@@ -295,6 +301,53 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
     int r = p.kind == QLIN_KIND_SKINNY ? qlin::launch_skinny(a, ip, s) : qlin::launch_tiled(a, ip, s);
     if (r) return fail(r, "no kernel variant for this path");
     return check_launch("quantized GEMM launch");
+}
+}  // namespace
+
+extern "C" {
+
+int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void *w,
+              const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
+              int input_group, int weight_group, void *workspace, size_t workspace_bytes,
+              qlin_stream_t stream) {
+    return gemm_impl(path, x, sx, w, sw, y, rows, N, K, fmt, out_type, input_group, weight_group,
+                     workspace, workspace_bytes, stream, false);
+}
+
+size_t qlin_packed_weight_bytes(int N, int K) {
+    if (N < 1 || K < 1 || N % 16) return 0;
+    return qlin::packed_weight_bytes(N, K);
+}
+
+int qlin_pack_weights(const void *w, int N, int K, void *packed, qlin_stream_t stream) {
+    if (N < 1 || K < 1 || N % 16 || K % 16)
+        return fail(QLIN_ERR_INVALID, "packed weights need N %% 16 == 0 and K %% 16 == 0 (N=%d K=%d)",
+                    N, K);
+    if (!w || !packed) return fail(QLIN_ERR_INVALID, "weight pointer is null");
+    if (!aligned(w, 16) || !aligned(packed, 16))
+        return fail(QLIN_ERR_ALIGNMENT, "weights must be 16-byte aligned");
+    qlin::launch_pack_weights(w, N, K, packed, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("weight packing launch");
+}
+
+int qlin_gemm_packed(const qlin_path *path, const void *x, const float *sx, const void *w,
+                     const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
+                     int input_group, int weight_group, void *workspace, size_t workspace_bytes,
+                     qlin_stream_t stream) {
+    return gemm_impl(path, x, sx, w, sw, y, rows, N, K, fmt, out_type, input_group, weight_group,
+                     workspace, workspace_bytes, stream, true);
+}
+
+int qlin_linear_packed(const qlin_path *path, const void *x, int ld, int src_type, void *xq,
+                       float *sx, const void *w, const float *sw, void *y, int rows, int N, int K,
+                       int fmt, int out_type, int input_group, int weight_group, int rotation,
+                       void *workspace, size_t workspace_bytes, qlin_stream_t stream) {
+    if (!xq || !sx) return fail(QLIN_ERR_INVALID, "linear needs the scratch activation (xq, sx)");
+    int status = qlin_row_quantize(x, ld, rows, K, src_type, xq, sx, fmt, input_group, rotation,
+                                   stream);
+    if (status) return status;
+    return qlin_gemm_packed(path, xq, sx, w, sw, y, rows, N, K, fmt, out_type, input_group,
+                            weight_group, workspace, workspace_bytes, stream);
 }
 
 int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void *xq, float *sx,

@@ -83,8 +83,12 @@ __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4
 // is loaded cooperatively, wave w moving a contiguous run of whole rows, and
 // a workgroup barrier precedes the fragment reads (each wave then reads its
 // K range of every row).
+//
+// Packed: w is the packed fragment-tile layout (weight_pack.hip); each wave
+// loads all NB blocks of its K range straight into registers up front, one
+// contiguous 1 KB piece per (16-row fragment, 64-K step).
 template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out, int NB = 0,
-          int SL = 1>
+          int SL = 1, bool Packed = false>
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
@@ -102,11 +106,15 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 
     const uint8_t *wrow[NF];
     bool wvalid[NF];
+    const int tiles_k = (K + 63) / 64;
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         int n = n0 + f * 16 + row16;
         wvalid[f] = n < N;
-        wrow[f] = w + size_t(wvalid[f] ? n : 0) * K + quad * 16;
+        if constexpr (Packed)
+            wrow[f] = w + size_t(wvalid[f] ? n0 / 16 + f : 0) * tiles_k * 1024 + lane * 16;
+        else
+            wrow[f] = w + size_t(wvalid[f] ? n : 0) * K + quad * 16;
     }
     const uint8_t *xrow[MT];
     bool xvalid[MT];
@@ -140,12 +148,13 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     }
 
     extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
-    constexpr int kSlabBytes = 16 * NF * NB * kBlockK;          // per wave
-    constexpr int kRowBytes = SL == 2 ? WK * NB * kBlockK : NB * kBlockK;
+    constexpr int SNB = Packed ? 0 : NB;                        // staged slab blocks
+    constexpr int kSlabBytes = 16 * NF * SNB * kBlockK;         // per wave
+    constexpr int kRowBytes = SL == 2 ? WK * SNB * kBlockK : SNB * kBlockK;
     constexpr int kRowGranules = kRowBytes / 16;
     uint8_t *slab = SL == 2 ? wlds : wlds + wave * kSlabBytes;
     const int slab_k0 = SL == 2 ? blockIdx.y * WK * span : k_begin;
-    if constexpr (NB > 0) {
+    if constexpr (SNB > 0) {
         typedef __attribute__((address_space(3))) void *lds_ptr_t;
         const int rows_valid = max(0, min(16 * NF, N - n0));
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -173,11 +182,11 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     using Red = std::conditional_t<Grouped, float, Scalar>;
     typedef Red Red4 __attribute__((ext_vector_type(4)));
     constexpr int kSlotVals = MT * NF * 64 * 4;
-    constexpr int kSlotStride = NB > 0 ? (SL == 2 ? kSlotVals : kSlabBytes / int(sizeof(Red)))
-                                       : kSlotVals;
-    static_assert(NB == 0 || kSlotVals * int(sizeof(Red)) <= kSlabBytes, "slot fits the slab");
-    __shared__ Red4 red_static[NB > 0 || WK == 1 ? 1 : WK * kSlotVals / 4];
-    Red *red = NB > 0 ? reinterpret_cast<Red *>(wlds) : reinterpret_cast<Red *>(red_static);
+    constexpr int kSlotStride = SNB > 0 ? (SL == 2 ? kSlotVals : kSlabBytes / int(sizeof(Red)))
+                                        : kSlotVals;
+    static_assert(SNB == 0 || kSlotVals * int(sizeof(Red)) <= kSlabBytes, "slot fits the slab");
+    __shared__ Red4 red_static[SNB > 0 || WK == 1 ? 1 : WK * kSlotVals / 4];
+    Red *red = SNB > 0 ? reinterpret_cast<Red *>(wlds) : reinterpret_cast<Red *>(red_static);
 
     // Grouped: fp32 running sums; per-channel: the raw accumulator.
     Acc acc[MT][NF];
@@ -205,19 +214,22 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // With a staged slab of NB blocks, all of the wave's activation blocks are
     // requested right behind the slab DMA (when they fit in registers), so no
     // block waits for its own L2 round trip inside the loop.
-    constexpr bool kPreX = NB > 0 && NB * MT <= 6;
+    constexpr bool kPreX = NB > 0 && NB * MT <= 6 && !Packed;
+    i32x4 wpre[1][NF][4];  // unused unless packed
     i32x4 xpre[kPreX ? NB : 1][MT][4];
     if constexpr (kPreX) {
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
-        // The slab DMA was issued before these loads: once at most they are
-        // outstanding, this wave's slab is in LDS.
-        constexpr int n = NB * MT * 4;
-        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-        if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
+        if constexpr (!Packed) {
+            // The slab DMA was issued before these loads: once at most they
+            // are outstanding, this wave's slab is in LDS.
+            constexpr int n = NB * MT * 4;
+            __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+            if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
+        }
     }
 
-    auto block = [&](int kb, const i32x4 (&b)[MT][4]) {
+    auto block = [&](int kb, const i32x4 (&b)[MT][4], const i32x4 (&wp)[NF][4]) {
         i32x4 a[NF][4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -226,7 +238,9 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             (void)in;
 #pragma unroll
             for (int f = 0; f < NF; ++f) {
-                if constexpr (NB > 0) {
+                if constexpr (Packed) {
+                    a[f][p] = wp[f][p];
+                } else if constexpr (NB > 0) {
                     const int r = f * 16 + row16;
                     const int g = ((kb - slab_k0) + p * 64) / 16 + quad;
                     a[f][p] = *reinterpret_cast<const i32x4 *>(slab + r * kRowBytes +
@@ -278,11 +292,35 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             }
         }
     };
-    if constexpr (kPreX) {
+    if constexpr (Packed) {
+        // Chunks of NB blocks: every weight fragment and activation block of
+        // a chunk is requested before its first MFMA.
+        for (int kc = k_begin; kc < k_end; kc += NB * kBlockK) {
+            i32x4 wc[NB][NF][4], xc[NB][MT][4];
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int k = kc + blk * kBlockK + p * 64;
+#pragma unroll
+                    for (int f = 0; f < NF; ++f)
+                        wc[blk][f][p] = (k < k_end && wvalid[f])
+                                            ? load16(wrow[f] + size_t(k / 64) * 1024)
+                                            : i32x4{0, 0, 0, 0};
+                }
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk) load_x(kc + blk * kBlockK, xc[blk]);
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk) {
+                const int kb = kc + blk * kBlockK;
+                if (kb < k_end) block(kb, xc[blk], wc[blk]);
+            }
+        }
+    } else if constexpr (kPreX) {
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) {
             const int kb = k_begin + blk * kBlockK;
-            if (kb < k_end) block(kb, xpre[blk]);
+            if (kb < k_end) block(kb, xpre[blk], wpre[0]);
         }
     } else {
         for (int kb = k_begin; kb < k_end; kb += kBlockK) {
@@ -297,14 +335,14 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
                 }
             }
-            block(kb, b);
+            block(kb, b, wpre[0]);
         }
     }
 
 
     if constexpr (WK > 1) {
         // A shared slab is read by every wave: all reads finish first.
-        if constexpr (NB > 0 && SL == 2) __syncthreads();
+        if constexpr (SNB > 0 && SL == 2) __syncthreads();
         Red *slot = red + wave * kSlotStride;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -427,8 +465,36 @@ int launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t 
     return 0;
 }
 
+template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
+int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1, true>), grid,
+                       dim3(64 * WK), 0, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N,
+                       a.K, span, a.input_group, a.weight_group);
+    return 0;
+}
+
 template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    if (a.packed) {
+        // Packed weights: the waves split K (no grid split-K); each wave
+        // streams its range in chunks of up to kMaxNB blocks held in
+        // registers (weights and activations of a chunk: NB*(NF+MT) 64-byte
+        // fragments per lane-quad, at most 10).
+        if (p.splits != 1 || p.staged) return -4;
+        const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
+        const int span = blocks_k / WK * kBlockK;
+        dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
+        constexpr int kMaxNB = 10 / (NF + MT) > 4 ? 4 : (10 / (NF + MT) < 1 ? 1 : 10 / (NF + MT));
+        const int nb = span / kBlockK < kMaxNB ? span / kBlockK : kMaxNB;
+        switch (nb) {
+        case 1: return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, stream);
+        case 2: if constexpr (kMaxNB >= 2) return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 2>(a, grid, span, stream); break;
+        case 3: if constexpr (kMaxNB >= 3) return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 3>(a, grid, span, stream); break;
+        case 4: if constexpr (kMaxNB >= 4) return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 4>(a, grid, span, stream); break;
+        default: break;
+        }
+        return -4;
+    }
     if (skinny_lds_bytes(a, p) > kLdsBytes) return -4;  // would not launch
     const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
     const int ranges = p.splits * WK;
@@ -511,6 +577,7 @@ int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 
 }  // namespace
 
+#ifndef QLIN_SKINNY_PART
 size_t skinny_lds_bytes(const GemmArgs &a, const GemmPath &p) {
     const int mt = p.tokens / 16, nf = p.channels / 16, wk = p.waves;
     const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
@@ -525,13 +592,28 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
     return p.splits > 1 ? size_t(p.splits) * a.M * a.N * 4 : 0;
 }
 
+#endif
+
+// The kernel variants are compiled in four translation units (format x
+// output type, see the Makefile) that each define one entry below.
+#ifdef QLIN_SKINNY_PART
+int QLIN_SKINNY_PART(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    return dispatch_grouped<QLIN_SKINNY_FMT, QLIN_SKINNY_OUT>(a, p, stream);
+}
+#else
+int launch_skinny_i8_bf16(const GemmArgs &, const GemmPath &, hipStream_t);
+int launch_skinny_i8_f16(const GemmArgs &, const GemmPath &, hipStream_t);
+int launch_skinny_fp8_bf16(const GemmArgs &, const GemmPath &, hipStream_t);
+int launch_skinny_fp8_f16(const GemmArgs &, const GemmPath &, hipStream_t);
+
 int launch_skinny(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (a.out_type == F16) {
-        if (a.fmt == I8) return dispatch_grouped<I8, f16_t>(a, p, stream);
-        return dispatch_grouped<FP8, f16_t>(a, p, stream);
+        if (a.fmt == I8) return launch_skinny_i8_f16(a, p, stream);
+        return launch_skinny_fp8_f16(a, p, stream);
     }
-    if (a.fmt == I8) return dispatch_grouped<I8, bf16_t>(a, p, stream);
-    return dispatch_grouped<FP8, bf16_t>(a, p, stream);
+    if (a.fmt == I8) return launch_skinny_i8_bf16(a, p, stream);
+    return launch_skinny_fp8_bf16(a, p, stream);
 }
+#endif
 
 }  // namespace qlin

@@ -72,7 +72,7 @@ __device__ __forceinline__ void lds_barrier() {
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, bool KFull,
-          class Out>
+          class Out, bool PackedW = false>
 __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
@@ -113,8 +113,14 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const int wave_n = wave % WN, wave_m = wave / WN;
     const int row16 = lane & 15, quad = lane >> 4;
 
-    const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(w + size_t(n_base) * K), 0, min(BN, N - n_base) * K, 0x00020000);
+    // Packed weights: the tile's row groups are (n_base/16 ..) x tiles_k 1 KB tiles.
+    const int tiles_k = (K + 63) / 64;
+    const __amdgpu_buffer_rsrc_t rsrc_w =
+        PackedW ? __builtin_amdgcn_make_buffer_rsrc(
+                      const_cast<uint8_t *>(w + size_t(n_base / 16) * tiles_k * 1024), 0,
+                      min(BN, N - n_base) / 16 * tiles_k * 1024, 0x00020000)
+                : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + size_t(n_base) * K),
+                                                    0, min(BN, N - n_base) * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsrc_x = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(x + size_t(m_base) * K), 0, min(BM, M - m_base) * K, 0x00020000);
 
@@ -126,17 +132,29 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const int lane_row = lane / CPR;
     const int lane_chunk = (lane % CPR) ^ swizzle<BK>(wave * RPI + lane_row);
     const uint32_t lane_voff = uint32_t(lane_row) * uint32_t(K) + uint32_t(lane_chunk * 16);
+    // Packed weights: logical chunk c of a stage row lies in 64-K tile c/4,
+    // fragment chunk (c%4)*16 + row%16; the stage's first tile and the row
+    // group go in the uniform offset.
+    const uint32_t lane_voff_p =
+        uint32_t((lane_chunk / 4) * 1024 + (lane_chunk % 4) * 256 + lane_row * 16);
     auto issue = [&](int stage, int k0) {
         uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
-        const uint32_t voff =
-            (KFull || k0 + lane_chunk * 16 < K) ? lane_voff + uint32_t(k0) : 0x80000000u;
+        const bool kin = KFull || k0 + lane_chunk * 16 < K;
+        const uint32_t voff = kin ? lane_voff + uint32_t(k0) : 0x80000000u;
+        const uint32_t voff_p = kin ? lane_voff_p : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < INSTS; ++i) {
             const int row = (i * NW + wave) * RPI;
-            const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
             lds_ptr_t dst = (lds_ptr_t)(base + (i * NW + wave) * 1024);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rsrc_w : rsrc_x, dst, 16, voff,
-                                                     soff, 0, 0);
+            if (PackedW && i < W_INSTS) {
+                const uint32_t soff = uint32_t((row / 16) * tiles_k * 1024 + (row % 16) * 16 +
+                                               (k0 / 64) * 1024);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w, dst, 16, voff_p, soff, 0, 0);
+            } else {
+                const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rsrc_w : rsrc_x, dst, 16,
+                                                         voff, soff, 0, 0);
+            }
         }
     };
 
@@ -473,7 +491,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 // The K ring is the same: 64-byte stages filled by buffer_load ... lds, 16-byte
 // chunk c of stage row r at c ^ ((r >> 2) & 3) (conflict-free for 32-row
 // fragment reads, where lanes l and l+32 read chunks 2h and 2h+1).
-template <int Fmt, int WN, int WM, int STAGES, bool KFull, class Out>
+template <int Fmt, int WN, int WM, int STAGES, bool KFull, class Out, bool PackedW = false>
 __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
@@ -497,8 +515,14 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wave_n = wave % WN, wave_m = wave / WN;
 
-    const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(w + size_t(n_base) * K), 0, min(BN, N - n_base) * K, 0x00020000);
+    // Packed weights: the tile's row groups are (n_base/16 ..) x tiles_k 1 KB tiles.
+    const int tiles_k = (K + 63) / 64;
+    const __amdgpu_buffer_rsrc_t rsrc_w =
+        PackedW ? __builtin_amdgcn_make_buffer_rsrc(
+                      const_cast<uint8_t *>(w + size_t(n_base / 16) * tiles_k * 1024), 0,
+                      min(BN, N - n_base) / 16 * tiles_k * 1024, 0x00020000)
+                : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + size_t(n_base) * K),
+                                                    0, min(BN, N - n_base) * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsrc_x = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(x + size_t(m_base) * K), 0, min(BM, M - m_base) * K, 0x00020000);
 
@@ -508,21 +532,29 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
     const int lane_row = lane >> 2;
     const int lane_chunk = (lane & 3) ^ ((lane >> 4) & 3);
     const uint32_t lane_voff = uint32_t(lane_row) * uint32_t(K) + uint32_t(lane_chunk * 16);
+    // Packed weights: 16-row x 64-K tiles, chunk (c * 16 + row % 16).
+    const uint32_t lane_voff_p = uint32_t(lane_chunk * 256 + lane_row * 16);
     constexpr int kRingBytes = STAGES * STAGE_BYTES > NW * 128 * 256 ? STAGES * STAGE_BYTES
                                                                       : NW * 128 * 256;
     float *scl = reinterpret_cast<float *>(lds + kRingBytes);
     const int stages = (K + BK - 1) / BK;
     auto issue = [&](int stage, int k0) {
         uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
-        const uint32_t voff =
-            (KFull || k0 + lane_chunk * 16 < K) ? lane_voff + uint32_t(k0) : 0x80000000u;
+        const bool kin = KFull || k0 + lane_chunk * 16 < K;
+        const uint32_t voff = kin ? lane_voff + uint32_t(k0) : 0x80000000u;
+        const uint32_t voff_p = kin ? lane_voff_p : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < INSTS; ++i) {
             const int row = (i * NW + wave) * RPI;
-            const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
             lds_ptr_t dst = (lds_ptr_t)(base + (i * NW + wave) * 1024);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rsrc_w : rsrc_x, dst, 16, voff,
-                                                     soff, 0, 0);
+            if (PackedW && i < W_INSTS) {
+                const uint32_t soff = uint32_t((row / 16) * tiles_k * 1024 + (k0 / 64) * 1024);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w, dst, 16, voff_p, soff, 0, 0);
+            } else {
+                const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rsrc_w : rsrc_x, dst, 16,
+                                                         voff, soff, 0, 0);
+            }
         }
     };
 
@@ -701,12 +733,12 @@ int launch_wide(const GemmArgs &a, hipStream_t stream) {
     const size_t lds = std::max(size_t(STAGES) * (BN + BM) * 64, size_t(WN * WM) * 128 * 256) +
                        size_t(BN + BM) * 4;
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
-    if (a.K % 64 == 0)
-        hipLaunchKernelGGL((wide_gemm<Fmt, WN, WM, STAGES, true, Out>), grid, block, lds, stream,
-                           a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n);
-    else
-        hipLaunchKernelGGL((wide_gemm<Fmt, WN, WM, STAGES, false, Out>), grid, block, lds, stream,
-                           a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n);
+#define QLIN_WIDE(KF, PW)                                                                      \
+    hipLaunchKernelGGL((wide_gemm<Fmt, WN, WM, STAGES, KF, Out, PW>), grid, block, lds, stream, \
+                       a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n)
+    if (a.K % 64 == 0) { if (a.packed) QLIN_WIDE(true, true); else QLIN_WIDE(true, false); }
+    else { if (a.packed) QLIN_WIDE(false, true); else QLIN_WIDE(false, false); }
+#undef QLIN_WIDE
     return 0;
 }
 
@@ -717,14 +749,13 @@ int launch_shape(const GemmArgs &a, hipStream_t stream) {
     const size_t lds = std::max(size_t(STAGES) * (BN + BM) * BK, size_t(BN) * BM * 2) +
                        size_t(BN + BM) * 4;
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
-    if (a.K % BK == 0)
-        hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, true, Out>),
-                           grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,
-                           tiles_m, tiles_n, a.input_group, a.weight_group);
-    else
-        hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, false, Out>),
-                           grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,
-                           tiles_m, tiles_n, a.input_group, a.weight_group);
+#define QLIN_TILED(KF, PW)                                                                      \
+    hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, KF, Out, PW>),   \
+                       grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,      \
+                       tiles_m, tiles_n, a.input_group, a.weight_group)
+    if (a.K % BK == 0) { if (a.packed) QLIN_TILED(true, true); else QLIN_TILED(true, false); }
+    else { if (a.packed) QLIN_TILED(false, true); else QLIN_TILED(false, false); }
+#undef QLIN_TILED
     return 0;
 }
 

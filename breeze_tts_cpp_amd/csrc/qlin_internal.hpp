@@ -50,6 +50,7 @@ struct GemmArgs {
     int M, N, K, fmt, out_type, input_group, weight_group;
     void *workspace;
     size_t workspace_bytes;
+    int packed = 0;    // w in the packed fragment-tile layout (weight_pack.hip)
 };
 struct GemmPath {
     int kind, tokens, channels, splits, waves, staged;
@@ -63,6 +64,9 @@ size_t skinny_workspace_bytes(const GemmArgs &, const GemmPath &);
 size_t skinny_lds_bytes(const GemmArgs &, const GemmPath &);
 constexpr size_t kLdsBytes = 160 * 1024;  // per workgroup on gfx950
 int launch_tiled(const GemmArgs &, const GemmPath &, hipStream_t);
+// Packed weight layout (weight_pack.hip): N % 16 == 0, bytes = N * ceil(K/64)*64.
+size_t packed_weight_bytes(int N, int K);
+void launch_pack_weights(const void *w, int N, int K, void *packed, hipStream_t);
 size_t tiled_workspace_bytes(const GemmArgs &, const GemmPath &);
 
 }  // namespace qlin

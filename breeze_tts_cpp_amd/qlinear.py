@@ -47,7 +47,8 @@ class Path:
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_workspace_bytes", "qlin_gemm", "qlin_linear", "qlin_quantized_norm",
-           "qlin_quantized_gated")
+           "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
+           "qlin_gemm_packed", "qlin_linear_packed")
 
 
 def load():
@@ -76,6 +77,14 @@ def load():
                               i, i, i, P, sz, P]
     L.qlin_quantized_norm.restype = i
     L.qlin_quantized_norm.argtypes = [P, P, P, P, i, i, i, ctypes.c_float, i, P, P, i, i, i, P]
+    L.qlin_packed_weight_bytes.restype = sz
+    L.qlin_packed_weight_bytes.argtypes = [i, i]
+    L.qlin_pack_weights.restype = i
+    L.qlin_pack_weights.argtypes = [P, i, i, P, P]
+    L.qlin_gemm_packed.restype = i
+    L.qlin_gemm_packed.argtypes = L.qlin_gemm.argtypes
+    L.qlin_linear_packed.restype = i
+    L.qlin_linear_packed.argtypes = L.qlin_linear.argtypes
     L.qlin_quantized_gated.restype = i
     L.qlin_quantized_gated.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
     _lib = L
@@ -177,6 +186,34 @@ def workspace_bytes(path: Path | None, rows: int, N: int, K: int, fmt: int,
                                            weight_group))
 
 
+@dataclass
+class PackedWeights:
+    """Weights [N, K] in the packed fragment-tile layout (qlin_pack_weights)."""
+    data: torch.Tensor  # uint8 [qlin_packed_weight_bytes(N, K)]
+    N: int
+    K: int
+
+    @property
+    def shape(self):
+        return (self.N, self.K)
+
+    def data_ptr(self):
+        return self.data.data_ptr()
+
+
+def pack_weights(wq: torch.Tensor, stream=None) -> PackedWeights:
+    """Repack row-major quantized weights [N, K] (once, at load time)."""
+    if wq.dim() != 2 or not wq.is_contiguous() or wq.dtype != torch.uint8:
+        raise ValueError("pack_weights expects dense uint8 [N, K] weights")
+    N, K = wq.shape
+    nbytes = int(load().qlin_packed_weight_bytes(N, K))
+    if nbytes == 0:
+        raise ValueError("packed weights need N % 16 == 0")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=wq.device)
+    _check(load().qlin_pack_weights(wq.data_ptr(), N, K, out.data_ptr(), _stream(stream)))
+    return PackedWeights(out, N, K)
+
+
 def gemm(xq: torch.Tensor, sx: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int,
          out_dtype=torch.bfloat16, input_group: int = 0, weight_group: int = 0,
          path: Path | None = None, workspace: torch.Tensor | None = None,
@@ -191,7 +228,8 @@ def gemm(xq: torch.Tensor, sx: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor,
     p = (path or Path()).to_c()
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    _check(load().qlin_gemm(ctypes.byref(p), xq.data_ptr(), sx.data_ptr(), wq.data_ptr(),
+    fn = load().qlin_gemm_packed if isinstance(wq, PackedWeights) else load().qlin_gemm
+    _check(fn(ctypes.byref(p), xq.data_ptr(), sx.data_ptr(), wq.data_ptr(),
                             sw.data_ptr(), out.data_ptr(), M, N, K, fmt,
                             F16 if out.dtype == torch.float16 else BF16, input_group,
                             weight_group, ws_ptr, ws_bytes, _stream(stream)))
@@ -223,7 +261,8 @@ def linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int, group:
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     p = (path or Path()).to_c()
-    _check(load().qlin_linear(ctypes.byref(p), x.data_ptr(), x.stride(0), _TYPES[x.dtype],
+    fn = load().qlin_linear_packed if isinstance(wq, PackedWeights) else load().qlin_linear
+    _check(fn(ctypes.byref(p), x.data_ptr(), x.stride(0), _TYPES[x.dtype],
                               scratch[0].data_ptr(), scratch[1].data_ptr(), wq.data_ptr(),
                               sw.data_ptr(), out.data_ptr(), rows, N, K, fmt, _TYPES[out.dtype],
                               group, group, rotation, ws_ptr, ws_bytes, _stream(stream)))

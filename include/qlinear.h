@@ -20,6 +20,10 @@
  *                          (ops::quantized_norm, ops/basic.h:33-34, ops/basic.cpp:54-58)
  *   qlin_quantized_gated<- launch_quantized_gated  ops/kernels/quant/quant_gated.h:7-8
  *                          (ops::quantized_gated, ops/basic.h:35, ops/basic.cpp:59-63)
+ *   qlin_pack_weights, qlin_packed_weight_bytes, qlin_gemm_packed, qlin_linear_packed
+ *                       <- no launcher of the reference: the packed weight layout that
+ *                          follows its load-time quantization (io/weights.cpp:80-87);
+ *                          qlin_gemm / qlin_linear on that layout
  *
  * Operand layouts (reference core/quantization.h:24-49):
  *   x  int8/e4m3 [rows, K] dense          sx f32 [rows] or [ceil(K/ig), rows]
@@ -148,6 +152,27 @@ int qlin_quantized_norm(void *residual, const void *update, const void *update_s
 int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,
                          void *values, float *scales, int fmt, int group, int rotation,
                          qlin_stream_t stream);
+
+/* Packed weight layout (for weights quantized once at load): tile (g, t) =
+ * rows [16g, 16g+16) x K bytes [64t, 64t+64) is 1 KB at offset
+ * (g*ceil(K/64) + t)*1024; inside it, 16-byte chunk 16q + r holds row 16g+r,
+ * K bytes [64t + 16q, +16). Bytes past K are zero. N % 16 == 0.
+ * qlin_packed_weight_bytes returns N * ceil(K/64)*64 (0 for an invalid shape). */
+size_t qlin_packed_weight_bytes(int N, int K);
+int qlin_pack_weights(const void *w, int N, int K, void *packed, qlin_stream_t stream);
+
+/* qlin_gemm / qlin_linear with w in the packed layout (same scales, same
+ * results bit for bit). Decode paths stream the packed tiles straight into
+ * MFMA registers (no LDS staging; path.staged and path.splits > 1 are not
+ * supported); prefill paths stage them through LDS like row-major weights. */
+int qlin_gemm_packed(const qlin_path *path, const void *x, const float *sx, const void *w,
+                     const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
+                     int input_group, int weight_group, void *workspace, size_t workspace_bytes,
+                     qlin_stream_t stream);
+int qlin_linear_packed(const qlin_path *path, const void *x, int ld, int src_type, void *xq,
+                       float *sx, const void *w, const float *sw, void *y, int rows, int N, int K,
+                       int fmt, int out_type, int input_group, int weight_group, int rotation,
+                       void *workspace, size_t workspace_bytes, qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

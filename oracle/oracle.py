@@ -78,6 +78,8 @@ def lib():
         L.orc_activate.argtypes = [ctypes.c_float, i]
         L.orc_quantized_gated.restype = i
         L.orc_quantized_gated.argtypes = [P, i, i, i, i, i, i, i, P, P, P]
+        L.orc_pack_weights.restype = i
+        L.orc_pack_weights.argtypes = [P, i, i, P]
         L.orc_cpu_qlinear.restype = i
         L.orc_cpu_qlinear.argtypes = [P, i, i, i, i, P, P, i, i, i, i, P, P, P, i]
         _lib = L
@@ -286,3 +288,13 @@ def quantized_gated(input_bits, kind: int, fmt: int, group: int = 0, rotation: i
     if rc:
         raise ValueError("oracle: unsupported quantized gated layout")
     return q, scales, a
+
+
+def pack_weights(wq: np.ndarray) -> np.ndarray:
+    """Packed fragment-tile layout of uint8 weights [N, K] (N % 16 == 0)."""
+    wq = np.ascontiguousarray(wq, np.uint8)
+    N, K = wq.shape
+    out = np.zeros(N * ((K + 63) // 64) * 64, np.uint8)
+    if lib().orc_pack_weights(_p(wq), N, K, _p(out)):
+        raise ValueError("oracle: packed weights need N % 16 == 0")
+    return out

@@ -313,6 +313,26 @@ int orc_quantized_gated(const uint16_t *input, int src_type, int rows, int width
     return status;
 }
 
+/* ---------------------------------------------------------------- packed weights */
+/* The packed layout of load-time-quantized weights (no reference counterpart;
+ * follows io/weights.cpp:80-87): tile (g, t) = rows [16g, 16g+16) x K bytes
+ * [64t, 64t+64) at (g*ceil(K/64) + t)*1024, chunk 16q + r of a tile = row
+ * 16g + r, K bytes [64t + 16q, +16); zero past K. Returns 0, -1 if N % 16. */
+int orc_pack_weights(const uint8_t *w, int N, int K, uint8_t *packed) {
+    if (N % 16) return -1;
+    int tk = (K + 63) / 64;
+    for (int g = 0; g < N / 16; ++g)
+        for (int t = 0; t < tk; ++t)
+            for (int q = 0; q < 4; ++q)
+                for (int r = 0; r < 16; ++r)
+                    for (int b = 0; b < 16; ++b) {
+                        int k = t * 64 + q * 16 + b;
+                        packed[((size_t)g * tk + t) * 1024 + (size_t)(q * 16 + r) * 16 + b] =
+                            k < K ? w[(size_t)(g * 16 + r) * K + k] : 0;
+                    }
+    return 0;
+}
+
 /* ---------------------------------------------------------------- GEMMs */
 /* Exact INT8 GEMM: acc[m][n] = sum_k x[m][k]*w[n][k] in int32. Any tiling or
  * split of the reference (quant_dispatch.cu:58-61 dp4a, quant_gemm_sm80.cu

@@ -168,3 +168,22 @@ def test_quantized_gated_matches_torch(orc, kind, fmt):
     assert np.array_equal(a, torch_to_bits(prod))
     q2, s2 = orc.quantize_rows(a, fmt)
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def test_pack_weights_is_the_fragment_permutation(orc):
+    """Packed layout: a bijection of the weight bytes onto fragment order,
+    zero-padded past K. Byte (n, k) sits in tile (n//16, k//64), chunk
+    ((k%64)//16)*16 + n%16, byte k%16; checked on distinct byte values."""
+    for N, K in ((32, 128), (48, 80), (16, 16)):
+        idx = np.arange(N * K, dtype=np.int64)
+        w = (idx % 251).astype(np.uint8)          # position tag
+        p = orc.pack_weights(w.reshape(N, K))
+        tk = -(-K // 64)
+        assert p.size == N * tk * 64
+        n, k = np.divmod(idx, K)
+        off = ((n // 16) * tk + k // 64) * 1024 + (((k % 64) // 16) * 16 + n % 16) * 16 + k % 16
+        assert np.array_equal(p[off], w)
+        assert len(np.unique(off)) == N * K
+        pad = np.ones(p.size, bool)
+        pad[off] = False
+        assert not p[pad].any()
