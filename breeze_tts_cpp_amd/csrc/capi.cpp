@@ -248,7 +248,7 @@ namespace {
 int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void *w,
               const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
               int input_group, int weight_group, void *workspace, size_t workspace_bytes,
-              qlin_stream_t stream, bool packed) {
+              qlin_stream_t stream, bool packed, const void *bias = nullptr, int act = 0) {
     // check_linear + make_plan rules (reference ops/cuda/quantization.cpp:94-102,
     // 206-222) and launch_quant_linear's type checks (quant_dispatch.cu:194-233).
     if (fmt != QLIN_I8 && fmt != QLIN_FP8)
@@ -288,7 +288,9 @@ int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void 
                      weight_group,
                      workspace,
                      workspace_bytes,
-                     packed ? 1 : 0};
+                     packed ? 1 : 0,
+                     static_cast<const uint16_t *>(bias),
+                     act};
     const qlin::GemmPath ip = to_internal(p);
     size_t need = 0;
     if (p.kind == QLIN_KIND_SKINNY) need = qlin::skinny_workspace_bytes(a, ip);
@@ -312,6 +314,20 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
               qlin_stream_t stream) {
     return gemm_impl(path, x, sx, w, sw, y, rows, N, K, fmt, out_type, input_group, weight_group,
                      workspace, workspace_bytes, stream, false);
+}
+
+int qlin_gemm_finish(const qlin_path *path, const void *x, const float *sx, const void *w,
+                     const float *sw, const void *bias, int activation, void *y, int rows, int N,
+                     int K, int fmt, int out_type, int input_group, int weight_group, int packed,
+                     void *workspace, size_t workspace_bytes, qlin_stream_t stream) {
+    // QuantizedGemm::linear_finish + check_finish_bias (reference
+    // ops/cuda/quantization.cpp:75-87,465-478): ReLU or tanh-GeLU (or none),
+    // optional bias [N] in the output type.
+    if (activation < QLIN_FINISH_NONE || activation > QLIN_FINISH_GELU_TANH)
+        return fail(QLIN_ERR_INVALID, "finish activation must be 0 (none), 1 (ReLU) or 2 (tanh-GeLU)");
+    if (bias && !aligned(bias, 2)) return fail(QLIN_ERR_ALIGNMENT, "bias must be 2-byte aligned");
+    return gemm_impl(path, x, sx, w, sw, y, rows, N, K, fmt, out_type, input_group, weight_group,
+                     workspace, workspace_bytes, stream, packed != 0, bias, activation);
 }
 
 size_t qlin_packed_weight_bytes(int N, int K) {

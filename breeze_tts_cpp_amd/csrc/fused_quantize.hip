@@ -35,10 +35,6 @@
 namespace qlin {
 namespace {
 
-template <class T> __device__ __forceinline__ float round16(float x) {
-    return to_float(from_float(x, T{}), T{});
-}
-
 template <class T, bool Vec>
 __device__ __forceinline__ void store16x8(uint16_t *row, int column, int cols, const float (&v)[8]) {
     if constexpr (Vec) {
@@ -111,9 +107,7 @@ template <int Kind> __device__ __forceinline__ float activate(float x) {
         const float e = float(exp(-double(x)));
         return (x * 0x1p-16f) / ((1.f + e) * 0x1p-16f);
     } else {
-        const float inner = x + ((0.044715f * x) * x) * x;
-        const float t = float(tanh(double(0.7978845608028654f * inner)));
-        return (0.5f * x) * (1.f + t);
+        return gelu_tanh(x);
     }
 }
 

@@ -24,9 +24,17 @@
 
 #include <type_traits>
 
+// Each kernel-variant translation unit is built with or without the fused
+// finish (bias + activation epilogue, see finish4); the plain build carries
+// no finish code at all.
+#ifndef QLIN_FIN
+#define QLIN_FIN 0
+#endif
+
 namespace qlin {
 namespace {
 
+constexpr bool kFin = QLIN_FIN;
 constexpr int kBlockK = 256;  // K handled per main-loop iteration (4 pieces of 64)
 
 template <int Fmt> struct Mfma;
@@ -92,7 +100,8 @@ template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out, 
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
-    int K, int span, int input_group, int weight_group) {
+    int K, int span, int input_group, int weight_group, const uint16_t *__restrict__ bias,
+    int act) {
     using M_ = Mfma<Fmt>;
     using Acc = typename M_::Acc;
     using Scalar = typename M_::Scalar;
@@ -419,6 +428,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     v[r] = s * pre_w[k][r];
                 }
             }
+            if constexpr (kFin) finish4<Out>(v, bias, n, N - 1, act);
             store4<Out>(y, size_t(m) * N + n, v);
         }
     }
@@ -431,7 +441,8 @@ __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ p
                                                     const float *__restrict__ sx,
                                                     const float *__restrict__ sw,
                                                     void *__restrict__ y, int M, int N,
-                                                    int splits) {
+                                                    int splits, const uint16_t *__restrict__ bias,
+                                                    int act) {
     const size_t i4 = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
     const size_t total = size_t(M) * N;
     if (i4 >= total) return;
@@ -448,6 +459,8 @@ __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ p
             v[r] = float(s);
         }
     }
+    // N % 4 == 0: the four values share a row.
+    if constexpr (kFin) finish4<Out>(v, bias, int(i4 % N), N - 1, act);
     store4<Out>(y, i4, v);
 }
 
@@ -457,11 +470,11 @@ int launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t 
     if (layout == 2)
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
-                           a.N, a.K, span, a.input_group, a.weight_group);
+                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act);
     else
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
-                           a.N, a.K, span, a.input_group, a.weight_group);
+                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act);
     return 0;
 }
 
@@ -469,7 +482,7 @@ template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
 int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1, true>), grid,
                        dim3(64 * WK), 0, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N,
-                       a.K, span, a.input_group, a.weight_group);
+                       a.K, span, a.input_group, a.weight_group, a.bias, a.act);
     return 0;
 }
 
@@ -517,24 +530,24 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         if (p.staged) return -4;
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out>), grid, block, 0,
                            stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span,
-                           a.input_group, a.weight_group);
+                           a.input_group, a.weight_group, a.bias, a.act);
         return 0;
     }
     if (p.staged) return -4;
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
-                       a.input_group, a.weight_group);
+                       a.input_group, a.weight_group, a.bias, a.act);
     const size_t quads = (size_t(a.M) * a.N) / 4;
     dim3 rgrid(unsigned((quads + 255) / 256));
     using Scalar = typename Mfma<Fmt>::Scalar;
     if constexpr (Grouped)
         hipLaunchKernelGGL((split_reduce<float, false, Out>), rgrid, dim3(256), 0, stream,
                            static_cast<const float *>(a.workspace), a.sx, a.sw, a.y, a.M, a.N,
-                           p.splits);
+                           p.splits, a.bias, a.act);
     else
         hipLaunchKernelGGL((split_reduce<Scalar, true, Out>), rgrid, dim3(256), 0, stream,
                            static_cast<const Scalar *>(a.workspace), a.sx, a.sw, a.y, a.M, a.N,
-                           p.splits);
+                           p.splits, a.bias, a.act);
     return 0;
 }
 
@@ -601,18 +614,25 @@ int QLIN_SKINNY_PART(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     return dispatch_grouped<QLIN_SKINNY_FMT, QLIN_SKINNY_OUT>(a, p, stream);
 }
 #else
-int launch_skinny_i8_bf16(const GemmArgs &, const GemmPath &, hipStream_t);
-int launch_skinny_i8_f16(const GemmArgs &, const GemmPath &, hipStream_t);
-int launch_skinny_fp8_bf16(const GemmArgs &, const GemmPath &, hipStream_t);
-int launch_skinny_fp8_f16(const GemmArgs &, const GemmPath &, hipStream_t);
+#define QLIN_PART_DECL(name)                                                  \
+    int name(const GemmArgs &, const GemmPath &, hipStream_t);              \
+    int name##_fin(const GemmArgs &, const GemmPath &, hipStream_t);
+QLIN_PART_DECL(launch_skinny_i8_bf16)
+QLIN_PART_DECL(launch_skinny_i8_f16)
+QLIN_PART_DECL(launch_skinny_fp8_bf16)
+QLIN_PART_DECL(launch_skinny_fp8_f16)
+#undef QLIN_PART_DECL
 
 int launch_skinny(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    const bool fin = a.bias || a.act;
     if (a.out_type == F16) {
-        if (a.fmt == I8) return launch_skinny_i8_f16(a, p, stream);
-        return launch_skinny_fp8_f16(a, p, stream);
+        if (a.fmt == I8)
+            return fin ? launch_skinny_i8_f16_fin(a, p, stream) : launch_skinny_i8_f16(a, p, stream);
+        return fin ? launch_skinny_fp8_f16_fin(a, p, stream) : launch_skinny_fp8_f16(a, p, stream);
     }
-    if (a.fmt == I8) return launch_skinny_i8_bf16(a, p, stream);
-    return launch_skinny_fp8_bf16(a, p, stream);
+    if (a.fmt == I8)
+        return fin ? launch_skinny_i8_bf16_fin(a, p, stream) : launch_skinny_i8_bf16(a, p, stream);
+    return fin ? launch_skinny_fp8_bf16_fin(a, p, stream) : launch_skinny_fp8_bf16(a, p, stream);
 }
 #endif
 

@@ -30,8 +30,16 @@
 #include <algorithm>
 #include <type_traits>
 
+// Built twice: without (launch_tiled_plain) and with (launch_tiled_fin) the
+// fused finish epilogue; the plain build carries no finish code.
+#ifndef QLIN_FIN
+#define QLIN_FIN 0
+#endif
+
 namespace qlin {
 namespace {
+
+constexpr bool kFin = QLIN_FIN;
 
 template <int Fmt> struct TileMma;
 template <> struct TileMma<I8> {
@@ -76,7 +84,7 @@ template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Gr
 __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
-    int tiles_n, int input_group, int weight_group) {
+    int tiles_n, int input_group, int weight_group, const uint16_t *__restrict__ bias, int act) {
     constexpr int NW = WN * WM;
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
     constexpr int CPR = BK / 16;          // 16-byte chunks per stage row
@@ -435,6 +443,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                         float t = acc32[i][j][blk * 4 + e] * sxm;
                         v[e] = t * swv[e];
                     }
+                    if constexpr (kFin) finish4<Out>(v, bias, n_base + wave_n * TN + n_l, N - 1, act);
                     emit(m_l, n_l, v);
                 }
         }
@@ -460,6 +469,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                         v[r] = t * swv[r];
                     }
                 }
+                if constexpr (kFin)
+                    finish4<Out>(v, bias, n_base + wave_n * TN + i * 16 + quad * 4, N - 1, act);
                 emit(m_l, i * 16 + quad * 4, v);
             }
         }
@@ -495,7 +506,7 @@ template <int Fmt, int WN, int WM, int STAGES, bool KFull, class Out, bool Packe
 __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
-    int tiles_n) {
+    int tiles_n, const uint16_t *__restrict__ bias, int act) {
     constexpr int NW = WN * WM, BN = 128 * WN, BM = 128 * WM, BK = 64, RPI = 16;
     constexpr int ROWS = BN + BM, INSTS = ROWS / (RPI * NW), W_INSTS = BN / (RPI * NW);
     constexpr int STAGE_BYTES = ROWS * BK;
@@ -700,6 +711,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
                     float t = float(acc[i][j][blk * 4 + e]) * sxm;
                     v[e] = t * swv[e];
                 }
+                if constexpr (kFin) finish4<Out>(v, bias, n_base + wave_n * TN + n_l, N - 1, act);
                 uint2 packed;
                 packed.x = pack2(v[0], v[1], Out{});
                 packed.y = pack2(v[2], v[3], Out{});
@@ -735,7 +747,7 @@ int launch_wide(const GemmArgs &a, hipStream_t stream) {
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
 #define QLIN_WIDE(KF, PW)                                                                      \
     hipLaunchKernelGGL((wide_gemm<Fmt, WN, WM, STAGES, KF, Out, PW>), grid, block, lds, stream, \
-                       a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n)
+                       a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n, a.bias, a.act)
     if (a.K % 64 == 0) { if (a.packed) QLIN_WIDE(true, true); else QLIN_WIDE(true, false); }
     else { if (a.packed) QLIN_WIDE(false, true); else QLIN_WIDE(false, false); }
 #undef QLIN_WIDE
@@ -752,7 +764,7 @@ int launch_shape(const GemmArgs &a, hipStream_t stream) {
 #define QLIN_TILED(KF, PW)                                                                      \
     hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, KF, Out, PW>),   \
                        grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,      \
-                       tiles_m, tiles_n, a.input_group, a.weight_group)
+                       tiles_m, tiles_n, a.input_group, a.weight_group, a.bias, a.act)
     if (a.K % BK == 0) { if (a.packed) QLIN_TILED(true, true); else QLIN_TILED(true, false); }
     else { if (a.packed) QLIN_TILED(false, true); else QLIN_TILED(false, false); }
 #undef QLIN_TILED
@@ -806,9 +818,8 @@ int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 
 }  // namespace
 
-size_t tiled_workspace_bytes(const GemmArgs &, const GemmPath &) { return 0; }
-
-int launch_tiled(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+#ifdef QLIN_TILED_PART
+int QLIN_TILED_PART(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (a.out_type == F16) {
         if (a.fmt == I8) return dispatch_grouped<I8, f16_t>(a, p, stream);
         return dispatch_grouped<FP8, f16_t>(a, p, stream);
@@ -816,5 +827,14 @@ int launch_tiled(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (a.fmt == I8) return dispatch_grouped<I8, bf16_t>(a, p, stream);
     return dispatch_grouped<FP8, bf16_t>(a, p, stream);
 }
+#else
+size_t tiled_workspace_bytes(const GemmArgs &, const GemmPath &) { return 0; }
+
+int launch_tiled_plain(const GemmArgs &, const GemmPath &, hipStream_t);
+int launch_tiled_fin(const GemmArgs &, const GemmPath &, hipStream_t);
+int launch_tiled(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    return (a.bias || a.act) ? launch_tiled_fin(a, p, stream) : launch_tiled_plain(a, p, stream);
+}
+#endif
 
 }  // namespace qlin

@@ -111,6 +111,40 @@ __device__ __forceinline__ float rotation_sign(int column) {
     return ((h ^ (h >> 16)) & 1u) ? 1.f : -1.f;
 }
 
+// Value rounded to the 16-bit storage type and widened back (exact).
+template <class T> __device__ __forceinline__ float round16(float x) {
+    return to_float(from_float(x, T{}), T{});
+}
+
+// tanh-GeLU of the reference (ops/kernels/common/activation.cuh:14-15,
+// quant_gated.cu:14-15): (0.5x)(1 + tanh(0.7978845608028654 (x +
+// ((0.044715x)x)x))) in fp32, tanh evaluated in fp64 and rounded once.
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float inner = x + ((0.044715f * x) * x) * x;
+    const float t = float(tanh(double(0.7978845608028654f * inner)));
+    return (0.5f * x) * (1.f + t);
+}
+
+// Finish of a quantized linear on its stored result d (the reference's
+// pointwise finish, ops/kernels/sequence/sequence_internal.cuh:61-73, with
+// value/output scale 1): s16(act(s16(s16(d) + bias[n]))); act 1 = ReLU,
+// 2 = tanh-GeLU, 0 = none. The caller's store performs the final rounding.
+enum Finish : int { FINISH_NONE = 0, FINISH_RELU = 1, FINISH_GELU_TANH = 2 };
+// Out of line: the GEMM epilogues call it only when a finish is requested,
+// so the fp64 tanh does not enlarge the register allocation of their loops.
+template <class Out>
+__device__ __noinline__ void finish4(float (&v)[4], const uint16_t *bias, int n, int n_last,
+                                     int act) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float x = round16<Out>(v[r]);
+        if (bias) x = round16<Out>(x + to_float(bias[min(n + r, n_last)], Out{}));
+        if (act == FINISH_RELU) x = fmaxf(x, 0.f);
+        else if (act == FINISH_GELU_TANH) x = gelu_tanh(x);
+        v[r] = x;
+    }
+}
+
 // ---------------------------------------------------------------- wave64 reductions
 // Max over a power-of-two lane group of width W (aligned), via xor shuffles.
 template <int W> __device__ __forceinline__ float group_max(float v) {

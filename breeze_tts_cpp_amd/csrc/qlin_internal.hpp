@@ -51,6 +51,8 @@ struct GemmArgs {
     void *workspace;
     size_t workspace_bytes;
     int packed = 0;    // w in the packed fragment-tile layout (weight_pack.hip)
+    const uint16_t *bias = nullptr;  // finish: [N] in the output type, or null
+    int act = 0;                     // finish: qlin::Finish (0 = none)
 };
 struct GemmPath {
     int kind, tokens, channels, splits, waves, staged;

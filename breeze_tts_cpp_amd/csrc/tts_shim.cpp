@@ -248,6 +248,39 @@ void QuantizedGemm::linear(RowScaledView input, RowScaledView weight, TensorView
                         stream_, format_, output.type);
 }
 
+bool QuantizedGemm::linear_finish(RowScaledView input, RowScaledView weight, TensorView output,
+                                  const ops::Epilogue &finish) {
+    // The reference fuses ReLU / tanh-GeLU; a bias-only finish (identity
+    // activation) is fused here as well.
+    int act;
+    if (finish.activation == ops::Activation::Relu) act = QLIN_FINISH_RELU;
+    else if (finish.activation == ops::Activation::GeluTanh) act = QLIN_FINISH_GELU_TANH;
+    else if (finish.activation == ops::Activation::Identity && finish.bias.data) act = QLIN_FINISH_NONE;
+    else return false;
+    input.validate();
+    weight.validate();
+    if (input.values.type != format_ || weight.values.type != format_ ||
+        input.rotation_size != weight.rotation_size || input.values.cols != weight.values.cols ||
+        input.values.rows != output.rows || weight.values.rows != output.cols ||
+        (output.type != Type::BF16 && output.type != Type::F16) || !output.dense())
+        throw std::invalid_argument("quantized linear dimensions/type mismatch");
+    // check_finish_bias (ops/cuda/quantization.cpp:83-87)
+    if (finish.bias.data && (finish.bias.type != output.type || !finish.bias.dense() ||
+                             finish.bias.numel() != size_t(output.cols)))
+        throw std::invalid_argument("quantized linear finish bias mismatch");
+    const QuantizationGroups groups{input.group_size, weight.group_size, input.rotation_size};
+    LinearPath path = planned(output.rows, output.cols, input.values.cols, output.type, groups);
+    qlin_path c{static_cast<int>(path.kind), path.tokens, path.channels, path.splits, path.waves,
+                path.staged};
+    check(qlin_gemm_finish(&c, input.values.data, input.scales.ptr<float>(), weight.values.data,
+                           weight.scales.ptr<float>(), finish.bias.data, act, output.data,
+                           output.rows, output.cols, input.values.cols, code(format_),
+                           code(output.type), input.group_size, weight.group_size, 0, workspace_,
+                           workspace_bytes_, stream_),
+          "quantized GEMM finish");
+    return true;
+}
+
 // ---------------------------------------------------------------- workspace
 QuantizationWorkspace::QuantizationWorkspace(int rows, Capacity capacity)
     : rows_(rows), capacity_(capacity) {
@@ -331,6 +364,26 @@ void linear(TensorView input, RowScaledView weight, TensorView output, RowScaled
         throw std::invalid_argument("quantized linear dimensions/layout mismatch");
     matmul(scratch, weight, output);
 }
+// ops/linear.cpp:71-93: quantize into the scratch, then the GEMM with the
+// fused finish; an epilogue the finish does not cover is rejected here (the
+// reference's generic pointwise pass is not part of this library).
+void linear(TensorView input, RowScaledView weight, TensorView bias, TensorView output,
+            Epilogue epilogue, RowScaledView scratch) {
+    weight.validate();
+    quantize_rows(input, scratch);
+    if (scratch.values.cols != weight.values.cols || output.rows != scratch.values.rows ||
+        output.cols != weight.values.rows || !output.dense())
+        throw std::invalid_argument("quantized linear dimensions/layout mismatch");
+    epilogue.bias = bias;
+    if (epilogue.activation == Activation::Identity && !bias.data) {
+        matmul(scratch, weight, output);
+        return;
+    }
+    Epilogue fused = epilogue;
+    if (!context(output.device).linear_finish(scratch, weight, output, fused))
+        throw std::invalid_argument("quantized linear epilogue is not a bias/ReLU/tanh-GeLU finish");
+}
+
 // ops/basic.cpp:54-58
 void quantized_norm(TensorView input, TensorView update, TensorView weight, RowScaledView output,
                     float epsilon, bool gemma, TensorView scale) {

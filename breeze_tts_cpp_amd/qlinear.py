@@ -48,7 +48,7 @@ class Path:
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_workspace_bytes", "qlin_gemm", "qlin_linear", "qlin_quantized_norm",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
-           "qlin_gemm_packed", "qlin_linear_packed")
+           "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish")
 
 
 def load():
@@ -85,6 +85,9 @@ def load():
     L.qlin_gemm_packed.argtypes = L.qlin_gemm.argtypes
     L.qlin_linear_packed.restype = i
     L.qlin_linear_packed.argtypes = L.qlin_linear.argtypes
+    L.qlin_gemm_finish.restype = i
+    L.qlin_gemm_finish.argtypes = [ctypes.POINTER(qlin_path), P, P, P, P, P, i, P, i, i, i, i, i,
+                                   i, i, i, P, sz, P]
     L.qlin_quantized_gated.restype = i
     L.qlin_quantized_gated.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
     _lib = L
@@ -233,6 +236,37 @@ def gemm(xq: torch.Tensor, sx: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor,
                             sw.data_ptr(), out.data_ptr(), M, N, K, fmt,
                             F16 if out.dtype == torch.float16 else BF16, input_group,
                             weight_group, ws_ptr, ws_bytes, _stream(stream)))
+    return out
+
+
+FINISH_NONE, FINISH_RELU, FINISH_GELU_TANH = 0, 1, 2
+
+
+def gemm_finish(xq: torch.Tensor, sx: torch.Tensor, wq, sw: torch.Tensor, fmt: int,
+                bias: torch.Tensor | None = None, activation: int = FINISH_NONE,
+                out_dtype=torch.bfloat16, input_group: int = 0, weight_group: int = 0,
+                path: Path | None = None, workspace: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """GEMM + the reference's finish, y = s16(act(s16(s16(d) + bias))), in one
+    epilogue (qlin_gemm_finish). `wq` may be PackedWeights."""
+    M, K = xq.shape
+    N = wq.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=xq.device)
+    if bias is not None and (bias.dtype != out.dtype or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError("finish bias must be a dense [N] tensor of the output dtype")
+    need = workspace_bytes(path, M, N, K, fmt, input_group, weight_group)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=xq.device)
+    p = (path or Path()).to_c()
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(load().qlin_gemm_finish(ctypes.byref(p), xq.data_ptr(), sx.data_ptr(), wq.data_ptr(),
+                                   sw.data_ptr(), None if bias is None else bias.data_ptr(),
+                                   activation, out.data_ptr(), M, N, K, fmt,
+                                   F16 if out.dtype == torch.float16 else BF16, input_group,
+                                   weight_group, int(isinstance(wq, PackedWeights)), ws_ptr,
+                                   ws_bytes, _stream(stream)))
     return out
 
 

@@ -20,6 +20,8 @@
  *                          (ops::quantized_norm, ops/basic.h:33-34, ops/basic.cpp:54-58)
  *   qlin_quantized_gated<- launch_quantized_gated  ops/kernels/quant/quant_gated.h:7-8
  *                          (ops::quantized_gated, ops/basic.h:35, ops/basic.cpp:59-63)
+ *   qlin_gemm_finish    <- QuantizedGemm::linear_finish  ops/cuda/quantization.cpp:465-478
+ *                          (bias + ReLU / tanh-GeLU finish of ops::linear, ops/linear.cpp:71-93)
  *   qlin_pack_weights, qlin_packed_weight_bytes, qlin_gemm_packed, qlin_linear_packed
  *                       <- no launcher of the reference: the packed weight layout that
  *                          follows its load-time quantization (io/weights.cpp:80-87);
@@ -152,6 +154,18 @@ int qlin_quantized_norm(void *residual, const void *update, const void *update_s
 int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,
                          void *values, float *scales, int fmt, int group, int rotation,
                          qlin_stream_t stream);
+
+/* Finish activations (tts::ops::Activation subset of the quantized finish). */
+enum { QLIN_FINISH_NONE = 0, QLIN_FINISH_RELU = 1, QLIN_FINISH_GELU_TANH = 2 };
+
+/* qlin_gemm followed, in the same epilogue, by the reference's finish on the
+ * stored result d: y = s16(act(s16(s16(d) + bias[n]))) (bias optional, in the
+ * output type; act none / ReLU / tanh-GeLU; s16 = rounding to the output type).
+ * `packed` = 1 when w is in the packed layout. */
+int qlin_gemm_finish(const qlin_path *path, const void *x, const float *sx, const void *w,
+                     const float *sw, const void *bias, int activation, void *y, int rows, int N,
+                     int K, int fmt, int out_type, int input_group, int weight_group, int packed,
+                     void *workspace, size_t workspace_bytes, qlin_stream_t stream);
 
 /* Packed weight layout (for weights quantized once at load): tile (g, t) =
  * rows [16g, 16g+16) x K bytes [64t, 64t+64) is 1 KB at offset

@@ -133,6 +133,19 @@ bool quant_gated_supports_clusters(int device);
 void launch_quantized_gated(TensorView input, RowScaledView output, int kind,
                             qlin_stream_t stream, int multiprocessors = 0, bool clusters = false);
 
+// ---------------------------------------------------------------- finish epilogue
+namespace ops {
+// Activation kinds (reference ops/activation.h:4); the quantized finish
+// supports Relu and GeluTanh (ops/cuda/quantization.cpp:75-82).
+enum class Activation { Identity, Relu, LeakyRelu, Silu, Gelu, GeluTanh, Mish, Tanh, Sigmoid };
+// The subset of the reference ops::Epilogue (ops/sequence.h:8-30) that the
+// fused quantized finish covers: bias [N] in the output type and activation.
+struct Epilogue {
+    TensorView bias;
+    Activation activation = Activation::Identity;
+};
+}  // namespace ops
+
 // ---------------------------------------------------------------- QuantizedGemm
 struct SelectionStats {
     size_t entries = 0, hits = 0, searches = 0;
@@ -155,6 +168,11 @@ class QuantizedGemm {
     void prepare(int rows, int output_channels, int input_channels, Type output_type = Type::BF16,
                  QuantizationGroups groups = {});
     void linear(RowScaledView input, RowScaledView weight, TensorView output);
+    // Fused bias + ReLU / tanh-GeLU finish (reference linear_finish,
+    // ops/cuda/quantization.cpp:465-478), also bias-only: false when the
+    // epilogue is none of those (the caller then finishes separately).
+    bool linear_finish(RowScaledView input, RowScaledView weight, TensorView output,
+                       const ops::Epilogue &finish);
     LinearPath planned(int rows, int output_channels, int input_channels,
                        Type output_type = Type::BF16, QuantizationGroups groups = {}) const;
     Type format() const { return format_; }
@@ -211,6 +229,10 @@ void linear(TensorView input, RowScaledView weight, TensorView output, RowScaled
 void quantized_norm(TensorView input, TensorView update, TensorView weight, RowScaledView output,
                     float epsilon, bool gemma = false, TensorView scale = {});
 void quantized_gated(TensorView input, RowScaledView output, int kind);
+// ops::linear quantized branch with a bias/activation epilogue: the finish is
+// fused into the GEMM (ops/linear.cpp:71-93).
+void linear(TensorView input, RowScaledView weight, TensorView bias, TensorView output,
+            Epilogue epilogue, RowScaledView scratch);
 }  // namespace ops
 
 }  // namespace tts

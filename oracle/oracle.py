@@ -78,6 +78,8 @@ def lib():
         L.orc_activate.argtypes = [ctypes.c_float, i]
         L.orc_quantized_gated.restype = i
         L.orc_quantized_gated.argtypes = [P, i, i, i, i, i, i, i, P, P, P]
+        L.orc_finish.restype = None
+        L.orc_finish.argtypes = [P, P, i, i, i, i]
         L.orc_pack_weights.restype = i
         L.orc_pack_weights.argtypes = [P, i, i, P]
         L.orc_cpu_qlinear.restype = i
@@ -298,3 +300,12 @@ def pack_weights(wq: np.ndarray) -> np.ndarray:
     if lib().orc_pack_weights(_p(wq), N, K, _p(out)):
         raise ValueError("oracle: packed weights need N % 16 == 0")
     return out
+
+
+def finish(y_bits: np.ndarray, bias_bits=None, act: int = 0, out_type: int = BF16) -> np.ndarray:
+    """s16(act(s16(y + bias))) on a stored 16-bit GEMM result [M, N]."""
+    y = np.ascontiguousarray(y_bits, np.uint16).copy()
+    M, N = y.shape
+    b = None if bias_bits is None else np.ascontiguousarray(bias_bits, np.uint16)
+    lib().orc_finish(_p(y), None if b is None else _p(b), M, N, act, out_type)
+    return y

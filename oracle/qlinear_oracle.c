@@ -313,6 +313,26 @@ int orc_quantized_gated(const uint16_t *input, int src_type, int rows, int width
     return status;
 }
 
+/* ---------------------------------------------------------------- finish */
+/* The finish of a quantized linear on its stored 16-bit result y (the
+ * reference's pointwise Finish::apply, ops/kernels/sequence/sequence_internal.cuh:61-73
+ * with value/output scale 1, activations of ops/kernels/common/activation.cuh:7,14):
+ * y' = s16(act(s16(y + bias[n]))), act 0 none, 1 ReLU, 2 tanh-GeLU (tanh
+ * rounded once from fp64; the reference uses cutlass::fast_tanh). In place. */
+void orc_finish(uint16_t *y, const uint16_t *bias, int M, int N, int act, int type) {
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            float v = load_src(y, type, (size_t)m * N + n);
+            if (bias) {
+                uint16_t h = store_out(v + load_src(bias, type, n), type);
+                v = load_src(&h, type, 0);
+            }
+            if (act == 1) v = fmaxf(v, 0.f);
+            else if (act == 2) v = orc_activate(v, 1);
+            y[(size_t)m * N + n] = store_out(v, type);
+        }
+}
+
 /* ---------------------------------------------------------------- packed weights */
 /* The packed layout of load-time-quantized weights (no reference counterpart;
  * follows io/weights.cpp:80-87): tile (g, t) = rows [16g, 16g+16) x K bytes

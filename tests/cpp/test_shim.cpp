@@ -180,8 +180,24 @@ static int gpu_test(const std::string &dir) {
         QuantizationWorkspace workspace(M, QuantizationWorkspace::Capacity::matrix(K, groups.activation));
         RowScaledView scratch = workspace.view(M, K, fmt, groups);
         scratch.values.device = scratch.scales.device = 0;
-        ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq, TensorView(dy, M, N, Type::BF16, 0, 0),
-                    scratch);
+        std::ifstream act_file(dir + "/finish.txt");
+        int act = 0;
+        if (act_file >> act && act) {
+            // ops::linear with a bias + activation epilogue (fused finish)
+            auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
+            void *db;
+            HIP(hipMalloc(&db, b.size() * 2));
+            HIP(hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice));
+            ops::Epilogue e;
+            e.activation = act == 1 ? ops::Activation::Relu : ops::Activation::GeluTanh;
+            ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq, TensorView(db, 1, N),
+                        TensorView(dy, M, N, Type::BF16, 0, 0), e, scratch);
+            HIP(hipStreamSynchronize(stream));
+            (void)hipFree(db);
+        } else {
+            ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq,
+                        TensorView(dy, M, N, Type::BF16, 0, 0), scratch);
+        }
         HIP(hipStreamSynchronize(stream));
         std::vector<uint16_t> y(size_t(M) * N);
         std::vector<uint8_t> wqh(size_t(N) * K);

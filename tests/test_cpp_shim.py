@@ -91,3 +91,28 @@ def test_producers_end_to_end(dev, orc, tmp_path, M, width, group):
     gq, gs, _ = orc.quantized_gated(g, 0, I8, group=group, rotation=rot)
     assert np.array_equal(np.fromfile(tmp_path / "gq.u8", np.uint8).reshape(M, width), gq)
     assert np.array_equal(np.fromfile(tmp_path / "gs.f32", np.float32), gs.ravel())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act", [1, 2])
+def test_linear_finish_end_to_end(dev, orc, tmp_path, act):
+    """ops::linear with a bias + ReLU / tanh-GeLU epilogue: the fused finish
+    on the INT8 GEMM, against the oracle GEMM followed by the oracle finish."""
+    M, N, K = 32, 512, 1024
+    xb = synthetic.activations(M, K, seed=act)
+    wb = synthetic.weights(N, K, seed=act)
+    bias = synthetic.f32_to_bf16_bits(np.random.default_rng(act).standard_normal(N) * 0.1)
+    xb.tofile(tmp_path / "x.bf16")
+    wb.tofile(tmp_path / "w.bf16")
+    bias.tofile(tmp_path / "bias.bf16")
+    (tmp_path / "shape.txt").write_text(f"{M} {N} {K} int8\n")
+    (tmp_path / "finish.txt").write_text(f"{act}\n")
+    print(f"test_shim gpu finish act={act}", flush=True)
+    r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    y = np.fromfile(tmp_path / "y.bf16", np.uint16).reshape(M, N)
+    wq, sw = orc.quantize_rows(wb, I8)
+    xq, sx = orc.quantize_rows(xb, I8)
+    plain = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw, order=0)
+    assert np.array_equal(y, orc.finish(plain, bias, act))

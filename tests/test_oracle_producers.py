@@ -187,3 +187,24 @@ def test_pack_weights_is_the_fragment_permutation(orc):
         pad = np.ones(p.size, bool)
         pad[off] = False
         assert not p[pad].any()
+
+
+@pytest.mark.parametrize("dtype,out_type", [(torch.bfloat16, 0), (torch.float16, 5)])
+def test_finish_matches_torch(orc, dtype, out_type):
+    """Finish of a stored GEMM result: bias added with torch's 16-bit rounding,
+    ReLU exactly, tanh-GeLU within one 16-bit ulp of torch's fp64 function
+    (plus the cancellation bound of the fp32 form for negative inputs)."""
+    g = torch.Generator().manual_seed(3)
+    y = (4 * torch.randn(8, 96, generator=g)).to(dtype)
+    b = torch.randn(96, generator=g).to(dtype)
+    yb, bb = torch_to_bits(y), torch_to_bits(b)
+    biased = (y.float() + b.float()).to(dtype)
+    assert np.array_equal(orc.finish(yb, bb, 0, out_type), torch_to_bits(biased))
+    assert np.array_equal(orc.finish(yb, None, 0, out_type), yb)
+    relu = torch.clamp_min(biased.float(), 0).to(dtype)
+    assert np.array_equal(orc.finish(yb, bb, 1, out_type), torch_to_bits(relu))
+    ref = torch.nn.functional.gelu(biased.double(), approximate="tanh")
+    got = bits_to_torch(orc.finish(yb, bb, 2, out_type), dtype).double()
+    ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    tol = ref.abs() * 2 * ulp + biased.double().abs() * 2.0 ** -22 + 1e-30
+    assert torch.all((got - ref).abs() <= tol)
