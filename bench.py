@@ -197,7 +197,8 @@ def main():
                           "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                           "path": [p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged],
                           "linear_us": round(us_linear, 3)}
-    dominant = max(per_proj, key=lambda n: per_proj[n]["us_per_launch"])
+    # the dominant kernel: the projection that moves the most bytes (gate_up)
+    dominant = max(per_proj, key=lambda n: per_proj[n]["bytes"])
     d = per_proj[dominant]
     roofline = {"bound": "hbm", "kernel": f"skinny_gemm INT8 {dominant} M={M_DECODE}",
                 "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
