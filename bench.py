@@ -319,9 +319,10 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
                     qlinear.gemm(xq, sx, wq, sw, fmt, path=path, out=y, workspace=ws,
                                  stream=stream)
             torch.cuda.synchronize()
-            g.replay()
+            for _ in range(4):  # warm-up: clocks settle under sustained MFMA load
+                g.replay()
             torch.cuda.synchronize()
-            n_rep = 5
+            n_rep = 10
             with torch.cuda.stream(stream):
                 start.record(stream)
                 for _ in range(n_rep):

@@ -109,6 +109,8 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         if (tiles >= 256) break;
     }
     if (p.channels == 256 && p.tokens == 256) p.waves = fmt == QLIN_FP8 ? 4 : 8;
+    // (The persistent INT8 kernel, tiled staged = 1, is not planned: at
+    // steady clocks the eight-wave kernel is faster on every BASELINE shape.)
     return p;
 }
 
@@ -176,8 +178,11 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
-        if (p.staged)
-            return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no staged variant");
+        // tiled staged = 1: the persistent 8-wave INT8 256x256 kernel
+        if (p.staged && !(p.staged == 1 && fmt == QLIN_I8 && p.waves == 8 && !input_group &&
+                          !weight_group))
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "tiled staged (persistent) path is the INT8 per-channel eight-wave 256x256");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
         return ok();

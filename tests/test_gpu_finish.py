@@ -30,7 +30,8 @@ def paths():
     return [("skinny", None, 32), ("split", Path(KIND_SKINNY, 32, 16, 2, 2), 32),
             ("tiled256x128", Path(KIND_TILED, 128, 256, 1, 1), 512),
             ("wide256x256", Path(KIND_TILED, 256, 256, 1, 4), 512),
-            ("tiled8wave", Path(KIND_TILED, 256, 256, 1, 8), 512)]
+            ("tiled8wave", Path(KIND_TILED, 256, 256, 1, 8), 512),
+            ("persistent", Path(KIND_TILED, 256, 256, 1, 8, 1), 1024)]
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])
@@ -39,7 +40,7 @@ def test_finish_all_paths(dev, orc, fmt, out_dtype, out_type):
     N, K = 512, 1024
     rng = np.random.default_rng(fmt)
     for name, path, M in paths():
-        if name == "tiled8wave" and fmt == FP8:
+        if name in ("tiled8wave", "persistent") and fmt == FP8:
             continue
         xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=M + fmt)
         plain = gpu_gemm(dev, xq, sx, wq, sw, fmt, path=path, out_dtype=out_dtype)

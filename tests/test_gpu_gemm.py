@@ -234,6 +234,8 @@ def _tiled_paths(grouped=False, fmt=I8):
             shapes = [(256, 256, 8)] + shapes
     for channels, tokens, waves in shapes:
         yield Path(KIND_TILED, tokens, channels, 1, waves)
+    if not grouped and fmt == I8:
+        yield Path(KIND_TILED, 256, 256, 1, 8, 1)  # persistent tile loop
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])

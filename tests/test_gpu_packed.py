@@ -83,9 +83,9 @@ def test_packed_prefill(dev, orc, fmt, N, K):
                                      np.random.default_rng(N).choice(M, 28, replace=False)]))
     shapes = [(256, 256, 4), (256, 128, 2), (256, 128, 1), (128, 128, 1)]
     if fmt == I8:
-        shapes.append((256, 256, 8))
-    for channels, tokens, waves in shapes:
-        p = Path(KIND_TILED, tokens, channels, 1, waves)
+        shapes += [(256, 256, 8), (256, 256, 8, 1)]
+    for channels, tokens, waves, *staged in shapes:
+        p = Path(KIND_TILED, tokens, channels, 1, waves, *staged)
         print(f"packed prefill fmt={fmt} N={N} K={K} path={p}", flush=True)
         y, _ = packed_gemm(dev, xq, sx, wq, sw, fmt, path=p)
         assert np.array_equal(y, gpu_gemm(dev, xq, sx, wq, sw, fmt, path=p))
