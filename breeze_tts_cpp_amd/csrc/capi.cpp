@@ -416,6 +416,42 @@ int qlin_quantized_norm(void *residual, const void *update, const void *update_s
     return check_launch("quantized norm launch");
 }
 
+int qlin_norm_linear(const void *x, const void *residual, const void *projection_bias,
+                     const void *norm_weight, const void *norm_bias, int src_type, int rows, int k,
+                     float eps, const void *w, const float *sw, int fmt, int n, const void *bias,
+                     int activation, void *y, void *normalized, void *encoded,
+                     float *encoded_scales, qlin_stream_t stream) {
+    // normalized_quantized_linear's conditions (reference
+    // ops/kernels/sequence/sequence_norm.cu:518-545) and check_norm_shape's
+    // epsilon rule (:396-397).
+    if (src_type != QLIN_BF16 && src_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "normalized linear input must be BF16 or F16");
+    if (fmt != QLIN_I8 && fmt != QLIN_FP8)
+        return fail(QLIN_ERR_INVALID, "quantized storage must be I8 or FP8");
+    if (rows < 1 || rows > 65535 || n < 1 || k < 4 || k % 4 || k > 512)
+        return fail(QLIN_ERR_INVALID,
+                    "normalized linear shape rows=%d n=%d k=%d (k %% 4 == 0, 4 <= k <= 512)", rows,
+                    n, k);
+    if (!(eps > 0) || eps != eps || eps > 3.4e38f)
+        return fail(QLIN_ERR_INVALID, "invalid layer normalization epsilon");
+    if (activation != QLIN_FINISH_NONE && activation != QLIN_FINISH_RELU)
+        return fail(QLIN_ERR_INVALID, "normalized linear activation must be none or ReLU");
+    if (!x || !w || !sw || !y) return fail(QLIN_ERR_INVALID, "normalized linear pointer is null");
+    if (bool(encoded) != bool(encoded_scales))
+        return fail(QLIN_ERR_INVALID, "encoded output needs values and scales");
+    if (!aligned(w, 4)) return fail(QLIN_ERR_ALIGNMENT, "weights must be 4-byte aligned");
+    for (const void *p : {x, residual, projection_bias, norm_weight, norm_bias, bias, (const void *)y,
+                          (const void *)normalized})
+        if (p && !aligned(p, 2)) return fail(QLIN_ERR_ALIGNMENT, "16-bit tensors must be 2-byte aligned");
+    if (!aligned(sw, 4) || (encoded_scales && !aligned(encoded_scales, 4)))
+        return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
+    qlin::NormLinearArgs a{x, residual, projection_bias, norm_weight, norm_bias, src_type, rows, k,
+                           eps, w, sw, fmt, n, bias, activation, y, normalized, encoded,
+                           encoded_scales};
+    qlin::launch_norm_linear(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("normalized linear launch");
+}
+
 int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,
                          void *values, float *scales, int fmt, int group, int rotation,
                          qlin_stream_t stream) {

@@ -37,6 +37,21 @@ struct GatedQuantizeArgs {
     int fmt, group, rotation, kind;  // kind 0 = SiLU, 1 = tanh-GeLU
 };
 void launch_quantized_gated(const GatedQuantizeArgs &, hipStream_t);
+struct NormLinearArgs {
+    const void *x, *residual, *projection_bias, *norm_weight, *norm_bias;  // 16-bit
+    int src_type, rows, k;                                                 // k <= 512
+    float eps;
+    const void *w;      // int8/e4m3 [n, k]
+    const float *sw;    // [n]
+    int fmt, n;
+    const void *bias;   // [n] or null
+    int act;            // FINISH_NONE / FINISH_RELU
+    void *y;            // [rows, n]
+    void *normalized;   // [rows, k] or null
+    void *encoded;      // [rows, k] or null
+    float *encoded_scales;  // [rows] or null
+};
+void launch_norm_linear(const NormLinearArgs &, hipStream_t);
 
 // Kernel families; numbering is part of the C ABI (qlin_path.kind).
 enum Kind : int { KIND_AUTO = 0, KIND_SKINNY = 1, KIND_TILED = 2 };

@@ -281,6 +281,54 @@ bool QuantizedGemm::linear_finish(RowScaledView input, RowScaledView weight, Ten
     return true;
 }
 
+bool QuantizedGemm::normalized_linear(TensorView input, TensorView normalized,
+                                      TensorView norm_weight, TensorView norm_bias, float epsilon,
+                                      const ops::NormFusion &fusion, RowScaledView weight,
+                                      TensorView output, const ops::Epilogue &epilogue,
+                                      RowScaledView encoded) {
+    // The conditions of normalized_quantized_linear (sequence_norm.cu:522-545).
+    if (weight.group_size || weight.rotation_size || encoded.group_size || encoded.rotation_size ||
+        fusion.raw.data || fusion.gate.data || fusion.shift.data || fusion.scale.data ||
+        fusion.source_rows || weight.values.type != format_)
+        return false;
+    if (epilogue.activation != ops::Activation::Identity &&
+        epilogue.activation != ops::Activation::Relu)
+        return false;
+    const int n = weight.values.rows, k = weight.values.cols;
+    if (!input.data || input.rows < 1 || input.rows > 65535 || k < 4 || k % 4 || k > 512 ||
+        input.cols != k || (input.type != Type::BF16 && input.type != Type::F16) ||
+        output.type != input.type || output.rows != input.rows || output.cols != n ||
+        !input.dense() || !output.dense())
+        return false;
+    if (normalized.data && (normalized.rows != input.rows || normalized.cols != k ||
+                            normalized.type != input.type))
+        return false;
+    for (const TensorView *v : std::initializer_list<const TensorView *>{&norm_weight, &norm_bias, &fusion.projection_bias})
+        if (v->data && (v->type != input.type || v->numel() != size_t(k)))
+            throw std::invalid_argument("normalization parameter mismatch");
+    if (fusion.residual.data && (fusion.residual.type != input.type ||
+                                 fusion.residual.rows != input.rows || fusion.residual.cols != k))
+        throw std::invalid_argument("normalization residual mismatch");
+    if (epilogue.bias.data && (epilogue.bias.type != output.type ||
+                               epilogue.bias.numel() != size_t(n)))
+        throw std::invalid_argument("quantized linear finish bias mismatch");
+    if ((encoded.values.data || encoded.scales.data) &&
+        (encoded.values.type != format_ || encoded.values.rows != input.rows ||
+         encoded.values.cols != k))
+        throw std::invalid_argument("normalized projection quantized output mismatch");
+    if (!(epsilon > 0)) throw std::invalid_argument("invalid layer normalization");
+    check(qlin_norm_linear(input.data, fusion.residual.data, fusion.projection_bias.data,
+                           norm_weight.data, norm_bias.data, code(input.type), input.rows, k,
+                           epsilon, weight.values.data, weight.scales.ptr<float>(), code(format_),
+                           n, epilogue.bias.data,
+                           epilogue.activation == ops::Activation::Relu ? QLIN_FINISH_RELU
+                                                                        : QLIN_FINISH_NONE,
+                           output.data, normalized.data, encoded.values.data,
+                           encoded.scales.ptr<float>(), stream_),
+          "normalized quantized linear");
+    return true;
+}
+
 // ---------------------------------------------------------------- workspace
 QuantizationWorkspace::QuantizationWorkspace(int rows, Capacity capacity)
     : rows_(rows), capacity_(capacity) {

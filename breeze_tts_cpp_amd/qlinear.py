@@ -48,7 +48,7 @@ class Path:
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_workspace_bytes", "qlin_gemm", "qlin_linear", "qlin_quantized_norm",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
-           "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish")
+           "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish", "qlin_norm_linear")
 
 
 def load():
@@ -88,6 +88,9 @@ def load():
     L.qlin_gemm_finish.restype = i
     L.qlin_gemm_finish.argtypes = [ctypes.POINTER(qlin_path), P, P, P, P, P, i, P, i, i, i, i, i,
                                    i, i, i, P, sz, P]
+    L.qlin_norm_linear.restype = i
+    L.qlin_norm_linear.argtypes = [P, P, P, P, P, i, i, i, ctypes.c_float, P, P, i, i, P, i, P, P,
+                                   P, P, P]
     L.qlin_quantized_gated.restype = i
     L.qlin_quantized_gated.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
     _lib = L
@@ -174,6 +177,32 @@ def quantized_gated(x: torch.Tensor, fmt: int, kind: int = 0, group: int = 0, ro
                                        values.data_ptr(), scales.data_ptr(), fmt, group,
                                        rotation, _stream(stream)))
     return values, scales
+
+
+def norm_linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int,
+                norm_weight: torch.Tensor | None = None, norm_bias: torch.Tensor | None = None,
+                residual: torch.Tensor | None = None, projection_bias: torch.Tensor | None = None,
+                bias: torch.Tensor | None = None, activation: int = 0, eps: float = 1e-5,
+                normalized: torch.Tensor | None = None, encoded: tuple | None = None,
+                out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """LayerNorm -> per-token quantization -> quantized GEMV (qlin_norm_linear),
+    hidden k <= 512. `encoded` = (codes uint8 [rows, k], scales f32 [rows])."""
+    if x.dim() != 2 or not x.is_contiguous() or x.dtype not in _TYPES:
+        raise ValueError("norm_linear expects a dense 2-D bf16/f16 input")
+    rows, k = x.shape
+    n = wq.shape[0]
+    if out is None:
+        out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+
+    def ptr(t):
+        return None if t is None else t.data_ptr()
+    codes, scales = encoded if encoded is not None else (None, None)
+    _check(load().qlin_norm_linear(x.data_ptr(), ptr(residual), ptr(projection_bias),
+                                   ptr(norm_weight), ptr(norm_bias), _TYPES[x.dtype], rows, k,
+                                   float(eps), wq.data_ptr(), sw.data_ptr(), fmt, n, ptr(bias),
+                                   activation, out.data_ptr(), ptr(normalized), ptr(codes),
+                                   ptr(scales), _stream(stream)))
+    return out
 
 
 def plan(rows: int, N: int, K: int, fmt: int, input_group: int = 0, weight_group: int = 0) -> Path:

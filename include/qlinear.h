@@ -20,6 +20,8 @@
  *                          (ops::quantized_norm, ops/basic.h:33-34, ops/basic.cpp:54-58)
  *   qlin_quantized_gated<- launch_quantized_gated  ops/kernels/quant/quant_gated.h:7-8
  *                          (ops::quantized_gated, ops/basic.h:35, ops/basic.cpp:59-63)
+ *   qlin_norm_linear    <- normalized_quantized_linear ops/kernels/sequence/norm_projection.h:15
+ *                          (QuantizedGemm::normalized_linear, ops/cuda/quantization.cpp:479-494)
  *   qlin_gemm_finish    <- QuantizedGemm::linear_finish  ops/cuda/quantization.cpp:465-478
  *                          (bias + ReLU / tanh-GeLU finish of ops::linear, ops/linear.cpp:71-93)
  *   qlin_pack_weights, qlin_packed_weight_bytes, qlin_gemm_packed, qlin_linear_packed
@@ -155,7 +157,8 @@ int qlin_quantized_gated(const void *input, int src_type, int rows, int width, i
                          void *values, float *scales, int fmt, int group, int rotation,
                          qlin_stream_t stream);
 
-/* Finish activations (tts::ops::Activation subset of the quantized finish). */
+/* Finish activations (tts::ops::Activation subset of the quantized finish;
+ * qlin_norm_linear accepts NONE and RELU). */
 enum { QLIN_FINISH_NONE = 0, QLIN_FINISH_RELU = 1, QLIN_FINISH_GELU_TANH = 2 };
 
 /* qlin_gemm followed, in the same epilogue, by the reference's finish on the
@@ -187,6 +190,21 @@ int qlin_linear_packed(const qlin_path *path, const void *x, int ld, int src_typ
                        float *sx, const void *w, const float *sw, void *y, int rows, int N, int K,
                        int fmt, int out_type, int input_group, int weight_group, int rotation,
                        void *workspace, size_t workspace_bytes, qlin_stream_t stream);
+
+/* LayerNorm -> per-token quantization -> quantized GEMV in one launch, for
+ * hidden sizes k <= 512 (the reference's fused small-M projection of the
+ * auxiliary models):
+ *   v = s16(s16(x + projection_bias) + residual)            (both optional)
+ *   u = s16((v - mean) * inv * norm_weight + norm_bias),    inv = 1/sqrt(var + eps)
+ *   u quantized per token (fmt); optionally written to `normalized` (16-bit)
+ *   and `encoded` / `encoded_scales` (codes and per-token scales);
+ *   y[r, c] = s16(act(s16(s16((acc * sw[c]) * sx[r]) + bias[c]))), act none or ReLU.
+ * w: int8/e4m3 [n, k] with per-channel scales sw; k % 4 == 0. */
+int qlin_norm_linear(const void *x, const void *residual, const void *projection_bias,
+                     const void *norm_weight, const void *norm_bias, int src_type, int rows, int k,
+                     float eps, const void *w, const float *sw, int fmt, int n, const void *bias,
+                     int activation, void *y, void *normalized, void *encoded,
+                     float *encoded_scales, qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@
 //   tts::launch_quantized_gated,
 //     quant_gated_supports_clusters          <- ops/kernels/quant/quant_gated.h:5-8
 //   tts::QuantizedGemm                       <- ops/cuda/quantization.h:15-42
+//     (normalized_linear                     <- ops/kernels/sequence/norm_projection.h:15)
 //   tts::QuantizationWorkspace               <- layers/quantization.h:9-49
 //   tts::ops::quantize_rows / matmul /
 //     prepare_quantized / linear             <- ops/storage.h:12, ops/basic.h:11,25-26,
@@ -144,6 +145,14 @@ struct Epilogue {
     TensorView bias;
     Activation activation = Activation::Identity;
 };
+// Fusions of a normalization's input (reference ops/sequence.h:55-59). The
+// fused normalized projection supports residual and projection_bias; a
+// request using the others is declined (normalized_linear returns false).
+struct NormFusion {
+    TensorView residual, projection_bias, raw, gate, shift, scale;
+    int rows_per_sequence = 1;
+    const int *source_rows = nullptr;
+};
 }  // namespace ops
 
 // ---------------------------------------------------------------- QuantizedGemm
@@ -173,6 +182,14 @@ class QuantizedGemm {
     // epilogue is none of those (the caller then finishes separately).
     bool linear_finish(RowScaledView input, RowScaledView weight, TensorView output,
                        const ops::Epilogue &finish);
+    // LayerNorm -> quantize -> GEMV in one launch for hidden sizes <= 512
+    // (reference QuantizedGemm::normalized_linear, ops/cuda/quantization.cpp:
+    // 479-494): false when the request is outside that kernel (the caller
+    // then normalizes and projects separately, as the reference does).
+    bool normalized_linear(TensorView input, TensorView normalized, TensorView norm_weight,
+                           TensorView norm_bias, float epsilon, const ops::NormFusion &fusion,
+                           RowScaledView weight, TensorView output,
+                           const ops::Epilogue &epilogue = {}, RowScaledView encoded = {});
     LinearPath planned(int rows, int output_channels, int input_channels,
                        Type output_type = Type::BF16, QuantizationGroups groups = {}) const;
     Type format() const { return format_; }

@@ -80,6 +80,11 @@ def lib():
         L.orc_quantized_gated.argtypes = [P, i, i, i, i, i, i, i, P, P, P]
         L.orc_finish.restype = None
         L.orc_finish.argtypes = [P, P, i, i, i, i]
+        L.orc_cub_sum256.restype = ctypes.c_float
+        L.orc_cub_sum256.argtypes = [P]
+        L.orc_norm_linear.restype = i
+        L.orc_norm_linear.argtypes = [P, P, P, P, P, i, i, i, ctypes.c_float, P, P, i, i, P, i, P,
+                                      P, P, P]
         L.orc_pack_weights.restype = i
         L.orc_pack_weights.argtypes = [P, i, i, P]
         L.orc_cpu_qlinear.restype = i
@@ -309,3 +314,33 @@ def finish(y_bits: np.ndarray, bias_bits=None, act: int = 0, out_type: int = BF1
     b = None if bias_bits is None else np.ascontiguousarray(bias_bits, np.uint16)
     lib().orc_finish(_p(y), None if b is None else _p(b), M, N, act, out_type)
     return y
+
+
+def cub_sum256(v: np.ndarray) -> float:
+    v = np.ascontiguousarray(v, np.float32)
+    assert v.size == 256
+    return lib().orc_cub_sum256(_p(v))
+
+
+def norm_linear(x_bits, wq, sw, fmt: int, norm_weight=None, norm_bias=None, residual=None,
+                projection_bias=None, bias=None, act: int = 0, eps: float = 1e-5,
+                src_type: int = BF16):
+    """Returns (y bits [rows, n], normalized bits [rows, k], codes [rows, k], scales [rows])."""
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    rows, k = x.shape
+    wq = np.ascontiguousarray(wq, np.uint8)
+    sw = np.ascontiguousarray(sw, np.float32)
+    n = wq.shape[0]
+    opt = [None if a is None else np.ascontiguousarray(a, np.uint16)
+           for a in (residual, projection_bias, norm_weight, norm_bias, bias)]
+    y = np.zeros((rows, n), np.uint16)
+    nrm = np.zeros((rows, k), np.uint16)
+    enc = np.zeros((rows, k), np.uint8)
+    esc = np.zeros(rows, np.float32)
+    P = [None if a is None else _p(a) for a in opt]
+    rc = lib().orc_norm_linear(_p(x), P[0], P[1], P[2], P[3], src_type, rows, k, float(eps),
+                               _p(wq), _p(sw), fmt, n, P[4], act, _p(y), _p(nrm), _p(enc),
+                               _p(esc))
+    if rc:
+        raise ValueError("oracle: unsupported normalized linear shape")
+    return y, nrm, enc, esc

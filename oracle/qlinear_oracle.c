@@ -333,6 +333,107 @@ void orc_finish(uint16_t *y, const uint16_t *bias, int M, int N, int act, int ty
         }
 }
 
+/* ---------------------------------------------------------------- LayerNorm -> GEMV */
+/* cub::BlockReduce<float, 256>::Sum, warp-reductions algorithm (CUDA 13 CUB,
+ * the NormReduce of ops/kernels/sequence/sequence_internal.cuh:135-136):
+ * per 32-thread warp, lane i adds lane i+s for s = 1, 2, 4, 8, 16 (when
+ * i+s < 32; all lanes update simultaneously), warp totals added in order. */
+float orc_cub_sum256(const float *v) {
+    float warp[32], next[32], total = 0.f;
+    for (int w = 0; w < 8; ++w) {
+        memcpy(warp, v + 32 * w, sizeof(warp));
+        for (int s = 1; s < 32; s *= 2) {
+            for (int i = 0; i < 32; ++i) next[i] = i + s < 32 ? warp[i] + warp[i + s] : warp[i];
+            memcpy(warp, next, sizeof(warp));
+        }
+        total = w ? total + warp[0] : warp[0];
+    }
+    return total;
+}
+
+/* normalized_quantized_linear / norm_project_kernel<T, QuantProjection>
+ * (ops/kernels/sequence/sequence_norm.cu:29-53 NormRow load/transform,
+ * :260-390 kernel, :518-575 host) with the fusions residual and
+ * projection_bias, no gate/scale/shift, Finish with bias and ReLU/identity.
+ * Thread t holds columns t and t+256 (k <= 512). The 1/sqrt is rounded once
+ * (the reference's rsqrtf is within 2 ulp). INT8 dot products are exact; FP8
+ * ones follow the reference order: lane l of a warp sums words c = 4l + 128j
+ * with fmaf over the 4 bytes, then a shfl-down tree 16..1.
+ * Outputs: y [rows, n]; normalized [rows, k] and encoded/escales optional. */
+int orc_norm_linear(const uint16_t *x, const uint16_t *residual, const uint16_t *pbias,
+                    const uint16_t *nw, const uint16_t *nb, int type, int rows, int k, float eps,
+                    const uint8_t *w, const float *sw, int fmt, int n, const uint16_t *bias, int act,
+                    uint16_t *y, uint16_t *normalized, uint8_t *encoded, float *escales) {
+    if (k < 4 || k % 4 || k > 512) return -1;
+    float v[512], part[256], r[512], a[512];
+    for (int row = 0; row < rows; ++row) {
+        for (int c = 0; c < 512; ++c) {
+            float val = 0.f;
+            if (c < k) {
+                val = load_src(x, type, (size_t)row * k + c);
+                uint16_t h = store_out(val + (pbias ? load_src(pbias, type, c) : 0.f), type);
+                val = load_src(&h, type, 0);
+                h = store_out(val + (residual ? load_src(residual, type, (size_t)row * k + c) : 0.f), type);
+                val = load_src(&h, type, 0);
+            }
+            v[c] = val;
+        }
+        for (int t = 0; t < 256; ++t) { float sum = 0.f; sum += v[t]; sum += v[t + 256]; part[t] = sum; }
+        float mean = orc_cub_sum256(part) / (float)k;
+        for (int t = 0; t < 256; ++t) {
+            float sum = 0.f;
+            for (int i = 0; i < 2; ++i)
+                if (t + 256 * i < k) { float d = v[t + 256 * i] - mean; sum += d * d; }
+            part[t] = sum;
+        }
+        float inv = orc_rsqrt_rn(orc_cub_sum256(part) / (float)k + eps);
+        float amax = 0.f;
+        for (int c = 0; c < k; ++c) {
+            float val = (v[c] - mean) * inv;
+            if (nw) val = val * load_src(nw, type, c);
+            uint16_t h = store_out(val + (nb ? load_src(nb, type, c) : 0.f), type);
+            r[c] = load_src(&h, type, 0);
+            amax = fmaxf(amax, fabsf(r[c]));
+            if (normalized) normalized[(size_t)row * k + c] = h;
+        }
+        float scale = orc_scale(amax, fmt), recip = 1.f / scale;
+        if (escales) escales[row] = scale;
+        for (int c = 0; c < k; ++c) {
+            uint8_t q = encode(r[c] * recip, fmt);
+            a[c] = fmt == T_I8 ? (float)(int8_t)q : orc_fp8_decode(q);
+            if (encoded) encoded[(size_t)row * k + c] = q;
+        }
+        for (int ch = 0; ch < n; ++ch) {
+            const uint8_t *wr = w + (size_t)ch * k;
+            float result;
+            if (fmt == T_I8) {
+                int64_t acc = 0;
+                for (int c = 0; c < k; ++c) acc += (int64_t)(int)a[c] * (int8_t)wr[c];
+                result = ((float)acc * sw[ch]) * scale;
+            } else {
+                float lane[32], next[32];
+                for (int l = 0; l < 32; ++l) {
+                    float acc = 0.f;
+                    for (int c = 4 * l; c < k; c += 128)
+                        for (int e = 0; e < 4; ++e) acc = fmaf(a[c + e], orc_fp8_decode(wr[c + e]), acc);
+                    lane[l] = acc;
+                }
+                for (int d = 16; d; d /= 2) {
+                    for (int l = 0; l < 32; ++l) next[l] = l + d < 32 ? lane[l] + lane[l + d] : lane[l];
+                    memcpy(lane, next, sizeof(lane));
+                }
+                result = (lane[0] * sw[ch]) * scale;
+            }
+            uint16_t h = store_out(result, type);
+            float o = load_src(&h, type, 0);
+            if (bias) { h = store_out(o + load_src(bias, type, ch), type); o = load_src(&h, type, 0); }
+            if (act == 1) o = fmaxf(o, 0.f);
+            y[(size_t)row * n + ch] = store_out(o, type);
+        }
+    }
+    return 0;
+}
+
 /* ---------------------------------------------------------------- packed weights */
 /* The packed layout of load-time-quantized weights (no reference counterpart;
  * follows io/weights.cpp:80-87): tile (g, t) = rows [16g, 16g+16) x K bytes

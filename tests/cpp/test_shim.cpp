@@ -120,6 +120,22 @@ static int host_tests() {
         launch_quantized_gated(TensorView(dummy, 4, 4096), nq, 2, nullptr);
     }));
     EXPECT(!quant_gated_supports_clusters(0));
+    // normalized_linear declines what its kernel does not cover (no launch)
+    {
+        QuantizedGemm g8(nullptr, nullptr, 0, Type::I8);
+        RowScaledView wsmall{TensorView(dummy, 64, 512, Type::I8), TensorView(dummy, 64, 1, Type::F32), 0, 0};
+        RowScaledView wbig{TensorView(dummy, 64, 1024, Type::I8), TensorView(dummy, 64, 1, Type::F32), 0, 0};
+        ops::NormFusion gated;
+        gated.gate = TensorView(dummy, 1, 512);
+        EXPECT(!g8.normalized_linear(TensorView(dummy, 2, 1024), {}, {}, {}, 1e-5f, {}, wbig,
+                                     TensorView(dummy, 2, 64)));  // k > 512
+        EXPECT(!g8.normalized_linear(TensorView(dummy, 2, 512), {}, {}, {}, 1e-5f, gated, wsmall,
+                                     TensorView(dummy, 2, 64)));  // gate fusion
+        ops::Epilogue gelu;
+        gelu.activation = ops::Activation::GeluTanh;
+        EXPECT(!g8.normalized_linear(TensorView(dummy, 2, 512), {}, {}, {}, 1e-5f, {}, wsmall,
+                                     TensorView(dummy, 2, 64), gelu));
+    }
     // ops without a bound context
     EXPECT(throws<std::logic_error>([&] { ops::matmul(x, w, TensorView(dummy, 30, 4096)); }));
     std::printf("host tests: %s\n", failures ? "FAILED" : "ok");

@@ -208,3 +208,59 @@ def test_finish_matches_torch(orc, dtype, out_type):
     ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
     tol = ref.abs() * 2 * ulp + biased.double().abs() * 2.0 ** -22 + 1e-30
     assert torch.all((got - ref).abs() <= tol)
+
+
+def test_cub_sum256_order(orc):
+    """The CUB block sum: each of 256 inputs counted exactly once, exact on
+    small integers, and it differs from a plain left-to-right fp32 sum on an
+    adversarial input (the order is pinned, not just the value)."""
+    for c in (0, 1, 31, 32, 200, 255):
+        v = np.zeros(256, np.float32)
+        v[c] = 5.0
+        assert orc.cub_sum256(v) == 5.0
+    ints = np.random.default_rng(2).integers(-100, 100, 256).astype(np.float32)
+    assert orc.cub_sum256(ints) == float(ints.astype(np.int64).sum())
+    # lanes 0, 2, 3 of warp 0 hold 2^24, 1, 1: the stride-1 step forms
+    # 1 + 1 = 2 before it meets 2^24 (2^24 + 2 is exact), while a sequential
+    # sum rounds 2^24 + 1 back to 2^24 twice.
+    v = np.zeros(256, np.float32)
+    v[0], v[2], v[3] = 2.0 ** 24, 1.0, 1.0
+    assert orc.cub_sum256(v) == 2.0 ** 24 + 2.0  # (1 + 1) formed before meeting 2^24
+    seq = np.float32(0)
+    for a in v:
+        seq = np.float32(seq + a)
+    assert float(seq) == 2.0 ** 24
+
+
+@pytest.mark.parametrize("fmt", [3, 4])
+@pytest.mark.parametrize("k", [512, 320, 8])
+def test_norm_linear_matches_torch(orc, fmt, k):
+    """LayerNorm against torch's fp64 layer_norm (within one bf16 ulp) and the
+    oracle's element-wise steps against torch's bf16 rounding given its own
+    mean/normalizer; codes = the row quantizer of the normalized row; INT8
+    outputs = numpy int64 dot products with the ((acc * sw) * sx) epilogue."""
+    rows, n = 5, 24
+    g = torch.Generator().manual_seed(k + fmt)
+    x = (torch.randn(rows, k, generator=g) * 2 + 0.5).to(torch.bfloat16)
+    res = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16)
+    nb = (0.1 * torch.randn(k, generator=g)).to(torch.bfloat16)
+    wq, sw = orc.quantize_rows(torch_to_bits((0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16)), fmt)
+    y, nrm, enc, esc = orc.norm_linear(torch_to_bits(x), wq, sw, fmt, norm_weight=torch_to_bits(nw),
+                                       norm_bias=torch_to_bits(nb), residual=torch_to_bits(res),
+                                       eps=1e-5)
+    v = (x.float() + res.float()).to(torch.bfloat16).double()
+    ref = torch.nn.functional.layer_norm(v, (k,), nw.double(), nb.double(), eps=1e-5)
+    got = bits_to_torch(nrm).double()
+    assert torch.all((got - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-6)
+    q2, s2 = orc.quantize_rows(nrm, fmt)
+    assert np.array_equal(enc, q2) and np.array_equal(esc, s2)
+    if fmt == 4:
+        acc = enc.view(np.int8).astype(np.int64) @ wq.view(np.int8).astype(np.int64).T
+        d = (acc.astype(np.float32) * sw[None, :]) * esc[:, None]
+        assert np.array_equal(y, torch_to_bits(torch.from_numpy(d).to(torch.bfloat16)))
+    else:
+        table = orc.fp8_decode_table().astype(np.float64)
+        ideal = (table[enc] @ table[wq].T) * sw[None, :] * esc[:, None]
+        got_y = bits_to_torch(y).double().numpy()
+        assert np.linalg.norm(got_y - ideal) / np.linalg.norm(ideal) <= 1e-2
