@@ -416,14 +416,104 @@ int qlin_quantized_norm(void *residual, const void *update, const void *update_s
     return check_launch("quantized norm launch");
 }
 
-int qlin_norm_linear(const void *x, const void *residual, const void *projection_bias,
-                     const void *norm_weight, const void *norm_bias, int src_type, int rows, int k,
-                     float eps, const void *w, const float *sw, int fmt, int n, const void *bias,
+void qlin_norm_fusion_init(qlin_norm_fusion *f) {
+    if (!f) return;
+    *f = qlin_norm_fusion{};
+    f->rows_per_sequence = 1;
+}
+
+void qlin_epilogue_init(qlin_epilogue *e) {
+    if (!e) return;
+    *e = qlin_epilogue{};
+    e->value_scale = e->output_scale = e->residual_scale = 1.f;
+    e->activation = QLIN_ACT_IDENTITY;
+    e->alpha = .1f;
+    e->rows_per_sequence = e->input_repeat = 1;
+}
+
+}  // extern "C"
+
+namespace {
+
+// A byte range of device memory (null = empty).
+struct Span {
+    const void *p;
+    size_t bytes;
+};
+Span span16(const void *p, size_t rows, size_t cols) { return {p, p ? rows * cols * 2 : 0}; }
+bool overlaps(Span a, Span b) {
+    if (!a.p || !b.p || !a.bytes || !b.bytes) return false;
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a.p), y = reinterpret_cast<uintptr_t>(b.p);
+    return x < y + b.bytes && y < x + a.bytes;
+}
+
+// Rows of a per-sequence modulation: 1 or the number of sequences.
+bool modulation_rows(const void *p, int rows, int sequences) {
+    return !p || rows == 1 || rows == sequences;
+}
+
+// The row quantizer output rules shared by the sequence producers
+// (check_quantized_output, ops/kernels/sequence/sequence_internal.cuh:182-197).
+int check_row_output(int src_type, int rows, int cols, const void *values, const float *scales,
+                     int fmt, int group, int rotation, const char *what) {
+    if (src_type != QLIN_BF16 && src_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "%s input must be BF16 or F16", what);
+    if (fmt != QLIN_I8 && fmt != QLIN_FP8)
+        return fail(QLIN_ERR_INVALID, "quantized storage must be I8 or FP8");
+    if (rows < 1 || cols < 1) return fail(QLIN_ERR_INVALID, "%s shape rows=%d cols=%d", what, rows, cols);
+    if (cols > qlin::kSequenceMaxCols)
+        return fail(QLIN_ERR_UNSUPPORTED, "%s supports cols <= %d (got %d)", what,
+                    qlin::kSequenceMaxCols, cols);
+    if (!values || !scales) return fail(QLIN_ERR_INVALID, "%s output pointer is null", what);
+    if (!valid_group(group))
+        return fail(QLIN_ERR_INVALID, "quantization group must be 0, 32, 64 or 128 (got %d)", group);
+    if (rotation && !group)
+        return fail(QLIN_ERR_INVALID, "rotated sequence fusion requires group scales");
+    if (rotation && (rotation != 128 || cols % 128))
+        return fail(QLIN_ERR_INVALID, "rotation must be 128 with cols %% 128 == 0");
+    if (!aligned(scales, 4)) return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
+    const size_t groups = group ? size_t((cols + group - 1) / group) : 1;
+    if (overlaps({values, size_t(rows) * cols}, {scales, groups * rows * 4}))
+        return fail(QLIN_ERR_INVALID, "quantized values/scales overlap");
+    return QLIN_OK;
+}
+
+int check_16bit_aligned(std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (p && !aligned(p, 2)) return fail(QLIN_ERR_ALIGNMENT, "16-bit tensors must be 2-byte aligned");
+    return QLIN_OK;
+}
+
+// check_norm_shape's NormFusion rules (sequence_norm.cu:371-397).
+int check_fusion(const qlin_norm_fusion &f, int rows, float eps, bool allow_source_rows) {
+    if (f.rows_per_sequence < 1 || rows % f.rows_per_sequence)
+        return fail(QLIN_ERR_INVALID, "invalid normalization sequence length");
+    const int sequences = rows / f.rows_per_sequence;
+    if (!modulation_rows(f.gate, f.gate_rows, sequences) ||
+        !modulation_rows(f.shift, f.shift_rows, sequences) ||
+        !modulation_rows(f.scale, f.scale_rows, sequences))
+        return fail(QLIN_ERR_INVALID, "invalid normalization modulation");
+    if (f.source_rows && (!allow_source_rows || f.gate || f.shift || f.scale))
+        return fail(QLIN_ERR_INVALID, "invalid indexed normalization");
+    if (!(eps > 0) || eps != eps || eps > 3.4e38f)
+        return fail(QLIN_ERR_INVALID, "invalid layer normalization");
+    return check_16bit_aligned({f.residual, f.projection_bias, f.gate, f.shift, f.scale, f.raw});
+}
+
+}  // namespace
+
+extern "C" {
+
+int qlin_norm_linear(const void *x, const qlin_norm_fusion *fusion, const void *norm_weight,
+                     const void *norm_bias, int src_type, int rows, int k, float eps,
+                     const void *w, const float *sw, int fmt, int n, const void *bias,
                      int activation, void *y, void *normalized, void *encoded,
                      float *encoded_scales, qlin_stream_t stream) {
     // normalized_quantized_linear's conditions (reference
-    // ops/kernels/sequence/sequence_norm.cu:518-545) and check_norm_shape's
-    // epsilon rule (:396-397).
+    // ops/kernels/sequence/sequence_norm.cu:518-558) and check_norm_shape.
+    qlin_norm_fusion f;
+    qlin_norm_fusion_init(&f);
+    if (fusion) f = *fusion;
     if (src_type != QLIN_BF16 && src_type != QLIN_F16)
         return fail(QLIN_ERR_INVALID, "normalized linear input must be BF16 or F16");
     if (fmt != QLIN_I8 && fmt != QLIN_FP8)
@@ -432,24 +522,145 @@ int qlin_norm_linear(const void *x, const void *residual, const void *projection
         return fail(QLIN_ERR_INVALID,
                     "normalized linear shape rows=%d n=%d k=%d (k %% 4 == 0, 4 <= k <= 512)", rows,
                     n, k);
-    if (!(eps > 0) || eps != eps || eps > 3.4e38f)
-        return fail(QLIN_ERR_INVALID, "invalid layer normalization epsilon");
     if (activation != QLIN_FINISH_NONE && activation != QLIN_FINISH_RELU)
         return fail(QLIN_ERR_INVALID, "normalized linear activation must be none or ReLU");
     if (!x || !w || !sw || !y) return fail(QLIN_ERR_INVALID, "normalized linear pointer is null");
     if (bool(encoded) != bool(encoded_scales))
         return fail(QLIN_ERR_INVALID, "encoded output needs values and scales");
+    if (int st = check_fusion(f, rows, eps, false)) return st;
     if (!aligned(w, 4)) return fail(QLIN_ERR_ALIGNMENT, "weights must be 4-byte aligned");
-    for (const void *p : {x, residual, projection_bias, norm_weight, norm_bias, bias, (const void *)y,
-                          (const void *)normalized})
-        if (p && !aligned(p, 2)) return fail(QLIN_ERR_ALIGNMENT, "16-bit tensors must be 2-byte aligned");
+    if (int st = check_16bit_aligned({x, norm_weight, norm_bias, bias, y, normalized})) return st;
     if (!aligned(sw, 4) || (encoded_scales && !aligned(encoded_scales, 4)))
         return fail(QLIN_ERR_ALIGNMENT, "scales must be 4-byte aligned");
-    qlin::NormLinearArgs a{x, residual, projection_bias, norm_weight, norm_bias, src_type, rows, k,
-                           eps, w, sw, fmt, n, bias, activation, y, normalized, encoded,
-                           encoded_scales};
+    // Outputs may not alias any operand (the reference declines the fusion).
+    const Span outputs[] = {span16(y, rows, n), span16(normalized, rows, k), span16(f.raw, rows, k),
+                            {encoded, encoded ? size_t(rows) * k : 0},
+                            {encoded_scales, encoded_scales ? size_t(rows) * 4 : 0}};
+    const Span sources[] = {span16(x, rows, k), span16(f.residual, rows, k),
+                            span16(f.projection_bias, 1, k), span16(norm_weight, 1, k),
+                            span16(norm_bias, 1, k), span16(bias, 1, n),
+                            span16(f.gate, f.gate_rows, k), span16(f.shift, f.shift_rows, k),
+                            span16(f.scale, f.scale_rows, k), {w, size_t(n) * k},
+                            {sw, size_t(n) * 4}};
+    for (size_t a = 0; a < 5; ++a) {
+        for (const Span &b : sources)
+            if (overlaps(outputs[a], b))
+                return fail(QLIN_ERR_INVALID, "normalized linear output overlaps an operand");
+        for (size_t b = a + 1; b < 5; ++b)
+            if (overlaps(outputs[a], outputs[b]))
+                return fail(QLIN_ERR_INVALID, "normalized linear outputs overlap");
+    }
+    qlin::NormLinearArgs a{x, f, norm_weight, norm_bias, src_type, rows, k, eps, w, sw, fmt, n,
+                           bias, activation, y, normalized, encoded, encoded_scales};
     qlin::launch_norm_linear(a, reinterpret_cast<hipStream_t>(stream));
     return check_launch("normalized linear launch");
+}
+
+int qlin_layer_norm_quantize(const void *x, int x_rows, int src_type, const void *norm_weight,
+                             const void *norm_bias, float eps, const qlin_norm_fusion *fusion,
+                             void *retained, int rows, int cols, void *values, float *scales,
+                             int fmt, int group, int rotation, qlin_stream_t stream) {
+    // layer_norm_quantize's checks (reference sequence_norm.cu:412-425).
+    qlin_norm_fusion f;
+    qlin_norm_fusion_init(&f);
+    if (fusion) f = *fusion;
+    if (int st = check_row_output(src_type, rows, cols, values, scales, fmt, group, rotation,
+                                  "layer norm quantize"))
+        return st;
+    if (!x || x_rows < 1) return fail(QLIN_ERR_INVALID, "layer norm quantize input is null");
+    if (!f.source_rows && x_rows != rows)
+        return fail(QLIN_ERR_INVALID, "layer norm input rows %d != output rows %d", x_rows, rows);
+    if (int st = check_fusion(f, f.source_rows ? x_rows : rows, eps, true)) return st;
+    if (int st = check_16bit_aligned({x, norm_weight, norm_bias, retained})) return st;
+    const Span q_values{values, size_t(rows) * cols};
+    const size_t groups = group ? size_t((cols + group - 1) / group) : 1;
+    const Span q_scales{scales, groups * rows * 4};
+    const Span sources[] = {span16(x, x_rows, cols), span16(retained, rows, cols),
+                            span16(norm_weight, 1, cols), span16(norm_bias, 1, cols),
+                            span16(f.residual, x_rows, cols), span16(f.projection_bias, 1, cols),
+                            span16(f.raw, rows, cols), span16(f.gate, f.gate_rows, cols),
+                            span16(f.shift, f.shift_rows, cols), span16(f.scale, f.scale_rows, cols)};
+    for (const Span &b : sources)
+        if (overlaps(q_values, b) || overlaps(q_scales, b))
+            return fail(QLIN_ERR_INVALID, "quantized output overlaps sequence storage");
+    // Row outputs (retained, raw) may replace x / residual only row for row.
+    const Span row_outputs[] = {span16(retained, rows, cols), span16(f.raw, rows, cols)};
+    if (overlaps(row_outputs[0], row_outputs[1]))
+        return fail(QLIN_ERR_INVALID, "raw and retained sequence outputs overlap");
+    for (const Span &o : row_outputs) {
+        for (const Span &b : {span16(norm_weight, 1, cols), span16(norm_bias, 1, cols),
+                              span16(f.projection_bias, 1, cols), span16(f.gate, f.gate_rows, cols),
+                              span16(f.shift, f.shift_rows, cols), span16(f.scale, f.scale_rows, cols)})
+            if (overlaps(o, b))
+                return fail(QLIN_ERR_INVALID, "quantized sequence output has unsafe row alias");
+        for (const void *src : {x, f.residual})
+            if (overlaps(o, span16(src, x_rows, cols)) && (o.p != src || f.source_rows))
+                return fail(QLIN_ERR_INVALID, "quantized sequence output has unsafe row alias");
+    }
+    qlin::LayerNormQuantizeArgs a{x, x_rows, src_type, norm_weight, norm_bias, eps, f, retained,
+                                  rows, cols, values, scales, fmt, group, rotation};
+    qlin::launch_layer_norm_quantize(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("layer norm quantize launch");
+}
+
+int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
+                            const qlin_epilogue *epilogue, void *retained, int rows, int cols,
+                            void *values, float *scales, int fmt, int group, int rotation,
+                            qlin_stream_t stream) {
+    // validate_pointwise_quantize (reference sequence_pointwise.cu:307-324) and
+    // check_epilogue (sequence_internal.cuh:154-178).
+    qlin_epilogue e;
+    qlin_epilogue_init(&e);
+    if (epilogue) e = *epilogue;
+    if (int st = check_row_output(src_type, rows, cols, values, scales, fmt, group, rotation,
+                                  "pointwise quantize"))
+        return st;
+    if (!x || x_rows < 1 || e.input_repeat < 1 || int64_t(x_rows) * e.input_repeat != rows ||
+        (e.input_repeat > 1 && retained && retained == x))
+        return fail(QLIN_ERR_INVALID, "invalid quantized pointwise input/repetition");
+    if (e.activation < QLIN_ACT_IDENTITY || e.activation > QLIN_ACT_SIGMOID)
+        return fail(QLIN_ERR_INVALID, "unknown activation %d", e.activation);
+    if (e.residual_index ? (!e.residual || e.residual_rows < 1)
+                         : (e.residual && e.residual_rows != rows))
+        return fail(QLIN_ERR_INVALID, "invalid indexed residual");
+    if (e.rows_per_sequence < 1 || rows % e.rows_per_sequence || e.valid_rows_per_sequence < 0 ||
+        e.valid_rows_per_sequence > e.rows_per_sequence)
+        return fail(QLIN_ERR_INVALID, "invalid epilogue sequence length");
+    const int sequences = rows / e.rows_per_sequence;
+    if (!modulation_rows(e.gate, e.gate_rows, sequences))
+        return fail(QLIN_ERR_INVALID, "invalid epilogue gate");
+    if (!modulation_rows(e.condition, e.condition_rows, sequences))
+        return fail(QLIN_ERR_INVALID, "invalid epilogue condition");
+    if (int st = check_16bit_aligned({x, retained, e.bias, e.residual, e.raw, e.gate, e.condition}))
+        return st;
+    const Span q_values{values, size_t(rows) * cols};
+    const size_t groups = group ? size_t((cols + group - 1) / group) : 1;
+    const Span q_scales{scales, groups * rows * 4};
+    const Span sources[] = {span16(x, x_rows, cols), span16(retained, rows, cols),
+                            span16(e.bias, 1, cols), span16(e.residual, e.residual_rows, cols),
+                            span16(e.raw, rows, cols), span16(e.gate, e.gate_rows, cols),
+                            span16(e.condition, e.condition_rows, cols)};
+    for (const Span &b : sources)
+        if (overlaps(q_values, b) || overlaps(q_scales, b))
+            return fail(QLIN_ERR_INVALID, "quantized output overlaps sequence storage");
+    const Span row_outputs[] = {span16(retained, rows, cols), span16(e.raw, rows, cols)};
+    if (overlaps(row_outputs[0], row_outputs[1]))
+        return fail(QLIN_ERR_INVALID, "raw and retained sequence outputs overlap");
+    for (const Span &o : row_outputs) {
+        for (const Span &b : {span16(e.bias, 1, cols), span16(e.gate, e.gate_rows, cols),
+                              span16(e.condition, e.condition_rows, cols)})
+            if (overlaps(o, b))
+                return fail(QLIN_ERR_INVALID, "quantized sequence output has unsafe row alias");
+        if (overlaps(o, span16(x, x_rows, cols)) && (o.p != x || e.input_repeat != 1))
+            return fail(QLIN_ERR_INVALID, "quantized sequence output has unsafe row alias");
+        if (overlaps(o, span16(e.residual, e.residual_rows, cols)) &&
+            (o.p != e.residual || e.residual_index))
+            return fail(QLIN_ERR_INVALID, "quantized sequence output has unsafe row alias");
+    }
+    qlin::PointwiseQuantizeArgs a{x, x_rows, src_type, e, retained, rows, cols, values, scales,
+                                  fmt, group, rotation};
+    qlin::launch_pointwise_quantize(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("pointwise quantize launch");
 }
 
 int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,

@@ -107,7 +107,7 @@ template <int Kind> __device__ __forceinline__ float activate(float x) {
         const float e = float(exp(-double(x)));
         return (x * 0x1p-16f) / ((1.f + e) * 0x1p-16f);
     } else {
-        return gelu_tanh(x);
+        return gelu_tanh<false>(x);
     }
 }
 
@@ -239,174 +239,6 @@ void launch_quantized_gated(const GatedQuantizeArgs &a, hipStream_t stream) {
         if (vec) launch_gated_f<FP8, true>(a, stream);
         else launch_gated_f<FP8, false>(a, stream);
     }
-}
-
-
-// ---------------------------------------------------------------- LayerNorm -> quantized GEMV
-// The reference's normalized_quantized_linear (ops/kernels/sequence/
-// sequence_norm.cu:260-390, 518-575; chosen by QuantizedGemm::normalized_linear,
-// ops/cuda/quantization.cpp:479-494): for small hidden sizes (k <= 512) one
-// workgroup of 256 threads per (token row, 8 output channels) loads the row
-// (x + projection bias, + residual, 16-bit rounding points), LayerNorms it
-// (mean, variance, (v - mean) * inv, * weight, + bias), quantizes it per token
-// into LDS and computes 8 channels, one per 32-lane half-wave (the reference's
-// warp per channel). Thread t holds columns t and t + 256.
-namespace {
-
-// cub::BlockReduce<float, 256>::Sum with the warp-reductions algorithm
-// (CUDA 13 CUB): each 32-lane group adds lane i + s into lane i for s = 1,
-// 2, 4, 8, 16 (when i + s < 32), then the eight group totals are added in
-// group order. Every thread returns the same total.
-__device__ __forceinline__ float block_sum_256(float v, float *red) {
-    const int l32 = threadIdx.x & 31;
-#pragma unroll
-    for (int s = 1; s < 32; s *= 2) {
-        const float o = __shfl_down(v, s, 32);
-        if (l32 + s < 32) v += o;
-    }
-    if (l32 == 0) red[threadIdx.x >> 5] = v;
-    __syncthreads();
-    float total = red[0];
-#pragma unroll
-    for (int w = 1; w < 8; ++w) total += red[w];
-    __syncthreads();
-    return total;
-}
-
-__device__ __forceinline__ float block_max_256(float v, float *red) {
-    v = group_max<64>(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    return r;
-}
-
-// Exact e4m3fn decode (OCP; 0x7f / 0xff NaN).
-__device__ __forceinline__ float decode_fp8(uint32_t c) {
-    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
-    float v;
-    if ((c & 0x7fu) == 0x7fu) v = __builtin_nanf("");
-    else if (e == 0) v = float(m) * 0x1p-9f;
-    else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
-    return (c & 0x80u) ? -v : v;
-}
-
-template <int Fmt, class T>
-__global__ __launch_bounds__(256) void norm_project(
-    const uint16_t *__restrict__ x, const uint16_t *__restrict__ residual,
-    const uint16_t *__restrict__ pbias, const uint16_t *__restrict__ nw,
-    const uint16_t *__restrict__ nb, int k, float eps, const uint8_t *__restrict__ w,
-    const float *__restrict__ sw, int n, const uint16_t *__restrict__ bias, int act,
-    uint16_t *__restrict__ y, uint16_t *__restrict__ normalized, uint8_t *__restrict__ encoded,
-    float *__restrict__ encoded_scales) {
-    __shared__ float red[8];
-    __shared__ __attribute__((aligned(16))) uint16_t act16[512];  // FP8: decoded T values
-    __shared__ __attribute__((aligned(16))) uint8_t act8[512];    // INT8: codes
-    const int row = blockIdx.y, t = threadIdx.x;
-    const bool first = blockIdx.x == 0;
-    float v[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = t + i * 256;
-        float a = 0.f;
-        if (c < k) {
-            a = to_float(x[size_t(row) * k + c], T{});
-            a = round16<T>(a + (pbias ? to_float(pbias[c], T{}) : 0.f));
-            a = round16<T>(a + (residual ? to_float(residual[size_t(row) * k + c], T{}) : 0.f));
-        }
-        v[i] = a;
-    }
-    float sum = 0.f;
-    sum += v[0];
-    sum += v[1];
-    const float mean = block_sum_256(sum, red) / float(k);
-    sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        if (t + i * 256 < k) {
-            const float d = v[i] - mean;
-            sum += d * d;
-        }
-    const float inv = rsqrt_rn(block_sum_256(sum, red) / float(k) + eps);
-    float r[2] = {0.f, 0.f}, amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = t + i * 256;
-        if (c < k) {
-            float val = (v[i] - mean) * inv;
-            if (nw) val = val * to_float(nw[c], T{});
-            val = round16<T>(val + (nb ? to_float(nb[c], T{}) : 0.f));
-            r[i] = val;
-            amax = fmaxf(amax, fabsf(val));
-            if (first && normalized) normalized[size_t(row) * k + c] = from_float(val, T{});
-        }
-    }
-    const float scale = quant_scale<Fmt>(block_max_256(amax, red));
-    const float recip = 1.f / scale;
-    if (first && t == 0 && encoded_scales) encoded_scales[row] = scale;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = t + i * 256;
-        if (c < k) {
-            const uint32_t q = encode<Fmt>(r[i] * recip);
-            if constexpr (Fmt == I8) act8[c] = uint8_t(q);
-            else act16[c] = from_float(decode_fp8(q), T{});
-            if (first && encoded) encoded[size_t(row) * k + c] = uint8_t(q);
-        }
-    }
-    __syncthreads();
-    // One channel per 32-lane group: lane l covers words c = 4l + 128j.
-    const int l32 = t & 31, channel = blockIdx.x * 8 + (t >> 5);
-    if (channel >= n) return;
-    const uint8_t *wr = w + size_t(channel) * k;
-    float result;
-    if constexpr (Fmt == I8) {
-        int acc = 0;
-        for (int c = l32 * 4; c < k; c += 128)
-            acc = __builtin_amdgcn_sdot4(*reinterpret_cast<const int *>(act8 + c),
-                                         *reinterpret_cast<const int *>(wr + c), acc, false);
-#pragma unroll
-        for (int d = 16; d; d /= 2) acc += __shfl_down(acc, d, 32);
-        result = (float(acc) * sw[channel]) * scale;
-    } else {
-        float acc = 0.f;
-        for (int c = l32 * 4; c < k; c += 128) {
-            const uint32_t wq = *reinterpret_cast<const uint32_t *>(wr + c);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                acc = __builtin_fmaf(to_float(act16[c + e], T{}), decode_fp8((wq >> (8 * e)) & 0xffu),
-                                     acc);
-        }
-#pragma unroll
-        for (int d = 16; d; d /= 2) acc += __shfl_down(acc, d, 32);
-        result = (acc * sw[channel]) * scale;
-    }
-    if (l32 == 0) {
-        float o = round16<T>(result);
-        if (bias) o = round16<T>(o + to_float(bias[channel], T{}));
-        if (act == FINISH_RELU) o = fmaxf(o, 0.f);
-        y[size_t(row) * n + channel] = from_float(o, T{});
-    }
-}
-
-}  // namespace
-
-void launch_norm_linear(const NormLinearArgs &a, hipStream_t stream) {
-    dim3 grid(unsigned((a.n + 7) / 8), unsigned(a.rows)), block(256);
-#define QLIN_NL(F, T)                                                                           \
-    hipLaunchKernelGGL((norm_project<F, T>), grid, block, 0, stream,                           \
-                       static_cast<const uint16_t *>(a.x), static_cast<const uint16_t *>(a.residual), \
-                       static_cast<const uint16_t *>(a.projection_bias),                       \
-                       static_cast<const uint16_t *>(a.norm_weight),                           \
-                       static_cast<const uint16_t *>(a.norm_bias), a.k, a.eps,                 \
-                       static_cast<const uint8_t *>(a.w), a.sw, a.n,                           \
-                       static_cast<const uint16_t *>(a.bias), a.act,                           \
-                       static_cast<uint16_t *>(a.y), static_cast<uint16_t *>(a.normalized),   \
-                       static_cast<uint8_t *>(a.encoded), a.encoded_scales)
-    if (a.fmt == I8) { if (a.src_type == F16) QLIN_NL(I8, f16_t); else QLIN_NL(I8, bf16_t); }
-    else { if (a.src_type == F16) QLIN_NL(FP8, f16_t); else QLIN_NL(FP8, bf16_t); }
-#undef QLIN_NL
 }
 
 }  // namespace qlin

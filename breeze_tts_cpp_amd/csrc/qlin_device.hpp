@@ -116,17 +116,22 @@ template <class T> __device__ __forceinline__ float round16(float x) {
     return to_float(from_float(x, T{}), T{});
 }
 
-// tanh-GeLU of the reference (ops/kernels/common/activation.cuh:14-15,
-// quant_gated.cu:14-15): (0.5x)(1 + tanh(0.7978845608028654 (x +
-// ((0.044715x)x)x))) in fp32, tanh evaluated in fp64 and rounded once.
+// tanh-GeLU of the reference: (0.5x)(1 + tanh(0.7978845608028654 * inner))
+// in fp32, tanh evaluated in fp64 and rounded once. The reference's TUs
+// differ in contraction: quant_gated.cu (built with --fmad=false,
+// quant_gated.cu:14-15) forms inner = x + ((0.044715x)x)x with separate
+// roundings; activation.cuh:15 as compiled into the GEMM epilogue and the
+// pointwise finish (FMA contraction on) forms inner = fma((0.044715x)x, x, x).
+template <bool Contracted>
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float inner = x + ((0.044715f * x) * x) * x;
+    const float cubic = (0.044715f * x) * x;
+    const float inner = Contracted ? __builtin_fmaf(cubic, x, x) : x + cubic * x;
     const float t = float(tanh(double(0.7978845608028654f * inner)));
     return (0.5f * x) * (1.f + t);
 }
 
 // Finish of a quantized linear on its stored result d (the reference's
-// pointwise finish, ops/kernels/sequence/sequence_internal.cuh:61-73, with
+// pointwise finish, ops/kernels/sequence/sequence_internal.cuh:59-73, with
 // value/output scale 1): s16(act(s16(s16(d) + bias[n]))); act 1 = ReLU,
 // 2 = tanh-GeLU, 0 = none. The caller's store performs the final rounding.
 enum Finish : int { FINISH_NONE = 0, FINISH_RELU = 1, FINISH_GELU_TANH = 2 };
@@ -138,9 +143,10 @@ __device__ __noinline__ void finish4(float (&v)[4], const uint16_t *bias, int n,
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         float x = round16<Out>(v[r]);
-        if (bias) x = round16<Out>(x + to_float(bias[min(n + r, n_last)], Out{}));
+        // The reference adds the bias read as 0 when absent (-0 becomes +0).
+        x = round16<Out>(x + (bias ? to_float(bias[min(n + r, n_last)], Out{}) : 0.f));
         if (act == FINISH_RELU) x = fmaxf(x, 0.f);
-        else if (act == FINISH_GELU_TANH) x = gelu_tanh(x);
+        else if (act == FINISH_GELU_TANH) x = gelu_tanh<true>(x);
         v[r] = x;
     }
 }

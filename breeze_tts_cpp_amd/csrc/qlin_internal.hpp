@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/qlinear.h"
+
 namespace qlin {
 
 struct RowQuantizeArgs {
@@ -37,9 +39,13 @@ struct GatedQuantizeArgs {
     int fmt, group, rotation, kind;  // kind 0 = SiLU, 1 = tanh-GeLU
 };
 void launch_quantized_gated(const GatedQuantizeArgs &, hipStream_t);
+// Sequence-fusion producers; the fusion structs are the C ABI's, validated by
+// the caller (dense rows, shapes and row counts checked).
 struct NormLinearArgs {
-    const void *x, *residual, *projection_bias, *norm_weight, *norm_bias;  // 16-bit
-    int src_type, rows, k;                                                 // k <= 512
+    const void *x;                      // 16-bit [rows, k]
+    qlin_norm_fusion f;                 // source_rows null
+    const void *norm_weight, *norm_bias;
+    int src_type, rows, k;              // k <= 512
     float eps;
     const void *w;      // int8/e4m3 [n, k]
     const float *sw;    // [n]
@@ -51,7 +57,37 @@ struct NormLinearArgs {
     void *encoded;      // [rows, k] or null
     float *encoded_scales;  // [rows] or null
 };
+struct LayerNormQuantizeArgs {
+    const void *x;
+    int x_rows, src_type;
+    const void *norm_weight, *norm_bias;
+    float eps;
+    qlin_norm_fusion f;
+    void *retained;     // [rows, cols] or null
+    int rows, cols;     // cols <= 16384
+    void *values;
+    float *scales;
+    int fmt, group, rotation;
+};
+struct PointwiseQuantizeArgs {
+    const void *x;
+    int x_rows, src_type;
+    qlin_epilogue e;
+    void *retained;     // [rows, cols] or null
+    int rows, cols;     // cols <= 16384
+    void *values;
+    float *scales;
+    int fmt, group, rotation;
+};
+constexpr int kSequenceMaxCols = 16384;
 void launch_norm_linear(const NormLinearArgs &, hipStream_t);
+void launch_layer_norm_quantize(const LayerNormQuantizeArgs &, hipStream_t);
+void launch_pointwise_quantize(const PointwiseQuantizeArgs &, hipStream_t);
+// Per-format parts of the two row quantizers (vec: 16-byte row access).
+void launch_layer_norm_quantize_i8(const LayerNormQuantizeArgs &, bool vec, hipStream_t);
+void launch_layer_norm_quantize_fp8(const LayerNormQuantizeArgs &, bool vec, hipStream_t);
+void launch_pointwise_quantize_i8(const PointwiseQuantizeArgs &, bool vec, hipStream_t);
+void launch_pointwise_quantize_fp8(const PointwiseQuantizeArgs &, bool vec, hipStream_t);
 
 // Kernel families; numbering is part of the C ABI (qlin_path.kind).
 enum Kind : int { KIND_AUTO = 0, KIND_SKINNY = 1, KIND_TILED = 2 };

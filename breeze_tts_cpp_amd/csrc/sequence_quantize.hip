@@ -1,0 +1,520 @@
+// Sequence-fusion producers of the quantized linear path for gfx950: the
+// kernels that turn a 16-bit activation into the next projection's quantized
+// input (or, for small hidden sizes, straight into the projection output):
+//
+//   layer_norm_quantize: NormFusion input (projection bias, gate, residual)
+//     -> LayerNorm (weight, bias, scale, shift) -> row quantization
+//     (reference layer_norm_quantize, ops/kernels/sequence/sequence_norm.cu:
+//     65-200,412-440).
+//   pointwise_quantize: the dense pointwise epilogue (bias, gate, scaled or
+//     indexed residual, condition, sequence-tail mask, output scale,
+//     activation) -> row quantization (reference pointwise_quantize,
+//     sequence_pointwise.cu:149-260,325-357).
+//   norm_project: LayerNorm -> per-token quantization -> GEMV in one launch,
+//     k <= 512 (reference normalized_quantized_linear, sequence_norm.cu:
+//     216-390,518-575).
+//
+// One 256-thread workgroup per row. The row quantizers hold the row in
+// registers in the row encoder's layout (lane t owns columns
+// (it * 256 + t) * 8 .. +8) and share its encoders (per token, H128-rotated
+// K groups, K groups), so their codes and scales are those of the row
+// quantizer applied to the 16-bit result.
+//
+// Arithmetic contract (this TU builds with -ffp-contract=off; the reference's
+// sequence TUs are compiled with FMA contraction, so the two places where the
+// reference's source has a contractible a*b+c use an explicit fma):
+//  - LayerNorm statistics in the reference's order: thread t sums the columns
+//    t, t + 256, t + 512, ... in order (values staged in LDS for that), then
+//    the 256 partials reduce in cub::BlockReduce order (32-lane trees with
+//    strides 1..16, then the 8 group totals in order); mean = sum / cols; the
+//    variance partial accumulates fma(d, d, sum); inv = the correctly rounded
+//    1/sqrt(var / cols + eps) (the reference's rsqrtf is within 2 ulp).
+//  - The normalization (v - mean) * inv and * weight are separate roundings
+//    (__fmul_rn in the reference), then the 16-bit rounding points of NormRow.
+//  - The epilogue forms value_scale * v + residual_scale * skip as
+//    fma(value_scale, v, residual_scale * skip).
+//  - Transcendental activations evaluate exp / erf / log1p / tanh in fp64 and
+//    round once to fp32 (the reference's expf, erff, log1pf, tanhf and
+//    cutlass::fast_tanh approximate the same values); tanh-GeLU's inner term
+//    is fma((0.044715x)x, x, x) as the contracting TUs compile it.
+#include "qlin_device.hpp"
+#include "qlin_internal.hpp"
+#include "row_encode.hpp"
+
+namespace qlin {
+namespace {
+
+// cub::BlockReduce<float, 256>::Sum with the warp-reductions algorithm
+// (CUDA 13 CUB): each 32-lane group adds lane i + s into lane i for s = 1,
+// 2, 4, 8, 16 (when i + s < 32), then the eight group totals are added in
+// group order. Every thread returns the same total.
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+    const int l32 = threadIdx.x & 31;
+#pragma unroll
+    for (int s = 1; s < 32; s *= 2) {
+        const float o = __shfl_down(v, s, 32);
+        if (l32 + s < 32) v += o;
+    }
+    if (l32 == 0) red[threadIdx.x >> 5] = v;
+    __syncthreads();
+    float total = red[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) total += red[w];
+    __syncthreads();
+    return total;
+}
+
+__device__ __forceinline__ float block_max_256(float v, float *red) {
+    v = group_max<64>(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return r;
+}
+
+// Correctly rounded 1/sqrt(a) in fp32.
+__device__ __forceinline__ float rsqrt_rn(float a) { return float(1.0 / sqrt(double(a))); }
+
+// Exact e4m3fn decode (OCP; 0x7f / 0xff NaN).
+__device__ __forceinline__ float decode_fp8(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    float v;
+    if ((c & 0x7fu) == 0x7fu) v = __builtin_nanf("");
+    else if (e == 0) v = float(m) * 0x1p-9f;
+    else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    return (c & 0x80u) ? -v : v;
+}
+
+// Activations with a transcendental (ops/kernels/common/activation.cuh:11-22),
+// out of line so the row loops keep their registers.
+__device__ __noinline__ float activate_slow(float x, int kind) {
+    switch (kind) {
+    case QLIN_ACT_SILU: return x / (1.f + float(exp(-double(x))));
+    case QLIN_ACT_GELU: return (0.5f * x) * (1.f + float(erf(double(x * 0.7071067811865475f))));
+    case QLIN_ACT_GELU_TANH: return gelu_tanh<true>(x);
+    case QLIN_ACT_MISH: {
+        const float softplus = x > 20.f ? x : float(log1p(double(float(exp(double(x))))));
+        return x * float(tanh(double(softplus)));
+    }
+    case QLIN_ACT_TANH: return float(tanh(double(x)));
+    case QLIN_ACT_SIGMOID: return 1.f / (1.f + float(exp(-double(x))));
+    default: return x;
+    }
+}
+
+__device__ __forceinline__ float activate(float x, int kind, float alpha) {
+    if (kind == QLIN_ACT_IDENTITY) return x;
+    if (kind == QLIN_ACT_RELU) return fmaxf(x, 0.f);
+    if (kind == QLIN_ACT_LEAKY_RELU) return x >= 0.f ? x : x * alpha;
+    return activate_slow(x, kind);
+}
+
+template <class T, bool Vec>
+__device__ __forceinline__ void store16x8(uint16_t *row, int column, int cols, const float (&v)[8]) {
+    if constexpr (Vec) {
+        if (column < cols) {
+            uint4 packed;
+            packed.x = pack2(v[0], v[1], T{});
+            packed.y = pack2(v[2], v[3], T{});
+            packed.z = pack2(v[4], v[5], T{});
+            packed.w = pack2(v[6], v[7], T{});
+            *reinterpret_cast<uint4 *>(row + column) = packed;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (column + i < cols) row[column + i] = from_float(v[i], T{});
+    }
+}
+
+// Row `r` of a [rows, cols] 16-bit tensor, row 0 when it has one row
+// (the reference View's broadcast), or null.
+__device__ __forceinline__ const uint16_t *row_of(const void *p, int rows, int r, int cols) {
+    return p ? static_cast<const uint16_t *>(p) + size_t(rows == 1 ? 0 : r) * cols : nullptr;
+}
+
+template <class T, bool Vec>
+__device__ __forceinline__ void load8_or(const uint16_t *row, int column, int cols, float (&v)[8],
+                                         float absent) {
+    if (row) load8<T, Vec>(row, column, cols, v);
+    else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = absent;
+    }
+}
+
+// ---------------------------------------------------------------- LayerNorm -> quant
+template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+__global__ __launch_bounds__(kThreads) void layer_norm_quantize(
+    const uint16_t *__restrict__ x, int x_rows, const uint16_t *__restrict__ nw,
+    const uint16_t *__restrict__ nb, float eps, qlin_norm_fusion f, uint16_t *__restrict__ retained,
+    int rows, int cols, uint8_t *__restrict__ q, float *__restrict__ scales) {
+    __shared__ float cache[Items * kChunk];
+    __shared__ float red[8];
+    const int out_row = blockIdx.x, t = threadIdx.x;
+    const int row = f.source_rows ? f.source_rows[out_row] : out_row;
+    float v[Items][8];
+    if (row < 0 || row >= x_rows) {
+        // An out-of-range source row: NaN outputs, unit scales, codes of NaN
+        // (norm_kernel's first branch, sequence_norm.cu:73-81).
+#pragma unroll
+        for (int it = 0; it < Items; ++it)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = __builtin_nanf("");
+#pragma unroll
+        for (int it = 0; it < Items; ++it) {
+            const int column = (it * kThreads + t) * 8;
+            if (retained) store16x8<T, Vec>(retained + size_t(out_row) * cols, column, cols, v[it]);
+            store8<Fmt, Vec>(q + size_t(out_row) * cols, column, cols, v[it], 1.f);
+        }
+        const int groups = G ? (cols + G - 1) / G : 1;
+        for (int g = t; g < groups; g += kThreads) scales[size_t(g) * rows + out_row] = 1.f;
+        return;
+    }
+    const int sequence = row / f.rows_per_sequence;
+    const uint16_t *xr = x + size_t(row) * cols;
+    const uint16_t *pb = row_of(f.projection_bias, 1, 0, cols);
+    const uint16_t *gate = row_of(f.gate, f.gate_rows, sequence, cols);
+    const uint16_t *res = row_of(f.residual, x_rows, row, cols);
+    const uint16_t *scale = row_of(f.scale, f.scale_rows, sequence, cols);
+    const uint16_t *shift = row_of(f.shift, f.shift_rows, sequence, cols);
+    uint16_t *raw = f.raw ? static_cast<uint16_t *>(f.raw) + size_t(out_row) * cols : nullptr;
+#pragma unroll
+    for (int it = 0; it < Items; ++it) {
+        const int column = (it * kThreads + t) * 8;
+        float a[8], b[8];
+        load8<T, Vec>(xr, column, cols, a);
+        load8_or<T, Vec>(pb, column, cols, b, 0.f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+        if (gate) {
+            load8<T, Vec>(gate, column, cols, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * b[i]);
+        }
+        load8_or<T, Vec>(res, column, cols, b, 0.f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[it][i] = column + i < cols ? round16<T>(a[i] + b[i]) : 0.f;
+            if (column + i < cols) cache[column + i] = v[it][i];
+        }
+        if (raw) store16x8<T, Vec>(raw, column, cols, v[it]);
+    }
+    __syncthreads();
+    float sum = 0.f;
+    for (int c = t; c < cols; c += kThreads) sum += cache[c];
+    const float mean = block_sum_256(sum, red) / float(cols);
+    sum = 0.f;
+    for (int c = t; c < cols; c += kThreads) {
+        const float d = cache[c] - mean;
+        sum = __builtin_fmaf(d, d, sum);
+    }
+    const float inv = rsqrt_rn(block_sum_256(sum, red) / float(cols) + eps);
+#pragma unroll
+    for (int it = 0; it < Items; ++it) {
+        const int column = (it * kThreads + t) * 8;
+        float w[8], b[8];
+        load8_or<T, Vec>(nw, column, cols, w, 1.f);
+        load8_or<T, Vec>(nb, column, cols, b, 0.f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float u = (v[it][i] - mean) * inv;
+            if (nw) u = u * w[i];
+            v[it][i] = round16<T>(u + b[i]);
+        }
+        if (scale) {
+            load8<T, Vec>(scale, column, cols, w);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(v[it][i] * round16<T>(1.f + w[i]));
+        }
+        load8_or<T, Vec>(shift, column, cols, b, 0.f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[it][i] = column + i < cols ? round16<T>(v[it][i] + b[i]) : 0.f;
+        if (retained) store16x8<T, Vec>(retained + size_t(out_row) * cols, column, cols, v[it]);
+    }
+    encode_row<Fmt, Items, Rot, G, Vec>(v, q, scales, out_row, rows, cols);
+}
+
+// ---------------------------------------------------------------- pointwise -> quant
+template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+__global__ __launch_bounds__(kThreads) void pointwise_quantize(
+    const uint16_t *__restrict__ x, int x_rows, qlin_epilogue e, uint16_t *__restrict__ retained,
+    int rows, int cols, uint8_t *__restrict__ q, float *__restrict__ scales) {
+    const int row = blockIdx.x, t = threadIdx.x;
+    const bool masked =
+        e.valid_rows_per_sequence && row % e.rows_per_sequence >= e.valid_rows_per_sequence;
+    const int sequence = row / e.rows_per_sequence;
+    const uint16_t *xr = row_of(x, x_rows, row / e.input_repeat, cols);
+    const uint16_t *bias = row_of(e.bias, 1, 0, cols);
+    const uint16_t *gate = row_of(e.gate, e.gate_rows, sequence, cols);
+    const uint16_t *cond = row_of(e.condition, e.condition_rows, sequence, cols);
+    const int r = e.residual_index ? e.residual_index[row] : row;
+    const bool skip_nan = e.residual && r >= e.residual_rows;
+    const uint16_t *res = e.residual && r >= 0 && !skip_nan
+                              ? row_of(e.residual, e.residual_rows, r, cols) : nullptr;
+    uint16_t *raw = e.raw ? static_cast<uint16_t *>(e.raw) + size_t(row) * cols : nullptr;
+    float v[Items][8];
+#pragma unroll
+    for (int it = 0; it < Items; ++it) {
+        const int column = (it * kThreads + t) * 8;
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
+            if (raw) store16x8<T, Vec>(raw, column, cols, v[it]);
+        } else {
+            float a[8], b[8];
+            load8<T, Vec>(xr, column, cols, a);
+            load8_or<T, Vec>(bias, column, cols, b, 0.f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+            if (gate) {
+                load8<T, Vec>(gate, column, cols, b);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * b[i]);
+            }
+            load8_or<T, Vec>(res, column, cols, b, skip_nan ? __builtin_nanf("") : 0.f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                a[i] = round16<T>(__builtin_fmaf(e.value_scale, a[i], e.residual_scale * b[i]));
+            if (cond) {
+                load8<T, Vec>(cond, column, cols, b);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+            }
+            if (raw) store16x8<T, Vec>(raw, column, cols, a);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[it][i] = column + i < cols
+                               ? round16<T>(activate(round16<T>(a[i] * e.output_scale),
+                                                     e.activation, e.alpha))
+                               : 0.f;
+        }
+        if (retained) store16x8<T, Vec>(retained + size_t(row) * cols, column, cols, v[it]);
+    }
+    encode_row<Fmt, Items, Rot, G, Vec>(v, q, scales, row, rows, cols);
+}
+
+// ---------------------------------------------------------------- LayerNorm -> GEMV
+// One workgroup per (token row, 8 output channels); thread t holds columns t
+// and t + 256. The row is LayerNormed and quantized per token into LDS
+// (INT8 codes, or FP8 codes decoded to the 16-bit type as the reference
+// stages them), then each 32-lane group computes one channel: INT8 by exact
+// 4-way dot products, FP8 by fp32 fma in the lane's ascending columns, then
+// a 32-lane shuffle-down tree, (acc * sw) * scale, bias and ReLU.
+template <int Fmt, class T>
+__global__ __launch_bounds__(256) void norm_project(
+    const uint16_t *__restrict__ x, qlin_norm_fusion f, const uint16_t *__restrict__ nw,
+    const uint16_t *__restrict__ nb, int k, float eps, const uint8_t *__restrict__ w,
+    const float *__restrict__ sw, int n, const uint16_t *__restrict__ bias, int act,
+    uint16_t *__restrict__ y, uint16_t *__restrict__ normalized, uint8_t *__restrict__ encoded,
+    float *__restrict__ encoded_scales) {
+    __shared__ float red[8];
+    __shared__ __attribute__((aligned(16))) uint16_t act16[512];  // FP8: decoded T values
+    __shared__ __attribute__((aligned(16))) uint8_t act8[512];    // INT8: codes
+    const int row = blockIdx.y, t = threadIdx.x;
+    const bool first = blockIdx.x == 0;
+    const int sequence = row / f.rows_per_sequence;
+    const uint16_t *pb = row_of(f.projection_bias, 1, 0, k);
+    const uint16_t *gate = row_of(f.gate, f.gate_rows, sequence, k);
+    const uint16_t *res = row_of(f.residual, gridDim.y, row, k);
+    const uint16_t *scale = row_of(f.scale, f.scale_rows, sequence, k);
+    const uint16_t *shift = row_of(f.shift, f.shift_rows, sequence, k);
+    uint16_t *raw = f.raw ? static_cast<uint16_t *>(f.raw) + size_t(row) * k : nullptr;
+    float v[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = t + i * 256;
+        float a = 0.f;
+        if (c < k) {
+            a = to_float(x[size_t(row) * k + c], T{});
+            a = round16<T>(a + (pb ? to_float(pb[c], T{}) : 0.f));
+            if (gate) a = round16<T>(a * to_float(gate[c], T{}));
+            a = round16<T>(a + (res ? to_float(res[c], T{}) : 0.f));
+            if (first && raw) raw[c] = from_float(a, T{});
+        }
+        v[i] = a;
+    }
+    float sum = 0.f;
+    sum += v[0];
+    sum += v[1];
+    const float mean = block_sum_256(sum, red) / float(k);
+    sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (t + i * 256 < k) {
+            const float d = v[i] - mean;
+            sum = __builtin_fmaf(d, d, sum);
+        }
+    const float inv = rsqrt_rn(block_sum_256(sum, red) / float(k) + eps);
+    float r[2] = {0.f, 0.f}, amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = t + i * 256;
+        if (c < k) {
+            float val = (v[i] - mean) * inv;
+            if (nw) val = val * to_float(nw[c], T{});
+            val = round16<T>(val + (nb ? to_float(nb[c], T{}) : 0.f));
+            if (scale) val = round16<T>(val * round16<T>(1.f + to_float(scale[c], T{})));
+            val = round16<T>(val + (shift ? to_float(shift[c], T{}) : 0.f));
+            r[i] = val;
+            amax = fmaxf(amax, fabsf(val));
+            if (first && normalized) normalized[size_t(row) * k + c] = from_float(val, T{});
+        }
+    }
+    const float step = quant_scale<Fmt>(block_max_256(amax, red));
+    const float recip = 1.f / step;
+    if (first && t == 0 && encoded_scales) encoded_scales[row] = step;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = t + i * 256;
+        if (c < k) {
+            const uint32_t code = encode<Fmt>(r[i] * recip);
+            if constexpr (Fmt == I8) act8[c] = uint8_t(code);
+            else act16[c] = from_float(decode_fp8(code), T{});
+            if (first && encoded) encoded[size_t(row) * k + c] = uint8_t(code);
+        }
+    }
+    __syncthreads();
+    // One channel per 32-lane group: lane l covers words c = 4l + 128j.
+    const int l32 = t & 31, channel = blockIdx.x * 8 + (t >> 5);
+    if (channel >= n) return;
+    const uint8_t *wr = w + size_t(channel) * k;
+    float result;
+    if constexpr (Fmt == I8) {
+        int acc = 0;
+        for (int c = l32 * 4; c < k; c += 128)
+            acc = __builtin_amdgcn_sdot4(*reinterpret_cast<const int *>(act8 + c),
+                                         *reinterpret_cast<const int *>(wr + c), acc, false);
+#pragma unroll
+        for (int d = 16; d; d /= 2) acc += __shfl_down(acc, d, 32);
+        result = (float(acc) * sw[channel]) * step;
+    } else {
+        float acc = 0.f;
+        for (int c = l32 * 4; c < k; c += 128) {
+            const uint32_t wq = *reinterpret_cast<const uint32_t *>(wr + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc = __builtin_fmaf(to_float(act16[c + e], T{}), decode_fp8((wq >> (8 * e)) & 0xffu),
+                                     acc);
+        }
+#pragma unroll
+        for (int d = 16; d; d /= 2) acc += __shfl_down(acc, d, 32);
+        result = (acc * sw[channel]) * step;
+    }
+    if (l32 == 0) {
+        float o = round16<T>(result);
+        o = round16<T>(o + (bias ? to_float(bias[channel], T{}) : 0.f));
+        if (act == FINISH_RELU) o = fmaxf(o, 0.f);
+        y[size_t(row) * n + channel] = from_float(o, T{});
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+// The row-quantizer variants (format x 16-bit type x items per lane x
+// group/rotation mode x vector access) compile in four parallel parts, one
+// per (family, format): QLIN_SEQ_PART names the part's launcher,
+// QLIN_SEQ_FAMILY is 0 (LayerNorm) or 1 (pointwise), QLIN_SEQ_FMT the format.
+// The build without QLIN_SEQ_PART holds the dispatchers and norm_project.
+#ifdef QLIN_SEQ_PART
+template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+void launch_one(const LayerNormQuantizeArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((layer_norm_quantize<Fmt, T, Items, Rot, G, Vec>), dim3(a.rows),
+                       dim3(kThreads), 0, s, static_cast<const uint16_t *>(a.x), a.x_rows,
+                       static_cast<const uint16_t *>(a.norm_weight),
+                       static_cast<const uint16_t *>(a.norm_bias), a.eps, a.f,
+                       static_cast<uint16_t *>(a.retained), a.rows, a.cols,
+                       static_cast<uint8_t *>(a.values), a.scales);
+}
+
+template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+void launch_one(const PointwiseQuantizeArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((pointwise_quantize<Fmt, T, Items, Rot, G, Vec>), dim3(a.rows),
+                       dim3(kThreads), 0, s, static_cast<const uint16_t *>(a.x), a.x_rows, a.e,
+                       static_cast<uint16_t *>(a.retained), a.rows, a.cols,
+                       static_cast<uint8_t *>(a.values), a.scales);
+}
+
+template <int Fmt, class T, int Items, bool Vec, class Args>
+void by_mode(const Args &a, hipStream_t s) {
+    if (a.group == 32) {
+        if (a.rotation) launch_one<Fmt, T, Items, true, 32, Vec>(a, s);
+        else launch_one<Fmt, T, Items, false, 32, Vec>(a, s);
+    } else if (a.group == 64) {
+        if (a.rotation) launch_one<Fmt, T, Items, true, 64, Vec>(a, s);
+        else launch_one<Fmt, T, Items, false, 64, Vec>(a, s);
+    } else if (a.group == 128) {
+        if (a.rotation) launch_one<Fmt, T, Items, true, 128, Vec>(a, s);
+        else launch_one<Fmt, T, Items, false, 128, Vec>(a, s);
+    } else {
+        launch_one<Fmt, T, Items, false, 0, Vec>(a, s);
+    }
+}
+
+template <int Fmt, class T, bool Vec, class Args>
+void by_items(const Args &a, hipStream_t s) {
+    // Items: 2 (cols <= 4096) or 8 (cols <= 16384) chunks of 2048 columns.
+    if (a.cols > 2 * kChunk) by_mode<Fmt, T, 8, Vec>(a, s);
+    else by_mode<Fmt, T, 2, Vec>(a, s);
+}
+#endif
+
+bool aligned16(const void *p) { return !p || reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+#ifdef QLIN_SEQ_PART
+#if QLIN_SEQ_FAMILY == 0
+using SeqArgs = LayerNormQuantizeArgs;
+#else
+using SeqArgs = PointwiseQuantizeArgs;
+#endif
+void QLIN_SEQ_PART(const SeqArgs &a, bool vec, hipStream_t s) {
+    if (a.src_type == F16) {
+        if (vec) by_items<QLIN_SEQ_FMT, f16_t, true>(a, s);
+        else by_items<QLIN_SEQ_FMT, f16_t, false>(a, s);
+    } else {
+        if (vec) by_items<QLIN_SEQ_FMT, bf16_t, true>(a, s);
+        else by_items<QLIN_SEQ_FMT, bf16_t, false>(a, s);
+    }
+}
+#else
+void launch_layer_norm_quantize(const LayerNormQuantizeArgs &a, hipStream_t stream) {
+    const qlin_norm_fusion &f = a.f;
+    const bool vec = a.cols % 8 == 0 && aligned16(a.x) && aligned16(a.norm_weight) &&
+                     aligned16(a.norm_bias) && aligned16(f.residual) &&
+                     aligned16(f.projection_bias) && aligned16(f.gate) && aligned16(f.shift) &&
+                     aligned16(f.scale) && aligned16(f.raw) && aligned16(a.retained) &&
+                     reinterpret_cast<uintptr_t>(a.values) % 8 == 0;
+    if (a.fmt == I8) launch_layer_norm_quantize_i8(a, vec, stream);
+    else launch_layer_norm_quantize_fp8(a, vec, stream);
+}
+
+void launch_pointwise_quantize(const PointwiseQuantizeArgs &a, hipStream_t stream) {
+    const qlin_epilogue &e = a.e;
+    const bool vec = a.cols % 8 == 0 && aligned16(a.x) && aligned16(e.bias) &&
+                     aligned16(e.residual) && aligned16(e.gate) && aligned16(e.condition) &&
+                     aligned16(e.raw) && aligned16(a.retained) &&
+                     reinterpret_cast<uintptr_t>(a.values) % 8 == 0;
+    if (a.fmt == I8) launch_pointwise_quantize_i8(a, vec, stream);
+    else launch_pointwise_quantize_fp8(a, vec, stream);
+}
+
+void launch_norm_linear(const NormLinearArgs &a, hipStream_t stream) {
+    dim3 grid(unsigned((a.n + 7) / 8), unsigned(a.rows)), block(256);
+#define QLIN_NL(F, T)                                                                           \
+    hipLaunchKernelGGL((norm_project<F, T>), grid, block, 0, stream,                           \
+                       static_cast<const uint16_t *>(a.x), a.f,                                \
+                       static_cast<const uint16_t *>(a.norm_weight),                           \
+                       static_cast<const uint16_t *>(a.norm_bias), a.k, a.eps,                 \
+                       static_cast<const uint8_t *>(a.w), a.sw, a.n,                           \
+                       static_cast<const uint16_t *>(a.bias), a.act,                           \
+                       static_cast<uint16_t *>(a.y), static_cast<uint16_t *>(a.normalized),   \
+                       static_cast<uint8_t *>(a.encoded), a.encoded_scales)
+    if (a.fmt == I8) { if (a.src_type == F16) QLIN_NL(I8, f16_t); else QLIN_NL(I8, bf16_t); }
+    else { if (a.src_type == F16) QLIN_NL(FP8, f16_t); else QLIN_NL(FP8, bf16_t); }
+#undef QLIN_NL
+}
+#endif  // QLIN_SEQ_PART
+
+}  // namespace qlin

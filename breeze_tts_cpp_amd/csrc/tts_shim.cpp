@@ -288,7 +288,6 @@ bool QuantizedGemm::normalized_linear(TensorView input, TensorView normalized,
                                       RowScaledView encoded) {
     // The conditions of normalized_quantized_linear (sequence_norm.cu:522-545).
     if (weight.group_size || weight.rotation_size || encoded.group_size || encoded.rotation_size ||
-        fusion.raw.data || fusion.gate.data || fusion.shift.data || fusion.scale.data ||
         fusion.source_rows || weight.values.type != format_)
         return false;
     if (epilogue.activation != ops::Activation::Identity &&
@@ -317,8 +316,26 @@ bool QuantizedGemm::normalized_linear(TensorView input, TensorView normalized,
          encoded.values.cols != k))
         throw std::invalid_argument("normalized projection quantized output mismatch");
     if (!(epsilon > 0)) throw std::invalid_argument("invalid layer normalization");
-    check(qlin_norm_linear(input.data, fusion.residual.data, fusion.projection_bias.data,
-                           norm_weight.data, norm_bias.data, code(input.type), input.rows, k,
+    const int sequences = fusion.rows_per_sequence > 0 ? input.rows / fusion.rows_per_sequence : 0;
+    for (const TensorView *v : std::initializer_list<const TensorView *>{&fusion.gate, &fusion.shift, &fusion.scale})
+        if (v->data && (v->type != input.type || v->cols != k || (v->rows != 1 && v->rows != sequences)))
+            throw std::invalid_argument("invalid normalization modulation");
+    if (fusion.raw.data && (fusion.raw.type != input.type || fusion.raw.rows != input.rows ||
+                            fusion.raw.cols != k))
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    qlin_norm_fusion f;
+    qlin_norm_fusion_init(&f);
+    f.residual = fusion.residual.data;
+    f.projection_bias = fusion.projection_bias.data;
+    f.gate = fusion.gate.data;
+    f.gate_rows = fusion.gate.rows;
+    f.shift = fusion.shift.data;
+    f.shift_rows = fusion.shift.rows;
+    f.scale = fusion.scale.data;
+    f.scale_rows = fusion.scale.rows;
+    f.raw = fusion.raw.data;
+    f.rows_per_sequence = fusion.rows_per_sequence;
+    check(qlin_norm_linear(input.data, &f, norm_weight.data, norm_bias.data, code(input.type), input.rows, k,
                            epsilon, weight.values.data, weight.scales.ptr<float>(), code(format_),
                            n, epilogue.bias.data,
                            epilogue.activation == ops::Activation::Relu ? QLIN_FINISH_RELU

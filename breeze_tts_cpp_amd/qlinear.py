@@ -48,7 +48,9 @@ class Path:
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_workspace_bytes", "qlin_gemm", "qlin_linear", "qlin_quantized_norm",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
-           "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish", "qlin_norm_linear")
+           "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish", "qlin_norm_linear",
+           "qlin_norm_fusion_init", "qlin_epilogue_init", "qlin_layer_norm_quantize",
+           "qlin_pointwise_quantize")
 
 
 def load():
@@ -89,8 +91,17 @@ def load():
     L.qlin_gemm_finish.argtypes = [ctypes.POINTER(qlin_path), P, P, P, P, P, i, P, i, i, i, i, i,
                                    i, i, i, P, sz, P]
     L.qlin_norm_linear.restype = i
-    L.qlin_norm_linear.argtypes = [P, P, P, P, P, i, i, i, ctypes.c_float, P, P, i, i, P, i, P, P,
+    L.qlin_norm_linear.argtypes = [P, P, P, P, i, i, i, ctypes.c_float, P, P, i, i, P, i, P, P,
                                    P, P, P]
+    L.qlin_norm_fusion_init.restype = None
+    L.qlin_norm_fusion_init.argtypes = [P]
+    L.qlin_epilogue_init.restype = None
+    L.qlin_epilogue_init.argtypes = [P]
+    L.qlin_layer_norm_quantize.restype = i
+    L.qlin_layer_norm_quantize.argtypes = [P, i, i, P, P, ctypes.c_float, P, P, i, i, P, P, i, i,
+                                           i, P]
+    L.qlin_pointwise_quantize.restype = i
+    L.qlin_pointwise_quantize.argtypes = [P, i, i, P, P, i, i, P, P, i, i, i, P]
     L.qlin_quantized_gated.restype = i
     L.qlin_quantized_gated.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
     _lib = L
@@ -179,30 +190,141 @@ def quantized_gated(x: torch.Tensor, fmt: int, kind: int = 0, group: int = 0, ro
     return values, scales
 
 
+class qlin_norm_fusion(ctypes.Structure):
+    """NormFusion of the LayerNorm producers (include/qlinear.h)."""
+    _fields_ = [("residual", ctypes.c_void_p), ("projection_bias", ctypes.c_void_p),
+                ("gate", ctypes.c_void_p), ("shift", ctypes.c_void_p), ("scale", ctypes.c_void_p),
+                ("gate_rows", ctypes.c_int), ("shift_rows", ctypes.c_int),
+                ("scale_rows", ctypes.c_int), ("raw", ctypes.c_void_p),
+                ("rows_per_sequence", ctypes.c_int), ("source_rows", ctypes.c_void_p)]
+
+
+class qlin_epilogue(ctypes.Structure):
+    """Dense pointwise epilogue of qlin_pointwise_quantize (include/qlinear.h)."""
+    _fields_ = [("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p),
+                ("residual_rows", ctypes.c_int), ("residual_index", ctypes.c_void_p),
+                ("value_scale", ctypes.c_float), ("output_scale", ctypes.c_float),
+                ("residual_scale", ctypes.c_float), ("activation", ctypes.c_int),
+                ("alpha", ctypes.c_float), ("raw", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("gate_rows", ctypes.c_int), ("condition", ctypes.c_void_p),
+                ("condition_rows", ctypes.c_int), ("rows_per_sequence", ctypes.c_int),
+                ("valid_rows_per_sequence", ctypes.c_int), ("input_repeat", ctypes.c_int)]
+
+
+# ops::Activation numbering (QLIN_ACT_*).
+(ACT_IDENTITY, ACT_RELU, ACT_LEAKY_RELU, ACT_SILU, ACT_GELU, ACT_GELU_TANH, ACT_MISH, ACT_TANH,
+ ACT_SIGMOID) = range(9)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _rows(t):
+    return 0 if t is None else (t.shape[0] if t.dim() == 2 else 1)
+
+
+def norm_fusion(residual=None, projection_bias=None, gate=None, shift=None, scale=None,
+                raw=None, rows_per_sequence: int = 1, source_rows=None) -> qlin_norm_fusion:
+    """A qlin_norm_fusion over device tensors (the caller keeps them alive)."""
+    f = qlin_norm_fusion()
+    load().qlin_norm_fusion_init(ctypes.byref(f))
+    f.residual, f.projection_bias = _ptr(residual), _ptr(projection_bias)
+    f.gate, f.shift, f.scale, f.raw = _ptr(gate), _ptr(shift), _ptr(scale), _ptr(raw)
+    f.gate_rows, f.shift_rows, f.scale_rows = _rows(gate), _rows(shift), _rows(scale)
+    f.rows_per_sequence = rows_per_sequence
+    f.source_rows = _ptr(source_rows)
+    return f
+
+
+def epilogue(bias=None, residual=None, residual_index=None, gate=None, condition=None, raw=None,
+             value_scale: float = 1.0, output_scale: float = 1.0, residual_scale: float = 1.0,
+             activation: int = ACT_IDENTITY, alpha: float = 0.1, rows_per_sequence: int = 1,
+             valid_rows_per_sequence: int = 0, input_repeat: int = 1) -> qlin_epilogue:
+    """A qlin_epilogue over device tensors (the caller keeps them alive)."""
+    e = qlin_epilogue()
+    load().qlin_epilogue_init(ctypes.byref(e))
+    e.bias, e.residual, e.residual_index = _ptr(bias), _ptr(residual), _ptr(residual_index)
+    e.residual_rows = _rows(residual)
+    e.gate, e.gate_rows = _ptr(gate), _rows(gate)
+    e.condition, e.condition_rows = _ptr(condition), _rows(condition)
+    e.raw = _ptr(raw)
+    e.value_scale, e.output_scale, e.residual_scale = value_scale, output_scale, residual_scale
+    e.activation, e.alpha = activation, alpha
+    e.rows_per_sequence, e.valid_rows_per_sequence = rows_per_sequence, valid_rows_per_sequence
+    e.input_repeat = input_repeat
+    return e
+
+
+def _quantized_out(rows, cols, group, device, values, scales):
+    if values is None:
+        values = torch.empty((rows, cols), dtype=torch.uint8, device=device)
+    if scales is None:
+        groups = (cols + group - 1) // group if group else 1
+        shape = (groups, rows) if group else (rows,)
+        scales = torch.empty(shape, dtype=torch.float32, device=device)
+    return values, scales
+
+
 def norm_linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int,
                 norm_weight: torch.Tensor | None = None, norm_bias: torch.Tensor | None = None,
-                residual: torch.Tensor | None = None, projection_bias: torch.Tensor | None = None,
-                bias: torch.Tensor | None = None, activation: int = 0, eps: float = 1e-5,
-                normalized: torch.Tensor | None = None, encoded: tuple | None = None,
-                out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+                fusion: qlin_norm_fusion | None = None, bias: torch.Tensor | None = None,
+                activation: int = 0, eps: float = 1e-5, normalized: torch.Tensor | None = None,
+                encoded: tuple | None = None, out: torch.Tensor | None = None,
+                stream=None) -> torch.Tensor:
     """LayerNorm -> per-token quantization -> quantized GEMV (qlin_norm_linear),
-    hidden k <= 512. `encoded` = (codes uint8 [rows, k], scales f32 [rows])."""
+    hidden k <= 512. `fusion` from norm_fusion(); `encoded` = (codes uint8
+    [rows, k], scales f32 [rows])."""
     if x.dim() != 2 or not x.is_contiguous() or x.dtype not in _TYPES:
         raise ValueError("norm_linear expects a dense 2-D bf16/f16 input")
     rows, k = x.shape
     n = wq.shape[0]
     if out is None:
         out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
-
-    def ptr(t):
-        return None if t is None else t.data_ptr()
     codes, scales = encoded if encoded is not None else (None, None)
-    _check(load().qlin_norm_linear(x.data_ptr(), ptr(residual), ptr(projection_bias),
-                                   ptr(norm_weight), ptr(norm_bias), _TYPES[x.dtype], rows, k,
-                                   float(eps), wq.data_ptr(), sw.data_ptr(), fmt, n, ptr(bias),
-                                   activation, out.data_ptr(), ptr(normalized), ptr(codes),
-                                   ptr(scales), _stream(stream)))
+    _check(load().qlin_norm_linear(x.data_ptr(), None if fusion is None else ctypes.byref(fusion),
+                                   _ptr(norm_weight), _ptr(norm_bias), _TYPES[x.dtype], rows, k,
+                                   float(eps), wq.data_ptr(), sw.data_ptr(), fmt, n, _ptr(bias),
+                                   activation, out.data_ptr(), _ptr(normalized), _ptr(codes),
+                                   _ptr(scales), _stream(stream)))
     return out
+
+
+def layer_norm_quantize(x: torch.Tensor, fmt: int, norm_weight: torch.Tensor | None = None,
+                        norm_bias: torch.Tensor | None = None, eps: float = 1e-5,
+                        fusion: qlin_norm_fusion | None = None, rows: int | None = None,
+                        retained: torch.Tensor | None = None, group: int = 0, rotation: int = 0,
+                        values=None, scales=None, stream=None):
+    """LayerNorm -> row quantization (qlin_layer_norm_quantize). Returns
+    (codes uint8 [rows, cols], scales)."""
+    if x.dim() != 2 or not x.is_contiguous() or x.dtype not in _TYPES:
+        raise ValueError("layer_norm_quantize expects a dense 2-D bf16/f16 input")
+    x_rows, cols = x.shape
+    rows = x_rows if rows is None else rows
+    values, scales = _quantized_out(rows, cols, group, x.device, values, scales)
+    _check(load().qlin_layer_norm_quantize(
+        x.data_ptr(), x_rows, _TYPES[x.dtype], _ptr(norm_weight), _ptr(norm_bias), float(eps),
+        None if fusion is None else ctypes.byref(fusion), _ptr(retained), rows, cols,
+        values.data_ptr(), scales.data_ptr(), fmt, group, rotation, _stream(stream)))
+    return values, scales
+
+
+def pointwise_quantize(x: torch.Tensor, fmt: int, epilogue: qlin_epilogue | None = None,
+                       rows: int | None = None, retained: torch.Tensor | None = None,
+                       group: int = 0, rotation: int = 0, values=None, scales=None, stream=None):
+    """Pointwise epilogue -> row quantization (qlin_pointwise_quantize). Returns
+    (codes uint8 [rows, cols], scales)."""
+    if x.dim() != 2 or not x.is_contiguous() or x.dtype not in _TYPES:
+        raise ValueError("pointwise_quantize expects a dense 2-D bf16/f16 input")
+    x_rows, cols = x.shape
+    if rows is None:
+        rows = x_rows * (epilogue.input_repeat if epilogue is not None else 1)
+    values, scales = _quantized_out(rows, cols, group, x.device, values, scales)
+    _check(load().qlin_pointwise_quantize(
+        x.data_ptr(), x_rows, _TYPES[x.dtype], None if epilogue is None else ctypes.byref(epilogue),
+        _ptr(retained), rows, cols, values.data_ptr(), scales.data_ptr(), fmt, group, rotation,
+        _stream(stream)))
+    return values, scales
 
 
 def plan(rows: int, N: int, K: int, fmt: int, input_group: int = 0, weight_group: int = 0) -> Path:

@@ -157,8 +157,8 @@ int qlin_quantized_gated(const void *input, int src_type, int rows, int width, i
                          void *values, float *scales, int fmt, int group, int rotation,
                          qlin_stream_t stream);
 
-/* Finish activations (tts::ops::Activation subset of the quantized finish;
- * qlin_norm_linear accepts NONE and RELU). */
+/* Finish activations of the quantized GEMM (the ops::Activation subset of the
+ * reference's quantized finish; qlin_norm_linear accepts NONE and RELU). */
 enum { QLIN_FINISH_NONE = 0, QLIN_FINISH_RELU = 1, QLIN_FINISH_GELU_TANH = 2 };
 
 /* qlin_gemm followed, in the same epilogue, by the reference's finish on the
@@ -191,20 +191,119 @@ int qlin_linear_packed(const qlin_path *path, const void *x, int ld, int src_typ
                        int fmt, int out_type, int input_group, int weight_group, int rotation,
                        void *workspace, size_t workspace_bytes, qlin_stream_t stream);
 
+/* Input fusions of a LayerNorm (the reference's ops::NormFusion,
+ * src/ops/sequence.h:55-59; arithmetic of NormRow, sequence_norm.cu:40-53).
+ * All tensors are dense, in the input's 16-bit type:
+ *   v = s16(s16(s16(x + projection_bias) * gate) + residual)   (each optional)
+ *   u = s16(s16(s16((v - mean) * inv * weight + bias) * s16(1 + scale)) + shift)
+ * with (v - mean) * inv and * weight rounded separately to fp32.
+ *   residual        [x_rows, cols]; projection_bias [cols]
+ *   gate/shift/scale [1 or rows / rows_per_sequence, cols] (1 = broadcast),
+ *                   indexed by the source row's sequence
+ *   raw             [rows, cols] receives v, or NULL
+ *   source_rows     output row r normalizes input row source_rows[r]; a
+ *                   source outside [0, x_rows) gives NaN outputs and unit
+ *                   scales (qlin_layer_norm_quantize only; excludes gate,
+ *                   shift and scale) */
+typedef struct qlin_norm_fusion {
+    const void *residual;
+    const void *projection_bias;
+    const void *gate;
+    const void *shift;
+    const void *scale;
+    int gate_rows, shift_rows, scale_rows;
+    void *raw;
+    int rows_per_sequence;
+    const int *source_rows;
+} qlin_norm_fusion;
+
+/* Activations of the reference's ops::Activation (src/ops/activation.h:4),
+ * same numbering. */
+enum {
+    QLIN_ACT_IDENTITY = 0,
+    QLIN_ACT_RELU = 1,
+    QLIN_ACT_LEAKY_RELU = 2,
+    QLIN_ACT_SILU = 3,
+    QLIN_ACT_GELU = 4,
+    QLIN_ACT_GELU_TANH = 5,
+    QLIN_ACT_MISH = 6,
+    QLIN_ACT_TANH = 7,
+    QLIN_ACT_SIGMOID = 8
+};
+
+/* The reference's dense pointwise epilogue (ops::Epilogue, src/ops/sequence.h:
+ * 8-27, without the packed/indirect addressing; arithmetic of Finish::apply,
+ * ops/kernels/sequence/sequence_internal.cuh:52-74). Per element of output
+ * row r, sequence b = r / rows_per_sequence:
+ *   masked (valid_rows_per_sequence > 0 and r % rows_per_sequence >=
+ *   valid_rows_per_sequence): raw = 0, result 0; otherwise
+ *   v = s16(x + bias);  v = s16(v * gate[b])              (gate optional)
+ *   v = s16(fma(value_scale, v, residual_scale * skip))    skip = residual row
+ *       residual_index[r] (or r), 0 when absent or negative, NaN past the end
+ *   v = s16(v + condition[b]);  raw = v;                   (both optional)
+ *   result = s16(act(s16(v * output_scale), alpha)).
+ * x row r reads input row r / input_repeat (row 0 when x_rows == 1). gate and
+ * condition have 1 (broadcast) or rows / rows_per_sequence rows. All 16-bit
+ * tensors are dense, in the input's type. */
+typedef struct qlin_epilogue {
+    const void *bias;
+    const void *residual;
+    int residual_rows;
+    const int *residual_index;
+    float value_scale, output_scale, residual_scale;
+    int activation;
+    float alpha;
+    void *raw;
+    const void *gate;
+    int gate_rows;
+    const void *condition;
+    int condition_rows;
+    int rows_per_sequence, valid_rows_per_sequence, input_repeat;
+} qlin_epilogue;
+
+/* The reference's defaults: no tensors, scales 1, identity, alpha 0.1,
+ * rows_per_sequence 1, input_repeat 1. */
+void qlin_norm_fusion_init(qlin_norm_fusion *fusion);
+void qlin_epilogue_init(qlin_epilogue *epilogue);
+
 /* LayerNorm -> per-token quantization -> quantized GEMV in one launch, for
- * hidden sizes k <= 512 (the reference's fused small-M projection of the
- * auxiliary models):
- *   v = s16(s16(x + projection_bias) + residual)            (both optional)
- *   u = s16((v - mean) * inv * norm_weight + norm_bias),    inv = 1/sqrt(var + eps)
+ * hidden sizes k <= 512 (the reference's normalized_quantized_linear,
+ * ops/kernels/sequence/sequence_norm.cu:216-390,518-575, chosen by
+ * QuantizedGemm::normalized_linear, ops/cuda/quantization.cpp:479-494):
+ *   u = LayerNorm of the fused input (qlin_norm_fusion; fusion may be NULL;
+ *       source_rows is not accepted)
  *   u quantized per token (fmt); optionally written to `normalized` (16-bit)
  *   and `encoded` / `encoded_scales` (codes and per-token scales);
  *   y[r, c] = s16(act(s16(s16((acc * sw[c]) * sx[r]) + bias[c]))), act none or ReLU.
  * w: int8/e4m3 [n, k] with per-channel scales sw; k % 4 == 0. */
-int qlin_norm_linear(const void *x, const void *residual, const void *projection_bias,
-                     const void *norm_weight, const void *norm_bias, int src_type, int rows, int k,
-                     float eps, const void *w, const float *sw, int fmt, int n, const void *bias,
+int qlin_norm_linear(const void *x, const qlin_norm_fusion *fusion, const void *norm_weight,
+                     const void *norm_bias, int src_type, int rows, int k, float eps,
+                     const void *w, const float *sw, int fmt, int n, const void *bias,
                      int activation, void *y, void *normalized, void *encoded,
                      float *encoded_scales, qlin_stream_t stream);
+
+/* LayerNorm -> row quantization (the reference's layer_norm_quantize,
+ * ops/kernels/sequence/sequence_norm.cu:65-200,412-440): u as above for each
+ * of `rows` output rows (x has x_rows rows; x_rows == rows unless
+ * fusion->source_rows is given), optionally stored to `retained` [rows, cols],
+ * then quantized as qlin_row_quantize (per token, or K groups with optional
+ * H128 rotation; rotation requires a group). 1 <= cols <= 16384. */
+int qlin_layer_norm_quantize(const void *x, int x_rows, int src_type, const void *norm_weight,
+                             const void *norm_bias, float eps, const qlin_norm_fusion *fusion,
+                             void *retained, int rows, int cols, void *values, float *scales,
+                             int fmt, int group, int rotation, qlin_stream_t stream);
+
+/* Pointwise epilogue -> row quantization (the reference's pointwise_quantize,
+ * ops/kernels/sequence/sequence_pointwise.cu:149-260,325-357, used by
+ * ops::linear to emit the next layer's quantized input, ops/linear.cpp:71-78):
+ * the qlin_epilogue result of each element of x (x_rows * input_repeat ==
+ * rows), optionally stored to `retained` [rows, cols], quantized as
+ * qlin_row_quantize (rotation requires a group). epilogue may be NULL
+ * (identity). 1 <= cols <= 16384. */
+int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
+                            const qlin_epilogue *epilogue, void *retained, int rows, int cols,
+                            void *values, float *scales, int fmt, int group, int rotation,
+                            qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -146,8 +146,8 @@ struct Epilogue {
     Activation activation = Activation::Identity;
 };
 // Fusions of a normalization's input (reference ops/sequence.h:55-59). The
-// fused normalized projection supports residual and projection_bias; a
-// request using the others is declined (normalized_linear returns false).
+// fused normalized projection declines source_rows (normalized_linear
+// returns false), as the reference's does.
 struct NormFusion {
     TensorView residual, projection_bias, raw, gate, shift, scale;
     int rows_per_sequence = 1;

@@ -83,8 +83,19 @@ def lib():
         L.orc_cub_sum256.restype = ctypes.c_float
         L.orc_cub_sum256.argtypes = [P]
         L.orc_norm_linear.restype = i
-        L.orc_norm_linear.argtypes = [P, P, P, P, P, i, i, i, ctypes.c_float, P, P, i, i, P, i, P,
+        L.orc_norm_linear.argtypes = [P, P, P, P, i, i, i, ctypes.c_float, P, P, i, i, P, i, P,
                                       P, P, P]
+        L.orc_norm_rows.restype = i
+        L.orc_norm_rows.argtypes = [P, i, i, i, i, P, P, ctypes.c_float, P, P]
+        L.orc_layer_norm_quantize.restype = i
+        L.orc_layer_norm_quantize.argtypes = [P, i, i, P, P, ctypes.c_float, P, P, i, i, P, P, i,
+                                              i, i]
+        L.orc_act.restype = ctypes.c_float
+        L.orc_act.argtypes = [ctypes.c_float, i, ctypes.c_float]
+        L.orc_gelu_tanh_contracted.restype = ctypes.c_float
+        L.orc_gelu_tanh_contracted.argtypes = [ctypes.c_float]
+        L.orc_pointwise_quantize.restype = i
+        L.orc_pointwise_quantize.argtypes = [P, i, i, P, P, i, i, P, P, i, i, i]
         L.orc_pack_weights.restype = i
         L.orc_pack_weights.argtypes = [P, i, i, P]
         L.orc_cpu_qlinear.restype = i
@@ -322,25 +333,165 @@ def cub_sum256(v: np.ndarray) -> float:
     return lib().orc_cub_sum256(_p(v))
 
 
-def norm_linear(x_bits, wq, sw, fmt: int, norm_weight=None, norm_bias=None, residual=None,
-                projection_bias=None, bias=None, act: int = 0, eps: float = 1e-5,
-                src_type: int = BF16):
-    """Returns (y bits [rows, n], normalized bits [rows, k], codes [rows, k], scales [rows])."""
+class NormFusion(ctypes.Structure):
+    """orc_norm_fusion (the library's qlin_norm_fusion layout)."""
+    _fields_ = [("residual", ctypes.c_void_p), ("projection_bias", ctypes.c_void_p),
+                ("gate", ctypes.c_void_p), ("shift", ctypes.c_void_p), ("scale", ctypes.c_void_p),
+                ("gate_rows", ctypes.c_int), ("shift_rows", ctypes.c_int),
+                ("scale_rows", ctypes.c_int), ("raw", ctypes.c_void_p),
+                ("rows_per_sequence", ctypes.c_int), ("source_rows", ctypes.c_void_p)]
+
+
+class Epilogue(ctypes.Structure):
+    """orc_epilogue (the library's qlin_epilogue layout)."""
+    _fields_ = [("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p),
+                ("residual_rows", ctypes.c_int), ("residual_index", ctypes.c_void_p),
+                ("value_scale", ctypes.c_float), ("output_scale", ctypes.c_float),
+                ("residual_scale", ctypes.c_float), ("activation", ctypes.c_int),
+                ("alpha", ctypes.c_float), ("raw", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("gate_rows", ctypes.c_int), ("condition", ctypes.c_void_p),
+                ("condition_rows", ctypes.c_int), ("rows_per_sequence", ctypes.c_int),
+                ("valid_rows_per_sequence", ctypes.c_int), ("input_repeat", ctypes.c_int)]
+
+
+def _u16(a):
+    return None if a is None else np.ascontiguousarray(a, np.uint16)
+
+
+def _opt(a):
+    return None if a is None else _p(a)
+
+
+def _fusion(keep, rows, cols, residual=None, projection_bias=None, gate=None, shift=None,
+            scale=None, rows_per_sequence=1, source_rows=None, raw=False):
+    """A NormFusion over numpy arrays (kept alive in `keep`); returns
+    (fusion, raw array or None)."""
+    f = NormFusion()
+    f.rows_per_sequence = rows_per_sequence
+    for name, a in (("residual", residual), ("projection_bias", projection_bias), ("gate", gate),
+                    ("shift", shift), ("scale", scale)):
+        a = _u16(a)
+        if a is not None:
+            keep.append(a)
+            setattr(f, name, _p(a).value)
+            if name in ("gate", "shift", "scale"):
+                setattr(f, name + "_rows", a.shape[0] if a.ndim == 2 else 1)
+    if source_rows is not None:
+        sr = np.ascontiguousarray(source_rows, np.int32)
+        keep.append(sr)
+        f.source_rows = _p(sr).value
+    raw_out = None
+    if raw:
+        raw_out = np.zeros((rows, cols), np.uint16)
+        keep.append(raw_out)
+        f.raw = _p(raw_out).value
+    return f, raw_out
+
+
+def norm_linear(x_bits, wq, sw, fmt: int, norm_weight=None, norm_bias=None, bias=None,
+                act: int = 0, eps: float = 1e-5, src_type: int = BF16, raw: bool = False,
+                **fusion):
+    """LayerNorm (NormFusion keywords: residual, projection_bias, gate, shift,
+    scale, rows_per_sequence) -> quant -> GEMV. Returns (y bits [rows, n],
+    normalized bits [rows, k], codes [rows, k], scales [rows], raw or None)."""
     x = np.ascontiguousarray(x_bits, np.uint16)
     rows, k = x.shape
     wq = np.ascontiguousarray(wq, np.uint8)
     sw = np.ascontiguousarray(sw, np.float32)
     n = wq.shape[0]
-    opt = [None if a is None else np.ascontiguousarray(a, np.uint16)
-           for a in (residual, projection_bias, norm_weight, norm_bias, bias)]
+    keep = []
+    f, raw_out = _fusion(keep, rows, k, raw=raw, **fusion)
+    nw, nb, b = _u16(norm_weight), _u16(norm_bias), _u16(bias)
     y = np.zeros((rows, n), np.uint16)
     nrm = np.zeros((rows, k), np.uint16)
     enc = np.zeros((rows, k), np.uint8)
     esc = np.zeros(rows, np.float32)
-    P = [None if a is None else _p(a) for a in opt]
-    rc = lib().orc_norm_linear(_p(x), P[0], P[1], P[2], P[3], src_type, rows, k, float(eps),
-                               _p(wq), _p(sw), fmt, n, P[4], act, _p(y), _p(nrm), _p(enc),
-                               _p(esc))
+    rc = lib().orc_norm_linear(_p(x), ctypes.byref(f), _opt(nw), _opt(nb), src_type, rows, k,
+                               float(eps), _p(wq), _p(sw), fmt, n, _opt(b), act, _p(y), _p(nrm),
+                               _p(enc), _p(esc))
     if rc:
         raise ValueError("oracle: unsupported normalized linear shape")
-    return y, nrm, enc, esc
+    return y, nrm, enc, esc, raw_out
+
+
+def norm_rows(x_bits, norm_weight=None, norm_bias=None, eps: float = 1e-5, rows=None,
+              src_type: int = BF16, **fusion):
+    """The LayerNorm rows alone (16-bit bits [rows, cols])."""
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    x_rows, cols = x.shape
+    rows = x_rows if rows is None else rows
+    keep = []
+    f, _ = _fusion(keep, rows, cols, **fusion)
+    nw, nb = _u16(norm_weight), _u16(norm_bias)
+    u = np.zeros((rows, cols), np.uint16)
+    lib().orc_norm_rows(_p(x), x_rows, src_type, rows, cols, _opt(nw), _opt(nb), float(eps),
+                        ctypes.byref(f), _p(u))
+    return u
+
+
+def layer_norm_quantize(x_bits, fmt: int, norm_weight=None, norm_bias=None, eps: float = 1e-5,
+                        rows=None, group: int = 0, rotation: int = 0, src_type: int = BF16,
+                        raw: bool = False, **fusion):
+    """Returns (codes [rows, cols], scales, retained bits [rows, cols], raw or None)."""
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    x_rows, cols = x.shape
+    rows = x_rows if rows is None else rows
+    keep = []
+    f, raw_out = _fusion(keep, rows, cols, raw=raw, **fusion)
+    nw, nb = _u16(norm_weight), _u16(norm_bias)
+    q = np.zeros((rows, cols), np.uint8)
+    groups = (cols + group - 1) // group if group else 1
+    sc = np.zeros((groups, rows) if group else (rows,), np.float32)
+    ret = np.zeros((rows, cols), np.uint16)
+    rc = lib().orc_layer_norm_quantize(_p(x), x_rows, src_type, _opt(nw), _opt(nb), float(eps),
+                                       ctypes.byref(f), _p(ret), rows, cols, _p(q), _p(sc), fmt,
+                                       group, rotation)
+    if rc:
+        raise ValueError("oracle: unsupported layer norm quantize layout")
+    return q, sc, ret, raw_out
+
+
+def act(x: float, kind: int, alpha: float = 0.1) -> float:
+    """ops::activate (numbering of ops::Activation)."""
+    return lib().orc_act(float(x), kind, float(alpha))
+
+
+def pointwise_quantize(x_bits, fmt: int, rows=None, group: int = 0, rotation: int = 0,
+                       src_type: int = BF16, raw: bool = False, bias=None, residual=None,
+                       residual_index=None, gate=None, condition=None, value_scale=1.0,
+                       output_scale=1.0, residual_scale=1.0, activation=0, alpha=0.1,
+                       rows_per_sequence=1, valid_rows_per_sequence=0, input_repeat=1):
+    """Returns (codes [rows, cols], scales, retained bits [rows, cols], raw or None)."""
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    x_rows, cols = x.shape
+    rows = x_rows * input_repeat if rows is None else rows
+    keep = []
+    e = Epilogue(value_scale=value_scale, output_scale=output_scale,
+                 residual_scale=residual_scale, activation=activation, alpha=alpha,
+                 rows_per_sequence=rows_per_sequence,
+                 valid_rows_per_sequence=valid_rows_per_sequence, input_repeat=input_repeat)
+    for name, a in (("bias", bias), ("residual", residual), ("gate", gate),
+                    ("condition", condition)):
+        a = _u16(a)
+        if a is not None:
+            keep.append(a)
+            setattr(e, name, _p(a).value)
+            if name != "bias":
+                setattr(e, name + "_rows", a.shape[0] if a.ndim == 2 else 1)
+    if residual_index is not None:
+        ri = np.ascontiguousarray(residual_index, np.int32)
+        keep.append(ri)
+        e.residual_index = _p(ri).value
+    raw_out = None
+    if raw:
+        raw_out = np.zeros((rows, cols), np.uint16)
+        e.raw = _p(raw_out).value
+    q = np.zeros((rows, cols), np.uint8)
+    groups = (cols + group - 1) // group if group else 1
+    sc = np.zeros((groups, rows) if group else (rows,), np.float32)
+    ret = np.zeros((rows, cols), np.uint16)
+    rc = lib().orc_pointwise_quantize(_p(x), x_rows, src_type, ctypes.byref(e), _p(ret), rows,
+                                      cols, _p(q), _p(sc), fmt, group, rotation)
+    if rc:
+        raise ValueError("oracle: unsupported pointwise quantize layout")
+    return q, sc, ret, raw_out

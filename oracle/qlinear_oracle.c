@@ -313,22 +313,31 @@ int orc_quantized_gated(const uint16_t *input, int src_type, int rows, int width
     return status;
 }
 
+/* tanh-GeLU as the reference's activation.cuh:15 compiles with FMA
+ * contraction (the GEMM epilogue and the pointwise finish TUs): inner =
+ * fma((0.044715x)x, x, x); tanh rounded once from fp64 (the reference uses
+ * cutlass::fast_tanh). */
+float orc_gelu_tanh_contracted(float x) {
+    float inner = fmaf((0.044715f * x) * x, x, x);
+    float t = (float)tanh((double)(0.7978845608028654f * inner));
+    return (0.5f * x) * (1.f + t);
+}
+
 /* ---------------------------------------------------------------- finish */
 /* The finish of a quantized linear on its stored 16-bit result y (the
  * reference's pointwise Finish::apply, ops/kernels/sequence/sequence_internal.cuh:61-73
  * with value/output scale 1, activations of ops/kernels/common/activation.cuh:7,14):
- * y' = s16(act(s16(y + bias[n]))), act 0 none, 1 ReLU, 2 tanh-GeLU (tanh
- * rounded once from fp64; the reference uses cutlass::fast_tanh). In place. */
+ * y' = s16(act(s16(y + bias[n]))), act 0 none, 1 ReLU, 2 tanh-GeLU (the
+ * contracted form above). An absent bias adds 0 as the reference's View::get
+ * does. In place. */
 void orc_finish(uint16_t *y, const uint16_t *bias, int M, int N, int act, int type) {
     for (int m = 0; m < M; ++m)
         for (int n = 0; n < N; ++n) {
             float v = load_src(y, type, (size_t)m * N + n);
-            if (bias) {
-                uint16_t h = store_out(v + load_src(bias, type, n), type);
-                v = load_src(&h, type, 0);
-            }
+            uint16_t h = store_out(v + (bias ? load_src(bias, type, n) : 0.f), type);
+            v = load_src(&h, type, 0);
             if (act == 1) v = fmaxf(v, 0.f);
-            else if (act == 2) v = orc_activate(v, 1);
+            else if (act == 2) v = orc_gelu_tanh_contracted(v);
             y[(size_t)m * N + n] = store_out(v, type);
         }
 }
@@ -351,50 +360,195 @@ float orc_cub_sum256(const float *v) {
     return total;
 }
 
-/* normalized_quantized_linear / norm_project_kernel<T, QuantProjection>
- * (ops/kernels/sequence/sequence_norm.cu:29-53 NormRow load/transform,
- * :260-390 kernel, :518-575 host) with the fusions residual and
- * projection_bias, no gate/scale/shift, Finish with bias and ReLU/identity.
- * Thread t holds columns t and t+256 (k <= 512). The 1/sqrt is rounded once
- * (the reference's rsqrtf is within 2 ulp). INT8 dot products are exact; FP8
- * ones follow the reference order: lane l of a warp sums words c = 4l + 128j
- * with fmaf over the 4 bytes, then a shfl-down tree 16..1.
- * Outputs: y [rows, n]; normalized [rows, k] and encoded/escales optional. */
-int orc_norm_linear(const uint16_t *x, const uint16_t *residual, const uint16_t *pbias,
-                    const uint16_t *nw, const uint16_t *nb, int type, int rows, int k, float eps,
-                    const uint8_t *w, const float *sw, int fmt, int n, const uint16_t *bias, int act,
-                    uint16_t *y, uint16_t *normalized, uint8_t *encoded, float *escales) {
-    if (k < 4 || k % 4 || k > 512) return -1;
-    float v[512], part[256], r[512], a[512];
-    for (int row = 0; row < rows; ++row) {
-        for (int c = 0; c < 512; ++c) {
-            float val = 0.f;
-            if (c < k) {
-                val = load_src(x, type, (size_t)row * k + c);
-                uint16_t h = store_out(val + (pbias ? load_src(pbias, type, c) : 0.f), type);
-                val = load_src(&h, type, 0);
-                h = store_out(val + (residual ? load_src(residual, type, (size_t)row * k + c) : 0.f), type);
-                val = load_src(&h, type, 0);
-            }
-            v[c] = val;
+/* NormFusion / Epilogue layouts (the library's qlin_norm_fusion and
+ * qlin_epilogue, restating ops::NormFusion, ops/sequence.h:55-59, and the
+ * dense part of ops::Epilogue, ops/sequence.h:8-27). */
+typedef struct {
+    const uint16_t *residual, *projection_bias, *gate, *shift, *scale;
+    int gate_rows, shift_rows, scale_rows;
+    uint16_t *raw;
+    int rows_per_sequence;
+    const int *source_rows;
+} orc_norm_fusion;
+
+typedef struct {
+    const uint16_t *bias, *residual;
+    int residual_rows;
+    const int *residual_index;
+    float value_scale, output_scale, residual_scale;
+    int activation;
+    float alpha;
+    uint16_t *raw;
+    const uint16_t *gate;
+    int gate_rows;
+    const uint16_t *condition;
+    int condition_rows;
+    int rows_per_sequence, valid_rows_per_sequence, input_repeat;
+} orc_epilogue;
+
+static inline float r16(float v, int type) { uint16_t h = store_out(v, type); return load_src(&h, type, 0); }
+/* View::get of a [rows, cols] tensor (row 0 when it has one row), 0 when absent
+ * (ops/kernels/sequence/sequence_internal.cuh:21-25, sequence_norm.cu:18-27). */
+static inline float view_get(const uint16_t *p, int rows, int r, int cols, int c, int type) {
+    return p ? load_src(p, type, (size_t)(rows == 1 ? 0 : r) * cols + c) : 0.f;
+}
+
+/* LayerNorm rows with NormFusion (NormRow::load / transform,
+ * sequence_norm.cu:40-53, statistics of norm_kernel :84-117 and
+ * norm_project_kernel :272-292): thread t of 256 sums columns t, t+256, ...
+ * in order; the partials reduce in cub::BlockReduce order; mean = sum/cols;
+ * the variance partial is fma(d, d, sum) (the TU contracts sum += d*d);
+ * inv = 1/sqrt(var/cols + eps) rounded once. u [rows, cols] receives the
+ * normalized 16-bit rows; an out-of-range source row gives NaN. raw (from
+ * f->raw) receives v. Returns 0. */
+int orc_norm_rows(const uint16_t *x, int x_rows, int type, int rows, int cols,
+                  const uint16_t *nw, const uint16_t *nb, float eps, const orc_norm_fusion *f,
+                  uint16_t *u) {
+    float *v = (float *)malloc(sizeof(float) * (size_t)cols);
+    if (!v) return -1;
+    float part[256];
+    for (int out = 0; out < rows; ++out) {
+        int row = f->source_rows ? f->source_rows[out] : out;
+        if (row < 0 || row >= x_rows) {
+            for (int c = 0; c < cols; ++c) u[(size_t)out * cols + c] = store_out(NAN, type);
+            continue;
         }
-        for (int t = 0; t < 256; ++t) { float sum = 0.f; sum += v[t]; sum += v[t + 256]; part[t] = sum; }
-        float mean = orc_cub_sum256(part) / (float)k;
+        int seq = row / f->rows_per_sequence;
+        for (int c = 0; c < cols; ++c) {
+            float a = r16(load_src(x, type, (size_t)row * cols + c) +
+                          view_get(f->projection_bias, 1, 0, cols, c, type), type);
+            if (f->gate) a = r16(a * view_get(f->gate, f->gate_rows, seq, cols, c, type), type);
+            a = r16(a + view_get(f->residual, x_rows, row, cols, c, type), type);
+            v[c] = a;
+            if (f->raw) f->raw[(size_t)out * cols + c] = store_out(a, type);
+        }
         for (int t = 0; t < 256; ++t) {
             float sum = 0.f;
-            for (int i = 0; i < 2; ++i)
-                if (t + 256 * i < k) { float d = v[t + 256 * i] - mean; sum += d * d; }
+            for (int c = t; c < cols; c += 256) sum += v[c];
             part[t] = sum;
         }
-        float inv = orc_rsqrt_rn(orc_cub_sum256(part) / (float)k + eps);
-        float amax = 0.f;
-        for (int c = 0; c < k; ++c) {
+        float mean = orc_cub_sum256(part) / (float)cols;
+        for (int t = 0; t < 256; ++t) {
+            float sum = 0.f;
+            for (int c = t; c < cols; c += 256) { float d = v[c] - mean; sum = fmaf(d, d, sum); }
+            part[t] = sum;
+        }
+        float inv = orc_rsqrt_rn(orc_cub_sum256(part) / (float)cols + eps);
+        for (int c = 0; c < cols; ++c) {
             float val = (v[c] - mean) * inv;
             if (nw) val = val * load_src(nw, type, c);
-            uint16_t h = store_out(val + (nb ? load_src(nb, type, c) : 0.f), type);
-            r[c] = load_src(&h, type, 0);
+            val = r16(val + (nb ? load_src(nb, type, c) : 0.f), type);
+            if (f->scale)
+                val = r16(val * r16(1.f + view_get(f->scale, f->scale_rows, seq, cols, c, type), type), type);
+            val = r16(val + view_get(f->shift, f->shift_rows, seq, cols, c, type), type);
+            u[(size_t)out * cols + c] = store_out(val, type);
+        }
+    }
+    free(v);
+    return 0;
+}
+
+/* layer_norm_quantize (sequence_norm.cu:65-200,412-440): the LayerNorm rows
+ * above, optionally retained, quantized by the row quantizer (RowOutput
+ * store/store_group, ops/kernels/quant/quant_output.cuh). A NaN row (bad
+ * source) gets scales 1 and the codes of NaN, as the row quantizer gives. */
+int orc_layer_norm_quantize(const uint16_t *x, int x_rows, int type, const uint16_t *nw,
+                            const uint16_t *nb, float eps, const orc_norm_fusion *f,
+                            uint16_t *retained, int rows, int cols, uint8_t *q, float *scales,
+                            int fmt, int group, int rotation) {
+    if (rotation && !group) return -1;
+    uint16_t *u = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)rows * cols);
+    if (!u) return -1;
+    orc_norm_rows(x, x_rows, type, rows, cols, nw, nb, eps, f, u);
+    int status = orc_quantize_rows(u, type, cols, rows, cols, fmt, group, rotation, q, scales);
+    if (retained) memcpy(retained, u, sizeof(uint16_t) * (size_t)rows * cols);
+    free(u);
+    return status;
+}
+
+/* ops::activate (ops/kernels/common/activation.cuh:5-26), Activation
+ * numbering of ops/activation.h:4. Transcendentals are evaluated in fp64 and
+ * rounded once to fp32 at the points the reference rounds its fp32 library
+ * calls (expf, erff, log1pf, tanhf, cutlass::fast_tanh approximate them);
+ * tanh-GeLU's inner term is contracted as the pointwise TU compiles it. */
+float orc_act(float x, int kind, float alpha) {
+    switch (kind) {
+    case 1: return fmaxf(x, 0.f);
+    case 2: return x >= 0.f ? x : x * alpha;
+    case 3: return x / (1.f + (float)exp(-(double)x));
+    case 4: return (0.5f * x) * (1.f + (float)erf((double)(x * 0.7071067811865475f)));
+    case 5: return orc_gelu_tanh_contracted(x);
+    case 6: {
+        float sp = x > 20.f ? x : (float)log1p((double)(float)exp((double)x));
+        return x * (float)tanh((double)sp);
+    }
+    case 7: return (float)tanh((double)x);
+    case 8: return 1.f / (1.f + (float)exp(-(double)x));
+    default: return x;
+    }
+}
+
+/* pointwise_quantize (sequence_pointwise.cu:149-260,325-357) with the dense
+ * Finish::apply (ops/kernels/sequence/sequence_internal.cuh:52-74), per
+ * element of output row r (x row r / input_repeat, row 0 when x_rows == 1):
+ * masked rows give raw 0 and 0; else v = s16(x + bias); v = s16(v * gate[b]);
+ * v = s16(fma(value_scale, v, residual_scale * skip)) (the TU contracts
+ * value_scale*v + scale*skip on its first product); v = s16(v + condition[b]);
+ * raw = v; out = s16(act(s16(v * output_scale))). Then the row quantizer. */
+int orc_pointwise_quantize(const uint16_t *x, int x_rows, int type, const orc_epilogue *e,
+                           uint16_t *retained, int rows, int cols, uint8_t *q, float *scales,
+                           int fmt, int group, int rotation) {
+    if (rotation && !group) return -1;
+    uint16_t *o = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)rows * cols);
+    if (!o) return -1;
+    for (int r = 0; r < rows; ++r) {
+        int masked = e->valid_rows_per_sequence &&
+                     r % e->rows_per_sequence >= e->valid_rows_per_sequence;
+        int seq = r / e->rows_per_sequence, xr = x_rows == 1 ? 0 : r / e->input_repeat;
+        int rr = e->residual_index ? e->residual_index[r] : r;
+        for (int c = 0; c < cols; ++c) {
+            float value = 0.f;
+            if (!masked) {
+                value = r16(load_src(x, type, (size_t)xr * cols + c) + view_get(e->bias, 1, 0, cols, c, type), type);
+                if (e->gate) value = r16(value * view_get(e->gate, e->gate_rows, seq, cols, c, type), type);
+                float skip = 0.f;
+                if (e->residual && rr >= 0)
+                    skip = rr < e->residual_rows ? view_get(e->residual, e->residual_rows, rr, cols, c, type) : NAN;
+                value = r16(fmaf(e->value_scale, value, e->residual_scale * skip), type);
+                if (e->condition) value = r16(value + view_get(e->condition, e->condition_rows, seq, cols, c, type), type);
+            }
+            if (e->raw) e->raw[(size_t)r * cols + c] = store_out(value, type);
+            if (!masked) value = r16(orc_act(r16(value * e->output_scale, type), e->activation, e->alpha), type);
+            o[(size_t)r * cols + c] = store_out(value, type);
+        }
+    }
+    int status = orc_quantize_rows(o, type, cols, rows, cols, fmt, group, rotation, q, scales);
+    if (retained) memcpy(retained, o, sizeof(uint16_t) * (size_t)rows * cols);
+    free(o);
+    return status;
+}
+
+/* normalized_quantized_linear / norm_project_kernel<T, QuantProjection>
+ * (ops/kernels/sequence/sequence_norm.cu:216-390, host :518-575): the
+ * LayerNorm rows above (no source_rows), quantized per token; the Finish
+ * with bias and ReLU/identity. INT8 dot products are exact; FP8 ones follow
+ * the reference order: lane l of a warp sums words c = 4l + 128j with fmaf
+ * over the 4 decoded bytes, then a shfl-down tree 16..1.
+ * Outputs: y [rows, n]; normalized [rows, k] and encoded/escales optional. */
+int orc_norm_linear(const uint16_t *x, const orc_norm_fusion *f, const uint16_t *nw,
+                    const uint16_t *nb, int type, int rows, int k, float eps, const uint8_t *w,
+                    const float *sw, int fmt, int n, const uint16_t *bias, int act, uint16_t *y,
+                    uint16_t *normalized, uint8_t *encoded, float *escales) {
+    if (k < 4 || k % 4 || k > 512 || f->source_rows) return -1;
+    uint16_t *u = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)rows * k);
+    if (!u) return -1;
+    orc_norm_rows(x, rows, type, rows, k, nw, nb, eps, f, u);
+    float r[512], a[512];
+    for (int row = 0; row < rows; ++row) {
+        float amax = 0.f;
+        for (int c = 0; c < k; ++c) {
+            r[c] = load_src(u, type, (size_t)row * k + c);
             amax = fmaxf(amax, fabsf(r[c]));
-            if (normalized) normalized[(size_t)row * k + c] = h;
         }
         float scale = orc_scale(amax, fmt), recip = 1.f / scale;
         if (escales) escales[row] = scale;
@@ -424,13 +578,13 @@ int orc_norm_linear(const uint16_t *x, const uint16_t *residual, const uint16_t 
                 }
                 result = (lane[0] * sw[ch]) * scale;
             }
-            uint16_t h = store_out(result, type);
-            float o = load_src(&h, type, 0);
-            if (bias) { h = store_out(o + load_src(bias, type, ch), type); o = load_src(&h, type, 0); }
+            float o = r16(r16(result, type) + (bias ? load_src(bias, type, ch) : 0.f), type);
             if (act == 1) o = fmaxf(o, 0.f);
             y[(size_t)row * n + ch] = store_out(o, type);
         }
     }
+    if (normalized) memcpy(normalized, u, sizeof(uint16_t) * (size_t)rows * k);
+    free(u);
     return 0;
 }
 

@@ -126,11 +126,12 @@ static int host_tests() {
         RowScaledView wsmall{TensorView(dummy, 64, 512, Type::I8), TensorView(dummy, 64, 1, Type::F32), 0, 0};
         RowScaledView wbig{TensorView(dummy, 64, 1024, Type::I8), TensorView(dummy, 64, 1, Type::F32), 0, 0};
         ops::NormFusion gated;
-        gated.gate = TensorView(dummy, 1, 512);
+        int source_rows[2] = {0, 1};
+        gated.source_rows = source_rows;
         EXPECT(!g8.normalized_linear(TensorView(dummy, 2, 1024), {}, {}, {}, 1e-5f, {}, wbig,
                                      TensorView(dummy, 2, 64)));  // k > 512
         EXPECT(!g8.normalized_linear(TensorView(dummy, 2, 512), {}, {}, {}, 1e-5f, gated, wsmall,
-                                     TensorView(dummy, 2, 64)));  // gate fusion
+                                     TensorView(dummy, 2, 64)));  // source-row gather
         ops::Epilogue gelu;
         gelu.activation = ops::Activation::GeluTanh;
         EXPECT(!g8.normalized_linear(TensorView(dummy, 2, 512), {}, {}, {}, 1e-5f, {}, wsmall,

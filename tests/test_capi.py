@@ -158,3 +158,82 @@ def test_quantized_gated_validation():
     assert call(g=16) == -1
     assert call(width=200, r=128) == -1
     assert call(x=FAKE + 1) == -2
+
+
+def test_sequence_producer_validation():
+    """qlin_layer_norm_quantize / qlin_pointwise_quantize / qlin_norm_linear
+    reject what the reference's check_quantized_output, check_norm_shape,
+    check_epilogue and normalized_quantized_linear reject
+    (ops/kernels/sequence/sequence_internal.cuh:154-197, sequence_norm.cu:
+    371-397,518-558, sequence_pointwise.cu:307-324)."""
+    L = qlinear.load()
+    f = qlinear.qlin_norm_fusion()
+    L.qlin_norm_fusion_init(ctypes.byref(f))
+    assert f.rows_per_sequence == 1 and not f.residual
+    e = qlinear.qlin_epilogue()
+    L.qlin_epilogue_init(ctypes.byref(e))
+    assert (e.value_scale, e.output_scale, e.residual_scale, e.input_repeat) == (1, 1, 1, 1)
+    assert abs(e.alpha - 0.1) < 1e-7 and e.activation == 0 and e.rows_per_sequence == 1
+
+    X, V, S = FAKE, FAKE + 0x100000, FAKE + 0x200000
+
+    def ln(x_rows=4, st=BF16, rows=4, cols=256, fmt=I8, g=0, r=0, fusion=None, eps=1e-5, x=X,
+           v=V, s=S):
+        return L.qlin_layer_norm_quantize(x, x_rows, st, None, None, eps,
+                                          None if fusion is None else ctypes.byref(fusion), None,
+                                          rows, cols, v, s, fmt, g, r, None)
+
+    assert ln(st=F32) == -1
+    assert ln(fmt=BF16) == -1
+    assert ln(cols=16385) == -4          # beyond this build's register-resident rows
+    assert ln(r=128, g=0) == -1          # rotation requires group scales
+    assert ln(g=128, r=128, cols=200) == -1
+    assert ln(x_rows=3) == -1            # rows differ without a gather
+    assert ln(eps=0.0) == -1
+    assert ln(s=V + 16) == -1            # scales overlap the codes
+    bad = qlinear.qlin_norm_fusion()
+    L.qlin_norm_fusion_init(ctypes.byref(bad))
+    bad.rows_per_sequence = 3
+    assert ln(fusion=bad) == -1
+    bad.rows_per_sequence = 2
+    bad.gate, bad.gate_rows = FAKE + 0x300000, 3   # neither 1 nor 4 / 2 sequences
+    assert ln(fusion=bad) == -1
+    bad.gate_rows = 2
+    bad.source_rows = FAKE + 0x400000  # a gather excludes modulation
+    assert ln(fusion=bad) == -1
+    assert ln(x=X + 1) == -2
+
+    def pw(x_rows=4, rows=4, cols=256, ep=None, g=0, r=0, x=X, ret=None):
+        return L.qlin_pointwise_quantize(x, x_rows, BF16, None if ep is None else ctypes.byref(ep),
+                                         ret, rows, cols, V, S, I8, g, r, None)
+
+    assert pw(rows=5) == -1
+    assert pw(r=128) == -1
+    ep = qlinear.epilogue(input_repeat=2)
+    assert pw(ep=ep) == -1                # x_rows * repeat != rows
+    assert pw(ep=ep, rows=8, ret=X) == -1  # repeated rows cannot update x in place
+    ep = qlinear.epilogue(activation=9)
+    assert pw(ep=ep) == -1
+    ep = qlinear.epilogue(rows_per_sequence=4, valid_rows_per_sequence=5)
+    assert pw(ep=ep) == -1
+    ep = qlinear.epilogue()
+    ep.residual, ep.residual_rows = FAKE + 0x300000, 3   # dense residual must match rows
+    assert pw(ep=ep) == -1
+    ep = qlinear.epilogue(rows_per_sequence=2)
+    ep.condition, ep.condition_rows = FAKE + 0x300000, 3
+    assert pw(ep=ep) == -1
+    assert pw(cols=16385) == -4
+
+    def nl(k=256, n=64, act=0, fusion=None, y=FAKE + 0x500000):
+        return L.qlin_norm_linear(X, None if fusion is None else ctypes.byref(fusion), None, None,
+                                  BF16, 4, k, 1e-5, FAKE + 0x600000, FAKE + 0x700000, I8, n, None,
+                                  act, y, None, None, None, None)
+
+    assert nl(k=513) == -1
+    assert nl(k=6) == -1
+    assert nl(act=2) == -1
+    gather = qlinear.qlin_norm_fusion()
+    L.qlin_norm_fusion_init(ctypes.byref(gather))
+    gather.source_rows = FAKE + 0x400000
+    assert nl(fusion=gather) == -1
+    assert nl(y=X + 2) == -1              # output overlaps the input

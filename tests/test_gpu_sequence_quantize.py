@@ -1,0 +1,154 @@
+"""GPU parity of the sequence-fusion row quantizers through the C ABI against
+the oracle: qlin_layer_norm_quantize (reference layer_norm_quantize,
+ops/kernels/sequence/sequence_norm.cu:65-200,412-440) and
+qlin_pointwise_quantize (reference pointwise_quantize, sequence_pointwise.cu:
+149-260,325-357). Codes, scales, retained and raw rows bit-exact in every
+encoding mode, for bf16/f16, ragged and vector row widths up to 16384, with
+every fusion, the source-row gather and every activation."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+BF16, FP8, I8, F16 = 0, 3, 4, 5
+MODES = [(0, 0), (32, 0), (128, 0), (64, 128), (128, 128)]
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def dev16(b, dtype, dev):
+    return None if b is None else torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(dtype).to(dev)
+
+
+def mk(g, dtype, *shape, sc=1.0, off=0.0):
+    return bits((off + sc * torch.randn(*shape, generator=g)).to(dtype))
+
+
+def same_codes(got, want):
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, BF16), (torch.float16, F16)])
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("cols", [7, 136, 1000, 2048, 6144, 16384])
+def test_layer_norm_quantize_parity(dev, orc, dtype, src_type, fmt, cols):
+    from breeze_tts_cpp_amd import qlinear
+    rows, rps = 6, 3
+    g = torch.Generator().manual_seed(cols + fmt)
+    x, res, pb = mk(g, dtype, rows, cols, sc=2.0, off=0.2), mk(g, dtype, rows, cols), mk(g, dtype, cols, sc=0.1)
+    nw, nb = mk(g, dtype, cols, sc=0.1, off=1.0), mk(g, dtype, cols, sc=0.1)
+    gate, shift, scale = (mk(g, dtype, 2, cols, sc=0.2, off=1.0), mk(g, dtype, 1, cols, sc=0.1),
+                          mk(g, dtype, 2, cols, sc=0.1))
+    for group, rot in MODES:
+        if rot and cols % 128:
+            continue
+        for full in (False, True):
+            print(f"layer_norm_quantize dtype={dtype} fmt={fmt} cols={cols} group={group} "
+                  f"rot={rot} full={full}", flush=True)
+            fus = dict(residual=res, projection_bias=pb, gate=gate, shift=shift, scale=scale) \
+                if full else {}
+            q, s, u, raw = orc.layer_norm_quantize(
+                x, fmt, norm_weight=nw if full else None, norm_bias=nb if full else None,
+                group=group, rotation=rot, src_type=src_type, raw=full,
+                rows_per_sequence=rps, **fus)
+            d = {k: dev16(v, dtype, dev) for k, v in fus.items()}
+            retained = torch.empty((rows, cols), dtype=dtype, device=dev)
+            raw_d = torch.empty((rows, cols), dtype=dtype, device=dev) if full else None
+            fusion = qlinear.norm_fusion(raw=raw_d, rows_per_sequence=rps, **d)
+            qd, sd = qlinear.layer_norm_quantize(
+                dev16(x, dtype, dev), fmt, norm_weight=dev16(nw, dtype, dev) if full else None,
+                norm_bias=dev16(nb, dtype, dev) if full else None, fusion=fusion,
+                retained=retained, group=group, rotation=rot)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(retained), u)
+            if full:
+                assert np.array_equal(bits(raw_d), raw)
+            same_codes(qd, q)
+            assert np.array_equal(sd.cpu().numpy(), s)
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+def test_layer_norm_quantize_gather(dev, orc, fmt):
+    """source_rows: gathered rows, and NaN rows with unit scales for sources
+    outside the input."""
+    from breeze_tts_cpp_amd import qlinear
+    x_rows, cols = 5, 2048
+    g = torch.Generator().manual_seed(fmt)
+    x, res = mk(g, torch.bfloat16, x_rows, cols, sc=2.0), mk(g, torch.bfloat16, x_rows, cols)
+    src = np.array([4, 0, -1, 2, 5, 2, 1], np.int32)
+    for group in (0, 128):
+        print(f"layer_norm_quantize gather fmt={fmt} group={group}", flush=True)
+        q, s, u, _ = orc.layer_norm_quantize(x, fmt, rows=len(src), group=group, residual=res,
+                                             source_rows=src)
+        retained = torch.empty((len(src), cols), dtype=torch.bfloat16, device=dev)
+        src_d = torch.from_numpy(src).to(dev)
+        res_d = dev16(res, torch.bfloat16, dev)  # alive across the call
+        fusion = qlinear.norm_fusion(residual=res_d, source_rows=src_d)
+        qd, sd = qlinear.layer_norm_quantize(dev16(x, torch.bfloat16, dev), fmt, fusion=fusion,
+                                             rows=len(src), retained=retained, group=group)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(retained), u)
+        assert np.array_equal(sd.cpu().numpy(), s)
+        valid = (src >= 0) & (src < x_rows)
+        same_codes(qd[torch.from_numpy(valid).to(dev)], q[valid])
+
+
+@pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, BF16), (torch.float16, F16)])
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("cols", [9, 256, 1000, 4096, 12288])
+def test_pointwise_quantize_parity(dev, orc, dtype, src_type, fmt, cols):
+    from breeze_tts_cpp_amd import qlinear
+    x_rows, repeat, rps, valid = 4, 2, 4, 3
+    rows = x_rows * repeat
+    g = torch.Generator().manual_seed(cols * 3 + fmt)
+    x, b = mk(g, dtype, x_rows, cols, sc=2.0), mk(g, dtype, cols, sc=0.3)
+    gate, cond = mk(g, dtype, 2, cols, sc=0.2, off=1.0), mk(g, dtype, 1, cols, sc=0.5)
+    res = mk(g, dtype, 3, cols)
+    idx = np.array([0, 1, 2, -1, 2, 1, 0, -5], np.int32)
+    cases = [dict(activation=a) for a in range(9)] + [
+        dict(bias=b, gate=gate, condition=cond, residual=res, residual_index=idx, value_scale=0.75,
+             residual_scale=1.5, output_scale=0.5, activation=5, rows_per_sequence=rps,
+             valid_rows_per_sequence=valid, input_repeat=repeat),
+        dict(bias=b, residual=mk(g, dtype, rows, cols), activation=3, input_repeat=repeat)]
+    for case in cases:
+        for group, rot in (MODES if case.get("input_repeat") else MODES[:2]):
+            if rot and cols % 128:
+                continue
+            tag = {k: v for k, v in case.items() if not isinstance(v, np.ndarray)}
+            print(f"pointwise dtype={dtype} fmt={fmt} cols={cols} group={group} rot={rot} {tag}",
+                  flush=True)
+            q, s, out, raw = orc.pointwise_quantize(x, fmt, group=group, rotation=rot,
+                                                    src_type=src_type, raw=True, **case)
+            n_rows = out.shape[0]
+            dev_args = {k: (torch.from_numpy(v).to(dev) if k == "residual_index" else
+                            dev16(v, dtype, dev)) if isinstance(v, np.ndarray) else v
+                        for k, v in case.items()}
+            raw_d = torch.empty((n_rows, cols), dtype=dtype, device=dev)
+            ep = qlinear.epilogue(raw=raw_d, **dev_args)
+            retained = torch.empty((n_rows, cols), dtype=dtype, device=dev)
+            qd, sd = qlinear.pointwise_quantize(dev16(x, dtype, dev), fmt, ep, retained=retained,
+                                                group=group, rotation=rot)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(raw_d), raw)
+            assert np.array_equal(bits(retained), out)
+            same_codes(qd, q)
+            assert np.array_equal(sd.cpu().numpy(), s)
+
+
+def test_pointwise_quantize_in_place(dev, orc):
+    """retained may replace x row for row (ops::linear's output reuse)."""
+    from breeze_tts_cpp_amd import qlinear
+    g = torch.Generator().manual_seed(9)
+    x = mk(g, torch.bfloat16, 32, 2048, sc=2.0)
+    b = mk(g, torch.bfloat16, 2048, sc=0.3)
+    q, s, out, _ = orc.pointwise_quantize(x, I8, bias=b, activation=1)
+    xd = dev16(x, torch.bfloat16, dev)
+    b_d = dev16(b, torch.bfloat16, dev)  # alive across the call
+    ep = qlinear.epilogue(bias=b_d, activation=1)
+    qd, sd = qlinear.pointwise_quantize(xd, I8, ep, retained=xd)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(xd), out)
+    same_codes(qd, q)
+    assert np.array_equal(sd.cpu().numpy(), s)

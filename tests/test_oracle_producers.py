@@ -246,7 +246,7 @@ def test_norm_linear_matches_torch(orc, fmt, k):
     nw = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16)
     nb = (0.1 * torch.randn(k, generator=g)).to(torch.bfloat16)
     wq, sw = orc.quantize_rows(torch_to_bits((0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16)), fmt)
-    y, nrm, enc, esc = orc.norm_linear(torch_to_bits(x), wq, sw, fmt, norm_weight=torch_to_bits(nw),
+    y, nrm, enc, esc, _ = orc.norm_linear(torch_to_bits(x), wq, sw, fmt, norm_weight=torch_to_bits(nw),
                                        norm_bias=torch_to_bits(nb), residual=torch_to_bits(res),
                                        eps=1e-5)
     v = (x.float() + res.float()).to(torch.bfloat16).double()
@@ -264,3 +264,121 @@ def test_norm_linear_matches_torch(orc, fmt, k):
         ideal = (table[enc] @ table[wq].T) * sw[None, :] * esc[:, None]
         got_y = bits_to_torch(y).double().numpy()
         assert np.linalg.norm(got_y - ideal) / np.linalg.norm(ideal) <= 1e-2
+
+
+# ---------------------------------------------------------------- sequence producers
+ACTS = {1: lambda x: torch.relu(x), 2: lambda x: torch.nn.functional.leaky_relu(x, 0.1),
+        3: torch.nn.functional.silu, 4: lambda x: torch.nn.functional.gelu(x),
+        5: lambda x: torch.nn.functional.gelu(x, approximate="tanh"),
+        6: torch.nn.functional.mish, 7: torch.tanh, 8: torch.sigmoid}
+
+
+@pytest.mark.parametrize("kind", sorted(ACTS))
+def test_act_matches_torch_fp64(orc, kind):
+    """ops::activate's set, each within a few fp32 ulp (plus the cancellation
+    bound of the fp32 forms) of torch's fp64 function; act(0) = 0 (sigmoid 1/2)."""
+    xs = np.concatenate([np.linspace(-30, 30, 2001), [-100.0, -20.5, 19.9, 20.1, 50.0]])
+    got = torch.tensor([orc.act(x, kind) for x in xs], dtype=torch.float64)
+    ref = ACTS[kind](torch.tensor(xs, dtype=torch.float64))
+    tol = ref.abs() * 2.0 ** -21 + torch.tensor(np.abs(xs)) * 2.0 ** -22 + 1e-30
+    assert torch.all((got - ref).abs() <= tol), kind
+    assert orc.act(0.0, kind) == (0.5 if kind == 8 else 0.0)
+    assert orc.act(-3.0, 2, alpha=0.25) == -0.75
+
+
+def _bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).float()
+
+
+def _rb(t):
+    """fp32/fp64 torch tensor -> bf16 (rounded once) -> float."""
+    return t.float().to(torch.bfloat16).float()
+
+
+def test_norm_rows_fusions_match_torch(orc):
+    """NormFusion: the 16-bit steps of load / transform reproduced with torch
+    given the oracle's statistics; statistics within fp64 bounds; raw = v;
+    per-sequence modulation rows; source-row gather and NaN rows."""
+    rows, cols, rps = 6, 1000, 3
+    g = torch.Generator().manual_seed(11)
+    mk = lambda *s, sc=1.0, off=0.0: torch_to_bits((off + sc * torch.randn(*s, generator=g)).to(torch.bfloat16))
+    x, res, pb = mk(rows, cols, sc=2.0), mk(rows, cols), mk(cols, sc=0.1)
+    gate, shift, scale = mk(2, cols, sc=0.2, off=1.0), mk(2, cols, sc=0.1), mk(2, cols, sc=0.1)
+    nw, nb = mk(cols, sc=0.1, off=1.0), mk(cols, sc=0.1)
+    q, sc_, u, raw = orc.layer_norm_quantize(
+        x, 4, norm_weight=nw, norm_bias=nb, residual=res, projection_bias=pb, gate=gate,
+        shift=shift, scale=scale, rows_per_sequence=rps, raw=True)
+    seq = torch.arange(rows) // rps
+    v = _rb(_rb(_rb(_bf(x) + _bf(pb)) * _bf(gate)[seq]) + _bf(res))
+    assert np.array_equal(raw, torch_to_bits(v.to(torch.bfloat16)))
+    vd = v.double()
+    mean = vd.mean(1, keepdim=True)
+    inv = 1 / torch.sqrt(((vd - mean) ** 2).mean(1, keepdim=True) + 1e-5)
+    ref = ((vd - mean) * inv * _bf(nw).double() + _bf(nb).double())
+    ref = ref * (1 + _bf(scale).double()[seq]) + _bf(shift).double()[seq]
+    got = _bf(u).double()
+    assert torch.all((got - ref).abs() <= ref.abs() * 2.0 ** -6 + 2e-2)
+    # codes = the (pinned) row quantizer of the retained rows
+    q2, s2 = orc.quantize_rows(u, 4)
+    assert np.array_equal(q, q2) and np.array_equal(sc_, s2)
+    # gather: output row r normalizes input row src[r]; bad sources -> NaN, scale 1
+    src = np.array([5, 0, -1, 2, 6], np.int32)
+    qg, sg, ug, _ = orc.layer_norm_quantize(x, 4, norm_weight=nw, rows=5, source_rows=src)
+    direct = orc.norm_rows(x, norm_weight=nw)
+    for r, s in enumerate(src):
+        if 0 <= s < rows:
+            assert np.array_equal(ug[r], direct[s])
+        else:
+            assert np.all(np.isnan(_bf(ug[r]).numpy())) and sg[r] == 1.0
+
+
+@pytest.mark.parametrize("group,rotation", [(0, 0), (32, 0), (128, 0), (128, 128), (64, 128)])
+def test_layer_norm_quantize_modes(orc, group, rotation):
+    """Every encoding mode: codes and scales are the row quantizer's on the
+    retained rows."""
+    x = synthetic.activations(7, 1024, seed=group + rotation)
+    for fmt in (3, 4):
+        q, s, u, _ = orc.layer_norm_quantize(x, fmt, group=group, rotation=rotation)
+        q2, s2 = orc.quantize_rows(u, fmt, group=group, rotation=rotation)
+        assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def test_pointwise_matches_torch(orc):
+    """The dense Finish steps reproduced with torch's bf16 rounding: bias,
+    per-sequence gate and condition, indexed residual (negative -> 0),
+    value/residual scales with the contracted fma, output scale, activation
+    (pinned above), sequence-tail mask, input repeat; codes = row quantizer."""
+    x_rows, repeat, cols, rps, valid = 4, 2, 136, 4, 3
+    rows = x_rows * repeat
+    g = torch.Generator().manual_seed(5)
+    mk = lambda *s, sc=1.0, off=0.0: torch_to_bits((off + sc * torch.randn(*s, generator=g)).to(torch.bfloat16))
+    x, b = mk(x_rows, cols, sc=2.0), mk(cols, sc=0.3)
+    gate, cond = mk(2, cols, sc=0.2, off=1.0), mk(2, cols, sc=0.5)
+    res = mk(3, cols)
+    idx = np.array([0, 1, 2, -1, 2, 1, 0, -5], np.int32)
+    for kind in (0, 3, 5, 6):
+        q, s, out, raw = orc.pointwise_quantize(
+            x, 4, bias=b, gate=gate, condition=cond, residual=res, residual_index=idx,
+            value_scale=0.75, residual_scale=1.5, output_scale=0.5, activation=kind,
+            rows_per_sequence=rps, valid_rows_per_sequence=valid, input_repeat=repeat, raw=True)
+        xr = _bf(x)[torch.arange(rows) // repeat]
+        seq = torch.arange(rows) // rps
+        v = _rb(xr + _bf(b))
+        v = _rb(v * _bf(gate)[seq])
+        skip = torch.where(torch.tensor(idx)[:, None] >= 0, _bf(res)[torch.tensor(idx).clamp_min(0)],
+                           torch.zeros(1))
+        v = _rb(torch.tensor(0.75, dtype=torch.float64) * v.double() +
+                (torch.tensor(1.5, dtype=torch.float32) * skip).double())
+        v = _rb(v + _bf(cond)[seq])
+        mask = (torch.arange(rows) % rps >= valid)[:, None]
+        v = torch.where(mask, torch.zeros(1), v)
+        assert np.array_equal(raw, torch_to_bits(v.to(torch.bfloat16)))
+        pre = _rb(v * 0.5)
+        act = torch.tensor([[orc.act(float(a), kind) for a in row] for row in pre.tolist()])
+        o = torch.where(mask, torch.zeros(1), _rb(act))
+        assert np.array_equal(out, torch_to_bits(o.to(torch.bfloat16))), kind
+        q2, s2 = orc.quantize_rows(out, 4)
+        assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    # an index past the residual's rows contributes NaN
+    _, _, out, _ = orc.pointwise_quantize(x, 4, residual=res, residual_index=np.array([0, 9, 1, 2], np.int32))
+    assert np.all(np.isnan(_bf(out[1]).numpy())) and not np.isnan(_bf(out[0]).numpy()).any()
