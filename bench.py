@@ -347,11 +347,13 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
 
 def bench_producers(torch, qlinear, synthetic, dev, stream, args):
     """The fused quantizing producers at the decoder's shapes (hidden 2048,
-    FFN 6144; INT8 per-token): residual update + RMSNorm -> quant, and
-    SiLU(gate) * up -> quant, at M=32 and M=4096. Algorithmic bytes: norm
-    reads x, update (2MK each) and weight (2K), writes the residual (2MK),
-    codes (MK) and scales (4M); gated reads gate|up (4MW), writes codes (MW)
-    and scales (4M)."""
+    FFN 6144; INT8 per-token): residual update + RMSNorm -> quant,
+    SiLU(gate) * up -> quant, LayerNorm -> quant and bias + tanh-GeLU -> quant
+    at M=32 and M=4096, and LayerNorm -> quantized GEMV at k=512. Algorithmic
+    bytes: norm reads x, update (2MK each) and weight (2K), writes the
+    residual (2MK), codes (MK) and scales (4M); gated reads gate|up (4MW),
+    writes codes (MW) and scales (4M); LayerNorm / pointwise read x (2MK) and
+    one [K] vector (2K), write codes (MK) and scales (4M)."""
     out = {}
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     H, W = 2048, 6144
@@ -387,13 +389,37 @@ def bench_producers(torch, qlinear, synthetic, dev, stream, args):
                                                     scales=ns, stream=stream))
         us_g = timed(lambda: qlinear.quantized_gated(gu, qlinear.I8, kind=0, values=gq,
                                                      scales=gs, stream=stream))
+        # LayerNorm -> quant (no fusions) and the linear output's pointwise
+        # epilogue (bias + tanh-GeLU) -> quant, at the decoder's hidden size.
+        bias = bf((1, H), 4).reshape(H)
+        lq = torch.empty((M, H), dtype=torch.uint8, device=dev)
+        ls = torch.empty((M,), dtype=torch.float32, device=dev)
+        ep = qlinear.epilogue(bias=bias, activation=qlinear.ACT_GELU_TANH)
+        us_l = timed(lambda: qlinear.layer_norm_quantize(x, qlinear.I8, norm_weight=w,
+                                                         values=lq, scales=ls, stream=stream))
+        us_p = timed(lambda: qlinear.pointwise_quantize(x, qlinear.I8, ep, values=lq, scales=ls,
+                                                        stream=stream))
         b_n = 7 * M * H + 2 * H + 4 * M
         b_g = 5 * M * W + 4 * M
-        out[f"M={M}"] = {
-            "quantized_norm": {"us": round(us_n, 2), "bytes": b_n,
-                               "GBps": round(b_n / (us_n * 1e-6) / 1e9, 1)},
-            "quantized_gated": {"us": round(us_g, 2), "bytes": b_g,
-                                "GBps": round(b_g / (us_g * 1e-6) / 1e9, 1)}}
+        b_l = 3 * M * H + 2 * H + 4 * M
+        b_p = 3 * M * H + 2 * H + 4 * M
+        leg = lambda us, b: {"us": round(us, 2), "bytes": b, "GBps": round(b / (us * 1e-6) / 1e9, 1)}
+        out[f"M={M}"] = {"quantized_norm": leg(us_n, b_n), "quantized_gated": leg(us_g, b_g),
+                         "layer_norm_quantize": leg(us_l, b_l),
+                         "pointwise_quantize": leg(us_p, b_p)}
+    # LayerNorm -> quantized GEMV for a small-hidden projection (k = 512,
+    # n = 2048, INT8): reads x (2·rows·k) and the weights (n·k + 4n), writes y.
+    rows, k, n = M_DECODE, 512, 2048
+    xs = torch.from_numpy(synthetic.activations(rows, k, seed=7).view(np.int16)).view(
+        torch.bfloat16).to(dev)
+    wq = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev).view(torch.uint8)
+    sw = torch.full((n,), 1e-3, dtype=torch.float32, device=dev)
+    y = torch.empty((rows, n), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    us_nl = timed(lambda: qlinear.norm_linear(xs, wq, sw, qlinear.I8, out=y, stream=stream))
+    b_nl = n * k + 4 * n + 2 * rows * k + 2 * rows * n
+    out[f"norm_linear rows={rows} k={k} n={n}"] = {
+        "us": round(us_nl, 2), "bytes": b_nl, "GBps": round(b_nl / (us_nl * 1e-6) / 1e9, 1)}
     return out
 
 

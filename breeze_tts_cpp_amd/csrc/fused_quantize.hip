@@ -26,8 +26,9 @@
 //    fp64); the reference's rsqrtf is an approximation within 2 ulp of it.
 //  - SiLU is (x*2^-16) / ((1 + e^-x) * 2^-16) and tanh-GeLU is
 //    (0.5x)(1 + tanh(0.7978845608028654 (x + ((0.044715x)x)x))) in fp32, with
-//    e^-x and tanh evaluated in fp64 and rounded to fp32 (the reference's
-//    __expf / __fdividef / tanhf are approximations of the same values).
+//    e^-x and tanh by this library's fp32 qexp / qtanh (within 1 and 2 ulp;
+//    the reference's __expf / __fdividef / tanhf approximate the same
+//    values).
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "row_encode.hpp"
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
 
 template <int Kind> __device__ __forceinline__ float activate(float x) {
     if constexpr (Kind == 0) {
-        const float e = float(exp(-double(x)));
+        const float e = qexp(-x);
         return (x * 0x1p-16f) / ((1.f + e) * 0x1p-16f);
     } else {
         return gelu_tanh<false>(x);

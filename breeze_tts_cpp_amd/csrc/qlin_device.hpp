@@ -49,16 +49,16 @@ __device__ __forceinline__ uint16_t from_float(float f, f16_t) {
 }
 
 // Two values rounded to nearest even and packed low|high<<16. bf16 uses
-// gfx950's v_cvt_pk_bf16_f32 (IEEE RNE, subnormals kept): the same bits as
-// the integer rounding above for every non-NaN input, one instruction per pair.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack2(float lo, float hi, bf16_t) {
-    const bf16x2_t h = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
+// gfx950's v_cvt_pk_bf16_f32 (IEEE round-to-nearest-even, subnormals kept,
+// NaN stays NaN): the bits of the integer rounding above for every non-NaN
+// input, in one instruction per pair (the compiler emulates the conversion
+// with integer operations).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
     uint32_t u;
-    __builtin_memcpy(&u, &h, 4);
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(u) : "v"(lo), "v"(hi));
     return u;
 }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, bf16_t) { return cvt_pk_bf16(lo, hi); }
 __device__ __forceinline__ uint32_t pack2(float lo, float hi, f16_t) {
     return uint32_t(from_float(lo, f16_t{})) | (uint32_t(from_float(hi, f16_t{})) << 16);
 }
@@ -115,19 +115,77 @@ __device__ __forceinline__ float rotation_sign(int column) {
 template <class T> __device__ __forceinline__ float round16(float x) {
     return to_float(from_float(x, T{}), T{});
 }
+// bf16: gfx950's conversion instruction (IEEE round-to-nearest-even,
+// subnormals kept; a NaN stays a NaN) and a widening shift: the value of the
+// integer rounding above in two instructions.
+template <> __device__ __forceinline__ float round16<bf16_t>(float x) {
+    return __uint_as_float(cvt_pk_bf16(x, 0.f) << 16);
+}
+
+// ---------------------------------------------------------------- fp32 exp / tanh
+// This library's exponential (the reference's expf / __expf approximate the
+// same function): Cody-Waite reduction x = k ln2 + r with ln2 split into a
+// 16-bit head (0x1.62e4p-1, so k * head is exact) and a tail, |r| <= 0.347;
+// e^r by its Taylor polynomial to degree 8 (next term < 2^-32 relative), in
+// Horner form with fma; the result scaled by 2^k in two exact power-of-two
+// factors so that only the final product rounds (subnormal results included).
+// inf above 89, 0 below -104, NaN kept.
+__device__ __forceinline__ float qexp(float x) {
+    if (x != x) return x;
+    x = fminf(fmaxf(x, -104.f), 89.f);
+    const float k = rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-k, 0x1.62e4p-1f, x);
+    r = __builtin_fmaf(-k, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-16f;
+    p = __builtin_fmaf(p, r, 0x1.a01a02p-13f);
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.f);
+    p = __builtin_fmaf(p, r, 1.f);
+    const int ki = int(k), k1 = ki / 2, k2 = ki - k1;
+    return (p * __uint_as_float(uint32_t(k1 + 127) << 23)) *
+           __uint_as_float(uint32_t(k2 + 127) << 23);
+}
+
+// This library's tanh: the odd Taylor series to degree 15 for |y| < 0.5
+// (next term < 2^-27 relative), else 1 - 2 / (e^{2|y|} + 1) with qexp, with
+// the sign of y; 1 beyond |y| = 9.1 (where tanh rounds to 1 in fp32).
+__device__ __forceinline__ float qtanh(float y) {
+    if (y != y) return y;
+    const float a = fabsf(y);
+    float t;
+    if (a < 0.5f) {
+        const float s = a * a;
+        float p = -0x1.7da364p-10f;
+        p = __builtin_fmaf(p, s, 0x1.d6d3d0p-9f);
+        p = __builtin_fmaf(p, s, -0x1.226e36p-7f);
+        p = __builtin_fmaf(p, s, 0x1.664f48p-6f);
+        p = __builtin_fmaf(p, s, -0x1.ba1ba2p-5f);
+        p = __builtin_fmaf(p, s, 0x1.111112p-3f);
+        p = __builtin_fmaf(p, s, -0x1.555556p-2f);
+        t = __builtin_fmaf(a * s, p, a);
+    } else if (a < 9.1f) {
+        t = 1.f - 2.f / (qexp(2.f * a) + 1.f);
+    } else {
+        t = 1.f;
+    }
+    return __builtin_copysignf(t, y);
+}
 
 // tanh-GeLU of the reference: (0.5x)(1 + tanh(0.7978845608028654 * inner))
-// in fp32, tanh evaluated in fp64 and rounded once. The reference's TUs
-// differ in contraction: quant_gated.cu (built with --fmad=false,
-// quant_gated.cu:14-15) forms inner = x + ((0.044715x)x)x with separate
-// roundings; activation.cuh:15 as compiled into the GEMM epilogue and the
-// pointwise finish (FMA contraction on) forms inner = fma((0.044715x)x, x, x).
+// in fp32 with qtanh. The reference's TUs differ in contraction:
+// quant_gated.cu (built with --fmad=false, quant_gated.cu:14-15) forms
+// inner = x + ((0.044715x)x)x with separate roundings; activation.cuh:15 as
+// compiled into the GEMM epilogue and the pointwise finish (FMA contraction
+// on) forms inner = fma((0.044715x)x, x, x).
 template <bool Contracted>
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float cubic = (0.044715f * x) * x;
     const float inner = Contracted ? __builtin_fmaf(cubic, x, x) : x + cubic * x;
-    const float t = float(tanh(double(0.7978845608028654f * inner)));
-    return (0.5f * x) * (1.f + t);
+    return (0.5f * x) * (1.f + qtanh(0.7978845608028654f * inner));
 }
 
 // Finish of a quantized linear on its stored result d (the reference's
@@ -136,7 +194,7 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // 2 = tanh-GeLU, 0 = none. The caller's store performs the final rounding.
 enum Finish : int { FINISH_NONE = 0, FINISH_RELU = 1, FINISH_GELU_TANH = 2 };
 // Out of line: the GEMM epilogues call it only when a finish is requested,
-// so the fp64 tanh does not enlarge the register allocation of their loops.
+// so the tanh does not enlarge the register allocation of their loops.
 template <class Out>
 __device__ __noinline__ void finish4(float (&v)[4], const uint16_t *bias, int n, int n_last,
                                      int act) {

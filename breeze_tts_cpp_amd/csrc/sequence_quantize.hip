@@ -33,8 +33,9 @@
 //    (__fmul_rn in the reference), then the 16-bit rounding points of NormRow.
 //  - The epilogue forms value_scale * v + residual_scale * skip as
 //    fma(value_scale, v, residual_scale * skip).
-//  - Transcendental activations evaluate exp / erf / log1p / tanh in fp64 and
-//    round once to fp32 (the reference's expf, erff, log1pf, tanhf and
+//  - SiLU, sigmoid, tanh and tanh-GeLU use this library's fp32 qexp / qtanh;
+//    GeLU's erf and Mish's exp / log1p / tanh are evaluated in fp64 and
+//    rounded once to fp32 (the reference's expf, erff, log1pf, tanhf and
 //    cutlass::fast_tanh approximate the same values); tanh-GeLU's inner term
 //    is fma((0.044715x)x, x, x) as the contracting TUs compile it.
 #include "qlin_device.hpp"
@@ -86,28 +87,49 @@ __device__ __forceinline__ float decode_fp8(uint32_t c) {
     return (c & 0x80u) ? -v : v;
 }
 
-// Activations with a transcendental (ops/kernels/common/activation.cuh:11-22),
-// out of line so the row loops keep their registers.
-__device__ __noinline__ float activate_slow(float x, int kind) {
-    switch (kind) {
-    case QLIN_ACT_SILU: return x / (1.f + float(exp(-double(x))));
-    case QLIN_ACT_GELU: return (0.5f * x) * (1.f + float(erf(double(x * 0.7071067811865475f))));
-    case QLIN_ACT_GELU_TANH: return gelu_tanh<true>(x);
-    case QLIN_ACT_MISH: {
-        const float softplus = x > 20.f ? x : float(log1p(double(float(exp(double(x))))));
-        return x * float(tanh(double(softplus)));
-    }
-    case QLIN_ACT_TANH: return float(tanh(double(x)));
-    case QLIN_ACT_SIGMOID: return 1.f / (1.f + float(exp(-double(x))));
-    default: return x;
-    }
+// GeLU (erf) and Mish (ops/kernels/common/activation.cuh:13-14,17-18) in
+// fp64, rounded once to fp32 at the reference's rounding points; out of line
+// so the row loops keep their registers.
+__device__ __noinline__ float activate_fp64(float x, int kind) {
+    if (kind == QLIN_ACT_GELU)
+        return (0.5f * x) * (1.f + float(erf(double(x * 0.7071067811865475f))));
+    const float softplus = x > 20.f ? x : float(log1p(double(float(exp(double(x))))));
+    return x * float(tanh(double(softplus)));
 }
 
-__device__ __forceinline__ float activate(float x, int kind, float alpha) {
-    if (kind == QLIN_ACT_IDENTITY) return x;
-    if (kind == QLIN_ACT_RELU) return fmaxf(x, 0.f);
-    if (kind == QLIN_ACT_LEAKY_RELU) return x >= 0.f ? x : x * alpha;
-    return activate_slow(x, kind);
+// ops::activate on 8 values; the kind is uniform, so the switch sits outside
+// the element loops. SiLU, sigmoid, tanh and tanh-GeLU use qexp / qtanh.
+__device__ __forceinline__ void activate8(float (&v)[8], int kind, float alpha) {
+    switch (kind) {
+    case QLIN_ACT_IDENTITY: break;
+    case QLIN_ACT_RELU:
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = fmaxf(v[i], 0.f);
+        break;
+    case QLIN_ACT_LEAKY_RELU:
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] >= 0.f ? v[i] : v[i] * alpha;
+        break;
+    case QLIN_ACT_SILU:
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] / (1.f + qexp(-v[i]));
+        break;
+    case QLIN_ACT_GELU_TANH:
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = gelu_tanh<true>(v[i]);
+        break;
+    case QLIN_ACT_TANH:
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = qtanh(v[i]);
+        break;
+    case QLIN_ACT_SIGMOID:
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 1.f / (1.f + qexp(-v[i]));
+        break;
+    default:
+        for (int i = 0; i < 8; ++i) v[i] = activate_fp64(v[i], kind);
+        break;
+    }
 }
 
 template <class T, bool Vec>
@@ -183,37 +205,65 @@ __global__ __launch_bounds__(kThreads) void layer_norm_quantize(
 #pragma unroll
     for (int it = 0; it < Items; ++it) {
         const int column = (it * kThreads + t) * 8;
+        if (column >= cols) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
+            continue;
+        }
+        // An absent operand adds 0 (exact; -0 becomes +0 as the reference's).
         float a[8], b[8];
         load8<T, Vec>(xr, column, cols, a);
-        load8_or<T, Vec>(pb, column, cols, b, 0.f);
+        if (pb) {
+            load8<T, Vec>(pb, column, cols, b);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] += 0.f;
+        }
         if (gate) {
             load8<T, Vec>(gate, column, cols, b);
 #pragma unroll
             for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * b[i]);
         }
-        load8_or<T, Vec>(res, column, cols, b, 0.f);
+        if (res) {
+            load8<T, Vec>(res, column, cols, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] += 0.f;
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            v[it][i] = column + i < cols ? round16<T>(a[i] + b[i]) : 0.f;
-            if (column + i < cols) cache[column + i] = v[it][i];
+            v[it][i] = Vec || column + i < cols ? a[i] : 0.f;
+            if (Vec || column + i < cols) cache[column + i] = v[it][i];
         }
         if (raw) store16x8<T, Vec>(raw, column, cols, v[it]);
     }
     __syncthreads();
+    // Thread t's columns t, t + 256, ... in order (the reference's per-thread
+    // partial), all LDS reads issued together.
+    float stat[Items * 8];
+#pragma unroll
+    for (int j = 0; j < Items * 8; ++j) stat[j] = t + j * kThreads < cols ? cache[t + j * kThreads] : 0.f;
     float sum = 0.f;
-    for (int c = t; c < cols; c += kThreads) sum += cache[c];
+#pragma unroll
+    for (int j = 0; j < Items * 8; ++j)
+        if (t + j * kThreads < cols) sum += stat[j];
     const float mean = block_sum_256(sum, red) / float(cols);
     sum = 0.f;
-    for (int c = t; c < cols; c += kThreads) {
-        const float d = cache[c] - mean;
-        sum = __builtin_fmaf(d, d, sum);
-    }
+#pragma unroll
+    for (int j = 0; j < Items * 8; ++j)
+        if (t + j * kThreads < cols) {
+            const float d = stat[j] - mean;
+            sum = __builtin_fmaf(d, d, sum);
+        }
     const float inv = rsqrt_rn(block_sum_256(sum, red) / float(cols) + eps);
 #pragma unroll
     for (int it = 0; it < Items; ++it) {
         const int column = (it * kThreads + t) * 8;
+        if (column >= cols) continue;
         float w[8], b[8];
         load8_or<T, Vec>(nw, column, cols, w, 1.f);
         load8_or<T, Vec>(nb, column, cols, b, 0.f);
@@ -228,9 +278,16 @@ __global__ __launch_bounds__(kThreads) void layer_norm_quantize(
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(v[it][i] * round16<T>(1.f + w[i]));
         }
-        load8_or<T, Vec>(shift, column, cols, b, 0.f);
+        if (shift) {
+            load8<T, Vec>(shift, column, cols, b);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[it][i] = column + i < cols ? round16<T>(v[it][i] + b[i]) : 0.f;
+            for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(v[it][i] + b[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] += 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[it][i] = Vec || column + i < cols ? v[it][i] : 0.f;
         if (retained) store16x8<T, Vec>(retained + size_t(out_row) * cols, column, cols, v[it]);
     }
     encode_row<Fmt, Items, Rot, G, Vec>(v, q, scales, out_row, rows, cols);
@@ -254,10 +311,24 @@ __global__ __launch_bounds__(kThreads) void pointwise_quantize(
     const uint16_t *res = e.residual && r >= 0 && !skip_nan
                               ? row_of(e.residual, e.residual_rows, r, cols) : nullptr;
     uint16_t *raw = e.raw ? static_cast<uint16_t *>(e.raw) + size_t(row) * cols : nullptr;
+    // Steps that leave a 16-bit value unchanged skip their rounding: without
+    // a residual, value_scale 1 and a positive finite residual_scale the
+    // residual step is v + 0 (exact; it turns -0 into +0 as the reference's
+    // does); output_scale 1 multiplies exactly; identity and ReLU return a
+    // 16-bit value.
+    const bool scaled_residual = res || skip_nan || e.value_scale != 1.f ||
+                                 !(e.residual_scale > 0.f && e.residual_scale <= 3.4e38f);
+    const bool scaled_output = e.output_scale != 1.f;
+    const bool rounded_act = e.activation != QLIN_ACT_IDENTITY && e.activation != QLIN_ACT_RELU;
     float v[Items][8];
 #pragma unroll
     for (int it = 0; it < Items; ++it) {
         const int column = (it * kThreads + t) * 8;
+        if (column >= cols) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
+            continue;
+        }
         if (masked) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
@@ -265,30 +336,45 @@ __global__ __launch_bounds__(kThreads) void pointwise_quantize(
         } else {
             float a[8], b[8];
             load8<T, Vec>(xr, column, cols, a);
-            load8_or<T, Vec>(bias, column, cols, b, 0.f);
+            if (bias) {
+                load8<T, Vec>(bias, column, cols, b);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] += 0.f;
+            }
             if (gate) {
                 load8<T, Vec>(gate, column, cols, b);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * b[i]);
             }
-            load8_or<T, Vec>(res, column, cols, b, skip_nan ? __builtin_nanf("") : 0.f);
+            if (scaled_residual) {
+                load8_or<T, Vec>(res, column, cols, b, skip_nan ? __builtin_nanf("") : 0.f);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                a[i] = round16<T>(__builtin_fmaf(e.value_scale, a[i], e.residual_scale * b[i]));
+                for (int i = 0; i < 8; ++i)
+                    a[i] = round16<T>(__builtin_fmaf(e.value_scale, a[i], e.residual_scale * b[i]));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] += 0.f;
+            }
             if (cond) {
                 load8<T, Vec>(cond, column, cols, b);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
             }
             if (raw) store16x8<T, Vec>(raw, column, cols, a);
+            if (scaled_output) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                v[it][i] = column + i < cols
-                               ? round16<T>(activate(round16<T>(a[i] * e.output_scale),
-                                                     e.activation, e.alpha))
-                               : 0.f;
+                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * e.output_scale);
+            }
+            activate8(a, e.activation, e.alpha);
+            if (rounded_act) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = Vec || column + i < cols ? a[i] : 0.f;
         }
         if (retained) store16x8<T, Vec>(retained + size_t(row) * cols, column, cols, v[it]);
     }
@@ -453,9 +539,10 @@ void by_mode(const Args &a, hipStream_t s) {
 
 template <int Fmt, class T, bool Vec, class Args>
 void by_items(const Args &a, hipStream_t s) {
-    // Items: 2 (cols <= 4096) or 8 (cols <= 16384) chunks of 2048 columns.
+    // Items: 1, 2 or 8 chunks of 2048 columns (cols <= 16384).
     if (a.cols > 2 * kChunk) by_mode<Fmt, T, 8, Vec>(a, s);
-    else by_mode<Fmt, T, 2, Vec>(a, s);
+    else if (a.cols > kChunk) by_mode<Fmt, T, 2, Vec>(a, s);
+    else by_mode<Fmt, T, 1, Vec>(a, s);
 }
 #endif
 

@@ -248,10 +248,20 @@ void QuantizedGemm::linear(RowScaledView input, RowScaledView weight, TensorView
                         stream_, format_, output.type);
 }
 
+namespace {
+// An epilogue with nothing beyond bias and activation.
+bool finish_only(const ops::Epilogue &e) {
+    return !e.residual.data && !e.raw.data && !e.gate.data && !e.condition.data &&
+           !e.residual_rows && e.value_scale == 1 && e.output_scale == 1 &&
+           !e.valid_rows_per_sequence && e.input_repeat == 1;
+}
+}  // namespace
+
 bool QuantizedGemm::linear_finish(RowScaledView input, RowScaledView weight, TensorView output,
                                   const ops::Epilogue &finish) {
     // The reference fuses ReLU / tanh-GeLU; a bias-only finish (identity
     // activation) is fused here as well.
+    if (!finish_only(finish)) return false;
     int act;
     if (finish.activation == ops::Activation::Relu) act = QLIN_FINISH_RELU;
     else if (finish.activation == ops::Activation::GeluTanh) act = QLIN_FINISH_GELU_TANH;
@@ -290,8 +300,8 @@ bool QuantizedGemm::normalized_linear(TensorView input, TensorView normalized,
     if (weight.group_size || weight.rotation_size || encoded.group_size || encoded.rotation_size ||
         fusion.source_rows || weight.values.type != format_)
         return false;
-    if (epilogue.activation != ops::Activation::Identity &&
-        epilogue.activation != ops::Activation::Relu)
+    if ((epilogue.activation != ops::Activation::Identity &&
+         epilogue.activation != ops::Activation::Relu) || !finish_only(epilogue))
         return false;
     const int n = weight.values.rows, k = weight.values.cols;
     if (!input.data || input.rows < 1 || input.rows > 65535 || k < 4 || k % 4 || k > 512 ||
@@ -429,24 +439,124 @@ void linear(TensorView input, RowScaledView weight, TensorView output, RowScaled
         throw std::invalid_argument("quantized linear dimensions/layout mismatch");
     matmul(scratch, weight, output);
 }
-// ops/linear.cpp:71-93: quantize into the scratch, then the GEMM with the
-// fused finish; an epilogue the finish does not cover is rejected here (the
-// reference's generic pointwise pass is not part of this library).
+// ops/linear.cpp:26-93, quantized weight and dense activation: quantize
+// into the scratch, then the GEMM with the fused finish; with a quantized
+// output, the fused finish + quantize_rows when the formats agree and the
+// epilogue is a finish, else the GEMM + pointwise_quantize.
 void linear(TensorView input, RowScaledView weight, TensorView bias, TensorView output,
-            Epilogue epilogue, RowScaledView scratch) {
+            Epilogue epilogue, RowScaledView scratch, RowScaledView quantized_output) {
     weight.validate();
+    epilogue.bias = bias;
     quantize_rows(input, scratch);
     if (scratch.values.cols != weight.values.cols || output.rows != scratch.values.rows ||
         output.cols != weight.values.rows || !output.dense())
         throw std::invalid_argument("quantized linear dimensions/layout mismatch");
-    epilogue.bias = bias;
-    if (epilogue.activation == Activation::Identity && !bias.data) {
+    QuantizedGemm &gemm = context(output.device);
+    if (quantized_output.values.data) {
+        if (quantized_output.values.type == weight.values.type &&
+            gemm.linear_finish(scratch, weight, output, epilogue)) {
+            quantize_rows(output, quantized_output);
+            return;
+        }
+        matmul(scratch, weight, output);
+        pointwise_quantize(output, quantized_output, epilogue);
+        return;
+    }
+    if (epilogue.activation == Activation::Identity && !bias.data && finish_only(epilogue)) {
         matmul(scratch, weight, output);
         return;
     }
-    Epilogue fused = epilogue;
-    if (!context(output.device).linear_finish(scratch, weight, output, fused))
+    if (!gemm.linear_finish(scratch, weight, output, epilogue))
         throw std::invalid_argument("quantized linear epilogue is not a bias/ReLU/tanh-GeLU finish");
+}
+
+namespace {
+qlin_epilogue to_c(const Epilogue &e) {
+    qlin_epilogue c;
+    qlin_epilogue_init(&c);
+    c.bias = e.bias.data;
+    c.residual = e.residual.data;
+    c.residual_rows = e.residual.rows;
+    c.residual_index = e.residual_rows;
+    c.value_scale = e.value_scale;
+    c.output_scale = e.output_scale;
+    c.residual_scale = e.residual_scale;
+    c.activation = static_cast<int>(e.activation);
+    c.alpha = e.alpha;
+    c.raw = e.raw.data;
+    c.gate = e.gate.data;
+    c.gate_rows = e.gate.rows;
+    c.condition = e.condition.data;
+    c.condition_rows = e.condition.rows;
+    c.rows_per_sequence = e.rows_per_sequence;
+    c.valid_rows_per_sequence = e.valid_rows_per_sequence;
+    c.input_repeat = e.input_repeat;
+    return c;
+}
+
+// The reference's check_same for a vector ([cols]) or row-matching operand.
+void check_operand(const TensorView &v, Type type, int cols, const char *what) {
+    if (v.data && (v.type != type || v.cols != cols || !v.dense()))
+        throw std::invalid_argument(what);
+}
+}  // namespace
+
+void pointwise_quantize(TensorView x, RowScaledView q, const Epilogue &e, TensorView retained, int) {
+    q.validate();
+    if (!x.dense() || (retained.data && (retained.type != x.type || retained.rows != q.values.rows ||
+                                         retained.cols != q.values.cols || !retained.dense())))
+        throw std::invalid_argument("quantized sequence output requires dense F16/BF16 rows");
+    if (e.bias.data && (e.bias.type != x.type || e.bias.numel() != size_t(q.values.cols)))
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    check_operand(e.residual, x.type, q.values.cols, "invalid indexed residual");
+    check_operand(e.raw, x.type, q.values.cols, "sequence operation shape/type mismatch");
+    check_operand(e.gate, x.type, q.values.cols, "invalid epilogue gate");
+    check_operand(e.condition, x.type, q.values.cols, "invalid epilogue condition");
+    if (e.raw.data && e.raw.rows != q.values.rows)
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    if (x.cols != q.values.cols)
+        throw std::invalid_argument("invalid quantized pointwise input/repetition");
+    const qlin_epilogue c = to_c(e);
+    check(qlin_pointwise_quantize(x.data, x.rows, code(x.type), &c, retained.data, q.values.rows,
+                                  q.values.cols, q.values.data, q.scales.ptr<float>(),
+                                  code(q.values.type), q.group_size, q.rotation_size,
+                                  context(x.device).stream()),
+          "pointwise quantize");
+}
+
+void layer_norm_quantize(TensorView x, RowScaledView q, TensorView weight, TensorView bias,
+                         float eps, const NormFusion &f, TensorView retained) {
+    q.validate();
+    const int cols = q.values.cols;
+    if (!x.dense() || x.cols != cols ||
+        (retained.data && (retained.type != x.type || retained.rows != q.values.rows ||
+                           retained.cols != cols || !retained.dense())))
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    for (const TensorView *v : std::initializer_list<const TensorView *>{&weight, &bias, &f.projection_bias})
+        if (v->data && (v->type != x.type || v->numel() != size_t(cols)))
+            throw std::invalid_argument("sequence operation shape/type mismatch");
+    for (const TensorView *v : std::initializer_list<const TensorView *>{&f.residual, &f.raw, &f.gate, &f.shift, &f.scale})
+        check_operand(*v, x.type, cols, "sequence operation shape/type mismatch");
+    if (f.residual.data && f.residual.rows != x.rows)
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    qlin_norm_fusion c;
+    qlin_norm_fusion_init(&c);
+    c.residual = f.residual.data;
+    c.projection_bias = f.projection_bias.data;
+    c.gate = f.gate.data;
+    c.gate_rows = f.gate.rows;
+    c.shift = f.shift.data;
+    c.shift_rows = f.shift.rows;
+    c.scale = f.scale.data;
+    c.scale_rows = f.scale.rows;
+    c.raw = f.raw.data;
+    c.rows_per_sequence = f.rows_per_sequence;
+    c.source_rows = f.source_rows;
+    check(qlin_layer_norm_quantize(x.data, x.rows, code(x.type), weight.data, bias.data, eps, &c,
+                                   retained.data, q.values.rows, cols, q.values.data,
+                                   q.scales.ptr<float>(), code(q.values.type), q.group_size,
+                                   q.rotation_size, context(x.device).stream()),
+          "layer norm quantize");
 }
 
 // ops/basic.cpp:54-58

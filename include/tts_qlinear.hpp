@@ -139,11 +139,24 @@ namespace ops {
 // Activation kinds (reference ops/activation.h:4); the quantized finish
 // supports Relu and GeluTanh (ops/cuda/quantization.cpp:75-82).
 enum class Activation { Identity, Relu, LeakyRelu, Silu, Gelu, GeluTanh, Mish, Tanh, Sigmoid };
-// The subset of the reference ops::Epilogue (ops/sequence.h:8-30) that the
-// fused quantized finish covers: bias [N] in the output type and activation.
+// The reference's ops::Epilogue (ops/sequence.h:8-27) without the packed /
+// indirect addressing (packed, condition_sources, output_rows), which only
+// its non-quantized pointwise consumers use. The quantized GEMM's fused
+// finish covers bias + ReLU / tanh-GeLU; pointwise_quantize covers all of it.
 struct Epilogue {
-    TensorView bias;
+    TensorView bias, residual;
+    float value_scale = 1;
+    float output_scale = 1;
+    float residual_scale = 1;
     Activation activation = Activation::Identity;
+    float alpha = .1f;
+    TensorView raw;
+    TensorView gate;
+    TensorView condition;
+    int rows_per_sequence = 1;
+    int valid_rows_per_sequence = 0;  // zero disables sequence-tail masking
+    int input_repeat = 1;
+    const int *residual_rows = nullptr;  // index into residual rows; negative = none
 };
 // Fusions of a normalization's input (reference ops/sequence.h:55-59). The
 // fused normalized projection declines source_rows (normalized_linear
@@ -238,6 +251,14 @@ void bind(int device, QuantizedGemm *gemm);
 QuantizedGemm &context(int device);
 
 void quantize_rows(TensorView input, RowScaledView output);
+// Pointwise epilogue -> row quantization (reference ops/sequence.h:38-42,
+// sequence_pointwise.cu:307-357); `multiprocessors` is accepted and unused.
+void pointwise_quantize(TensorView x, RowScaledView quantized, const Epilogue &e = {},
+                        TensorView retained = {}, int multiprocessors = 0);
+// LayerNorm -> row quantization (reference ops/sequence.h:63-65,
+// sequence_norm.cu:412-440).
+void layer_norm_quantize(TensorView x, RowScaledView quantized, TensorView weight, TensorView bias,
+                         float eps, const NormFusion &fusion = {}, TensorView retained = {});
 void matmul(RowScaledView input, RowScaledView weight, TensorView output);
 void prepare_quantized(TensorView weight, int rows, int output_channels, int input_channels,
                        Type type, QuantizationGroups groups = {});
@@ -246,10 +267,15 @@ void linear(TensorView input, RowScaledView weight, TensorView output, RowScaled
 void quantized_norm(TensorView input, TensorView update, TensorView weight, RowScaledView output,
                     float epsilon, bool gemma = false, TensorView scale = {});
 void quantized_gated(TensorView input, RowScaledView output, int kind);
-// ops::linear quantized branch with a bias/activation epilogue: the finish is
-// fused into the GEMM (ops/linear.cpp:71-93).
+// ops::linear's quantized branch with an epilogue (ops/linear.cpp:26-93):
+// bias + ReLU / tanh-GeLU is fused into the GEMM; with `quantized_output`
+// the output is also quantized for the next layer, through the fused finish
+// and quantize_rows, or the GEMM and pointwise_quantize for any other dense
+// epilogue. Without `quantized_output`, an epilogue beyond the fused finish
+// is rejected (the reference's non-quantized pointwise pass is not part of
+// this library).
 void linear(TensorView input, RowScaledView weight, TensorView bias, TensorView output,
-            Epilogue epilogue, RowScaledView scratch);
+            Epilogue epilogue, RowScaledView scratch, RowScaledView quantized_output = {});
 }  // namespace ops
 
 }  // namespace tts

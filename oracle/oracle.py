@@ -90,6 +90,10 @@ def lib():
         L.orc_layer_norm_quantize.restype = i
         L.orc_layer_norm_quantize.argtypes = [P, i, i, P, P, ctypes.c_float, P, P, i, i, P, P, i,
                                               i, i]
+        L.orc_qexp.restype = ctypes.c_float
+        L.orc_qexp.argtypes = [ctypes.c_float]
+        L.orc_qtanh.restype = ctypes.c_float
+        L.orc_qtanh.argtypes = [ctypes.c_float]
         L.orc_act.restype = ctypes.c_float
         L.orc_act.argtypes = [ctypes.c_float, i, ctypes.c_float]
         L.orc_gelu_tanh_contracted.restype = ctypes.c_float
@@ -449,6 +453,14 @@ def layer_norm_quantize(x_bits, fmt: int, norm_weight=None, norm_bias=None, eps:
     if rc:
         raise ValueError("oracle: unsupported layer norm quantize layout")
     return q, sc, ret, raw_out
+
+
+def qexp(x: float) -> float:
+    return lib().orc_qexp(float(x))
+
+
+def qtanh(x: float) -> float:
+    return lib().orc_qtanh(float(x))
 
 
 def act(x: float, kind: int, alpha: float = 0.1) -> float:

@@ -275,19 +275,66 @@ int orc_quantized_norm(uint16_t *residual, const uint16_t *update, const uint16_
     return status;
 }
 
+/* The library's fp32 exponential (the reference's expf / __expf approximate
+ * the same function): Cody-Waite reduction x = k ln2 + r with ln2 split into
+ * a 16-bit head 0x1.62e4p-1 (k * head exact) and a tail, e^r by its Taylor
+ * polynomial to degree 8 in Horner form with fmaf, scaled by 2^k as two
+ * exact power-of-two factors (one final rounding). inf above 89, 0 below
+ * -104, NaN kept. */
+float orc_qexp(float x) {
+    if (x != x) return x;
+    x = fminf(fmaxf(x, -104.f), 89.f);
+    float k = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-k, 0x1.62e4p-1f, x);
+    r = fmaf(-k, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-16f;
+    p = fmaf(p, r, 0x1.a01a02p-13f);
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.f);
+    p = fmaf(p, r, 1.f);
+    int ki = (int)k, k1 = ki / 2, k2 = ki - k1;
+    return (p * u2f((uint32_t)(k1 + 127) << 23)) * u2f((uint32_t)(k2 + 127) << 23);
+}
+
+/* The library's fp32 tanh: odd Taylor series to degree 15 for |y| < 0.5,
+ * else 1 - 2/(e^{2|y|} + 1) with orc_qexp; 1 beyond 9.1; sign of y. */
+float orc_qtanh(float y) {
+    if (y != y) return y;
+    float a = fabsf(y), t;
+    if (a < 0.5f) {
+        float s = a * a;
+        float p = -0x1.7da364p-10f;
+        p = fmaf(p, s, 0x1.d6d3d0p-9f);
+        p = fmaf(p, s, -0x1.226e36p-7f);
+        p = fmaf(p, s, 0x1.664f48p-6f);
+        p = fmaf(p, s, -0x1.ba1ba2p-5f);
+        p = fmaf(p, s, 0x1.111112p-3f);
+        p = fmaf(p, s, -0x1.555556p-2f);
+        t = fmaf(a * s, p, a);
+    } else if (a < 9.1f) {
+        t = 1.f - 2.f / (orc_qexp(2.f * a) + 1.f);
+    } else {
+        t = 1.f;
+    }
+    return copysignf(t, y);
+}
+
 /* activate<Kind> (quant_gated.cu:9-16): SiLU (kind 0) as
  * (x*2^-16) / ((1 + e^-x) * 2^-16), tanh-GeLU (kind 1) as
  * (0.5x)(1 + tanh(0.7978845608028654f * (x + ((0.044715f*x)*x)*x))), fp32
- * arithmetic with e^-x and tanh rounded once from fp64 (the reference's
- * __expf, __fdividef and tanhf approximate these within a few ulp). */
+ * arithmetic with e^-x and tanh from orc_qexp / orc_qtanh (the reference's
+ * __expf, __fdividef and tanhf approximate the same functions). */
 float orc_activate(float x, int kind) {
     if (kind == 0) {
-        float e = (float)exp(-(double)x);
+        float e = orc_qexp(-x);
         return (x * 0x1p-16f) / ((1.f + e) * 0x1p-16f);
     }
     float inner = x + ((0.044715f * x) * x) * x;
-    float t = (float)tanh((double)(0.7978845608028654f * inner));
-    return (0.5f * x) * (1.f + t);
+    return (0.5f * x) * (1.f + orc_qtanh(0.7978845608028654f * inner));
 }
 
 /* launch_quantized_gated / vector_gated_quantize (quant_gated.cu:18-85,
@@ -315,12 +362,11 @@ int orc_quantized_gated(const uint16_t *input, int src_type, int rows, int width
 
 /* tanh-GeLU as the reference's activation.cuh:15 compiles with FMA
  * contraction (the GEMM epilogue and the pointwise finish TUs): inner =
- * fma((0.044715x)x, x, x); tanh rounded once from fp64 (the reference uses
+ * fma((0.044715x)x, x, x); tanh by orc_qtanh (the reference uses
  * cutlass::fast_tanh). */
 float orc_gelu_tanh_contracted(float x) {
     float inner = fmaf((0.044715f * x) * x, x, x);
-    float t = (float)tanh((double)(0.7978845608028654f * inner));
-    return (0.5f * x) * (1.f + t);
+    return (0.5f * x) * (1.f + orc_qtanh(0.7978845608028654f * inner));
 }
 
 /* ---------------------------------------------------------------- finish */
@@ -467,23 +513,25 @@ int orc_layer_norm_quantize(const uint16_t *x, int x_rows, int type, const uint1
 }
 
 /* ops::activate (ops/kernels/common/activation.cuh:5-26), Activation
- * numbering of ops/activation.h:4. Transcendentals are evaluated in fp64 and
- * rounded once to fp32 at the points the reference rounds its fp32 library
- * calls (expf, erff, log1pf, tanhf, cutlass::fast_tanh approximate them);
- * tanh-GeLU's inner term is contracted as the pointwise TU compiles it. */
+ * numbering of ops/activation.h:4. SiLU, sigmoid, tanh and tanh-GeLU use
+ * orc_qexp / orc_qtanh; GeLU's erf and Mish's exp / log1p / tanh are
+ * evaluated in fp64 and rounded once to fp32 at the points the reference
+ * rounds its fp32 library calls (expf, erff, log1pf and tanhf approximate
+ * them); tanh-GeLU's inner term is contracted as the pointwise TU compiles
+ * it. */
 float orc_act(float x, int kind, float alpha) {
     switch (kind) {
     case 1: return fmaxf(x, 0.f);
     case 2: return x >= 0.f ? x : x * alpha;
-    case 3: return x / (1.f + (float)exp(-(double)x));
+    case 3: return x / (1.f + orc_qexp(-x));
     case 4: return (0.5f * x) * (1.f + (float)erf((double)(x * 0.7071067811865475f)));
     case 5: return orc_gelu_tanh_contracted(x);
     case 6: {
         float sp = x > 20.f ? x : (float)log1p((double)(float)exp((double)x));
         return x * (float)tanh((double)sp);
     }
-    case 7: return (float)tanh((double)x);
-    case 8: return 1.f / (1.f + (float)exp(-(double)x));
+    case 7: return orc_qtanh(x);
+    case 8: return 1.f / (1.f + orc_qexp(-x));
     default: return x;
     }
 }

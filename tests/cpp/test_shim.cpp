@@ -197,9 +197,35 @@ static int gpu_test(const std::string &dir) {
         QuantizationWorkspace workspace(M, QuantizationWorkspace::Capacity::matrix(K, groups.activation));
         RowScaledView scratch = workspace.view(M, K, fmt, groups);
         scratch.values.device = scratch.scales.device = 0;
-        std::ifstream act_file(dir + "/finish.txt");
-        int act = 0;
-        if (act_file >> act && act) {
+        std::ifstream act_file(dir + "/finish.txt"), epi_file(dir + "/epilogue.txt");
+        int act = 0, activation = 0, use_residual = 0;
+        if (epi_file >> activation >> use_residual) {
+            // ops::linear with a quantized output for the next layer
+            // (ops/linear.cpp:35-78): bias + activation (+ residual), then codes.
+            auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
+            auto r = read_file<uint16_t>(dir + "/residual.bf16", size_t(M) * N);
+            void *db, *dr, *dq, *dqs;
+            HIP(hipMalloc(&db, b.size() * 2));
+            HIP(hipMalloc(&dr, r.size() * 2));
+            HIP(hipMalloc(&dq, size_t(M) * N));
+            HIP(hipMalloc(&dqs, size_t(M) * 4));
+            HIP(hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice));
+            HIP(hipMemcpy(dr, r.data(), r.size() * 2, hipMemcpyHostToDevice));
+            ops::Epilogue e;
+            e.activation = static_cast<ops::Activation>(activation);
+            if (use_residual) e.residual = TensorView(dr, M, N, Type::BF16, 0, 0);
+            RowScaledView next{TensorView(dq, M, N, fmt, 0, 0), TensorView(dqs, M, 1, Type::F32, 0, 0)};
+            ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq, TensorView(db, 1, N),
+                        TensorView(dy, M, N, Type::BF16, 0, 0), e, scratch, next);
+            HIP(hipStreamSynchronize(stream));
+            std::vector<uint8_t> qh(size_t(M) * N);
+            std::vector<float> qsh(M);
+            HIP(hipMemcpy(qh.data(), dq, qh.size(), hipMemcpyDeviceToHost));
+            HIP(hipMemcpy(qsh.data(), dqs, qsh.size() * 4, hipMemcpyDeviceToHost));
+            write_file(dir + "/next.u8", qh);
+            write_file(dir + "/next_scales.f32", qsh);
+            for (void *p : {db, dr, dq, dqs}) (void)hipFree(p);
+        } else if (act_file >> act && act) {
             // ops::linear with a bias + activation epilogue (fused finish)
             auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
             void *db;

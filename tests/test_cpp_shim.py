@@ -116,3 +116,41 @@ def test_linear_finish_end_to_end(dev, orc, tmp_path, act):
     xq, sx = orc.quantize_rows(xb, I8)
     plain = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw, order=0)
     assert np.array_equal(y, orc.finish(plain, bias, act))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("activation,use_residual", [(1, 0), (5, 0), (3, 1), (6, 0)])
+def test_linear_quantized_output_end_to_end(dev, orc, tmp_path, activation, use_residual):
+    """ops::linear with a quantized output (ops/linear.cpp:35-78): a bias +
+    ReLU / tanh-GeLU epilogue takes the fused finish then quantize_rows; SiLU,
+    Mish or a residual take the GEMM then pointwise_quantize. The stored
+    output and the next layer's codes/scales against the oracle."""
+    M, N, K = 32, 512, 1024
+    xb = synthetic.activations(M, K, seed=activation)
+    wb = synthetic.weights(N, K, seed=activation)
+    rng = np.random.default_rng(activation)
+    bias = synthetic.f32_to_bf16_bits(rng.standard_normal(N) * 0.1)
+    res = synthetic.f32_to_bf16_bits(rng.standard_normal((M, N)))
+    for name, a in (("x", xb), ("w", wb), ("bias", bias), ("residual", res)):
+        a.tofile(tmp_path / f"{name}.bf16")
+    (tmp_path / "shape.txt").write_text(f"{M} {N} {K} int8\n")
+    (tmp_path / "epilogue.txt").write_text(f"{activation} {use_residual}\n")
+    print(f"test_shim gpu quantized output act={activation} residual={use_residual}", flush=True)
+    r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    y = np.fromfile(tmp_path / "y.bf16", np.uint16).reshape(M, N)
+    codes = np.fromfile(tmp_path / "next.u8", np.uint8).reshape(M, N)
+    scales = np.fromfile(tmp_path / "next_scales.f32", np.float32)
+    wq, sw = orc.quantize_rows(wb, I8)
+    xq, sx = orc.quantize_rows(xb, I8)
+    plain = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw, order=0)
+    if activation in (1, 5) and not use_residual:
+        assert np.array_equal(y, orc.finish(plain, bias, 1 if activation == 1 else 2))
+        q, s = orc.quantize_rows(y, I8)
+    else:
+        assert np.array_equal(y, plain)
+        q, s, _, _ = orc.pointwise_quantize(plain, I8, bias=bias, activation=activation,
+                                            residual=res if use_residual else None)
+    assert np.array_equal(codes, q)
+    assert np.array_equal(scales, s)

@@ -382,3 +382,38 @@ def test_pointwise_matches_torch(orc):
     # an index past the residual's rows contributes NaN
     _, _, out, _ = orc.pointwise_quantize(x, 4, residual=res, residual_index=np.array([0, 9, 1, 2], np.int32))
     assert np.all(np.isnan(_bf(out[1]).numpy())) and not np.isnan(_bf(out[0]).numpy()).any()
+
+
+def _ulps(got, ref):
+    """|got - ref| in units of the fp32 spacing at ref (denormal spacing floor)."""
+    ref = np.asarray(ref, np.float64)
+    sp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    return np.abs(np.asarray(got, np.float64) - ref) / np.maximum(sp, 2.0 ** -149)
+
+
+def test_qexp_within_one_ulp(orc):
+    """The fp32 exponential: within 1 ulp of fp64 exp over its whole finite
+    range (incl. subnormal results), exact at 0, inf above / 0 below the
+    range, NaN kept."""
+    rng = np.random.default_rng(1)
+    xs = np.concatenate([rng.uniform(-104, 88.7, 40000), rng.uniform(-1, 1, 20000),
+                         np.linspace(-103.9, -87, 3000)]).astype(np.float32)
+    got = np.array([orc.qexp(x) for x in xs], np.float32)
+    assert _ulps(got, np.exp(xs.astype(np.float64))).max() < 1.0
+    assert orc.qexp(0.0) == 1.0
+    assert orc.qexp(89.0) == np.inf and orc.qexp(1e4) == np.inf
+    assert orc.qexp(-104.0) == 0.0 and orc.qexp(-1e4) == 0.0
+    assert np.isnan(orc.qexp(float("nan")))
+
+
+def test_qtanh_within_two_ulp(orc):
+    """The fp32 tanh: within 2 ulp of fp64 tanh on both branches, odd, 1
+    beyond 9.1, tanh(0) = 0, NaN kept."""
+    rng = np.random.default_rng(2)
+    xs = np.concatenate([rng.uniform(-10, 10, 40000), rng.uniform(-0.6, 0.6, 40000),
+                         np.float32([0.4999999, 0.5, 0.5000001, 9.0999, 9.1])]).astype(np.float32)
+    got = np.array([orc.qtanh(x) for x in xs], np.float32)
+    assert _ulps(got, np.tanh(xs.astype(np.float64))).max() < 2.0
+    assert all(orc.qtanh(-x) == -orc.qtanh(x) for x in xs[:1000])
+    assert orc.qtanh(0.0) == 0.0 and orc.qtanh(12.0) == 1.0 and orc.qtanh(-30.0) == -1.0
+    assert np.isnan(orc.qtanh(float("nan")))
