@@ -38,6 +38,8 @@
 //    rounded once to fp32 (the reference's expf, erff, log1pf, tanhf and
 //    cutlass::fast_tanh approximate the same values); tanh-GeLU's inner term
 //    is fma((0.044715x)x, x, x) as the contracting TUs compile it.
+#include <algorithm>
+
 #include "qlin_device.hpp"
 #include "qlin_internal.hpp"
 #include "row_encode.hpp"
@@ -392,7 +394,7 @@ template <int Fmt, class T>
 __global__ __launch_bounds__(256) void norm_project(
     const uint16_t *__restrict__ x, qlin_norm_fusion f, const uint16_t *__restrict__ nw,
     const uint16_t *__restrict__ nb, int k, float eps, const uint8_t *__restrict__ w,
-    const float *__restrict__ sw, int n, const uint16_t *__restrict__ bias, int act,
+    const float *__restrict__ sw, int n, int reps, const uint16_t *__restrict__ bias, int act,
     uint16_t *__restrict__ y, uint16_t *__restrict__ normalized, uint8_t *__restrict__ encoded,
     float *__restrict__ encoded_scales) {
     __shared__ float red[8];
@@ -462,8 +464,11 @@ __global__ __launch_bounds__(256) void norm_project(
         }
     }
     __syncthreads();
-    // One channel per 32-lane group: lane l covers words c = 4l + 128j.
-    const int l32 = t & 31, channel = blockIdx.x * 8 + (t >> 5);
+    // Channels blockIdx.x * 8 * reps + 8r + g for r < reps, one per 32-lane
+    // group g at a time: lane l covers words c = 4l + 128j.
+    const int l32 = t & 31;
+    for (int r = 0; r < reps; ++r) {
+    const int channel = (blockIdx.x * reps + r) * 8 + (t >> 5);
     if (channel >= n) return;
     const uint8_t *wr = w + size_t(channel) * k;
     float result;
@@ -493,6 +498,7 @@ __global__ __launch_bounds__(256) void norm_project(
         o = round16<T>(o + (bias ? to_float(bias[channel], T{}) : 0.f));
         if (act == FINISH_RELU) o = fmaxf(o, 0.f);
         y[size_t(row) * n + channel] = from_float(o, T{});
+    }
     }
 }
 
@@ -588,13 +594,17 @@ void launch_pointwise_quantize(const PointwiseQuantizeArgs &a, hipStream_t strea
 }
 
 void launch_norm_linear(const NormLinearArgs &a, hipStream_t stream) {
-    dim3 grid(unsigned((a.n + 7) / 8), unsigned(a.rows)), block(256);
+    // Each workgroup repeats the row's LayerNorm; give it 8 * reps channels so
+    // that about 2048 workgroups (8 per CU) cover the output.
+    const int blocks8 = (a.n + 7) / 8;
+    const int reps = std::max(1, std::min(16, int((size_t(blocks8) * a.rows + 2047) / 2048)));
+    dim3 grid(unsigned((blocks8 + reps - 1) / reps), unsigned(a.rows)), block(256);
 #define QLIN_NL(F, T)                                                                           \
     hipLaunchKernelGGL((norm_project<F, T>), grid, block, 0, stream,                           \
                        static_cast<const uint16_t *>(a.x), a.f,                                \
                        static_cast<const uint16_t *>(a.norm_weight),                           \
                        static_cast<const uint16_t *>(a.norm_bias), a.k, a.eps,                 \
-                       static_cast<const uint8_t *>(a.w), a.sw, a.n,                           \
+                       static_cast<const uint8_t *>(a.w), a.sw, a.n, reps,                     \
                        static_cast<const uint16_t *>(a.bias), a.act,                           \
                        static_cast<uint16_t *>(a.y), static_cast<uint16_t *>(a.normalized),   \
                        static_cast<uint8_t *>(a.encoded), a.encoded_scales)

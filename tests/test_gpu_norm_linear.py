@@ -22,7 +22,7 @@ def dev16(b, dtype, dev):
 @pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, BF16), (torch.float16, F16)])
 @pytest.mark.parametrize("fmt", [I8, FP8])
 @pytest.mark.parametrize("rows,k,n", [(1, 512, 600), (5, 320, 7), (64, 256, 96), (3, 4, 8),
-                                      (17, 100, 33)])
+                                      (17, 100, 33), (64, 512, 2040), (300, 128, 1000)])
 def test_norm_linear_parity(dev, orc, dtype, src_type, fmt, rows, k, n):
     from breeze_tts_cpp_amd import qlinear
     g = torch.Generator().manual_seed(rows * 31 + k + n + fmt)
