@@ -36,29 +36,6 @@
 namespace qlin {
 namespace {
 
-template <class T, bool Vec>
-__device__ __forceinline__ void store16x8(uint16_t *row, int column, int cols, const float (&v)[8]) {
-    if constexpr (Vec) {
-        if (column < cols) {
-            uint4 packed;
-            packed.x = pack2(v[0], v[1], T{});
-            packed.y = pack2(v[2], v[3], T{});
-            packed.z = pack2(v[4], v[5], T{});
-            packed.w = pack2(v[6], v[7], T{});
-            *reinterpret_cast<uint4 *>(row + column) = packed;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (column + i < cols) row[column + i] = from_float(v[i], T{});
-    }
-}
-
-// Correctly rounded 1/sqrt(a) in fp32.
-__device__ __forceinline__ float rsqrt_rn(float a) {
-    return float(1.0 / sqrt(double(a)));
-}
-
 // One 256-thread workgroup per row; lane t holds columns [8t, 8t+8).
 template <int Fmt, class T, bool Add, bool Scaled, bool Gemma, bool Rot, int G, bool Vec>
 __global__ __launch_bounds__(kThreads) void residual_rms_quantize(

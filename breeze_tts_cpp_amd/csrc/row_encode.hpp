@@ -1,5 +1,6 @@
 // Row encoders shared by the row quantizer and the fused quantizing producers
-// (residual + RMSNorm -> quant, gated activation -> quant): a 256-thread
+// (residual + RMSNorm, gated activation, LayerNorm and pointwise epilogue ->
+// quant), with their 8-column load/store helpers: a 256-thread
 // workgroup holds a row in registers, lane t owning the 8 columns
 // (it * 256 + t) * 8 .. +8 of each 2048-column chunk `it`, and encodes it per
 // token, per token after the H128 rotation, or per K group (optionally
@@ -54,6 +55,30 @@ __device__ __forceinline__ void store8(uint8_t *row, int column, int cols, const
         for (int i = 0; i < 8; ++i)
             if (column + i < cols) row[column + i] = uint8_t(code[i]);
     }
+}
+
+// 16-bit values of 8 columns [column, column+8) stored (rounded to T).
+template <class T, bool Vec>
+__device__ __forceinline__ void store16x8(uint16_t *row, int column, int cols, const float (&v)[8]) {
+    if constexpr (Vec) {
+        if (column < cols) {
+            uint4 packed;
+            packed.x = pack2(v[0], v[1], T{});
+            packed.y = pack2(v[2], v[3], T{});
+            packed.z = pack2(v[4], v[5], T{});
+            packed.w = pack2(v[6], v[7], T{});
+            *reinterpret_cast<uint4 *>(row + column) = packed;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (column + i < cols) row[column + i] = from_float(v[i], T{});
+    }
+}
+
+// Correctly rounded 1/sqrt(a) in fp32.
+__device__ __forceinline__ float rsqrt_rn(float a) {
+    return float(1.0 / sqrt(double(a)));
 }
 
 // H128 rotation of the 8 columns [column, column+8) held by this lane; the 16

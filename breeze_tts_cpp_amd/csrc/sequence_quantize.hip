@@ -76,9 +76,6 @@ __device__ __forceinline__ float block_max_256(float v, float *red) {
     return r;
 }
 
-// Correctly rounded 1/sqrt(a) in fp32.
-__device__ __forceinline__ float rsqrt_rn(float a) { return float(1.0 / sqrt(double(a))); }
-
 // Exact e4m3fn decode (OCP; 0x7f / 0xff NaN).
 __device__ __forceinline__ float decode_fp8(uint32_t c) {
     const uint32_t e = (c >> 3) & 15u, m = c & 7u;
@@ -131,24 +128,6 @@ __device__ __forceinline__ void activate8(float (&v)[8], int kind, float alpha) 
     default:
         for (int i = 0; i < 8; ++i) v[i] = activate_fp64(v[i], kind);
         break;
-    }
-}
-
-template <class T, bool Vec>
-__device__ __forceinline__ void store16x8(uint16_t *row, int column, int cols, const float (&v)[8]) {
-    if constexpr (Vec) {
-        if (column < cols) {
-            uint4 packed;
-            packed.x = pack2(v[0], v[1], T{});
-            packed.y = pack2(v[2], v[3], T{});
-            packed.z = pack2(v[4], v[5], T{});
-            packed.w = pack2(v[6], v[7], T{});
-            *reinterpret_cast<uint4 *>(row + column) = packed;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (column + i < cols) row[column + i] = from_float(v[i], T{});
     }
 }
 

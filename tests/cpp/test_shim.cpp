@@ -320,10 +320,82 @@ static int producers_test(const std::string &dir) {
     return 0;
 }
 
+// ops::layer_norm_quantize (hidden 2048, K128 groups + rotation) and
+// QuantizedGemm::normalized_linear (LayerNorm + residual -> INT8 GEMV, k 512)
+// through the C++ interface.
+static int sequence_test(const std::string &dir) {
+    int M;
+    std::ifstream(dir + "/shape.txt") >> M;
+    const int H = 2048, k = 512, n = 384;
+    auto x = read_file<uint16_t>(dir + "/x.bf16", size_t(M) * H);
+    auto lw = read_file<uint16_t>(dir + "/lw.bf16", size_t(H));
+    auto xs = read_file<uint16_t>(dir + "/xs.bf16", size_t(M) * k);
+    auto rs = read_file<uint16_t>(dir + "/rs.bf16", size_t(M) * k);
+    auto ws = read_file<uint16_t>(dir + "/ws.bf16", size_t(n) * k);
+    void *dx, *dlw, *dq, *dqs, *dxs, *drs, *dws, *dwq, *dsw, *dy, *dnorm, *dgemm;
+    HIP(hipMalloc(&dx, x.size() * 2));
+    HIP(hipMalloc(&dlw, lw.size() * 2));
+    HIP(hipMalloc(&dq, size_t(M) * H));
+    HIP(hipMalloc(&dqs, size_t(H / 128) * M * 4));
+    HIP(hipMalloc(&dxs, xs.size() * 2));
+    HIP(hipMalloc(&drs, rs.size() * 2));
+    HIP(hipMalloc(&dws, ws.size() * 2));
+    HIP(hipMalloc(&dwq, size_t(n) * k));
+    HIP(hipMalloc(&dsw, size_t(n) * 4));
+    HIP(hipMalloc(&dy, size_t(M) * n * 2));
+    HIP(hipMalloc(&dnorm, size_t(M) * k * 2));
+    HIP(hipMalloc(&dgemm, 1 << 20));
+    HIP(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(dlw, lw.data(), lw.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(dxs, xs.data(), xs.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(drs, rs.data(), rs.size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMemcpy(dws, ws.data(), ws.size() * 2, hipMemcpyHostToDevice));
+    hipStream_t stream;
+    HIP(hipStreamCreate(&stream));
+    {
+        QuantizedGemm gemm(reinterpret_cast<qlin_stream_t>(stream), dgemm, 1 << 20, Type::I8);
+        ops::bind(0, &gemm);
+        RowScaledView q{TensorView(dq, M, H, Type::I8, 0, 0), TensorView(dqs, H / 128, M, Type::F32, 0, 0),
+                        128, 128};
+        ops::layer_norm_quantize(TensorView(dx, M, H, Type::BF16, 0, 0), q,
+                                 TensorView(dlw, 1, H, Type::BF16, 0, 0), TensorView(), 1e-5f);
+        RowScaledView wq{TensorView(dwq, n, k, Type::I8, 0, 0), TensorView(dsw, n, 1, Type::F32, 0, 0)};
+        ops::quantize_rows(TensorView(dws, n, k, Type::BF16, 0, 0), wq);
+        ops::NormFusion fusion;
+        fusion.residual = TensorView(drs, M, k, Type::BF16, 0, 0);
+        const bool fused = gemm.normalized_linear(
+            TensorView(dxs, M, k, Type::BF16, 0, 0), TensorView(dnorm, M, k, Type::BF16, 0, 0),
+            TensorView(), TensorView(), 1e-5f, fusion, wq, TensorView(dy, M, n, Type::BF16, 0, 0));
+        EXPECT(fused);
+        HIP(hipStreamSynchronize(stream));
+        std::vector<uint8_t> qh(size_t(M) * H), wqh(size_t(n) * k);
+        std::vector<float> qsh(size_t(H / 128) * M), swh(n);
+        std::vector<uint16_t> yh(size_t(M) * n), nh(size_t(M) * k);
+        HIP(hipMemcpy(qh.data(), dq, qh.size(), hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(qsh.data(), dqs, qsh.size() * 4, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(wqh.data(), dwq, wqh.size(), hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(swh.data(), dsw, swh.size() * 4, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(yh.data(), dy, yh.size() * 2, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(nh.data(), dnorm, nh.size() * 2, hipMemcpyDeviceToHost));
+        write_file(dir + "/lq.u8", qh);
+        write_file(dir + "/lqs.f32", qsh);
+        write_file(dir + "/wq.u8", wqh);
+        write_file(dir + "/sw.f32", swh);
+        write_file(dir + "/y.bf16", yh);
+        write_file(dir + "/norm.bf16", nh);
+        ops::bind(0, nullptr);
+    }
+    for (void *p : {dx, dlw, dq, dqs, dxs, drs, dws, dwq, dsw, dy, dnorm, dgemm}) (void)hipFree(p);
+    (void)hipStreamDestroy(stream);
+    std::printf("sequence test M=%d: %s\n", M, failures ? "FAILED" : "done");
+    return failures ? 1 : 0;
+}
+
 int main(int argc, char **argv) {
     if (argc >= 2 && std::string(argv[1]) == "host") return host_tests();
     if (argc >= 3 && std::string(argv[1]) == "gpu") return gpu_test(argv[2]);
     if (argc >= 3 && std::string(argv[1]) == "producers") return producers_test(argv[2]);
+    if (argc >= 3 && std::string(argv[1]) == "sequence") return sequence_test(argv[2]);
     std::fprintf(stderr, "usage: test_shim host | gpu DIR | producers DIR\n");
     return 2;
 }

@@ -154,3 +154,32 @@ def test_linear_quantized_output_end_to_end(dev, orc, tmp_path, activation, use_
                                             residual=res if use_residual else None)
     assert np.array_equal(codes, q)
     assert np.array_equal(scales, s)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 32])
+def test_sequence_end_to_end(dev, orc, tmp_path, M):
+    """ops::layer_norm_quantize (K128 groups + H128 rotation) and
+    QuantizedGemm::normalized_linear (LayerNorm + residual -> INT8 GEMV)
+    through the C++ interface, against the oracle."""
+    rng = np.random.default_rng(M)
+    x = synthetic.activations(M, 2048, seed=M)
+    lw = synthetic.f32_to_bf16_bits(1.0 + 0.05 * rng.standard_normal(2048))
+    xs = synthetic.activations(M, 512, seed=M + 1)
+    rs = synthetic.activations(M, 512, seed=M + 2)
+    ws = synthetic.weights(384, 512, seed=M)
+    for name, a in (("x", x), ("lw", lw), ("xs", xs), ("rs", rs), ("ws", ws)):
+        a.tofile(tmp_path / f"{name}.bf16")
+    (tmp_path / "shape.txt").write_text(f"{M}\n")
+    print(f"test_shim sequence M={M}", flush=True)
+    r = subprocess.run([_binary(), "sequence", str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    q, s, _, _ = orc.layer_norm_quantize(x, I8, norm_weight=lw, group=128, rotation=128)
+    assert np.array_equal(np.fromfile(tmp_path / "lq.u8", np.uint8).reshape(M, 2048), q)
+    assert np.array_equal(np.fromfile(tmp_path / "lqs.f32", np.float32), s.ravel())
+    wq, sw = orc.quantize_rows(ws, I8)
+    assert np.array_equal(np.fromfile(tmp_path / "wq.u8", np.uint8).reshape(384, 512), wq)
+    y, nrm, _, _, _ = orc.norm_linear(xs, wq, sw, I8, residual=rs)
+    assert np.array_equal(np.fromfile(tmp_path / "norm.bf16", np.uint16).reshape(M, 512), nrm)
+    assert np.array_equal(np.fromfile(tmp_path / "y.bf16", np.uint16).reshape(M, 384), y)
