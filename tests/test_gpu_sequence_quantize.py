@@ -152,3 +152,48 @@ def test_pointwise_quantize_in_place(dev, orc):
     assert np.array_equal(bits(xd), out)
     same_codes(qd, q)
     assert np.array_equal(sd.cpu().numpy(), s)
+
+
+def test_sequence_producers_in_a_graph(dev, orc):
+    """Graph capture: LayerNorm -> quant, pointwise -> quant and the LayerNorm
+    GEMV captured once on a side stream and replayed four times, with eager
+    launches and synchronizations between replays and the inputs changed in
+    place; every replay equals the oracle on the current inputs."""
+    from breeze_tts_cpp_amd import qlinear
+    M, H, k, n = 32, 2048, 512, 256
+    g = torch.Generator().manual_seed(17)
+    bfd = lambda t: t.to(torch.bfloat16).to(dev)
+    x, bias = bfd(torch.randn(M, H, generator=g)), bfd(0.3 * torch.randn(H, generator=g))
+    xs = bfd(torch.randn(M, k, generator=g))
+    wq_np, sw_np = orc.quantize_rows(bits(bfd(0.05 * torch.randn(n, k, generator=g))), I8)
+    wq, sw = torch.from_numpy(wq_np).to(dev), torch.from_numpy(sw_np).to(dev)
+    lq = torch.empty((M, H), dtype=torch.uint8, device=dev)
+    ls = torch.empty((M,), dtype=torch.float32, device=dev)
+    pq = torch.empty((M, H), dtype=torch.uint8, device=dev)
+    ps = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, n), dtype=torch.bfloat16, device=dev)
+    ep = qlinear.epilogue(bias=bias, activation=qlinear.ACT_SILU)
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        qlinear.layer_norm_quantize(x, I8, values=lq, scales=ls, stream=stream)
+        qlinear.pointwise_quantize(x, I8, ep, values=pq, scales=ps, stream=stream)
+        qlinear.norm_linear(xs, wq, sw, I8, out=y, stream=stream)
+    for replay in range(4):
+        print(f"sequence graph replay {replay}", flush=True)
+        with torch.no_grad():
+            x.copy_(bfd(torch.randn(M, H, generator=g) * (1 + replay)))
+            xs.copy_(bfd(torch.randn(M, k, generator=g)))
+        qlinear.row_quantize(x, I8)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        xb, xsb = bits(x), bits(xs)
+        q, s, _, _ = orc.layer_norm_quantize(xb, I8)
+        same_codes(lq, q)
+        assert np.array_equal(ls.cpu().numpy(), s)
+        q, s, _, _ = orc.pointwise_quantize(xb, I8, bias=bits(bias), activation=3)
+        same_codes(pq, q)
+        assert np.array_equal(ps.cpu().numpy(), s)
+        yo, _, _, _, _ = orc.norm_linear(xsb, wq_np, sw_np, I8)
+        assert np.array_equal(bits(y), yo)
