@@ -109,35 +109,37 @@ __device__ __forceinline__ void rotate8(float (&v)[8], int column) {
     for (int i = 0; i < 8; ++i) v[i] *= 0.08838834764831845f;
 }
 
-__device__ __forceinline__ float block_max(float v) {
-    __shared__ float partial[kThreads / 64];
+// Max over the NT threads of the workgroup.
+template <int NT = kThreads> __device__ __forceinline__ float block_max(float v) {
+    __shared__ float partial[NT / 64];
     v = group_max<64>(v);
     if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = v;
     __syncthreads();
     float r = partial[0];
 #pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, partial[w]);
+    for (int w = 1; w < NT / 64; ++w) r = fmaxf(r, partial[w]);
     return r;
 }
 
-// Encode a row held in registers (v[it][i] = column (it*kThreads + t)*8 + i;
-// columns past `cols` hold 0): optional H128 rotation, then per-(row, G) scales
-// ([ceil(cols/G), rows]) when G > 0, else one per-token scale ([rows]).
-// The reference's rotated_quantize / encode_group / token paths
-// (quant_device.cuh:63-88,145-195, row_quantize.cu:24-165).
-template <int Fmt, int Items, bool Rot, int G, bool Vec>
+// Encode a row held in registers by NT threads (v[it][i] = column
+// (it*NT + t)*8 + i; columns past `cols` hold 0): optional H128 rotation, then
+// per-(row, G) scales ([ceil(cols/G), rows]) when G > 0, else one per-token
+// scale ([rows]). The reference's rotated_quantize / encode_group / token
+// paths (quant_device.cuh:63-88,145-195, row_quantize.cu:24-165). Groups and
+// rotation blocks stay inside one wave for any NT (multiples of 64).
+template <int Fmt, int Items, bool Rot, int G, bool Vec, int NT = kThreads>
 __device__ __forceinline__ void encode_row(float (&v)[Items][8], uint8_t *__restrict__ q,
                                            float *__restrict__ scales, int row, int rows,
                                            int cols) {
     uint8_t *dst = q + size_t(row) * cols;
     if constexpr (Rot) {
 #pragma unroll
-        for (int it = 0; it < Items; ++it) rotate8(v[it], (it * kThreads + threadIdx.x) * 8);
+        for (int it = 0; it < Items; ++it) rotate8(v[it], (it * NT + threadIdx.x) * 8);
     }
     if constexpr (G > 0) {
 #pragma unroll
         for (int it = 0; it < Items; ++it) {
-            const int column = (it * kThreads + threadIdx.x) * 8;
+            const int column = (it * NT + threadIdx.x) * 8;
             float amax = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[it][i]));
@@ -152,12 +154,12 @@ __device__ __forceinline__ void encode_row(float (&v)[Items][8], uint8_t *__rest
         for (int it = 0; it < Items; ++it)
 #pragma unroll
             for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[it][i]));
-        const float step = quant_scale<Fmt>(block_max(amax));
+        const float step = quant_scale<Fmt>(block_max<NT>(amax));
         const float inverse = 1.f / step;
         if (threadIdx.x == 0) scales[row] = step;
 #pragma unroll
         for (int it = 0; it < Items; ++it)
-            store8<Fmt, Vec>(dst, (it * kThreads + threadIdx.x) * 8, cols, v[it], inverse);
+            store8<Fmt, Vec>(dst, (it * NT + threadIdx.x) * 8, cols, v[it], inverse);
     }
 }
 

@@ -118,3 +118,21 @@ def test_quantized_gated_extremes(dev, orc):
             qd, sd = qlinear.quantized_gated(to_dev(inp, torch.bfloat16, dev), fmt, kind=kind)
             assert np.array_equal(qd.cpu().numpy(), q)
             assert np.array_equal(sd.cpu().numpy(), sc)
+
+
+@pytest.mark.parametrize("width", [6144, 8192])
+def test_quantized_gated_many_rows(dev, orc, width):
+    """Above the spread threshold (512 rows) each lane walks several 2048-column
+    chunks; both layouts give the oracle's codes and scales."""
+    from breeze_tts_cpp_amd import qlinear
+    rows = 520
+    for kind in (0, 1):
+        for group, rot in ((0, 0), (128, 128)):
+            print(f"gated many rows width={width} kind={kind} group={group} rot={rot}", flush=True)
+            inp = rand_bits((rows, 2 * width), torch.bfloat16, width + kind + group, 2.0)
+            q, sc, _ = orc.quantized_gated(inp, kind, 4, group=group, rotation=rot)
+            qd, sd = qlinear.quantized_gated(to_dev(inp, torch.bfloat16, dev), 4, kind=kind,
+                                             group=group, rotation=rot)
+            torch.cuda.synchronize()
+            assert np.array_equal(qd.cpu().numpy(), q)
+            assert np.array_equal(sd.cpu().numpy(), sc)
