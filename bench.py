@@ -292,13 +292,17 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
 
 def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
     """M=4096 INT8 and FP8 GEMMs over the four projections (BASELINE configs 2
-    and 4): TOPS = 2*M*N*K / kernel time, averaged over graph replays."""
+    and 4): TOPS = 2*M*N*K / kernel time. Per format, the four projections'
+    graphs (10 GEMMs each) are built, warmed up together for about 30 replays
+    each (the clock settles upward under sustained MFMA load), then timed in
+    5 interleaved rounds of 3 replays; each projection reports its median."""
+    import statistics
     out = {}
     M = M_PREFILL
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps, rounds, per_round = 10, 5, 3
     for fmt_name, fmt in (("int8", qlinear.I8), ("fp8", qlinear.FP8)):
-        rows = {}
-        total_ops, total_us = 0, 0.0
+        legs = {}
         for name, (N, K) in synthetic.PROJECTIONS.items():
             x = torch.from_numpy(synthetic.activations(M, K, seed=1).view(np.int16)).view(
                 torch.bfloat16).to(dev)
@@ -313,31 +317,40 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
                 ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
-            reps = 10
             with torch.cuda.graph(g, stream=stream):
                 for _ in range(reps):
                     qlinear.gemm(xq, sx, wq, sw, fmt, path=path, out=y, workspace=ws,
                                  stream=stream)
-            torch.cuda.synchronize()
-            for _ in range(4):  # warm-up: clocks settle under sustained MFMA load
-                g.replay()
-            torch.cuda.synchronize()
-            n_rep = 10
-            with torch.cuda.stream(stream):
-                start.record(stream)
-                for _ in range(n_rep):
-                    g.replay()
-                end.record(stream)
-            torch.cuda.synchronize()
-            us = start.elapsed_time(end) * 1e3 / (n_rep * reps)
-            ops = 2 * M * N * K
+            legs[name] = {"graph": g, "N": N, "K": K, "path": path, "keep": (xq, sx, wq, sw, y, ws),
+                          "us": []}
+            del x, w
+        torch.cuda.synchronize()
+        for _ in range(30):
+            for leg in legs.values():
+                leg["graph"].replay()
+        torch.cuda.synchronize()
+        for r in range(rounds):
+            order = list(legs) if r % 2 == 0 else list(reversed(legs))
+            for name in order:
+                with torch.cuda.stream(stream):
+                    start.record(stream)
+                    for _ in range(per_round):
+                        legs[name]["graph"].replay()
+                    end.record(stream)
+                torch.cuda.synchronize()
+                legs[name]["us"].append(start.elapsed_time(end) * 1e3 / (per_round * reps))
+        rows = {}
+        total_ops, total_us = 0, 0.0
+        for name, leg in legs.items():
+            us = statistics.median(leg["us"])
+            ops = 2 * M * leg["N"] * leg["K"]
             total_ops += ops
             total_us += us
-            rows[name] = {"N": N, "K": K, "us": round(us, 2),
+            p = leg["path"]
+            rows[name] = {"N": leg["N"], "K": leg["K"], "us": round(us, 2),
                           "TOPS": round(ops / (us * 1e-6) / 1e12, 1),
-                          "path": [path.kind, path.tokens, path.channels, path.splits,
-                                   path.waves]}
-            del g, x, w, xq, wq, y, ws
+                          "path": [p.kind, p.tokens, p.channels, p.splits, p.waves]}
+        del legs
         tops = total_ops / (total_us * 1e-6) / 1e12
         peak = I8_PEAK_TOPS if fmt_name == "int8" else FP8_PEAK_TFLOPS
         out[fmt_name] = {"TOPS": round(tops, 1), "frac_mfma": round(tops / peak, 4),

@@ -92,23 +92,46 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         if (p.staged && qlin::skinny_lds_bytes(a, to_internal(p)) > qlin::kLdsBytes) p.staged = 0;
         return p;
     }
-    // Prefill: the largest macro tile that still gives every CU a tile.
-    // 256x256 runs eight waves of 128x64 for INT8 (16x16x64 MFMA) and four
-    // waves of 128x128 for FP8 (32x32x64 MFMA), the faster shape of each
-    // format on MI355X at M=4096; 256x128 and 128x128 run four waves.
+    // Prefill: the macro tile by measured MI355X rules (BASELINE projections
+    // at M = 1024 and 4096, per-channel and K128 groups, realistic data).
+    // A grid is run in rounds of 256 workgroups (one per CU); `full` says its
+    // last round is at least 90% occupied.
+    //  - INT8 per-channel: 256x256 with eight 128x64 waves when it has >= 192
+    //    tiles (qkv/gate_up at 4096, gate_up at 1024), else 128x128: at 4096,
+    //    o_proj 26.4 us on 128x128 against 31.5 us on 256x128.
+    //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
+    //    when it has >= 256 tiles; else 256x128 (one workgroup of 128x64
+    //    waves) for >= 256 tiles in full rounds: o_proj at 4096 26.1 us
+    //    against 28.5 us on 128x128; else 128x128.
+    //  (Variants timed interleaved after a warm-up, median of 5 rounds: the
+    //  clock settles upward under sustained MFMA load.)
+    //  - K groups (no wide-kernel variant): 256x128 for >= 256 tiles in full
+    //    rounds, else 128x128 (gate_up at M = 1024: 384 tiles, 88 us on
+    //    128x128 against 112 us).
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;
-    static const int shapes[3][2] = {{256, 256}, {256, 128}, {128, 128}};
     const bool grouped = input_group || weight_group;
-    for (const auto &s : shapes) {
-        if (grouped && s[1] == 256) continue;
-        long tiles = long((N + s[0] - 1) / s[0]) * ((rows + s[1] - 1) / s[1]);
-        p.channels = s[0];
-        p.tokens = s[1];
-        if (tiles >= 256) break;
+    const long tiles_256 = long((N + 255) / 256) * ((rows + 255) / 256);
+    const long tiles_256x128 = long((N + 255) / 256) * ((rows + 127) / 128);
+    const bool full = tiles_256x128 * 10 >= (tiles_256x128 + 255) / 256 * 256 * 9;
+    p.channels = 128;
+    p.tokens = 128;
+    if (!grouped && fmt == QLIN_I8) {
+        if (tiles_256 >= 192) {
+            p.channels = p.tokens = 256;
+            p.waves = 8;
+        }
+    } else if (!grouped) {
+        if (tiles_256 >= 256) {
+            p.channels = p.tokens = 256;
+            p.waves = 4;
+        } else if (tiles_256x128 >= 256 && full) {
+            p.channels = 256;
+        }
+    } else if (tiles_256x128 >= 256 && full) {
+        p.channels = 256;
     }
-    if (p.channels == 256 && p.tokens == 256) p.waves = fmt == QLIN_FP8 ? 4 : 8;
     // (The persistent INT8 kernel, tiled staged = 1, is not planned: at
     // steady clocks the eight-wave kernel is faster on every BASELINE shape.)
     return p;
