@@ -97,12 +97,14 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     // A grid is run in rounds of 256 workgroups (one per CU); `full` says its
     // last round is at least 90% occupied.
     //  - INT8 per-channel: 256x256 with eight 128x64 waves when it has >= 192
-    //    tiles (qkv/gate_up at 4096, gate_up at 1024), else 128x128: at 4096,
-    //    o_proj 26.4 us on 128x128 against 31.5 us on 256x128.
+    //    tiles (qkv/gate_up at 4096, gate_up at 1024), else 128x128 with eight
+    //    64x32 waves: o_proj at 4096 24.4 us against 30.7 us on 256x128; qkv
+    //    at 1024 14.1 us against 18.7 us with four 64x64 waves.
     //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
     //    when it has >= 256 tiles; else 256x128 (one workgroup of 128x64
     //    waves) for >= 256 tiles in full rounds: o_proj at 4096 26.1 us
-    //    against 28.5 us on 128x128; else 128x128.
+    //    against 28.5 us on 128x128; else 128x128 with four 64x64 waves (the
+    //    eight-wave 128x128 is not faster for FP8).
     //  (Variants timed interleaved after a warm-up, median of 5 rounds: the
     //  clock settles upward under sustained MFMA load.)
     //  - K groups (no wide-kernel variant): 256x128 for >= 256 tiles in full
@@ -118,10 +120,8 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     p.channels = 128;
     p.tokens = 128;
     if (!grouped && fmt == QLIN_I8) {
-        if (tiles_256 >= 192) {
-            p.channels = p.tokens = 256;
-            p.waves = 8;
-        }
+        p.waves = 8;
+        if (tiles_256 >= 192) p.channels = p.tokens = 256;
     } else if (!grouped) {
         if (tiles_256 >= 256) {
             p.channels = p.tokens = 256;
@@ -193,12 +193,12 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         // of 128x128; 128x128: four waves of 64x64.
         const bool wave_ok = (p.channels == 256 && p.tokens == 256) ? (p.waves == 8 || p.waves == 4)
                              : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2)
-                                                                       : p.waves == 1;
+                                                                       : (p.waves == 1 || p.waves == 8);
         if (!wave_ok)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,
                         p.tokens, p.waves);
-        if ((p.waves == 2 || p.waves == 4) && (input_group || weight_group))
-            return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
+        if (p.waves != 1 && p.tokens != 256 && (input_group || weight_group))
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has only the one-workgroup variants");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
         // tiled staged = 1: the persistent 8-wave INT8 256x256 kernel

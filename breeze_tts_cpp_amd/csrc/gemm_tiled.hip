@@ -97,7 +97,9 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
     constexpr bool kMF32 = Fmt == FP8 && !Grouped;
-    static_assert(Fmt == I8 || BK == 128 || (kMF32 && BK == 64), "FP8 K per stage");
+    // K bytes per stage: per-channel pipelines (INT8 16x16x64, FP8 32x32x64)
+    // consume exactly 64, the K-group pipeline one 128-wide group.
+    static_assert(Grouped ? BK == 128 : BK == 64, "K bytes per stage");
     static_assert(!Grouped || BK == 128, "one K group of 128 per stage");
     using MMA = TileMma<Fmt>;
     using Acc = typename MMA::Acc;
@@ -1032,6 +1034,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
+        // 128x128: eight waves of 64x32 (waves 8) or four of 64x64 (waves 1).
+        if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 4, 2, 64, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         return -4;
@@ -1044,6 +1049,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
+        // 128x128: eight waves of 64x32 (waves 8) or four of 64x64 (waves 1).
+        if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 4, 2, 64, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         return -4;

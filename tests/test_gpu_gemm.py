@@ -228,8 +228,9 @@ def _tiled_paths(grouped=False, fmt=I8):
     from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
     shapes = [(256, 128, 1), (128, 128, 1)]
     if not grouped:
-        # 32x32-MFMA kernels: four waves of 128x128, two waves of 128x128
-        shapes = [(256, 256, 4), (256, 128, 2)] + shapes
+        # 32x32-MFMA kernels: four waves of 128x128, two waves of 128x128;
+        # 128x128 with eight 64x32 waves
+        shapes = [(256, 256, 4), (256, 128, 2), (128, 128, 8)] + shapes
         if fmt == I8:
             shapes = [(256, 256, 8)] + shapes
     for channels, tokens, waves in shapes:
