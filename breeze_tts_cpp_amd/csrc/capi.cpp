@@ -96,10 +96,11 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     // at M = 1024 and 4096, per-channel and K128 groups, realistic data).
     // A grid is run in rounds of 256 workgroups (one per CU); `full` says its
     // last round is at least 90% occupied.
-    //  - INT8 per-channel: 256x256 with eight 128x64 waves when it has >= 192
-    //    tiles (qkv/gate_up at 4096, gate_up at 1024), else 128x128 with eight
-    //    64x32 waves: o_proj at 4096 24.4 us against 30.7 us on 256x128; qkv
-    //    at 1024 14.1 us against 18.7 us with four 64x64 waves.
+    //  - INT8 per-channel, all with eight waves: 256x256 (128x64 waves) when
+    //    it has >= 192 tiles (qkv/gate_up at 4096, gate_up at 1024); else
+    //    256x128 (128x32 waves) for >= 256 tiles in full rounds: down at 4096
+    //    57.6 us against 68.6 us on 128x128; else 128x128 (64x32 waves): qkv
+    //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
     //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
     //    when it has >= 256 tiles; else 256x128 (one workgroup of 128x64
     //    waves) for >= 256 tiles in full rounds: o_proj at 4096 26.1 us
@@ -122,6 +123,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     if (!grouped && fmt == QLIN_I8) {
         p.waves = 8;
         if (tiles_256 >= 192) p.channels = p.tokens = 256;
+        else if (tiles_256x128 >= 256 && full) p.channels = 256;
     } else if (!grouped) {
         if (tiles_256 >= 256) {
             p.channels = p.tokens = 256;
@@ -189,10 +191,11 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         if (p.splits != 1)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no split-K variant");
         // 256x256: eight waves of 128x64 (16x16 MFMA) or four of 128x128
-        // (32x32 MFMA); 256x128: one workgroup of 128x64 waves, or two waves
-        // of 128x128; 128x128: four waves of 64x64.
+        // (32x32 MFMA); 256x128: one workgroup of 128x64 waves (1), two waves
+        // of 128x128 (2) or eight of 128x32 (8); 128x128: four waves of 64x64
+        // (1) or eight of 64x32 (8).
         const bool wave_ok = (p.channels == 256 && p.tokens == 256) ? (p.waves == 8 || p.waves == 4)
-                             : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2)
+                             : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2 || p.waves == 8)
                                                                        : (p.waves == 1 || p.waves == 8);
         if (!wave_ok)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,

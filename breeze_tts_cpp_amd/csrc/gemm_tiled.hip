@@ -1026,6 +1026,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     } else if constexpr (Fmt == I8) {
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8 && p.staged == 1)
             return launch_persist<2, 4, 8, 4, 4, Out>(a, s);
+        // 256x128 with eight waves of 128x32.
+        if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 8, 2, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
@@ -1041,6 +1044,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         return -4;
     } else {
+        // 256x128 with eight waves of 128x32.
+        if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 8, 2, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)

@@ -32,6 +32,7 @@ def paths():
             ("wide256x256", Path(KIND_TILED, 256, 256, 1, 4), 512),
             ("tiled8wave", Path(KIND_TILED, 256, 256, 1, 8), 512),
             ("tiled128x8wave", Path(KIND_TILED, 128, 128, 1, 8), 512),
+            ("tiled256x128x8wave", Path(KIND_TILED, 128, 256, 1, 8), 512),
             ("persistent", Path(KIND_TILED, 256, 256, 1, 8, 1), 1024)]
 
 

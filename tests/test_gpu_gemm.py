@@ -230,7 +230,7 @@ def _tiled_paths(grouped=False, fmt=I8):
     if not grouped:
         # 32x32-MFMA kernels: four waves of 128x128, two waves of 128x128;
         # 128x128 with eight 64x32 waves
-        shapes = [(256, 256, 4), (256, 128, 2), (128, 128, 8)] + shapes
+        shapes = [(256, 256, 4), (256, 128, 2), (256, 128, 8), (128, 128, 8)] + shapes
         if fmt == I8:
             shapes = [(256, 256, 8)] + shapes
     for channels, tokens, waves in shapes:

@@ -81,7 +81,7 @@ def test_packed_prefill(dev, orc, fmt, N, K):
     xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=N + K)
     rows = np.unique(np.concatenate([[0, 255, 256, M - 1],
                                      np.random.default_rng(N).choice(M, 28, replace=False)]))
-    shapes = [(256, 256, 4), (256, 128, 2), (256, 128, 1), (128, 128, 1), (128, 128, 8)]
+    shapes = [(256, 256, 4), (256, 128, 2), (256, 128, 1), (256, 128, 8), (128, 128, 1), (128, 128, 8)]
     if fmt == I8:
         shapes += [(256, 256, 8), (256, 256, 8, 1)]
     for channels, tokens, waves, *staged in shapes:
