@@ -14,7 +14,7 @@ as a HIP graph and replayed.
 
 value = algorithmic bytes per step / step time (GB/s), with per projection
 B = N*K + M*K + 4N + 4M + 2*M*N (GEMM) + 3*M*K + 4*M (quantizer).
-Also reported: per-projection decode GB/s, prefill (M=4096) INT8/FP8 TOPS,
+Also reported: per-projection decode GB/s, prefill (M=4096) INT8/FP8/group TOPS,
 the roofline fraction of the dominant kernel and a CPU baseline (the oracle's
 multithreaded C restatement) on a bounded sample.
 """
@@ -291,8 +291,8 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
 
 
 def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
-    """M=4096 INT8 and FP8 GEMMs over the four projections (BASELINE configs 2
-    and 4): TOPS = 2*M*N*K / kernel time. Per format, the four projections'
+    """M=4096 INT8, FP8, group_int8 and group_fp8 GEMMs over the four
+    projections: TOPS = 2*M*N*K / kernel time. Per format, the four projections'
     graphs (10 GEMMs each) are built, warmed up together for about 30 replays
     each (the clock settles upward under sustained MFMA load), then timed in
     5 interleaved rounds of 3 replays; each projection reports its median."""
@@ -301,26 +301,29 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
     M = M_PREFILL
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps, rounds, per_round = 10, 5, 3
-    for fmt_name, fmt in (("int8", qlinear.I8), ("fp8", qlinear.FP8)):
+    modes = (("int8", qlinear.I8, 0), ("fp8", qlinear.FP8, 0), ("group_int8", qlinear.I8, 128),
+             ("group_fp8", qlinear.FP8, 128))
+    for fmt_name, fmt, group in modes:
         legs = {}
+        rot = 128 if group else 0
         for name, (N, K) in synthetic.PROJECTIONS.items():
             x = torch.from_numpy(synthetic.activations(M, K, seed=1).view(np.int16)).view(
                 torch.bfloat16).to(dev)
             w = torch.from_numpy(synthetic.weights(N, K, seed=1).view(np.int16)).view(
                 torch.bfloat16).to(dev)
             with torch.cuda.stream(stream):
-                xq, sx = qlinear.row_quantize(x, fmt, stream=stream)
-                wq, sw = qlinear.row_quantize(w, fmt, stream=stream)
+                xq, sx = qlinear.row_quantize(x, fmt, group=group, rotation=rot, stream=stream)
+                wq, sw = qlinear.row_quantize(w, fmt, group=group, rotation=rot, stream=stream)
                 y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-                path = qlinear.plan(M, N, K, fmt)
-                need = qlinear.workspace_bytes(path, M, N, K, fmt)
+                path = qlinear.plan(M, N, K, fmt, group, group)
+                need = qlinear.workspace_bytes(path, M, N, K, fmt, group, group)
                 ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
                 for _ in range(reps):
-                    qlinear.gemm(xq, sx, wq, sw, fmt, path=path, out=y, workspace=ws,
-                                 stream=stream)
+                    qlinear.gemm(xq, sx, wq, sw, fmt, input_group=group, weight_group=group,
+                                 path=path, out=y, workspace=ws, stream=stream)
             legs[name] = {"graph": g, "N": N, "K": K, "path": path, "keep": (xq, sx, wq, sw, y, ws),
                           "us": []}
             del x, w
@@ -352,7 +355,7 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
                           "path": [p.kind, p.tokens, p.channels, p.splits, p.waves]}
         del legs
         tops = total_ops / (total_us * 1e-6) / 1e12
-        peak = I8_PEAK_TOPS if fmt_name == "int8" else FP8_PEAK_TFLOPS
+        peak = I8_PEAK_TOPS if fmt == qlinear.I8 else FP8_PEAK_TFLOPS
         out[fmt_name] = {"TOPS": round(tops, 1), "frac_mfma": round(tops / peak, 4),
                          "peak": peak, "projections": rows}
     return out

@@ -108,9 +108,10 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    eight-wave 128x128 is not faster for FP8).
     //  (Variants timed interleaved after a warm-up, median of 5 rounds: the
     //  clock settles upward under sustained MFMA load.)
-    //  - K groups (no wide-kernel variant): 256x128 for >= 256 tiles in full
-    //    rounds, else 128x128 (gate_up at M = 1024: 384 tiles, 88 us on
-    //    128x128 against 112 us).
+    //  - K groups (no wide-kernel variant), eight waves: INT8 256x128 (128x32
+    //    waves) for >= 256 tiles in full rounds (gate_up at 4096 230 us
+    //    against 326 us with four 128x64 waves), else 128x128 (64x32 waves);
+    //    FP8 128x128 (gate_up at 4096 265 us against 276 us on 256x128).
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;
@@ -131,8 +132,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         } else if (tiles_256x128 >= 256 && full) {
             p.channels = 256;
         }
-    } else if (tiles_256x128 >= 256 && full) {
-        p.channels = 256;
+    } else {
+        p.waves = 8;
+        if (fmt == QLIN_I8 && tiles_256x128 >= 256 && full) p.channels = 256;
     }
     // (The persistent INT8 kernel, tiled staged = 1, is not planned: at
     // steady clocks the eight-wave kernel is faster on every BASELINE shape.)
@@ -200,8 +202,8 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         if (!wave_ok)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,
                         p.tokens, p.waves);
-        if (p.waves != 1 && p.tokens != 256 && (input_group || weight_group))
-            return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has only the one-workgroup variants");
+        if (p.waves != 1 && p.waves != 8 && p.tokens != 256 && (input_group || weight_group))
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
         // tiled staged = 1: the persistent 8-wave INT8 256x256 kernel

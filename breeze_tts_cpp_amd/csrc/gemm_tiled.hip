@@ -1018,6 +1018,10 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if constexpr (Grouped) {
         // No 256x256: the fp32 group accumulators would double the 128x128
         // register tile per wave and spill.
+        if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, true, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, true, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 128, 3, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)

@@ -81,7 +81,7 @@ def test_gemm_validation():
     assert call(K=512, path=split, ws=FAKE, wsb=10) == -3
     T = qlinear.KIND_TILED
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 4)) == -4          # no 4-wave 128x128 variant
-    assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 8), ig=128, wg=128) == -4  # K groups: 1 wave config
+    assert call(M=256, path=qlinear.Path(T, 128, 256, 1, 2), ig=128, wg=128) == -4  # K groups: no 32x32 tiles
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 2)) == -4
 
 
@@ -97,7 +97,8 @@ def test_prefill_plan_rules():
     assert tile(4096, "o_proj", I8) == (256, 128, 8) and tile(1024, "qkv", I8) == (128, 128, 8)
     assert tile(4096, "gate_up", FP8) == (256, 256, 4) and tile(4096, "down", FP8) == (256, 128, 1)
     assert tile(1024, "gate_up", FP8) == (128, 128, 1)   # 384 256x128 tiles: 1.5 rounds
-    assert tile(4096, "qkv", I8, 128) == (256, 128, 1) and tile(1024, "gate_up", FP8, 128) == (128, 128, 1)
+    assert tile(4096, "qkv", I8, 128) == (256, 128, 8) and tile(4096, "qkv", FP8, 128) == (128, 128, 8)
+    assert tile(1024, "gate_up", I8, 128) == (128, 128, 8) and tile(1024, "gate_up", FP8, 128) == (128, 128, 8)
 
 
 def test_plan_and_workspace():
