@@ -51,27 +51,44 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     qlin_path p{};
     if (rows <= 64) {
         // Decode: the weights are streamed once and each CU's share of them
-        // bounds the time, so the grid is sized to one workgroup per CU
-        // (256 on MI355X): the token tile and the weight rows per workgroup
-        // are chosen so that ceil(N/channels) * ceil(rows/tokens) is the
-        // largest count not above 256 (a second workgroup on some CUs would
-        // double their share). Wave64s split K eight ways; weight slabs are
-        // staged through LDS when they fit (whole-row runs per load).
+        // bounds the time, so the grid is sized to about one workgroup per
+        // CU (256 on MI355X). Rules measured on the BASELINE projections at
+        // M = 1, 8, 16, 32, 64 (weights rotated through > 512 MB so they come
+        // from HBM; variants interleaved, median of 5):
+        //  - above 16 rows with weights under 16 MB (qkv, o_proj, down):
+        //    16-token tiles and the fewest weight rows (16/32/48) that keep
+        //    <= 256 workgroups, else 32: qkv at M = 32 4.9 us against 5.8 us
+        //    with one 32-token tile;
+        //  - otherwise the largest workgroup count up to 256, then wider token
+        //    tiles (fewer activation re-reads), then fewer weight rows
+        //    (gate_up keeps 32/64-token tiles).
+        // Wave64s split K eight ways; weight slabs are staged through LDS,
+        // one slab per wave (2-4% faster than the cooperative slab), when
+        // they fit.
         p.kind = QLIN_KIND_SKINNY;
         p.splits = 1;
         const int full_tokens = (rows + 15) / 16 * 16;
-        long best = -1;
-        for (int channels : {16, 32, 48}) {
-            for (int tokens = full_tokens; tokens >= 16; tokens -= 16) {
-                if (full_tokens % tokens && tokens != 16) continue;
-                const long wgs = long((N + channels - 1) / channels) * ((rows + tokens - 1) / tokens);
-                // Prefer more workgroups up to 256, then wider token tiles
-                // (fewer activation re-reads), then fewer weight rows.
-                const long score = (wgs <= 256 ? wgs : 256 - (wgs - 256)) * 4096 + tokens * 64 - channels;
-                if (score > best) {
-                    best = score;
-                    p.tokens = tokens;
+        if (rows > 16 && long(N) * K < (16L << 20)) {
+            const int token_tiles = (rows + 15) / 16;
+            p.tokens = 16;
+            p.channels = 32;
+            for (int channels : {16, 32, 48})
+                if (long((N + channels - 1) / channels) * token_tiles <= 256) {
                     p.channels = channels;
+                    break;
+                }
+        } else {
+            long best = -1;
+            for (int channels : {16, 32, 48}) {
+                for (int tokens = full_tokens; tokens >= 16; tokens -= 16) {
+                    if (full_tokens % tokens && tokens != 16) continue;
+                    const long wgs = long((N + channels - 1) / channels) * ((rows + tokens - 1) / tokens);
+                    const long score = (wgs <= 256 ? wgs : 256 - (wgs - 256)) * 4096 + tokens * 64 - channels;
+                    if (score > best) {
+                        best = score;
+                        p.tokens = tokens;
+                        p.channels = channels;
+                    }
                 }
             }
         }
@@ -81,7 +98,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         p.waves = waves;
         const bool slab_fits = waves == 8 && blocks_k / 8 <= 3 &&
                                long(p.channels) * blocks_k * 256 <= 160 * 1024;
-        p.staged = slab_fits ? (p.channels >= 32 ? 1 : 2) : 0;
+        p.staged = slab_fits ? 1 : 0;
         qlin::GemmArgs a{};
         a.M = rows;
         a.N = N;
