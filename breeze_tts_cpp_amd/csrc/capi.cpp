@@ -121,8 +121,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
     //    when it has >= 256 tiles; else 256x128 (one workgroup of 128x64
     //    waves) for >= 256 tiles in full rounds: o_proj at 4096 26.1 us
-    //    against 28.5 us on 128x128; else 128x128 with four 64x64 waves (the
-    //    eight-wave 128x128 is not faster for FP8).
+    //    against 28.5 us on 128x128; else 128x128 with eight 64x32 waves on
+    //    the 16x16x128 MFMA over 128-byte K stages: down at 1024 35.5 us
+    //    against 45.3 us with four 32x32x64 waves.
     //  (Variants timed interleaved after a warm-up, median of 5 rounds: the
     //  clock settles upward under sustained MFMA load.)
     //  - K groups (no wide-kernel variant), eight waves: INT8 256x128 (128x32
@@ -148,6 +149,8 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
             p.waves = 4;
         } else if (tiles_256x128 >= 256 && full) {
             p.channels = 256;
+        } else {
+            p.waves = 8;
         }
     } else {
         p.waves = 8;

@@ -96,10 +96,12 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
     // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
-    constexpr bool kMF32 = Fmt == FP8 && !Grouped;
-    // K bytes per stage: per-channel pipelines (INT8 16x16x64, FP8 32x32x64)
-    // consume exactly 64, the K-group pipeline one 128-wide group.
-    static_assert(Grouped ? BK == 128 : BK == 64, "K bytes per stage");
+    constexpr bool kMF32 = Fmt == FP8 && !Grouped && BK == 64;
+    // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
+    // exactly 64, the FP8 16x16x128 pipeline 128, the K-group pipeline one
+    // 128-wide group.
+    static_assert(Grouped ? BK == 128 : (Fmt == I8 ? BK == 64 : (BK == 64 || BK == 128)),
+                  "K bytes per stage");
     static_assert(!Grouped || BK == 128, "one K group of 128 per stage");
     using MMA = TileMma<Fmt>;
     using Acc = typename MMA::Acc;
@@ -1059,9 +1061,10 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
-        // 128x128: eight waves of 64x32 (waves 8) or four of 64x64 (waves 1).
+        // 128x128: eight waves of 64x32 on the 16x16x128 FP8 MFMA over
+        // 128-byte K stages (waves 8), or four 64x64 waves of 32x32x64 (1).
         if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 4, 2, 64, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         return -4;
