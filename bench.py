@@ -442,7 +442,8 @@ def bench_producers(torch, qlinear, synthetic, dev, stream, args):
 def cpu_baseline(args, gpu_value):
     """The oracle's multithreaded C restatement of quant + INT8 GEMM + dequant
     (oracle/qlinear_oracle.c, orc_cpu_qlinear) on one layer's four projections
-    at M=32: a bounded sample of the step (1 of 16 layers)."""
+    at M=32: a bounded sample of the step (1 of 16 layers), repeated for about
+    12 s; the median rep is reported."""
     from breeze_tts_cpp_amd import synthetic
     from oracle import oracle
 
@@ -456,8 +457,9 @@ def cpu_baseline(args, gpu_value):
         total_bytes += gemm_bytes(M_DECODE, N, K) + quant_bytes(M_DECODE, K)
     oracle.cpu_qlinear(*jobs[0], oracle.I8, threads=threads)  # warm-up
     times = []
-    t_end = time.time() + 20.0
-    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+    # About 10-12 s of CPU work: reps until 12 s have passed (at most 1000).
+    t_end = time.time() + 12.0
+    while len(times) < 5 or (time.time() < t_end and len(times) < 1000):
         t0 = time.perf_counter()
         for xb, wq, sw in jobs:
             oracle.cpu_qlinear(xb, wq, sw, oracle.I8, threads=threads)
