@@ -298,10 +298,12 @@ size_t qlin_workspace_bytes(const qlin_path *path, int rows, int N, int K, int f
 }  // extern "C"
 
 namespace {
+constexpr int kNotFused = 1;  // gemm_impl with a fused source: no such variant, nothing launched
 int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void *w,
               const float *sw, void *y, int rows, int N, int K, int fmt, int out_type,
               int input_group, int weight_group, void *workspace, size_t workspace_bytes,
-              qlin_stream_t stream, bool packed, const void *bias = nullptr, int act = 0) {
+              qlin_stream_t stream, bool packed, const void *bias = nullptr, int act = 0,
+              const qlin::FusedSource *fq = nullptr) {
     // check_linear + make_plan rules (reference ops/cuda/quantization.cpp:94-102,
     // 206-222) and launch_quant_linear's type checks (quant_dispatch.cu:194-233).
     if (fmt != QLIN_I8 && fmt != QLIN_FP8)
@@ -345,6 +347,15 @@ int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void 
                      static_cast<const uint16_t *>(bias),
                      act};
     const qlin::GemmPath ip = to_internal(p);
+    if (fq) {
+        // qlin_linear's one-launch form: taken only where a fused variant
+        // exists, else the caller quantizes and launches the GEMM separately.
+        a.fq = *fq;
+        if (!qlin::skinny_fused_supported(a, ip)) return kNotFused;
+        int r = qlin::launch_skinny_fused(a, ip, reinterpret_cast<hipStream_t>(stream));
+        if (r) return fail(r, "no fused kernel variant for this path");
+        return check_launch("fused quantize + GEMM launch");
+    }
     size_t need = 0;
     if (p.kind == QLIN_KIND_SKINNY) need = qlin::skinny_workspace_bytes(a, ip);
     if (need && (!workspace || workspace_bytes < need))
@@ -426,6 +437,18 @@ int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void
     // ops::linear, quantized branch (reference ops/linear.cpp:51-71):
     // quantize_rows into the scratch activation, then the GEMM.
     if (!xq || !sx) return fail(QLIN_ERR_INVALID, "linear needs the scratch activation (xq, sx)");
+    // Decode shapes with per-token scales: one launch in which the GEMM
+    // quantizes its own token rows (and fills the scratch as the quantizer
+    // would), when the planned path has a fused variant.
+    if (!input_group && !rotation && (src_type == QLIN_BF16 || src_type == QLIN_F16) && x &&
+        aligned(x, 16) && ld % 8 == 0 && ld >= K && rows >= 1 && aligned(xq, 16) &&
+        aligned(sx, 4)) {
+        const qlin::FusedSource fq{static_cast<const uint16_t *>(x), ld, src_type == QLIN_F16 ? 1 : 0,
+                                   static_cast<uint8_t *>(xq), sx};
+        int r = gemm_impl(path, xq, sx, w, sw, y, rows, N, K, fmt, out_type, input_group,
+                          weight_group, workspace, workspace_bytes, stream, false, nullptr, 0, &fq);
+        if (r != kNotFused) return r;
+    }
     int status = qlin_row_quantize(x, ld, rows, K, src_type, xq, sx, fmt, input_group, rotation,
                                    stream);
     if (status) return status;

@@ -96,12 +96,12 @@ __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4
 // loads all NB blocks of its K range straight into registers up front, one
 // contiguous 1 KB piece per (16-row fragment, 64-K step).
 template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out, int NB = 0,
-          int SL = 1, bool Packed = false>
+          int SL = 1, bool Packed = false, int FQ = 0>
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
     int K, int span, int input_group, int weight_group, const uint16_t *__restrict__ bias,
-    int act) {
+    int act, FusedSource fq) {
     using M_ = Mfma<Fmt>;
     using Acc = typename M_::Acc;
     using Scalar = typename M_::Scalar;
@@ -150,10 +150,39 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         const int m = m0 + (tf / NF) * 16 + (l & 15);
         const int n = n0 + (tf % NF) * 16 + (l >> 4) * 4;
         const bool live = u < kUnits && m < M && n < N;
-        pre_x[k] = (live && !(Grouped && input_group)) ? sx[m] : 1.f;
+        // FQ: sx is produced by this kernel; the factor comes from LDS below.
+        pre_x[k] = (live && !(Grouped && input_group) && !FQ) ? sx[m] : 1.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             pre_w[k][r] = (live && !(Grouped && weight_group)) ? sw[n + r] : 1.f;
+    }
+
+    // FQ: the 16-bit activation fragments of every block of this wave's K
+    // range, requested before the weight slab so that they land first. Lane
+    // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
+    // row m0 + 16t + row16: exactly the codes its MFMA B fragments need.
+    static_assert(!FQ || (NB > 0 && SL == 1 && !Packed && !Grouped && !Split && MT == 1 && NB == 1),
+                  "fused quantization: per-wave slab, activation blocks in registers");
+    uint4 xraw[FQ ? NB : 1][MT][4][2];
+    if constexpr (FQ) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int k = k_begin + blk * kBlockK + p * 64 + quad * 16;
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const int m = m0 + t * 16 + row16;
+                    if (k < k_end && xvalid[t]) {
+                        const uint4 *src = reinterpret_cast<const uint4 *>(
+                            fq.src + size_t(m) * fq.ld + k);
+                        xraw[blk][t][p][0] = src[0];
+                        xraw[blk][t][p][1] = src[1];
+                    } else {
+                        xraw[blk][t][p][0] = xraw[blk][t][p][1] = uint4{0, 0, 0, 0};
+                    }
+                }
+            }
     }
 
     extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
@@ -226,7 +255,102 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     constexpr bool kPreX = NB > 0 && NB * MT <= 6 && !Packed;
     i32x4 wpre[1][NF][4];  // unused unless packed
     i32x4 xpre[kPreX ? NB : 1][MT][4];
-    if constexpr (kPreX) {
+    __shared__ float fq_amax[FQ ? WK : 1][FQ ? MT * 16 : 1];
+    __shared__ float fq_scale[FQ ? MT * 16 : 1];
+    if constexpr (FQ) {
+        // The per-token quantizer's arithmetic (row_quantize.hip
+        // token_quantize; reference row_quantize.cu:24-87): row absmax over
+        // all K (this wave's range, its four lane quads, then the WK waves
+        // through LDS), scale = quant_scale(amax), codes = encode(v * (1 /
+        // scale)). Max is order-free, so the codes and scales are the
+        // quantizer's bit for bit.
+        constexpr int ns = kSlabBytes / 1024;  // slab DMA loads, issued last
+        __builtin_amdgcn_s_waitcnt((ns & 15) | ((ns >> 4) << 14) | (7 << 4) | (15 << 8));
+        // FQ 1: bf16 source, 2: f16 source.
+        using Tin = std::conditional_t<FQ == 2, f16_t, bf16_t>;
+        auto widen = [](uint32_t h) { return to_float(uint16_t(h), Tin{}); };
+        // |v| of a 16-bit float orders as its sign-cleared bits, so the
+        // absmax is a packed unsigned 16-bit max of the bits; a NaN (bits
+        // above the infinity pattern) makes the lane redo its values with
+        // fmaxf, which ignores NaN as the quantizer's reduction does.
+        constexpr uint32_t kInfBits = FQ == 2 ? 0x7c00u : 0x7f80u;
+        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+        float amax[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            u16x2 top = {0, 0};
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
+                                                xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            top = __builtin_elementwise_max(
+                                top, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
+                    }
+            const uint32_t bits = top.x > top.y ? top.x : top.y;
+            if (bits <= kInfBits) {
+                amax[t] = widen(bits);
+            } else {
+                amax[t] = 0.f;
+#pragma unroll
+                for (int blk = 0; blk < NB; ++blk)
+                    for (int p = 0; p < 4; ++p)
+                        for (int h = 0; h < 2; ++h) {
+                            const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
+                                                    xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
+                            for (int i = 0; i < 4; ++i) {
+                                amax[t] = fmaxf(amax[t], fabsf(widen(wd[i] & 0xffffu)));
+                                amax[t] = fmaxf(amax[t], fabsf(widen(wd[i] >> 16)));
+                            }
+                        }
+            }
+            amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 16, 64));
+            amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 32, 64));
+            if (quad == 0) fq_amax[wave][t * 16 + row16] = amax[t];
+        }
+        // A workgroup barrier that waits for LDS only: __syncthreads' fence
+        // would also wait for the weight slab DMA still in flight.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            float a = fq_amax[0][t * 16 + row16];
+#pragma unroll
+            for (int q = 1; q < WK; ++q) a = fmaxf(a, fq_amax[q][t * 16 + row16]);
+            const float step = quant_scale<Fmt>(a);
+            const float inverse = 1.f / step;
+            if (wave == 0 && quad == 0) fq_scale[t * 16 + row16] = step;
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    i32x4 codes;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
+                                                xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const uint32_t c0 = encode<Fmt>(widen(wd[2 * j] & 0xffffu) * inverse);
+                            const uint32_t c1 = encode<Fmt>(widen(wd[2 * j] >> 16) * inverse);
+                            const uint32_t c2 = encode<Fmt>(widen(wd[2 * j + 1] & 0xffffu) * inverse);
+                            const uint32_t c3 = encode<Fmt>(widen(wd[2 * j + 1] >> 16) * inverse);
+                            codes[2 * h + j] = int(c0 | (c1 << 8) | (c2 << 16) | (c3 << 24));
+                        }
+                    }
+                    // Columns past the range (or rows past M) encode zeros,
+                    // as the zero-filled plain activation loads.
+                    const int k = k_begin + blk * kBlockK + p * 64 + quad * 16;
+                    const bool in = k < k_end && xvalid[t];
+                    xpre[blk][t][p] = in ? codes : i32x4{0, 0, 0, 0};
+                }
+        }
+        __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));  // slab in LDS
+    } else if constexpr (kPreX) {
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
         if constexpr (!Packed) {
@@ -331,6 +455,26 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             const int kb = k_begin + blk * kBlockK;
             if (kb < k_end) block(kb, xpre[blk], wpre[0]);
         }
+        if constexpr (FQ) {
+            // Column tile 0 fills the scratch activation, after its MFMAs so
+            // that the stores do not delay the slab wait.
+            if (blockIdx.x == 0) {
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const int m = m0 + t * 16 + row16;
+                    if (!xvalid[t]) continue;
+                    if (wave == 0 && quad == 0) fq.sx[m] = fq_scale[t * 16 + row16];
+#pragma unroll
+                    for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                        for (int p = 0; p < 4; ++p) {
+                            const int k = k_begin + blk * kBlockK + p * 64 + quad * 16;
+                            if (k < k_end)
+                                *reinterpret_cast<i32x4 *>(fq.xq + size_t(m) * K + k) = xpre[blk][t][p];
+                        }
+                }
+            }
+        }
     } else {
         for (int kb = k_begin; kb < k_end; kb += kBlockK) {
             i32x4 b[MT][4];
@@ -395,6 +539,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         const int m = m0 + t * 16 + (l & 15);
         const int n = n0 + f * 16 + (l >> 4) * 4;
         if (m >= M || n >= N) continue;
+        if constexpr (FQ) pre_x[k] = fq_scale[t * 16 + (l & 15)];
         Red sum[4];
         total(tf, l, t, f, sum);
         float v[4];
@@ -470,11 +615,11 @@ int launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t 
     if (layout == 2)
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
-                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act);
+                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
     else
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
-                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act);
+                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
     return 0;
 }
 
@@ -482,7 +627,7 @@ template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
 int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1, true>), grid,
                        dim3(64 * WK), 0, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N,
-                       a.K, span, a.input_group, a.weight_group, a.bias, a.act);
+                       a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
     return 0;
 }
 
@@ -530,13 +675,13 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         if (p.staged) return -4;
         hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out>), grid, block, 0,
                            stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span,
-                           a.input_group, a.weight_group, a.bias, a.act);
+                           a.input_group, a.weight_group, a.bias, a.act, a.fq);
         return 0;
     }
     if (p.staged) return -4;
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
-                       a.input_group, a.weight_group, a.bias, a.act);
+                       a.input_group, a.weight_group, a.bias, a.act, a.fq);
     const size_t quads = (size_t(a.M) * a.N) / 4;
     dim3 rgrid(unsigned((quads + 255) / 256));
     using Scalar = typename Mfma<Fmt>::Scalar;
@@ -569,6 +714,56 @@ int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if (p.channels == 48) return dispatch_wk<Fmt, MT, 3, Grouped, Out>(a, p, s);
     if (p.channels == 64) return dispatch_wk<Fmt, MT, 4, Grouped, Out>(a, p, s);
     return -4;
+}
+
+// Fused activation quantization (FQ): eight waves, per-wave slabs of NB
+// blocks, per-channel scales, no split.
+template <int Fmt, int MT, int NF, class Out, int NB>
+int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
+    // Every workgroup quantizes its 16 x K token rows again (the activation
+    // is re-encoded once per column tile), which hides under the weight slab
+    // DMA only while it is small: measured on MI355X at M = 32, K = 2048 with
+    // 16-token tiles the single launch beats quantizer + GEMM (qkv 6.6 us vs
+    // 7.0, o_proj 6.2 vs 6.5), while 32-token tiles (gate_up 12.2 vs 11.4)
+    // and K = 6144 (down 14.1 vs 9.8) are slower.
+    if constexpr (MT == 1 && NB == 1) {
+        const int span = NB * kBlockK;
+        dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
+        const size_t lds = size_t(8) * 16 * NF * NB * kBlockK;
+        if (a.fq.f16)
+            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, 8, false, false, Out, NB, 1, false, 2>),
+                               grid, dim3(512), lds, stream, nullptr, nullptr, a.w, a.sw, a.y,
+                               nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0, a.fq);
+        else
+            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, 8, false, false, Out, NB, 1, false, 1>),
+                               grid, dim3(512), lds, stream, nullptr, nullptr, a.w, a.sw, a.y,
+                               nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0, a.fq);
+        return 0;
+    }
+    return -4;
+}
+template <int Fmt, int MT, int NF, class Out>
+int launch_fused_nf(const GemmArgs &a, hipStream_t s) {
+    switch (a.K / (8 * kBlockK)) {
+    case 1: return launch_fused_nb<Fmt, MT, NF, Out, 1>(a, s);
+    default: return -4;
+    }
+}
+template <int Fmt, int MT, class Out>
+int launch_fused_mt(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    switch (p.channels) {
+    case 16: return launch_fused_nf<Fmt, MT, 1, Out>(a, s);
+    case 32: return launch_fused_nf<Fmt, MT, 2, Out>(a, s);
+    case 48: return launch_fused_nf<Fmt, MT, 3, Out>(a, s);
+    default: return -4;
+    }
+}
+template <int Fmt, class Out>
+int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    switch (p.tokens) {
+    case 16: return launch_fused_mt<Fmt, 1, Out>(a, p, s);
+    default: return -4;
+    }
 }
 
 template <int Fmt, bool Grouped, class Out>
@@ -605,6 +800,14 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
     return p.splits > 1 ? size_t(p.splits) * a.M * a.N * 4 : 0;
 }
 
+bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
+    const int nb = a.K / (8 * kBlockK), mt = p.tokens / 16;
+    return a.fq.src && !a.packed && !a.bias && !a.act && !a.input_group && !a.weight_group &&
+           p.kind == KIND_SKINNY && p.splits == 1 && p.waves == 8 && p.staged == 1 &&
+           a.K == 8 * kBlockK && nb == 1 && mt == 1 && (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
+           p.tokens % 16 == 0 && skinny_lds_bytes(a, p) <= kLdsBytes;
+}
+
 #endif
 
 // The kernel variants are compiled in four translation units (format x
@@ -613,10 +816,18 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
 int QLIN_SKINNY_PART(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     return dispatch_grouped<QLIN_SKINNY_FMT, QLIN_SKINNY_OUT>(a, p, stream);
 }
+#if !QLIN_FIN
+#define QLIN_CAT_(a, b) a##b
+#define QLIN_CAT(a, b) QLIN_CAT_(a, b)
+int QLIN_CAT(QLIN_SKINNY_PART, _fused)(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    return launch_fused<QLIN_SKINNY_FMT, QLIN_SKINNY_OUT>(a, p, stream);
+}
+#endif
 #else
 #define QLIN_PART_DECL(name)                                                  \
     int name(const GemmArgs &, const GemmPath &, hipStream_t);              \
-    int name##_fin(const GemmArgs &, const GemmPath &, hipStream_t);
+    int name##_fin(const GemmArgs &, const GemmPath &, hipStream_t);        \
+    int name##_fused(const GemmArgs &, const GemmPath &, hipStream_t);
 QLIN_PART_DECL(launch_skinny_i8_bf16)
 QLIN_PART_DECL(launch_skinny_i8_f16)
 QLIN_PART_DECL(launch_skinny_fp8_bf16)
@@ -633,6 +844,15 @@ int launch_skinny(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (a.fmt == I8)
         return fin ? launch_skinny_i8_bf16_fin(a, p, stream) : launch_skinny_i8_bf16(a, p, stream);
     return fin ? launch_skinny_fp8_bf16_fin(a, p, stream) : launch_skinny_fp8_bf16(a, p, stream);
+}
+
+int launch_skinny_fused(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    if (!skinny_fused_supported(a, p)) return -4;
+    if (a.out_type == F16)
+        return a.fmt == I8 ? launch_skinny_i8_f16_fused(a, p, stream)
+                           : launch_skinny_fp8_f16_fused(a, p, stream);
+    return a.fmt == I8 ? launch_skinny_i8_bf16_fused(a, p, stream)
+                       : launch_skinny_fp8_bf16_fused(a, p, stream);
 }
 #endif
 

@@ -92,6 +92,17 @@ void launch_pointwise_quantize_fp8(const PointwiseQuantizeArgs &, bool vec, hipS
 // Kernel families; numbering is part of the C ABI (qlin_path.kind).
 enum Kind : int { KIND_AUTO = 0, KIND_SKINNY = 1, KIND_TILED = 2 };
 
+// Fused per-token quantization of the 16-bit activation inside the decode
+// GEMM (qlin_linear): the GEMM reads src [M, ld] instead of x, encodes it as
+// the per-token quantizer does and, in the workgroups of output-column tile 0,
+// stores the codes and scales to xq [M, K] / sx [M].
+struct FusedSource {
+    const uint16_t *src = nullptr;
+    int ld = 0, f16 = 0;
+    uint8_t *xq = nullptr;
+    float *sx = nullptr;
+};
+
 struct GemmArgs {
     const uint8_t *x;  // [M, K]
     const float *sx;   // [M] or [K/ig, M]
@@ -104,6 +115,7 @@ struct GemmArgs {
     int packed = 0;    // w in the packed fragment-tile layout (weight_pack.hip)
     const uint16_t *bias = nullptr;  // finish: [N] in the output type, or null
     int act = 0;                     // finish: qlin::Finish (0 = none)
+    FusedSource fq{};                // src set: fused activation quantization
 };
 struct GemmPath {
     int kind, tokens, channels, splits, waves, staged;
@@ -111,6 +123,11 @@ struct GemmPath {
 // Skinny (decode) family: returns 0, or a negative status if the path's
 // parameters are not an instantiated variant.
 int launch_skinny(const GemmArgs &, const GemmPath &, hipStream_t);
+// Fused-quantization decode GEMM (a.fq.src set, per-token scales, no finish):
+// true when a variant exists for the path (staged per-wave slabs, 8 waves,
+// no split, K a multiple of 2048, activation blocks held in registers).
+bool skinny_fused_supported(const GemmArgs &, const GemmPath &);
+int launch_skinny_fused(const GemmArgs &, const GemmPath &, hipStream_t);
 size_t skinny_workspace_bytes(const GemmArgs &, const GemmPath &);
 // LDS of a skinny launch (weight slab + cross-wave reduction buffer); a path
 // above kLdsBytes must not be launched.

@@ -1,0 +1,116 @@
+"""qlin_linear's one-launch decode form: for per-token scales on a decode
+path with 16-token tiles, per-wave weight slabs and K = 2048, the GEMM
+quantizes its own token rows (the arithmetic of the per-token quantizer, reference
+row_quantize.cu:24-87) instead of a separate quantizer launch. Checked
+against the two-launch form on the same inputs (qlin_row_quantize +
+qlin_gemm with the same path): output bits identical for INT8 and FP8, and
+the scratch activation (codes and scales) equal to the oracle's quantizer."""
+import numpy as np
+import pytest
+import torch
+
+from breeze_tts_cpp_amd import synthetic
+
+BF16, F32, I32, FP8, I8, F16 = 0, 1, 2, 3, 4, 5
+pytestmark = pytest.mark.gpu
+
+
+def bits(y):
+    return y.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def dev16(xb, dtype, dev):
+    t = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+    return (t if dtype == torch.bfloat16 else t.float().to(dtype)).to(dev)
+
+
+def fused_eligible(path, M, K):
+    """The library's rule for the fused form (per-token, planned skinny path
+    with per-wave slabs, eight waves, no split, 16-token tiles, K == 2048)."""
+    return (path.kind == 1 and path.splits == 1 and path.waves == 8 and path.staged == 1
+            and path.tokens == 16 and K == 2048)
+
+
+def run_pair(dev, orc, xb, fmt, N, K, path=None, src=torch.bfloat16, out=torch.bfloat16, ld=None):
+    from breeze_tts_cpp_amd import qlinear
+    M = xb.shape[0]
+    wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=N + K), fmt)
+    wq_d, sw_d = torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev)
+    x = dev16(xb, src, dev)
+    if ld is not None:
+        wide = torch.zeros((M, ld), dtype=src, device=dev)
+        wide[:, :K] = x
+        x = wide[:, :K]
+    xq_f = torch.full((M, K), 0x5a, dtype=torch.uint8, device=dev)
+    sx_f = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    y_f = qlinear.linear(x, wq_d, sw_d, fmt, out_dtype=out, path=path, scratch=(xq_f, sx_f))
+    xq_s, sx_s = qlinear.row_quantize(x, fmt)
+    y_s = qlinear.gemm(xq_s, sx_s, wq_d, sw_d, fmt, out_dtype=out, path=path)
+    torch.cuda.synchronize()
+    assert np.array_equal(xq_f.cpu().numpy(), xq_s.cpu().numpy()), "scratch codes differ"
+    assert np.array_equal(sx_f.cpu().numpy(), sx_s.cpu().numpy()), "scratch scales differ"
+    assert np.array_equal(bits(y_f), bits(y_s)), \
+        f"{np.count_nonzero(bits(y_f) != bits(y_s))} outputs differ from the two-launch form"
+    if src == torch.bfloat16 and ld is None:
+        xq, sx = orc.quantize_rows(xb, fmt)
+        assert np.array_equal(xq_f.cpu().numpy(), xq) and np.array_equal(sx_f.cpu().numpy(), sx)
+        if fmt == I8 and out == torch.bfloat16:
+            assert np.array_equal(bits(y_f), orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw))
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 2048), (8, 2048, 2048), (16, 2048, 2048),
+                                   (17, 4096, 2048), (32, 4096, 2048), (32, 12288, 2048),
+                                   (5, 48, 4096), (32, 2048, 4096), (32, 2048, 6144),
+                                   (16, 12288, 2048), (8, 2048, 6144), (64, 12288, 2048)])
+def test_fused_linear_planned(dev, orc, fmt, M, N, K):
+    from breeze_tts_cpp_amd import qlinear
+    path = qlinear.plan(M, N, K, fmt)
+    print(f"fused linear fmt={fmt} M={M} N={N} K={K} path={path}", flush=True)
+    run_pair(dev, orc, synthetic.activations(M, K, seed=M + N), fmt, N, K)
+
+
+@pytest.mark.parametrize("tokens,channels,K", [(16, 16, 2048), (16, 32, 2048), (16, 48, 2048),
+                                               (16, 32, 4096), (16, 16, 6144), (32, 32, 2048)])
+def test_fused_linear_tiles(dev, orc, tokens, channels, K):
+    """Every fused channel tile and K range, partial token and channel tiles;
+    a 32-token tile and K != 2048 take the two-launch form."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N = 29, 16 * 37
+    path = qlinear.Path(1, tokens, channels, 1, 8, 1)
+    assert fused_eligible(path, M, K) == (tokens == 16 and K == 2048)
+    print(f"fused tile {tokens}x{channels} K={K}", flush=True)
+    run_pair(dev, orc, synthetic.activations(M, K, seed=tokens * channels + K), I8, N, K, path=path)
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+def test_fused_linear_f16_strided_special_rows(dev, orc, fmt):
+    """f16 source and output, row stride > K, a zero row (scale 1), a row
+    with one huge value and a row of tiny values."""
+    M, N, K = 24, 2048, 2048
+    xb = synthetic.activations(M, K, seed=9)
+    xb[3] = 0
+    xb[7, 100] = synthetic.f32_to_bf16_bits(np.float32(3.0e4)).item()
+    xb[11] = synthetic.f32_to_bf16_bits(np.full(K, 1e-3, np.float32))
+    print(f"fused f16 strided fmt={fmt}", flush=True)
+    run_pair(dev, orc, xb, fmt, N, K, src=torch.float16, out=torch.float16, ld=K + 64)
+    run_pair(dev, orc, xb, fmt, N, K, src=torch.bfloat16, out=torch.bfloat16, ld=K + 8)
+
+
+def test_fused_linear_repeated_calls(dev, orc):
+    """Two calls in a row into one scratch, the second with fewer rows: the
+    second call's scratch rows and output are its own."""
+    from breeze_tts_cpp_amd import qlinear
+    N, K = 4096, 2048
+    wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=3), I8)
+    wq_d, sw_d = torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev)
+    xq = torch.empty((32, K), dtype=torch.uint8, device=dev)
+    sx = torch.empty((32,), dtype=torch.float32, device=dev)
+    for M, seed in ((32, 1), (9, 2)):
+        xb = synthetic.activations(M, K, seed=seed)
+        y = qlinear.linear(dev16(xb, torch.bfloat16, dev), wq_d, sw_d, I8,
+                           scratch=(xq[:M], sx[:M]))
+        torch.cuda.synchronize()
+        xr, sr = orc.quantize_rows(xb, I8)
+        assert np.array_equal(xq[:M].cpu().numpy(), xr) and np.array_equal(sx[:M].cpu().numpy(), sr)
+        assert np.array_equal(bits(y), orc.epilogue_i8(orc.gemm_i8_acc(xr, wq), sr, sw))
