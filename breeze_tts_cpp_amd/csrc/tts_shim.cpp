@@ -248,6 +248,29 @@ void QuantizedGemm::linear(RowScaledView input, RowScaledView weight, TensorView
                         stream_, format_, output.type);
 }
 
+void QuantizedGemm::quantize_linear(TensorView input, RowScaledView scratch,
+                                    RowScaledView weight, TensorView output) {
+    // The checks of linear() on the scratch as its input, then qlin_linear.
+    scratch.validate();
+    weight.validate();
+    if (scratch.values.type != format_ || weight.values.type != format_ ||
+        scratch.rotation_size != weight.rotation_size || scratch.values.cols != weight.values.cols ||
+        scratch.values.rows != output.rows || weight.values.rows != output.cols ||
+        (output.type != Type::BF16 && output.type != Type::F16) || !output.dense())
+        throw std::invalid_argument("quantized linear dimensions/type mismatch");
+    const QuantizationGroups groups{scratch.group_size, weight.group_size, scratch.rotation_size};
+    const LinearPath path = planned(output.rows, output.cols, scratch.values.cols, output.type,
+                                    groups);
+    qlin_path p{static_cast<int>(path.kind), path.tokens, path.channels, path.splits,
+                path.waves, path.staged};
+    check(qlin_linear(&p, input.data, input.ld(), code(input.type), scratch.values.data,
+                      scratch.scales.ptr<float>(), weight.values.data, weight.scales.ptr<float>(),
+                      output.data, int(output.rows), int(output.cols), int(scratch.values.cols),
+                      code(format_), code(output.type), scratch.group_size, weight.group_size,
+                      scratch.rotation_size, workspace_, workspace_bytes_, stream_),
+          "quantized linear");
+}
+
 namespace {
 // An epilogue with nothing beyond bias and activation.
 bool finish_only(const ops::Epilogue &e) {
@@ -431,13 +454,18 @@ void prepare_quantized(TensorView weight, int rows, int output_channels, int inp
 }
 
 // ops/linear.cpp:71-90 (quantized weight, dense activation, no epilogue).
+// quantize_rows' checks, then both steps in QuantizedGemm::quantize_linear.
 void linear(TensorView input, RowScaledView weight, TensorView output, RowScaledView scratch) {
     weight.validate();
-    quantize_rows(input, scratch);
+    scratch.validate();
+    if ((input.type != Type::BF16 && input.type != Type::F16) || input.rows < 1 ||
+        input.cols < 1 || !input.data || !scratch.values.data || !scratch.scales.data ||
+        input.rows != scratch.values.rows || input.cols != scratch.values.cols)
+        throw std::invalid_argument("quantization source/destination shape/type mismatch");
     if (scratch.values.cols != weight.values.cols || output.rows != scratch.values.rows ||
         output.cols != weight.values.rows || !output.dense())
         throw std::invalid_argument("quantized linear dimensions/layout mismatch");
-    matmul(scratch, weight, output);
+    context(output.device).quantize_linear(input, scratch, weight, output);
 }
 // ops/linear.cpp:26-93, quantized weight and dense activation: quantize
 // into the scratch, then the GEMM with the fused finish; with a quantized

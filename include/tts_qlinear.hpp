@@ -190,6 +190,12 @@ class QuantizedGemm {
     void prepare(int rows, int output_channels, int input_channels, Type output_type = Type::BF16,
                  QuantizationGroups groups = {});
     void linear(RowScaledView input, RowScaledView weight, TensorView output);
+    // ops::linear's quantize_rows + linear as one call (no reference
+    // counterpart; qlin_linear): `scratch` receives the quantized input as
+    // quantize_rows would fill it, then `linear(scratch, weight, output)`,
+    // in one launch on decode paths that quantize inside the GEMM.
+    void quantize_linear(TensorView input, RowScaledView scratch, RowScaledView weight,
+                         TensorView output);
     // Fused bias + ReLU / tanh-GeLU finish (reference linear_finish,
     // ops/cuda/quantization.cpp:465-478), also bias-only: false when the
     // epilogue is none of those (the caller then finishes separately).
