@@ -161,7 +161,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // range, requested before the weight slab so that they land first. Lane
     // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
     // row m0 + 16t + row16: exactly the codes its MFMA B fragments need.
-    static_assert(!FQ || (NB > 0 && SL == 1 && !Packed && !Grouped && !Split && MT == 1 && NB == 1),
+    static_assert(!FQ || (NB > 0 && SL == 1 && !Packed && !Grouped && !Split && MT <= 2 && NB == 1),
                   "fused quantization: per-wave slab, activation blocks in registers");
     uint4 xraw[FQ ? NB : 1][MT][4][2];
     if constexpr (FQ) {
@@ -335,6 +335,14 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                                                 xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
 #pragma unroll
                         for (int j = 0; j < 2; ++j) {
+                            if constexpr (Fmt == I8) {
+                                codes[2 * h + j] = int(encode_i8x4(
+                                    widen(wd[2 * j] & 0xffffu) * inverse,
+                                    widen(wd[2 * j] >> 16) * inverse,
+                                    widen(wd[2 * j + 1] & 0xffffu) * inverse,
+                                    widen(wd[2 * j + 1] >> 16) * inverse));
+                                continue;
+                            }
                             const uint32_t c0 = encode<Fmt>(widen(wd[2 * j] & 0xffffu) * inverse);
                             const uint32_t c1 = encode<Fmt>(widen(wd[2 * j] >> 16) * inverse);
                             const uint32_t c2 = encode<Fmt>(widen(wd[2 * j + 1] & 0xffffu) * inverse);
@@ -720,13 +728,12 @@ int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 // blocks, per-channel scales, no split.
 template <int Fmt, int MT, int NF, class Out, int NB>
 int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
-    // Every workgroup quantizes its 16 x K token rows again (the activation
-    // is re-encoded once per column tile), which hides under the weight slab
-    // DMA only while it is small: measured on MI355X at M = 32, K = 2048 with
-    // 16-token tiles the single launch beats quantizer + GEMM (qkv 6.6 us vs
-    // 7.0, o_proj 6.2 vs 6.5), while 32-token tiles (gate_up 12.2 vs 11.4)
-    // and K = 6144 (down 14.1 vs 9.8) are slower.
-    if constexpr (MT == 1 && NB == 1) {
+    // Every workgroup quantizes its token rows again (the activation is
+    // re-encoded once per column tile), which pays only while that ALU work
+    // is small. Measured on MI355X at M = 32, single launch against quantizer
+    // + GEMM: K = 2048 qkv 6.1 us vs 7.0, o_proj 6.0 vs 6.5 (16-token tiles),
+    // gate_up 11.24 vs 11.31 (32-token tiles); K = 6144 down 14.1 vs 9.8.
+    if constexpr (MT <= 2 && NB == 1) {
         const int span = NB * kBlockK;
         dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
         const size_t lds = size_t(8) * 16 * NF * NB * kBlockK;
@@ -762,6 +769,7 @@ template <int Fmt, class Out>
 int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.tokens) {
     case 16: return launch_fused_mt<Fmt, 1, Out>(a, p, s);
+    case 32: return launch_fused_mt<Fmt, 2, Out>(a, p, s);
     default: return -4;
     }
 }
@@ -804,7 +812,7 @@ bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
     const int nb = a.K / (8 * kBlockK), mt = p.tokens / 16;
     return a.fq.src && !a.packed && !a.bias && !a.act && !a.input_group && !a.weight_group &&
            p.kind == KIND_SKINNY && p.splits == 1 && p.waves == 8 && p.staged == 1 &&
-           a.K == 8 * kBlockK && nb == 1 && mt == 1 && (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
+           a.K == 8 * kBlockK && nb == 1 && mt >= 1 && mt <= 2 && (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
            p.tokens % 16 == 0 && skinny_lds_bytes(a, p) <= kLdsBytes;
 }
 

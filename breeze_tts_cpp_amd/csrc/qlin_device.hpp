@@ -71,6 +71,22 @@ __device__ __forceinline__ uint32_t encode_i8(float x) {
     return uint32_t(int(__builtin_rintf(x))) & 0xffu;
 }
 
+// Four INT8 codes, packed low to high, equal to encode_i8 of each value.
+// After the same clamp, adding 1.5 * 2^23 rounds to an integer with the
+// current round-to-nearest-even mode (the value rintf gives for |x| <= 127)
+// and leaves that integer, two's complement, in the low mantissa byte of the
+// sum; three byte permutes gather the four low bytes.
+__device__ __forceinline__ uint32_t encode_i8x4(float a, float b, float c, float d) {
+    constexpr float kMagic = 12582912.f;  // 1.5 * 2^23
+    const uint32_t qa = __float_as_uint(fminf(127.f, fmaxf(-127.f, a)) + kMagic);
+    const uint32_t qb = __float_as_uint(fminf(127.f, fmaxf(-127.f, b)) + kMagic);
+    const uint32_t qc = __float_as_uint(fminf(127.f, fmaxf(-127.f, c)) + kMagic);
+    const uint32_t qd = __float_as_uint(fminf(127.f, fmaxf(-127.f, d)) + kMagic);
+    const uint32_t lo = __builtin_amdgcn_perm(qb, qa, 0x0c0c0400u);  // [a, b, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm(qd, qc, 0x0c0c0400u);  // [c, d, 0, 0]
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);               // [a, b, c, d]
+}
+
 // OCP e4m3fn, round-to-nearest-even, saturating to +-448 (the satfinite
 // conversion of reference quant_format.cuh:12-17). Integer rounding on the
 // fp32 bit pattern: exponent range [-6, 8] normal, 2^-9 subnormal step.

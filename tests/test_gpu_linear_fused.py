@@ -1,5 +1,5 @@
 """qlin_linear's one-launch decode form: for per-token scales on a decode
-path with 16-token tiles, per-wave weight slabs and K = 2048, the GEMM
+path with 16- or 32-token tiles, per-wave weight slabs and K = 2048, the GEMM
 quantizes its own token rows (the arithmetic of the per-token quantizer, reference
 row_quantize.cu:24-87) instead of a separate quantizer launch. Checked
 against the two-launch form on the same inputs (qlin_row_quantize +
@@ -26,9 +26,9 @@ def dev16(xb, dtype, dev):
 
 def fused_eligible(path, M, K):
     """The library's rule for the fused form (per-token, planned skinny path
-    with per-wave slabs, eight waves, no split, 16-token tiles, K == 2048)."""
+    with per-wave slabs, eight waves, no split, 16- or 32-token tiles, K == 2048)."""
     return (path.kind == 1 and path.splits == 1 and path.waves == 8 and path.staged == 1
-            and path.tokens == 16 and K == 2048)
+            and path.tokens in (16, 32) and K == 2048)
 
 
 def run_pair(dev, orc, xb, fmt, N, K, path=None, src=torch.bfloat16, out=torch.bfloat16, ld=None):
@@ -71,14 +71,15 @@ def test_fused_linear_planned(dev, orc, fmt, M, N, K):
 
 
 @pytest.mark.parametrize("tokens,channels,K", [(16, 16, 2048), (16, 32, 2048), (16, 48, 2048),
-                                               (16, 32, 4096), (16, 16, 6144), (32, 32, 2048)])
+                                               (16, 32, 4096), (16, 16, 6144), (32, 16, 2048),
+                                               (32, 32, 2048), (32, 48, 2048), (48, 16, 2048)])
 def test_fused_linear_tiles(dev, orc, tokens, channels, K):
     """Every fused channel tile and K range, partial token and channel tiles;
-    a 32-token tile and K != 2048 take the two-launch form."""
+    48-token tiles and K != 2048 take the two-launch form."""
     from breeze_tts_cpp_amd import qlinear
     M, N = 29, 16 * 37
     path = qlinear.Path(1, tokens, channels, 1, 8, 1)
-    assert fused_eligible(path, M, K) == (tokens == 16 and K == 2048)
+    assert fused_eligible(path, M, K) == (tokens <= 32 and K == 2048)
     print(f"fused tile {tokens}x{channels} K={K}", flush=True)
     run_pair(dev, orc, synthetic.activations(M, K, seed=tokens * channels + K), I8, N, K, path=path)
 
@@ -92,6 +93,12 @@ def test_fused_linear_f16_strided_special_rows(dev, orc, fmt):
     xb[3] = 0
     xb[7, 100] = synthetic.f32_to_bf16_bits(np.float32(3.0e4)).item()
     xb[11] = synthetic.f32_to_bf16_bits(np.full(K, 1e-3, np.float32))
+    # absmax 127 / 448: unit INT8 / FP8 scale, so the codes round exact
+    # half-integers (ties to even) and every representable magnitude.
+    ties = np.resize(np.arange(-127.0, 127.5, 0.5, dtype=np.float32), K)
+    ties[0] = 127.0
+    xb[13] = synthetic.f32_to_bf16_bits(ties)
+    xb[14] = synthetic.f32_to_bf16_bits(np.resize(np.linspace(-448, 448, 97, dtype=np.float32), K))
     print(f"fused f16 strided fmt={fmt}", flush=True)
     run_pair(dev, orc, xb, fmt, N, K, src=torch.float16, out=torch.float16, ld=K + 64)
     run_pair(dev, orc, xb, fmt, N, K, src=torch.bfloat16, out=torch.bfloat16, ld=K + 8)
