@@ -49,7 +49,10 @@ qlin::GemmPath to_internal(const qlin_path &p) {
 // LDS-tiled MFMA GEMM.
 qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_group) {
     qlin_path p{};
-    if (rows <= 64) {
+    // K groups of 32 / 64 have partials only in the skinny kernel, which
+    // also serves more than 64 rows in 64-token tiles.
+    const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
+    if (rows <= 64 || small_group) {
         // Decode: the weights are streamed once and each CU's share of them
         // bounds the time, so the grid is sized to about one workgroup per
         // CU (256 on MI355X). Rules measured on the BASELINE projections at
@@ -68,7 +71,10 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         p.kind = QLIN_KIND_SKINNY;
         p.splits = 1;
         const int full_tokens = (rows + 15) / 16 * 16;
-        if (rows > 16 && long(N) * K < (16L << 20)) {
+        if (rows > 64) {
+            p.tokens = 64;
+            p.channels = 32;
+        } else if (rows > 16 && long(N) * K < (16L << 20)) {
             const int token_tiles = (rows + 15) / 16;
             p.tokens = 16;
             p.channels = 32;
@@ -181,8 +187,9 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED,
                         "skinny path splits*waves (%d) must divide ceil(K/256) = %d",
                         p.splits * p.waves, blocks_k);
-        if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
-            return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
+        const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
+        if (small_group && p.splits != 1)
+            return fail(QLIN_ERR_UNSUPPORTED, "K groups of 32/64 have no split-K skinny variant");
         if (p.staged < 0 || p.staged > 2)
             return fail(QLIN_ERR_UNSUPPORTED, "staged must be 0, 1 or 2");
         if (p.staged && (p.waves != 8 || p.channels > 48 || p.splits != 1 ||
@@ -232,7 +239,8 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED,
                         "tiled staged (persistent) path is the INT8 per-channel eight-wave 256x256");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
-            return fail(QLIN_ERR_UNSUPPORTED, "K-group GEMM supports group size 128");
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "tiled K-group GEMM supports group size 128 (32/64: skinny path)");
         return ok();
     }
     return fail(QLIN_ERR_UNSUPPORTED, "unknown path kind %d", p.kind);
@@ -329,6 +337,8 @@ int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void 
     if (packed && !(path && path->kind)) p.staged = 0;
     int status = check_path(p, rows, N, K, fmt, input_group, weight_group);
     if (status) return status;
+    if (packed && ((input_group && input_group < 128) || (weight_group && weight_group < 128)))
+        return fail(QLIN_ERR_UNSUPPORTED, "packed weights support K groups of 128 only");
     qlin::GemmArgs a{static_cast<const uint8_t *>(x),
                      sx,
                      static_cast<const uint8_t *>(w),

@@ -96,7 +96,7 @@ __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4
 // loads all NB blocks of its K range straight into registers up front, one
 // contiguous 1 KB piece per (16-row fragment, 64-K step).
 template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out, int NB = 0,
-          int SL = 1, bool Packed = false, int FQ = 0>
+          int SL = 1, bool Packed = false, int FQ = 0, int GS = 128>
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
@@ -362,10 +362,10 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
         if constexpr (!Packed) {
-            // The slab DMA was issued before these loads: once at most they
-            // are outstanding, this wave's slab is in LDS.
-            constexpr int n = NB * MT * 4;
-            __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+            // The slab is in LDS once no load is outstanding. (A count of the
+            // newer activation loads would not do: the compiler may order
+            // them before the DMA, or skip a wave's out-of-range pieces.)
+            __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));
             if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
         }
     }
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     for (int f = 0; f < NF; ++f)
                         M_::run(acc[t][f], a[f][2 * h], a[f][2 * h + 1], b[t][2 * h],
                                 b[t][2 * h + 1]);
-        } else {
+        } else if constexpr (GS == 128) {
             // Two 128-K groups per block, each reduced natively then scaled.
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -430,6 +430,70 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                                 __builtin_fmaf(float(p[r]), sxg * swg[f][r], facc[t][f][r]);
                     }
                 }
+            }
+        } else {
+            // K groups of GS = 64 or 32 (the smaller of the two group sizes,
+            // as the reference's grouped_gemm dispatch, quant_grouped.cu:
+            // 185-202): each group reduced natively, then
+            // r = fmaf(p_g, sx_g * sw_g, r), groups ascending. A 64-K piece
+            // holds K bytes [16q, 16q + 16) in lane quad q of both operands,
+            // so a 32-K group is the piece with the other half's activation
+            // quads zeroed; a 64-K group of FP8 is the 128-K MFMA with the
+            // second piece zeroed.
+            const i32x4 zero = {0, 0, 0, 0};
+            // One group starting at K = k: scales, then per (token tile,
+            // fragment) the native partial from `part` and the fma.
+            auto group = [&](int k, auto part) {
+                const int g_in = input_group ? k / input_group : 0;
+                const int g_w = weight_group ? k / weight_group : 0;
+                float swg[NF][4];
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        int n = n0 + f * 16 + quad * 4 + r;
+                        swg[f][r] = (weight_group && n < N) ? sw[size_t(g_w) * N + n] : 1.f;
+                    }
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    int m = m0 + t * 16 + row16;
+                    float sxg = (input_group && m < M) ? sx[size_t(g_in) * M + m] : 1.f;
+#pragma unroll
+                    for (int f = 0; f < NF; ++f) {
+                        const Acc p = part(t, f);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            facc[t][f][r] =
+                                __builtin_fmaf(float(p[r]), sxg * swg[f][r], facc[t][f][r]);
+                    }
+                }
+            };
+            // Partial over one 64-K piece of the activation fragment bq.
+            auto piece = [&](const i32x4 &aq, const i32x4 &bq) {
+                Acc p = Acc{0, 0, 0, 0};
+                if constexpr (Fmt == I8) p = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq, bq, p, 0, 0, 0);
+                else M_::run(p, aq, zero, bq, zero);
+                return p;
+            };
+            if constexpr (GS == 64) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int k = kb + q * 64;
+                    if (k >= k_end) break;
+                    group(k, [&](int t, int f) { return piece(a[f][q], b[t][q]); });
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        const int k = kb + q * 64 + half * 32;
+                        if (k >= k_end) break;
+                        const bool mine = (quad >> 1) == half;
+                        group(k, [&](int t, int f) {
+                            return piece(a[f][q], mine ? b[t][q] : zero);
+                        });
+                    }
             }
         }
     };
@@ -488,11 +552,9 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             i32x4 b[MT][4];
             load_x(kb, b);
             if constexpr (NB > 0) {
-                // The slab DMA was issued before these MT*4 activation loads:
-                // once at most they are outstanding, this wave's slab is in LDS.
+                // The slab is in LDS once no load is outstanding.
                 if (kb == k_begin) {
-                    constexpr int n = MT * 4;
-                    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+                    __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));
                     if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
                 }
             }
@@ -617,15 +679,15 @@ __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ p
     store4<Out>(y, i4, v);
 }
 
-template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
+template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB, int GS = 128>
 int launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t stream) {
     const size_t lds = size_t(WK) * 16 * NF * NB * kBlockK;
     if (layout == 2)
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2>), grid,
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2, false, 0, GS>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
                            a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
     else
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1>), grid,
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1, false, 0, GS>), grid,
                            dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
                            a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
     return 0;
@@ -639,9 +701,12 @@ int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
     return 0;
 }
 
-template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out>
+// GS: K-group size of the grouped partials (128, or 64 / 32 on the
+// row-major, unsplit paths only).
+template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int GS = 128>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
-    if (a.packed) {
+    if (GS != 128 && (a.packed || p.splits != 1)) return -4;
+    if constexpr (GS == 128) if (a.packed) {
         // Packed weights: the waves split K (no grid split-K); each wave
         // streams its range in chunks of up to kMaxNB blocks held in
         // registers (weights and activations of a chunk: NB*(NF+MT) 64-byte
@@ -673,20 +738,21 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         if constexpr (WK == 8 && NF <= 3) {
             if (p.staged) {
                 switch (span / kBlockK) {
-                case 1: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, p.staged, stream);
-                case 2: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 2>(a, grid, span, p.staged, stream);
-                case 3: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 3>(a, grid, span, p.staged, stream);
+                case 1: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1, GS>(a, grid, span, p.staged, stream);
+                case 2: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 2, GS>(a, grid, span, p.staged, stream);
+                case 3: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 3, GS>(a, grid, span, p.staged, stream);
                 default: return -4;
                 }
             }
         }
         if (p.staged) return -4;
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out>), grid, block, 0,
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, 0, 1, false, 0, GS>), grid, block, 0,
                            stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span,
                            a.input_group, a.weight_group, a.bias, a.act, a.fq);
         return 0;
     }
     if (p.staged) return -4;
+    if constexpr (GS != 128) return -4;
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
                        a.input_group, a.weight_group, a.bias, a.act, a.fq);
@@ -704,23 +770,23 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     return 0;
 }
 
-template <int Fmt, int MT, int NF, bool Grouped, class Out>
+template <int Fmt, int MT, int NF, bool Grouped, class Out, int GS>
 int dispatch_wk(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.waves) {
-    case 1: return launch_variant<Fmt, MT, NF, 1, Grouped, Out>(a, p, s);
-    case 2: return launch_variant<Fmt, MT, NF, 2, Grouped, Out>(a, p, s);
-    case 4: return launch_variant<Fmt, MT, NF, 4, Grouped, Out>(a, p, s);
-    case 8: return launch_variant<Fmt, MT, NF, 8, Grouped, Out>(a, p, s);
+    case 1: return launch_variant<Fmt, MT, NF, 1, Grouped, Out, GS>(a, p, s);
+    case 2: return launch_variant<Fmt, MT, NF, 2, Grouped, Out, GS>(a, p, s);
+    case 4: return launch_variant<Fmt, MT, NF, 4, Grouped, Out, GS>(a, p, s);
+    case 8: return launch_variant<Fmt, MT, NF, 8, Grouped, Out, GS>(a, p, s);
     default: return -4;
     }
 }
 
-template <int Fmt, int MT, bool Grouped, class Out>
+template <int Fmt, int MT, bool Grouped, class Out, int GS>
 int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    if (p.channels == 16) return dispatch_wk<Fmt, MT, 1, Grouped, Out>(a, p, s);
-    if (p.channels == 32) return dispatch_wk<Fmt, MT, 2, Grouped, Out>(a, p, s);
-    if (p.channels == 48) return dispatch_wk<Fmt, MT, 3, Grouped, Out>(a, p, s);
-    if (p.channels == 64) return dispatch_wk<Fmt, MT, 4, Grouped, Out>(a, p, s);
+    if (p.channels == 16) return dispatch_wk<Fmt, MT, 1, Grouped, Out, GS>(a, p, s);
+    if (p.channels == 32) return dispatch_wk<Fmt, MT, 2, Grouped, Out, GS>(a, p, s);
+    if (p.channels == 48) return dispatch_wk<Fmt, MT, 3, Grouped, Out, GS>(a, p, s);
+    if (p.channels == 64) return dispatch_wk<Fmt, MT, 4, Grouped, Out, GS>(a, p, s);
     return -4;
 }
 
@@ -774,20 +840,28 @@ int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     }
 }
 
-template <int Fmt, bool Grouped, class Out>
+template <int Fmt, bool Grouped, class Out, int GS = 128>
 int dispatch_mt(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.tokens) {
-    case 16: return dispatch_nf<Fmt, 1, Grouped, Out>(a, p, s);
-    case 32: return dispatch_nf<Fmt, 2, Grouped, Out>(a, p, s);
-    case 48: return dispatch_nf<Fmt, 3, Grouped, Out>(a, p, s);
-    case 64: return dispatch_nf<Fmt, 4, Grouped, Out>(a, p, s);
+    case 16: return dispatch_nf<Fmt, 1, Grouped, Out, GS>(a, p, s);
+    case 32: return dispatch_nf<Fmt, 2, Grouped, Out, GS>(a, p, s);
+    case 48: return dispatch_nf<Fmt, 3, Grouped, Out, GS>(a, p, s);
+    case 64: return dispatch_nf<Fmt, 4, Grouped, Out, GS>(a, p, s);
     default: return -4;
     }
 }
 
 template <int Fmt, class Out>
 int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    if (a.input_group || a.weight_group) return dispatch_mt<Fmt, true, Out>(a, p, s);
+    if (a.input_group || a.weight_group) {
+        // Partials per the smaller group size (quant_grouped.cu:185-187).
+        const int g = a.input_group && (!a.weight_group || a.input_group <= a.weight_group)
+                          ? a.input_group : a.weight_group;
+        if (g == 64) return dispatch_mt<Fmt, true, Out, 64>(a, p, s);
+        if (g == 32) return dispatch_mt<Fmt, true, Out, 32>(a, p, s);
+        if (g != 128) return -4;
+        return dispatch_mt<Fmt, true, Out>(a, p, s);
+    }
     return dispatch_mt<Fmt, false, Out>(a, p, s);
 }
 

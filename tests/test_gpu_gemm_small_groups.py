@@ -1,0 +1,98 @@
+"""K groups of 32 and 64 in the quantized GEMM, as the reference's
+grouped_gemm dispatch accepts them (quant_grouped.cu:185-202): partials per
+the smaller of the two group sizes, each scaled by its own activation and
+weight scales (a 32-column partial of a 128-column activation group takes
+that group's scale) and fma-accumulated in ascending K order
+(quant_grouped.cu:85-146). INT8 bit-exact against the oracle's grouped
+GEMM with the planned wave split; FP8 within rel-L2 1e-2 of the exact
+product. More than 64 rows run in 64-token skinny tiles."""
+import numpy as np
+import pytest
+import torch
+
+from breeze_tts_cpp_amd import synthetic
+
+BF16, F32, I32, FP8, I8, F16 = 0, 1, 2, 3, 4, 5
+pytestmark = pytest.mark.gpu
+
+
+def bits(y):
+    return y.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def quantize(orc, b, fmt, group):
+    return orc.quantize_rows(b, fmt, group=group) if group else orc.quantize_rows(b, fmt)
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("ig,wg", [(32, 32), (64, 64), (128, 32), (32, 128), (64, 128),
+                                   (128, 64), (0, 64), (32, 0)])
+@pytest.mark.parametrize("M,N,K", [(8, 256, 2048), (32, 4096, 2048), (100, 272, 1536),
+                                   (3, 48, 4000)])
+def test_small_groups(dev, orc, fmt, ig, wg, M, N, K):
+    from breeze_tts_cpp_amd import qlinear
+    print(f"small groups fmt={fmt} ig={ig} wg={wg} M={M} N={N} K={K}", flush=True)
+    xq, sx = quantize(orc, synthetic.activations(M, K, seed=M + ig), fmt, ig)
+    wq, sw = quantize(orc, synthetic.weights(N, K, seed=N + wg), fmt, wg)
+    p = qlinear.plan(M, N, K, fmt, ig, wg)
+    assert p.kind == qlinear.KIND_SKINNY and p.splits == 1
+    y = qlinear.gemm(torch.from_numpy(xq).to(dev), torch.from_numpy(sx).to(dev),
+                     torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev), fmt,
+                     input_group=ig, weight_group=wg, path=p)
+    torch.cuda.synchronize()
+    got = bits(y)
+    if fmt == I8:
+        span = -(-K // 256) * 256 // p.waves
+        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, 1, p.waves, span)
+        assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    else:
+        ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, ig, wg)
+        f = synthetic.bf16_bits_to_f32(got).astype(np.float64)
+        assert np.linalg.norm(f - ideal) / np.linalg.norm(ideal) <= 1e-2
+
+
+def test_small_groups_unsupported_forms(dev, orc):
+    """Split-K, packed weights and the tiled kernel decline 32/64 groups."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N, K = 8, 64, 1024
+    xq, sx = orc.quantize_rows(synthetic.activations(M, K, seed=1), I8, group=32)
+    wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=1), I8, group=32)
+    args = [torch.from_numpy(a).to(dev) for a in (xq, sx, wq, sw)]
+    for path in (qlinear.Path(1, 16, 16, 2, 2, 0), qlinear.Path(2, 128, 128, 1, 8, 0)):
+        with pytest.raises(qlinear.QLinearError):
+            qlinear.gemm(*args, I8, input_group=32, weight_group=32, path=path,
+                         workspace=torch.empty(1 << 20, dtype=torch.uint8, device=dev))
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("group", [0, 128, 64, 32])
+@pytest.mark.parametrize("M,K", [(3, 3968), (8, 4000), (20, 2000), (33, 1808), (40, 6000)])
+def test_staged_ragged_k(dev, orc, fmt, group, M, K):
+    """Staged (LDS slab) decode paths with K not a multiple of 256: the last
+    wave's range ends inside a 256-K block, so some of its activation pieces
+    lie past K. The slab wait counts the activation loads issued behind the
+    slab DMA; every one must be issued for the wait to cover the whole slab
+    (weight rows 14-15 of each tile came from the last DMA instruction)."""
+    from breeze_tts_cpp_amd import qlinear
+    N = 48
+    print(f"staged ragged fmt={fmt} group={group} M={M} K={K}", flush=True)
+    xq, sx = quantize(orc, synthetic.activations(M, K, seed=K), fmt, group)
+    wq, sw = quantize(orc, synthetic.weights(N, K, seed=K + 1), fmt, group)
+    p = qlinear.plan(M, N, K, fmt, group, group)
+    y = qlinear.gemm(torch.from_numpy(xq).to(dev), torch.from_numpy(sx).to(dev),
+                     torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev), fmt,
+                     input_group=group, weight_group=group, path=p)
+    torch.cuda.synchronize()
+    got = bits(y)
+    if fmt == I8 and group:
+        span = -(-K // 256) * 256 // p.waves
+        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, group, group, 1, p.waves, span)
+        assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches, {p}"
+    elif fmt == I8:
+        ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw)
+        assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches, {p}"
+    else:
+        ideal = (orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, group, group) if group
+                 else orc.gemm_fp8_ideal(xq, sx, wq, sw))
+        f = synthetic.bf16_bits_to_f32(got).astype(np.float64)
+        assert np.linalg.norm(f - ideal) / np.linalg.norm(ideal) <= 1e-2
