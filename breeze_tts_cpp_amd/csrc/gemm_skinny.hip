@@ -161,7 +161,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // range, requested before the weight slab so that they land first. Lane
     // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
     // row m0 + 16t + row16: exactly the codes its MFMA B fragments need.
-    static_assert(!FQ || (NB > 0 && SL == 1 && !Packed && !Grouped && !Split && MT <= 2 && NB == 1),
+    static_assert(!FQ || (NB > 0 && SL == 1 && !Packed && !Grouped && !Split && MT == 1 && NB == 1 && Fmt == I8),
                   "fused quantization: per-wave slab, activation blocks in registers");
     uint4 xraw[FQ ? NB : 1][MT][4][2];
     if constexpr (FQ) {
@@ -796,10 +796,13 @@ template <int Fmt, int MT, int NF, class Out, int NB>
 int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     // Every workgroup quantizes its token rows again (the activation is
     // re-encoded once per column tile), which pays only while that ALU work
-    // is small. Measured on MI355X at M = 32, single launch against quantizer
-    // + GEMM: K = 2048 qkv 6.1 us vs 7.0, o_proj 6.0 vs 6.5 (16-token tiles),
-    // gate_up 11.24 vs 11.31 (32-token tiles); K = 6144 down 14.1 vs 9.8.
-    if constexpr (MT <= 2 && NB == 1) {
+    // is small. Measured on MI355X (graphs of 16 launches over distinct
+    // weights), single launch against quantizer + GEMM: INT8 K = 2048 with
+    // 16-token tiles qkv 5.7-6.9 us vs 6.7-7.7, o_proj 5.4-6.6 vs 5.9-7.0,
+    // gate_up (M <= 16) 8.5-8.6 vs 9.6-9.9; a 32-token tile (gate_up M = 32)
+    // 12.0 vs 11.8; K = 6144 (down) 14.1 vs 9.8; FP8 (integer e4m3 encoder,
+    // ~15 VALU ops per value) 13-26 us vs 6.4-12.
+    if constexpr (MT == 1 && NB == 1 && Fmt == I8) {
         const int span = NB * kBlockK;
         dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
         const size_t lds = size_t(8) * 16 * NF * NB * kBlockK;
@@ -835,7 +838,6 @@ template <int Fmt, class Out>
 int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.tokens) {
     case 16: return launch_fused_mt<Fmt, 1, Out>(a, p, s);
-    case 32: return launch_fused_mt<Fmt, 2, Out>(a, p, s);
     default: return -4;
     }
 }
@@ -886,7 +888,7 @@ bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
     const int nb = a.K / (8 * kBlockK), mt = p.tokens / 16;
     return a.fq.src && !a.packed && !a.bias && !a.act && !a.input_group && !a.weight_group &&
            p.kind == KIND_SKINNY && p.splits == 1 && p.waves == 8 && p.staged == 1 &&
-           a.K == 8 * kBlockK && nb == 1 && mt >= 1 && mt <= 2 && (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
+           a.fmt == I8 && a.K == 8 * kBlockK && nb == 1 && mt == 1 && (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
            p.tokens % 16 == 0 && skinny_lds_bytes(a, p) <= kLdsBytes;
 }
 

@@ -130,7 +130,7 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
  * rotation) into the scratch activation (xq [rows, K], sx), as
  * qlin_row_quantize, then y = D(xq . w^T) as qlin_gemm with `path` (NULL =
  * planned). Two launches on `stream` (quantizer, GEMM), or one where the
- * path is a decode path with 16- or 32-token tiles, per-wave weight slabs and
+ * path is an INT8 decode path with 16-token tiles, per-wave weight slabs and
  * K = 2048 with per-token scales, no rotation and a 16-byte-aligned source
  * with ld % 8 == 0: there the GEMM quantizes its own token rows and fills
  * (xq, sx) with the same bits. The first failing check's status is

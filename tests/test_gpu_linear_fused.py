@@ -1,5 +1,5 @@
 """qlin_linear's one-launch decode form: for per-token scales on a decode
-path with 16- or 32-token tiles, per-wave weight slabs and K = 2048, the GEMM
+INT8 path with 16-token tiles, per-wave weight slabs and K = 2048, the GEMM
 quantizes its own token rows (the arithmetic of the per-token quantizer, reference
 row_quantize.cu:24-87) instead of a separate quantizer launch. Checked
 against the two-launch form on the same inputs (qlin_row_quantize +
@@ -26,9 +26,10 @@ def dev16(xb, dtype, dev):
 
 def fused_eligible(path, M, K):
     """The library's rule for the fused form (per-token, planned skinny path
-    with per-wave slabs, eight waves, no split, 16- or 32-token tiles, K == 2048)."""
+    with per-wave slabs, eight waves, no split, 16-token tiles, K == 2048;
+    INT8 only)."""
     return (path.kind == 1 and path.splits == 1 and path.waves == 8 and path.staged == 1
-            and path.tokens in (16, 32) and K == 2048)
+            and path.tokens == 16 and K == 2048)
 
 
 def run_pair(dev, orc, xb, fmt, N, K, path=None, src=torch.bfloat16, out=torch.bfloat16, ld=None):
@@ -75,11 +76,11 @@ def test_fused_linear_planned(dev, orc, fmt, M, N, K):
                                                (32, 32, 2048), (32, 48, 2048), (48, 16, 2048)])
 def test_fused_linear_tiles(dev, orc, tokens, channels, K):
     """Every fused channel tile and K range, partial token and channel tiles;
-    48-token tiles and K != 2048 take the two-launch form."""
+    wider token tiles and K != 2048 take the two-launch form."""
     from breeze_tts_cpp_amd import qlinear
     M, N = 29, 16 * 37
     path = qlinear.Path(1, tokens, channels, 1, 8, 1)
-    assert fused_eligible(path, M, K) == (tokens <= 32 and K == 2048)
+    assert fused_eligible(path, M, K) == (tokens == 16 and K == 2048)
     print(f"fused tile {tokens}x{channels} K={K}", flush=True)
     run_pair(dev, orc, synthetic.activations(M, K, seed=tokens * channels + K), I8, N, K, path=path)
 
