@@ -705,8 +705,10 @@ int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
 // row-major, unsplit paths only).
 template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int GS = 128>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
+    // 32/64 groups: row-major weights and no split only (checked first, so
+    // the packed and split-K launches below run with GS == 128).
     if (GS != 128 && (a.packed || p.splits != 1)) return -4;
-    if constexpr (GS == 128) if (a.packed) {
+    if (a.packed) {
         // Packed weights: the waves split K (no grid split-K); each wave
         // streams its range in chunks of up to kMaxNB blocks held in
         // registers (weights and activations of a chunk: NB*(NF+MT) 64-byte
@@ -752,7 +754,6 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         return 0;
     }
     if (p.staged) return -4;
-    if constexpr (GS != 128) return -4;
     hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
                        a.input_group, a.weight_group, a.bias, a.act, a.fq);
