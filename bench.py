@@ -244,19 +244,21 @@ def measured_traffic(name):
     """HBM bytes per launch of the decode linear for projection `name`, from the
     committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (profiles/hbm_traffic_decode_linear.md, copy-kernel calibrated: a row per
-    projection, the last column the scaled bytes per dispatch); None when that
-    summary has no row for it."""
+    projection, the last column the scaled bytes per dispatch; the last row for
+    a projection is the current measurement); None when that summary has no
+    row for it."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_linear.md")
     if not os.path.exists(path):
         return None
+    found = None
     for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) >= 3 and cells[0] == name:
             try:
-                return int(cells[-1].replace(",", ""))
+                found = int(cells[-1].replace(",", ""))
             except ValueError:
-                return None
-    return None
+                found = None
+    return found
 
 
 def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections):
