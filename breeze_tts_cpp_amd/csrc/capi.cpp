@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <utility>
 
 #include "qlin_internal.hpp"
 
@@ -65,9 +66,6 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         //  - otherwise the largest workgroup count up to 256, then wider token
         //    tiles (fewer activation re-reads), then fewer weight rows
         //    (gate_up keeps 32/64-token tiles).
-        // Wave64s split K eight ways; weight slabs are staged through LDS,
-        // one slab per wave (2-4% faster than the cooperative slab), when
-        // they fit.
         p.kind = QLIN_KIND_SKINNY;
         p.splits = 1;
         const int full_tokens = (rows + 15) / 16 * 16;
@@ -84,10 +82,13 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
                     break;
                 }
         } else {
+            // Token tiles of 16, 32 or 64 rows that divide the rows rounded
+            // up to 16 (48 rows count as one padded 64-row tile).
+            const int cap = full_tokens == 48 ? 64 : full_tokens;
             long best = -1;
             for (int channels : {16, 32, 48}) {
-                for (int tokens = full_tokens; tokens >= 16; tokens -= 16) {
-                    if (full_tokens % tokens && tokens != 16) continue;
+                for (int tokens : {64, 32, 16}) {
+                    if (tokens > cap || (cap % tokens && tokens != 16)) continue;
                     const long wgs = long((N + channels - 1) / channels) * ((rows + tokens - 1) / tokens);
                     const long score = (wgs <= 256 ? wgs : 256 - (wgs - 256)) * 4096 + tokens * 64 - channels;
                     if (score > best) {
@@ -98,13 +99,12 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
                 }
             }
         }
-        const int blocks_k = (K + 255) / 256;
-        int waves = 8;
-        while (waves > 1 && blocks_k % waves) waves /= 2;
-        p.waves = waves;
-        const bool slab_fits = waves == 8 && blocks_k / 8 <= 3 &&
-                               long(p.channels) * blocks_k * 256 <= 160 * 1024;
-        p.staged = slab_fits ? 1 : 0;
+        // Eight wave64s split K inside a workgroup; weight slabs are staged
+        // through LDS, one slab per wave, when a wave's range is at most
+        // three 256-byte blocks and the slab fits.
+        p.waves = 8;
+        const int nb = qlin::skinny_span(K, 1) / 256;
+        p.staged = nb <= 3 && long(p.channels) * nb * 8 * 256 <= 160 * 1024 ? 1 : 0;
         qlin::GemmArgs a{};
         a.M = rows;
         a.N = N;
@@ -162,8 +162,6 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         p.waves = 8;
         if (fmt == QLIN_I8 && tiles_256x128 >= 256 && full) p.channels = 256;
     }
-    // (The persistent INT8 kernel, tiled staged = 1, is not planned: at
-    // steady clocks the eight-wave kernel is faster on every BASELINE shape.)
     return p;
 }
 
@@ -173,30 +171,27 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
     (void)N;
     (void)fmt;
     if (p.kind == QLIN_KIND_SKINNY) {
-        if (p.tokens != 16 && p.tokens != 32 && p.tokens != 48 && p.tokens != 64)
-            return fail(QLIN_ERR_UNSUPPORTED, "skinny path tokens must be 16/32/48/64 (got %d)",
+        if (p.tokens != 16 && p.tokens != 32 && p.tokens != 64)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny path tokens must be 16/32/64 (got %d)",
                         p.tokens);
-        if (p.channels != 16 && p.channels != 32 && p.channels != 48 && p.channels != 64)
+        if (p.channels != 16 && p.channels != 32 && p.channels != 48)
             return fail(QLIN_ERR_UNSUPPORTED,
-                        "skinny path channels must be 16, 32, 48 or 64 (got %d)", p.channels);
-        if (p.waves != 1 && p.waves != 2 && p.waves != 4 && p.waves != 8)
-            return fail(QLIN_ERR_UNSUPPORTED, "skinny path waves must be 1/2/4/8 (got %d)",
-                        p.waves);
+                        "skinny path channels must be 16, 32 or 48 (got %d)", p.channels);
+        if (p.waves != 8)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny path waves must be 8 (got %d)", p.waves);
         const int blocks_k = (K + 255) / 256;
-        if (p.splits < 1 || blocks_k % (p.splits * p.waves))
+        if (p.splits < 1 || p.splits > blocks_k)
             return fail(QLIN_ERR_UNSUPPORTED,
-                        "skinny path splits*waves (%d) must divide ceil(K/256) = %d",
-                        p.splits * p.waves, blocks_k);
+                        "skinny path splits (%d) must be in 1..ceil(K/256) = %d", p.splits,
+                        blocks_k);
         const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
         if (small_group && p.splits != 1)
             return fail(QLIN_ERR_UNSUPPORTED, "K groups of 32/64 have no split-K skinny variant");
-        if (p.staged < 0 || p.staged > 2)
-            return fail(QLIN_ERR_UNSUPPORTED, "staged must be 0, 1 or 2");
-        if (p.staged && (p.waves != 8 || p.channels > 48 || p.splits != 1 ||
-                         blocks_k / p.waves > 3 || p.channels * blocks_k * 256 > 160 * 1024))
+        if (p.staged < 0 || p.staged > 1)
+            return fail(QLIN_ERR_UNSUPPORTED, "skinny staged must be 0 or 1");
+        if (p.staged && (p.splits != 1 || qlin::skinny_span(K, 1) > 3 * 256))
             return fail(QLIN_ERR_UNSUPPORTED,
-                        "staged skinny path needs waves 8, channels 16/32/48, no split, "
-                        "ceil(K/256) <= 24 and a weight slab within 160 KiB of LDS");
+                        "staged skinny path needs no split and ceil(K/256) <= 24");
         qlin::GemmArgs a{};
         a.M = rows;
         a.N = N;
@@ -233,11 +228,7 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
-        // tiled staged = 1: the persistent 8-wave INT8 256x256 kernel
-        if (p.staged && !(p.staged == 1 && fmt == QLIN_I8 && p.waves == 8 && !input_group &&
-                          !weight_group))
-            return fail(QLIN_ERR_UNSUPPORTED,
-                        "tiled staged (persistent) path is the INT8 per-channel eight-wave 256x256");
+        if (p.staged) return fail(QLIN_ERR_UNSUPPORTED, "tiled path staged must be 0");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED,
                         "tiled K-group GEMM supports group size 128 (32/64: skinny path)");
@@ -247,6 +238,10 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
 }
 
 }  // namespace
+
+namespace qlin {
+int set_error(int status, const char *message) { return fail(status, "%s", message); }
+}  // namespace qlin
 
 extern "C" {
 
@@ -449,10 +444,25 @@ int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void
     if (!xq || !sx) return fail(QLIN_ERR_INVALID, "linear needs the scratch activation (xq, sx)");
     // Decode shapes with per-token scales: one launch in which the GEMM
     // quantizes its own token rows (and fills the scratch as the quantizer
-    // would), when the planned path has a fused variant.
+    // would), when the planned path has a fused variant. In that launch some
+    // workgroups still read x while others write y and the scratch, so an
+    // output or scratch overlapping x takes the two-launch form, which
+    // reads all of x before the GEMM writes.
+    const auto span_of = [](const void *p, size_t bytes) {
+        const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+        return std::pair<uintptr_t, uintptr_t>{b, b + bytes};
+    };
+    const auto overlaps = [](std::pair<uintptr_t, uintptr_t> a, std::pair<uintptr_t, uintptr_t> b) {
+        return a.first < b.second && b.first < a.second;
+    };
+    const bool disjoint =
+        rows >= 1 && N >= 1 && K >= 1 && ld >= 1 && x && y &&
+        !overlaps(span_of(x, size_t(rows) * ld * 2), span_of(y, size_t(rows) * N * 2)) &&
+        !overlaps(span_of(x, size_t(rows) * ld * 2), span_of(xq, size_t(rows) * K)) &&
+        !overlaps(span_of(x, size_t(rows) * ld * 2), span_of(sx, size_t(rows) * 4));
     if (!input_group && !rotation && (src_type == QLIN_BF16 || src_type == QLIN_F16) && x &&
         aligned(x, 16) && ld % 8 == 0 && ld >= K && rows >= 1 && aligned(xq, 16) &&
-        aligned(sx, 4)) {
+        aligned(sx, 4) && disjoint) {
         const qlin::FusedSource fq{static_cast<const uint16_t *>(x), ld, src_type == QLIN_F16 ? 1 : 0,
                                    static_cast<uint8_t *>(xq), sx};
         int r = gemm_impl(path, xq, sx, w, sw, y, rows, N, K, fmt, out_type, input_group,

@@ -37,11 +37,13 @@ namespace qlin {
 namespace {
 
 // One 256-thread workgroup per row; lane t holds columns [8t, 8t+8).
-template <int Fmt, class T, bool Add, bool Scaled, bool Gemma, bool Rot, int G, bool Vec>
+// update_scale (optional) and gemma are uniform run-time choices.
+template <int Fmt, class T, bool Add, bool Rot, int G, bool Vec>
 __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
     uint16_t *__restrict__ x, const uint16_t *__restrict__ update,
     const uint16_t *__restrict__ update_scale, const uint16_t *__restrict__ weight,
-    uint8_t *__restrict__ q, float *__restrict__ scales, int rows, int cols, float eps) {
+    uint8_t *__restrict__ q, float *__restrict__ scales, int rows, int cols, float eps,
+    int gemma) {
     const int row = blockIdx.x, column = threadIdx.x * 8;
     uint16_t *xr = x + size_t(row) * cols;
     float v[1][8], w[8];
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
     if constexpr (Add) {
         float u[8];
         load8<T, Vec>(update + size_t(row) * cols, column, cols, u);
-        if constexpr (Scaled) {
+        if (update_scale) {
             float s[8];
             load8<T, Vec>(update_scale, column, cols, s);
 #pragma unroll
@@ -72,10 +74,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
 #pragma unroll
     for (int p = 0; p < kThreads / 32; ++p) total += partial[p];
     const float inv_norm = rsqrt_rn(total / float(cols) + eps);
+    if (gemma) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if constexpr (Gemma) v[0][i] = round16<T>((v[0][i] * inv_norm) * (w[i] + 1.f));
-        else v[0][i] = round16<T>(round16<T>(v[0][i] * inv_norm) * w[i]);
+        for (int i = 0; i < 8; ++i) v[0][i] = round16<T>((v[0][i] * inv_norm) * (w[i] + 1.f));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[0][i] = round16<T>(round16<T>(v[0][i] * inv_norm) * w[i]);
     }
     encode_row<Fmt, 1, Rot, G, Vec>(v, q, scales, row, rows, cols);
 }
@@ -93,11 +97,12 @@ template <int Kind> __device__ __forceinline__ float activate(float x) {
 // columns (it*NT + t)*8 .. +8 (gate at that column, up at width + column).
 // Few rows (decode) use NT = 256 * chunks and one chunk per lane, so the
 // activation chains of a row run on more SIMDs at once.
-template <int Fmt, class T, int Kind, int Items, bool Rot, int G, bool Vec, int NT = kThreads>
+// The activation kind is a uniform run-time choice.
+template <int Fmt, class T, int Items, bool Rot, int G, bool Vec, int NT = kThreads>
 __global__ __launch_bounds__(NT) void gated_quantize(const uint16_t *__restrict__ input,
                                                      uint8_t *__restrict__ q,
                                                      float *__restrict__ scales, int rows,
-                                                     int width) {
+                                                     int width, int kind) {
     const int row = blockIdx.x;
     const uint16_t *gate = input + size_t(row) * width * 2, *up = gate + width;
     float v[Items][8];
@@ -107,14 +112,19 @@ __global__ __launch_bounds__(NT) void gated_quantize(const uint16_t *__restrict_
         float g[8], u[8];
         load8<T, Vec>(gate, column, width, g);
         load8<T, Vec>(up, column, width, u);
+        if (kind) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(round16<T>(activate<Kind>(g[i])) * u[i]);
+            for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(round16<T>(activate<1>(g[i])) * u[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(round16<T>(activate<0>(g[i])) * u[i]);
+        }
     }
     encode_row<Fmt, Items, Rot, G, Vec, NT>(v, q, scales, row, rows, width);
 }
 
 // ---------------------------------------------------------------- launchers
-template <int Fmt, class T, bool Add, bool Scaled, bool Gemma, bool Vec>
+template <int Fmt, class T, bool Add, bool Vec>
 void launch_norm_enc(const NormQuantizeArgs &a, hipStream_t s) {
     auto *x = static_cast<uint16_t *>(a.residual);
     auto *u = static_cast<const uint16_t *>(a.update);
@@ -122,9 +132,9 @@ void launch_norm_enc(const NormQuantizeArgs &a, hipStream_t s) {
     auto *w = static_cast<const uint16_t *>(a.weight);
     auto *q = static_cast<uint8_t *>(a.values);
 #define QLIN_NORM(R, G)                                                                        \
-    hipLaunchKernelGGL((residual_rms_quantize<Fmt, T, Add, Scaled, Gemma, R, G, Vec>),         \
-                       dim3(a.rows), dim3(kThreads), 0, s, x, u, us, w, q, a.scales, a.rows,  \
-                       a.cols, a.eps)
+    hipLaunchKernelGGL((residual_rms_quantize<Fmt, T, Add, R, G, Vec>), dim3(a.rows),          \
+                       dim3(kThreads), 0, s, x, u, Add ? us : nullptr, w, q, a.scales, a.rows, \
+                       a.cols, a.eps, a.gemma)
     if (a.group == 32) { if (a.rotation) QLIN_NORM(true, 32); else QLIN_NORM(false, 32); }
     else if (a.group == 64) { if (a.rotation) QLIN_NORM(true, 64); else QLIN_NORM(false, 64); }
     else if (a.group == 128) { if (a.rotation) QLIN_NORM(true, 128); else QLIN_NORM(false, 128); }
@@ -135,25 +145,17 @@ void launch_norm_enc(const NormQuantizeArgs &a, hipStream_t s) {
 
 template <int Fmt, class T, bool Vec>
 void launch_norm_t(const NormQuantizeArgs &a, hipStream_t s) {
-    if (!a.update) {
-        if (a.gemma) launch_norm_enc<Fmt, T, false, false, true, Vec>(a, s);
-        else launch_norm_enc<Fmt, T, false, false, false, Vec>(a, s);
-    } else if (!a.update_scale) {
-        if (a.gemma) launch_norm_enc<Fmt, T, true, false, true, Vec>(a, s);
-        else launch_norm_enc<Fmt, T, true, false, false, Vec>(a, s);
-    } else {
-        if (a.gemma) launch_norm_enc<Fmt, T, true, true, true, Vec>(a, s);
-        else launch_norm_enc<Fmt, T, true, true, false, Vec>(a, s);
-    }
+    if (a.update) launch_norm_enc<Fmt, T, true, Vec>(a, s);
+    else launch_norm_enc<Fmt, T, false, Vec>(a, s);
 }
 
-template <int Fmt, class T, int Kind, int Items, bool Vec, int NT = kThreads>
+template <int Fmt, class T, int Items, bool Vec, int NT = kThreads>
 void launch_gated_enc(const GatedQuantizeArgs &a, hipStream_t s) {
     auto *in = static_cast<const uint16_t *>(a.input);
     auto *q = static_cast<uint8_t *>(a.values);
 #define QLIN_GATED(R, G)                                                                       \
-    hipLaunchKernelGGL((gated_quantize<Fmt, T, Kind, Items, R, G, Vec, NT>), dim3(a.rows),     \
-                       dim3(NT), 0, s, in, q, a.scales, a.rows, a.width)
+    hipLaunchKernelGGL((gated_quantize<Fmt, T, Items, R, G, Vec, NT>), dim3(a.rows),           \
+                       dim3(NT), 0, s, in, q, a.scales, a.rows, a.width, a.kind)
     if (a.group == 32) { if (a.rotation) QLIN_GATED(true, 32); else QLIN_GATED(false, 32); }
     else if (a.group == 64) { if (a.rotation) QLIN_GATED(true, 64); else QLIN_GATED(false, 64); }
     else if (a.group == 128) { if (a.rotation) QLIN_GATED(true, 128); else QLIN_GATED(false, 128); }
@@ -167,27 +169,21 @@ void launch_gated_enc(const GatedQuantizeArgs &a, hipStream_t s) {
 // chunks per lane; at M = 4096 it is 3% slower.
 constexpr int kSpreadRows = 512;
 
-template <int Fmt, class T, int Kind, bool Vec>
+template <int Fmt, class T, bool Vec>
 void launch_gated_items(const GatedQuantizeArgs &a, hipStream_t s) {
     const int chunks = (a.width + kChunk - 1) / kChunk;
     if (a.rows <= kSpreadRows && chunks > 1) {
-        if (chunks == 2) launch_gated_enc<Fmt, T, Kind, 1, Vec, 2 * kThreads>(a, s);
-        else if (chunks == 3) launch_gated_enc<Fmt, T, Kind, 1, Vec, 3 * kThreads>(a, s);
-        else launch_gated_enc<Fmt, T, Kind, 1, Vec, 4 * kThreads>(a, s);
+        if (chunks == 2) launch_gated_enc<Fmt, T, 1, Vec, 2 * kThreads>(a, s);
+        else if (chunks == 3) launch_gated_enc<Fmt, T, 1, Vec, 3 * kThreads>(a, s);
+        else launch_gated_enc<Fmt, T, 1, Vec, 4 * kThreads>(a, s);
         return;
     }
     switch (chunks) {
-    case 1: launch_gated_enc<Fmt, T, Kind, 1, Vec>(a, s); break;
-    case 2: launch_gated_enc<Fmt, T, Kind, 2, Vec>(a, s); break;
-    case 3: launch_gated_enc<Fmt, T, Kind, 3, Vec>(a, s); break;
-    default: launch_gated_enc<Fmt, T, Kind, 4, Vec>(a, s); break;
+    case 1: launch_gated_enc<Fmt, T, 1, Vec>(a, s); break;
+    case 2: launch_gated_enc<Fmt, T, 2, Vec>(a, s); break;
+    case 3: launch_gated_enc<Fmt, T, 3, Vec>(a, s); break;
+    default: launch_gated_enc<Fmt, T, 4, Vec>(a, s); break;
     }
-}
-
-template <int Fmt, class T, bool Vec>
-void launch_gated_t(const GatedQuantizeArgs &a, hipStream_t s) {
-    if (a.kind == 0) launch_gated_items<Fmt, T, 0, Vec>(a, s);
-    else launch_gated_items<Fmt, T, 1, Vec>(a, s);
 }
 
 template <int Fmt, bool Vec>
@@ -198,8 +194,8 @@ void launch_norm_f(const NormQuantizeArgs &a, hipStream_t s) {
 
 template <int Fmt, bool Vec>
 void launch_gated_f(const GatedQuantizeArgs &a, hipStream_t s) {
-    if (a.src_type == F16) launch_gated_t<Fmt, f16_t, Vec>(a, s);
-    else launch_gated_t<Fmt, bf16_t, Vec>(a, s);
+    if (a.src_type == F16) launch_gated_items<Fmt, f16_t, Vec>(a, s);
+    else launch_gated_items<Fmt, bf16_t, Vec>(a, s);
 }
 
 bool aligned_to(const void *p, uintptr_t bytes) {

@@ -74,6 +74,21 @@ __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4
     *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + index) = packed;
 }
 
+// Four consecutive outputs of one row: the finish (finish TUs only), then the
+// store in the output type, chosen at run time (a uniform branch at the end
+// of the kernel, so one kernel serves bf16 and f16 outputs).
+__device__ __forceinline__ void store_out(void *y, size_t index, float (&v)[4],
+                                          const uint16_t *bias, int n, int n_last, int act,
+                                          int out_f16) {
+    if (out_f16) {
+        if constexpr (kFin) finish4<f16_t>(v, bias, n, n_last, act);
+        store4<f16_t>(y, index, v);
+    } else {
+        if constexpr (kFin) finish4<bf16_t>(v, bias, n, n_last, act);
+        store4<bf16_t>(y, index, v);
+    }
+}
+
 // One workgroup = WK waves over K, sharing 16*NF weight rows; tokens
 // [m0, m0 + 16*MT). Split: store raw (per-channel) or outer-scaled (grouped)
 // partials to workspace[blockIdx.y] instead of the output.
@@ -87,21 +102,16 @@ __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4
 // granule) on distinct banks. Each wave reads back only what it loaded, so
 // no workgroup barrier is needed. NB == 0: weights load straight to registers.
 //
-// SL == 2 (with NB > 0): the workgroup's slab (16*NF rows x WK*NB*256 bytes)
-// is loaded cooperatively, wave w moving a contiguous run of whole rows, and
-// a workgroup barrier precedes the fragment reads (each wave then reads its
-// K range of every row).
-//
 // Packed: w is the packed fragment-tile layout (weight_pack.hip); each wave
 // loads all NB blocks of its K range straight into registers up front, one
 // contiguous 1 KB piece per (16-row fragment, 64-K step).
-template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, class Out, int NB = 0,
-          int SL = 1, bool Packed = false, int FQ = 0, int GS = 128>
+template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, int NB = 0,
+          bool Packed = false, int FQ = 0, int GS = 128>
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
     int K, int span, int input_group, int weight_group, const uint16_t *__restrict__ bias,
-    int act, FusedSource fq) {
+    int act, int out_f16, FusedSource fq) {
     using M_ = Mfma<Fmt>;
     using Acc = typename M_::Acc;
     using Scalar = typename M_::Scalar;
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // range, requested before the weight slab so that they land first. Lane
     // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
     // row m0 + 16t + row16: exactly the codes its MFMA B fragments need.
-    static_assert(!FQ || (NB > 0 && SL == 1 && !Packed && !Grouped && !Split && MT == 1 && NB == 1 && Fmt == I8),
+    static_assert(!FQ || (NB > 0 && !Packed && !Grouped && !Split && MT == 1 && NB == 1 && Fmt == I8),
                   "fused quantization: per-wave slab, activation blocks in registers");
     uint4 xraw[FQ ? NB : 1][MT][4][2];
     if constexpr (FQ) {
@@ -188,26 +198,25 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
     constexpr int SNB = Packed ? 0 : NB;                        // staged slab blocks
     constexpr int kSlabBytes = 16 * NF * SNB * kBlockK;         // per wave
-    constexpr int kRowBytes = SL == 2 ? WK * SNB * kBlockK : SNB * kBlockK;
+    constexpr int kRowBytes = SNB * kBlockK;
     constexpr int kRowGranules = kRowBytes / 16;
-    uint8_t *slab = SL == 2 ? wlds : wlds + wave * kSlabBytes;
-    const int slab_k0 = SL == 2 ? blockIdx.y * WK * span : k_begin;
+    uint8_t *slab = wlds + wave * kSlabBytes;
+    const int slab_k0 = k_begin;
     if constexpr (SNB > 0) {
         typedef __attribute__((address_space(3))) void *lds_ptr_t;
         const int rows_valid = max(0, min(16 * NF, N - n0));
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(w + size_t(n0) * K), 0, rows_valid * K, 0x00020000);
-        const int k_stop = SL == 2 ? min(K, slab_k0 + WK * span) : k_end;
+        const int k_stop = k_end;
 #pragma unroll
         for (int i = 0; i < kSlabBytes / 1024; ++i) {
-            // SL 2: this wave's contiguous share of the workgroup slab.
-            const int q = (SL == 2 ? wave * (kSlabBytes / 16) : 0) + i * 64 + lane;
+            const int q = i * 64 + lane;
             const int r = q / kRowGranules, slot = q % kRowGranules;
             const int g = slot ^ (r & 15);
             const int k = slab_k0 + g * 16;
             const uint32_t off = k < k_stop ? uint32_t(r) * uint32_t(K) + uint32_t(k) : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc, (lds_ptr_t)(slab + (SL == 2 ? wave * kSlabBytes : 0) + i * 1024), 16, off,
+                rsrc, (lds_ptr_t)(slab + i * 1024), 16, off,
                 0, 0, 0);
         }
     }
@@ -220,8 +229,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     using Red = std::conditional_t<Grouped, float, Scalar>;
     typedef Red Red4 __attribute__((ext_vector_type(4)));
     constexpr int kSlotVals = MT * NF * 64 * 4;
-    constexpr int kSlotStride = SNB > 0 ? (SL == 2 ? kSlotVals : kSlabBytes / int(sizeof(Red)))
-                                        : kSlotVals;
+    constexpr int kSlotStride = SNB > 0 ? kSlabBytes / int(sizeof(Red)) : kSlotVals;
     static_assert(SNB == 0 || kSlotVals * int(sizeof(Red)) <= kSlabBytes, "slot fits the slab");
     __shared__ Red4 red_static[SNB > 0 || WK == 1 ? 1 : WK * kSlotVals / 4];
     Red *red = SNB > 0 ? reinterpret_cast<Red *>(wlds) : reinterpret_cast<Red *>(red_static);
@@ -366,7 +374,6 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             // newer activation loads would not do: the compiler may order
             // them before the DMA, or skip a wave's out-of-range pieces.)
             __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));
-            if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
         }
     }
 
@@ -555,7 +562,6 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 // The slab is in LDS once no load is outstanding.
                 if (kb == k_begin) {
                     __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));
-                    if constexpr (SL == 2) __builtin_amdgcn_s_barrier();
                 }
             }
             block(kb, b, wpre[0]);
@@ -564,8 +570,6 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 
 
     if constexpr (WK > 1) {
-        // A shared slab is read by every wave: all reads finish first.
-        if constexpr (SNB > 0 && SL == 2) __syncthreads();
         Red *slot = red + wave * kSlotStride;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -643,21 +647,20 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     v[r] = s * pre_w[k][r];
                 }
             }
-            if constexpr (kFin) finish4<Out>(v, bias, n, N - 1, act);
-            store4<Out>(y, size_t(m) * N + n, v);
+            store_out(y, size_t(m) * N + n, v, bias, n, N - 1, act, out_f16);
         }
     }
 }
 
 // y = D((sum_s p_s) * sx * sw) or D(0 + sum_s p_s) for pre-scaled grouped
 // partials; splits summed in ascending order (reference quant_reduce.cuh:9-19).
-template <class Scalar, bool Scaled, class Out>
+template <class Scalar, bool Scaled>
 __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ partial,
                                                     const float *__restrict__ sx,
                                                     const float *__restrict__ sw,
                                                     void *__restrict__ y, int M, int N,
                                                     int splits, const uint16_t *__restrict__ bias,
-                                                    int act) {
+                                                    int act, int out_f16) {
     const size_t i4 = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
     const size_t total = size_t(M) * N;
     if (i4 >= total) return;
@@ -675,125 +678,113 @@ __global__ __launch_bounds__(256) void split_reduce(const Scalar *__restrict__ p
         }
     }
     // N % 4 == 0: the four values share a row.
-    if constexpr (kFin) finish4<Out>(v, bias, int(i4 % N), N - 1, act);
-    store4<Out>(y, i4, v);
+    store_out(y, i4, v, bias, int(i4 % N), N - 1, act, out_f16);
 }
 
-template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB, int GS = 128>
-int launch_slab(const GemmArgs &a, dim3 grid, int span, int layout, hipStream_t stream) {
-    const size_t lds = size_t(WK) * 16 * NF * NB * kBlockK;
-    if (layout == 2)
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 2, false, 0, GS>), grid,
-                           dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
-                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
-    else
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1, false, 0, GS>), grid,
-                           dim3(64 * WK), lds, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M,
-                           a.N, a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
+// Every launch uses eight wave64s per workgroup splitting K; K ranges are
+// ceil(ceil(K/256) / (splits*8)) blocks, so trailing ranges may be short or
+// empty (an empty range contributes zeros).
+constexpr int kWaves = 8;
+
+int span_of(int K, int splits) {
+    const int blocks_k = (K + kBlockK - 1) / kBlockK;
+    return (blocks_k + splits * kWaves - 1) / (splits * kWaves) * kBlockK;
+}
+
+#define QLIN_SKINNY_ARGS                                                                   \
+    a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span, a.input_group, a.weight_group, \
+        a.bias, a.act, int(a.out_type == F16), a.fq
+
+template <int Fmt, int MT, int NF, bool Grouped, int NB, int GS = 128>
+int launch_slab(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
+    const size_t lds = size_t(kWaves) * 16 * NF * NB * kBlockK;
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, false, 0, GS>), grid,
+                       dim3(64 * kWaves), lds, stream, QLIN_SKINNY_ARGS);
     return 0;
 }
 
-template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int NB>
+template <int Fmt, int MT, int NF, bool Grouped, int NB>
 int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
-    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, NB, 1, true>), grid,
-                       dim3(64 * WK), 0, stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N,
-                       a.K, span, a.input_group, a.weight_group, a.bias, a.act, a.fq);
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, true>), grid,
+                       dim3(64 * kWaves), 0, stream, QLIN_SKINNY_ARGS);
     return 0;
 }
 
 // GS: K-group size of the grouped partials (128, or 64 / 32 on the
 // row-major, unsplit paths only).
-template <int Fmt, int MT, int NF, int WK, bool Grouped, class Out, int GS = 128>
+template <int Fmt, int MT, int NF, bool Grouped, int GS = 128>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     // 32/64 groups: row-major weights and no split only (checked first, so
     // the packed and split-K launches below run with GS == 128).
     if (GS != 128 && (a.packed || p.splits != 1)) return -4;
+    if (p.waves != kWaves) return -4;
+    const int span = span_of(a.K, p.splits);
     if (a.packed) {
         // Packed weights: the waves split K (no grid split-K); each wave
         // streams its range in chunks of up to kMaxNB blocks held in
         // registers (weights and activations of a chunk: NB*(NF+MT) 64-byte
         // fragments per lane-quad, at most 10).
         if (p.splits != 1 || p.staged) return -4;
-        const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
-        const int span = blocks_k / WK * kBlockK;
         dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
         constexpr int kMaxNB = 10 / (NF + MT) > 4 ? 4 : (10 / (NF + MT) < 1 ? 1 : 10 / (NF + MT));
         const int nb = span / kBlockK < kMaxNB ? span / kBlockK : kMaxNB;
         switch (nb) {
-        case 1: return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 1>(a, grid, span, stream);
-        case 2: if constexpr (kMaxNB >= 2) return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 2>(a, grid, span, stream); break;
-        case 3: if constexpr (kMaxNB >= 3) return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 3>(a, grid, span, stream); break;
-        case 4: if constexpr (kMaxNB >= 4) return launch_packed<Fmt, MT, NF, WK, Grouped, Out, 4>(a, grid, span, stream); break;
+        case 1: return launch_packed<Fmt, MT, NF, Grouped, 1>(a, grid, span, stream);
+        case 2: if constexpr (kMaxNB >= 2) return launch_packed<Fmt, MT, NF, Grouped, 2>(a, grid, span, stream); break;
+        case 3: if constexpr (kMaxNB >= 3) return launch_packed<Fmt, MT, NF, Grouped, 3>(a, grid, span, stream); break;
+        case 4: if constexpr (kMaxNB >= 4) return launch_packed<Fmt, MT, NF, Grouped, 4>(a, grid, span, stream); break;
         default: break;
         }
         return -4;
     }
     if (skinny_lds_bytes(a, p) > kLdsBytes) return -4;  // would not launch
-    const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
-    const int ranges = p.splits * WK;
-    const int span = blocks_k / ranges * kBlockK;
     dim3 grid((a.N + 16 * NF - 1) / (16 * NF), p.splits, (a.M + 16 * MT - 1) / (16 * MT));
-    dim3 block(64 * WK);
+    dim3 block(64 * kWaves);
     if (p.splits == 1) {
-        // LDS-staged weight slabs (path.kind flag bit): one-shot streaming of
-        // whole weight rows; slab LDS per workgroup = WK * 16*NF * span bytes.
-        if constexpr (WK == 8 && NF <= 3) {
-            if (p.staged) {
-                switch (span / kBlockK) {
-                case 1: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 1, GS>(a, grid, span, p.staged, stream);
-                case 2: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 2, GS>(a, grid, span, p.staged, stream);
-                case 3: return launch_slab<Fmt, MT, NF, WK, Grouped, Out, 3, GS>(a, grid, span, p.staged, stream);
-                default: return -4;
-                }
+        // LDS-staged weight slabs: one-shot streaming of whole weight rows;
+        // slab LDS per workgroup = 8 * 16*NF * span bytes.
+        if (p.staged == 1) {
+            switch (span / kBlockK) {
+            case 1: return launch_slab<Fmt, MT, NF, Grouped, 1, GS>(a, grid, span, stream);
+            case 2: return launch_slab<Fmt, MT, NF, Grouped, 2, GS>(a, grid, span, stream);
+            case 3: return launch_slab<Fmt, MT, NF, Grouped, 3, GS>(a, grid, span, stream);
+            default: return -4;
             }
         }
         if (p.staged) return -4;
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, false, Out, 0, 1, false, 0, GS>), grid, block, 0,
-                           stream, a.x, a.sx, a.w, a.sw, a.y, nullptr, a.M, a.N, a.K, span,
-                           a.input_group, a.weight_group, a.bias, a.act, a.fq);
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, 0, false, 0, GS>), grid,
+                           block, 0, stream, QLIN_SKINNY_ARGS);
         return 0;
     }
     if (p.staged) return -4;
-    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, WK, Grouped, true, Out>), grid, block, 0, stream,
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, true>), grid, block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
-                       a.input_group, a.weight_group, a.bias, a.act, a.fq);
+                       a.input_group, a.weight_group, a.bias, a.act, int(a.out_type == F16), a.fq);
     const size_t quads = (size_t(a.M) * a.N) / 4;
     dim3 rgrid(unsigned((quads + 255) / 256));
     using Scalar = typename Mfma<Fmt>::Scalar;
     if constexpr (Grouped)
-        hipLaunchKernelGGL((split_reduce<float, false, Out>), rgrid, dim3(256), 0, stream,
+        hipLaunchKernelGGL((split_reduce<float, false>), rgrid, dim3(256), 0, stream,
                            static_cast<const float *>(a.workspace), a.sx, a.sw, a.y, a.M, a.N,
-                           p.splits, a.bias, a.act);
+                           p.splits, a.bias, a.act, int(a.out_type == F16));
     else
-        hipLaunchKernelGGL((split_reduce<Scalar, true, Out>), rgrid, dim3(256), 0, stream,
+        hipLaunchKernelGGL((split_reduce<Scalar, true>), rgrid, dim3(256), 0, stream,
                            static_cast<const Scalar *>(a.workspace), a.sx, a.sw, a.y, a.M, a.N,
-                           p.splits, a.bias, a.act);
+                           p.splits, a.bias, a.act, int(a.out_type == F16));
     return 0;
 }
 
-template <int Fmt, int MT, int NF, bool Grouped, class Out, int GS>
-int dispatch_wk(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    switch (p.waves) {
-    case 1: return launch_variant<Fmt, MT, NF, 1, Grouped, Out, GS>(a, p, s);
-    case 2: return launch_variant<Fmt, MT, NF, 2, Grouped, Out, GS>(a, p, s);
-    case 4: return launch_variant<Fmt, MT, NF, 4, Grouped, Out, GS>(a, p, s);
-    case 8: return launch_variant<Fmt, MT, NF, 8, Grouped, Out, GS>(a, p, s);
-    default: return -4;
-    }
-}
-
-template <int Fmt, int MT, bool Grouped, class Out, int GS>
+template <int Fmt, int MT, bool Grouped, int GS>
 int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    if (p.channels == 16) return dispatch_wk<Fmt, MT, 1, Grouped, Out, GS>(a, p, s);
-    if (p.channels == 32) return dispatch_wk<Fmt, MT, 2, Grouped, Out, GS>(a, p, s);
-    if (p.channels == 48) return dispatch_wk<Fmt, MT, 3, Grouped, Out, GS>(a, p, s);
-    if (p.channels == 64) return dispatch_wk<Fmt, MT, 4, Grouped, Out, GS>(a, p, s);
+    if (p.channels == 16) return launch_variant<Fmt, MT, 1, Grouped, GS>(a, p, s);
+    if (p.channels == 32) return launch_variant<Fmt, MT, 2, Grouped, GS>(a, p, s);
+    if (p.channels == 48) return launch_variant<Fmt, MT, 3, Grouped, GS>(a, p, s);
     return -4;
 }
 
 // Fused activation quantization (FQ): eight waves, per-wave slabs of NB
 // blocks, per-channel scales, no split.
-template <int Fmt, int MT, int NF, class Out, int NB>
+template <int Fmt, int MT, int NF, int NB>
 int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     // Every workgroup quantizes its token rows again (the activation is
     // re-encoded once per column tile), which pays only while that ALU work
@@ -806,106 +797,95 @@ int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     if constexpr (MT == 1 && NB == 1 && Fmt == I8) {
         const int span = NB * kBlockK;
         dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
-        const size_t lds = size_t(8) * 16 * NF * NB * kBlockK;
+        const size_t lds = size_t(kWaves) * 16 * NF * NB * kBlockK;
         if (a.fq.f16)
-            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, 8, false, false, Out, NB, 1, false, 2>),
-                               grid, dim3(512), lds, stream, nullptr, nullptr, a.w, a.sw, a.y,
-                               nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0, a.fq);
+            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 2>),
+                               grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
+                               a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
+                               int(a.out_type == F16), a.fq);
         else
-            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, 8, false, false, Out, NB, 1, false, 1>),
-                               grid, dim3(512), lds, stream, nullptr, nullptr, a.w, a.sw, a.y,
-                               nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0, a.fq);
+            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 1>),
+                               grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
+                               a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
+                               int(a.out_type == F16), a.fq);
         return 0;
     }
     return -4;
 }
-template <int Fmt, int MT, int NF, class Out>
-int launch_fused_nf(const GemmArgs &a, hipStream_t s) {
-    switch (a.K / (8 * kBlockK)) {
-    case 1: return launch_fused_nb<Fmt, MT, NF, Out, 1>(a, s);
-    default: return -4;
-    }
-}
-template <int Fmt, int MT, class Out>
-int launch_fused_mt(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    switch (p.channels) {
-    case 16: return launch_fused_nf<Fmt, MT, 1, Out>(a, s);
-    case 32: return launch_fused_nf<Fmt, MT, 2, Out>(a, s);
-    case 48: return launch_fused_nf<Fmt, MT, 3, Out>(a, s);
-    default: return -4;
-    }
-}
-template <int Fmt, class Out>
+template <int Fmt>
 int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    switch (p.tokens) {
-    case 16: return launch_fused_mt<Fmt, 1, Out>(a, p, s);
+    if (p.tokens != 16 || a.K != kWaves * kBlockK) return -4;
+    switch (p.channels) {
+    case 16: return launch_fused_nb<Fmt, 1, 1, 1>(a, s);
+    case 32: return launch_fused_nb<Fmt, 1, 2, 1>(a, s);
+    case 48: return launch_fused_nb<Fmt, 1, 3, 1>(a, s);
     default: return -4;
     }
 }
 
-template <int Fmt, bool Grouped, class Out, int GS = 128>
+template <int Fmt, bool Grouped, int GS = 128>
 int dispatch_mt(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.tokens) {
-    case 16: return dispatch_nf<Fmt, 1, Grouped, Out, GS>(a, p, s);
-    case 32: return dispatch_nf<Fmt, 2, Grouped, Out, GS>(a, p, s);
-    case 48: return dispatch_nf<Fmt, 3, Grouped, Out, GS>(a, p, s);
-    case 64: return dispatch_nf<Fmt, 4, Grouped, Out, GS>(a, p, s);
+    case 16: return dispatch_nf<Fmt, 1, Grouped, GS>(a, p, s);
+    case 32: return dispatch_nf<Fmt, 2, Grouped, GS>(a, p, s);
+    case 64: return dispatch_nf<Fmt, 4, Grouped, GS>(a, p, s);
     default: return -4;
     }
 }
 
-template <int Fmt, class Out>
+template <int Fmt>
 int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if (a.input_group || a.weight_group) {
         // Partials per the smaller group size (quant_grouped.cu:185-187).
         const int g = a.input_group && (!a.weight_group || a.input_group <= a.weight_group)
                           ? a.input_group : a.weight_group;
-        if (g == 64) return dispatch_mt<Fmt, true, Out, 64>(a, p, s);
-        if (g == 32) return dispatch_mt<Fmt, true, Out, 32>(a, p, s);
+        if (g == 64) return dispatch_mt<Fmt, true, 64>(a, p, s);
+        if (g == 32) return dispatch_mt<Fmt, true, 32>(a, p, s);
         if (g != 128) return -4;
-        return dispatch_mt<Fmt, true, Out>(a, p, s);
+        return dispatch_mt<Fmt, true>(a, p, s);
     }
-    return dispatch_mt<Fmt, false, Out>(a, p, s);
+    return dispatch_mt<Fmt, false>(a, p, s);
 }
 
 }  // namespace
 
 #ifndef QLIN_SKINNY_PART
 size_t skinny_lds_bytes(const GemmArgs &a, const GemmPath &p) {
-    const int mt = p.tokens / 16, nf = p.channels / 16, wk = p.waves;
-    const int blocks_k = (a.K + kBlockK - 1) / kBlockK;
-    const int nb = blocks_k / (p.splits * wk);
-    const size_t slab = p.staged ? size_t(wk) * 16 * nf * nb * kBlockK : 0;
+    const int mt = p.tokens / 16, nf = p.channels / 16;
+    const int nb = span_of(a.K, p.splits < 1 ? 1 : p.splits) / kBlockK;
+    const size_t slab = p.staged ? size_t(kWaves) * 16 * nf * nb * kBlockK : 0;
     // Reduction slots reuse a staged slab; otherwise one static slot per wave.
-    const size_t red = p.staged || wk == 1 ? 16 : size_t(wk) * mt * nf * 64 * 4 * 4;
+    const size_t red = p.staged ? 16 : size_t(kWaves) * mt * nf * 64 * 4 * 4;
     return red + slab;
 }
+
+int skinny_span(int K, int splits) { return span_of(K, splits); }
 
 size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
     return p.splits > 1 ? size_t(p.splits) * a.M * a.N * 4 : 0;
 }
 
 bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
-    const int nb = a.K / (8 * kBlockK), mt = p.tokens / 16;
     return a.fq.src && !a.packed && !a.bias && !a.act && !a.input_group && !a.weight_group &&
-           p.kind == KIND_SKINNY && p.splits == 1 && p.waves == 8 && p.staged == 1 &&
-           a.fmt == I8 && a.K == 8 * kBlockK && nb == 1 && mt == 1 && (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
-           p.tokens % 16 == 0 && skinny_lds_bytes(a, p) <= kLdsBytes;
+           p.kind == KIND_SKINNY && p.splits == 1 && p.waves == kWaves && p.staged == 1 &&
+           a.fmt == I8 && a.K == kWaves * kBlockK && p.tokens == 16 &&
+           (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
+           skinny_lds_bytes(a, p) <= kLdsBytes;
 }
 
 #endif
 
-// The kernel variants are compiled in four translation units (format x
-// output type, see the Makefile) that each define one entry below.
+// The kernel variants are compiled in four translation units (format, with
+// and without the finish; see the Makefile) that each define one entry below.
 #ifdef QLIN_SKINNY_PART
 int QLIN_SKINNY_PART(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
-    return dispatch_grouped<QLIN_SKINNY_FMT, QLIN_SKINNY_OUT>(a, p, stream);
+    return dispatch_grouped<QLIN_SKINNY_FMT>(a, p, stream);
 }
 #if !QLIN_FIN
 #define QLIN_CAT_(a, b) a##b
 #define QLIN_CAT(a, b) QLIN_CAT_(a, b)
 int QLIN_CAT(QLIN_SKINNY_PART, _fused)(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
-    return launch_fused<QLIN_SKINNY_FMT, QLIN_SKINNY_OUT>(a, p, stream);
+    return launch_fused<QLIN_SKINNY_FMT>(a, p, stream);
 }
 #endif
 #else
@@ -913,31 +893,19 @@ int QLIN_CAT(QLIN_SKINNY_PART, _fused)(const GemmArgs &a, const GemmPath &p, hip
     int name(const GemmArgs &, const GemmPath &, hipStream_t);              \
     int name##_fin(const GemmArgs &, const GemmPath &, hipStream_t);        \
     int name##_fused(const GemmArgs &, const GemmPath &, hipStream_t);
-QLIN_PART_DECL(launch_skinny_i8_bf16)
-QLIN_PART_DECL(launch_skinny_i8_f16)
-QLIN_PART_DECL(launch_skinny_fp8_bf16)
-QLIN_PART_DECL(launch_skinny_fp8_f16)
+QLIN_PART_DECL(launch_skinny_i8)
+QLIN_PART_DECL(launch_skinny_fp8)
 #undef QLIN_PART_DECL
 
 int launch_skinny(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     const bool fin = a.bias || a.act;
-    if (a.out_type == F16) {
-        if (a.fmt == I8)
-            return fin ? launch_skinny_i8_f16_fin(a, p, stream) : launch_skinny_i8_f16(a, p, stream);
-        return fin ? launch_skinny_fp8_f16_fin(a, p, stream) : launch_skinny_fp8_f16(a, p, stream);
-    }
-    if (a.fmt == I8)
-        return fin ? launch_skinny_i8_bf16_fin(a, p, stream) : launch_skinny_i8_bf16(a, p, stream);
-    return fin ? launch_skinny_fp8_bf16_fin(a, p, stream) : launch_skinny_fp8_bf16(a, p, stream);
+    if (a.fmt == I8) return fin ? launch_skinny_i8_fin(a, p, stream) : launch_skinny_i8(a, p, stream);
+    return fin ? launch_skinny_fp8_fin(a, p, stream) : launch_skinny_fp8(a, p, stream);
 }
 
 int launch_skinny_fused(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (!skinny_fused_supported(a, p)) return -4;
-    if (a.out_type == F16)
-        return a.fmt == I8 ? launch_skinny_i8_f16_fused(a, p, stream)
-                           : launch_skinny_fp8_f16_fused(a, p, stream);
-    return a.fmt == I8 ? launch_skinny_i8_bf16_fused(a, p, stream)
-                       : launch_skinny_fp8_bf16_fused(a, p, stream);
+    return a.fmt == I8 ? launch_skinny_i8_fused(a, p, stream) : launch_skinny_fp8_fused(a, p, stream);
 }
 #endif
 

@@ -756,246 +756,6 @@ int launch_wide(const GemmArgs &a, hipStream_t stream) {
     return 0;
 }
 
-// Persistent INT8 per-channel variant of the 16x16-MFMA tiled kernel: a grid
-// of at most kPersistCUs workgroups walks the tiles t = blockIdx.x + i*G
-// (every tile of a workgroup on its XCD). After a tile's last MFMA stage the
-// ring is free: the next tile's first STAGES-1 stages are issued at once,
-// then the finished tile's epilogue writes straight from registers (8-byte
-// buffer stores, no LDS), so the next tile's loads and the previous tile's
-// stores overlap. Tile scales are double-buffered in LDS. Every store is a
-// buffer store (an out-of-range offset writes nothing but still counts), so
-// the wait counts below are exact: stores issued after the prologue loads
-// are allowed outstanding while the next tile waits for its first stages.
-constexpr int kPersistCUs = 256;  // MI355X compute units
-
-template <int WN, int WM, int WTN, int WTM, int STAGES, bool KFull, class Out, bool PackedW>
-__global__ __launch_bounds__(64 * WN * WM) void persist_gemm(
-    const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
-    const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
-    int tiles_n, const uint16_t *__restrict__ bias, int act) {
-    constexpr int NW = WN * WM, BK = 64, CPR = 4, RPI = 16;
-    constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
-    constexpr int ROWS = BN + BM, INSTS = ROWS / (RPI * NW), W_INSTS = BN / (RPI * NW);
-    constexpr int STAGE_BYTES = ROWS * BK;
-    constexpr int kStores = WTN * WTM;  // 8-byte stores per lane per tile
-    static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
-    static_assert(INSTS * (STAGES - 2) + kStores < 64, "vmcnt range");
-    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    float *scl_base = reinterpret_cast<float *>(lds + STAGES * STAGE_BYTES);  // [2][BN + BM]
-
-    const int tiles = tiles_m * tiles_n;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wave_n = wave % WN, wave_m = wave / WN;
-    const int row16 = lane & 15, quad = lane >> 4;
-    const int tiles_k = (K + 63) / 64;
-    const int stages = (K + BK - 1) / BK;
-
-    auto coords = [&](int t, int &n_base, int &m_base) {
-        int b = t;
-        if (tiles % 8 == 0) b = (b % 8) * (tiles / 8) + b / 8;
-        constexpr int kGroupN = 4;
-        const int group = b / (kGroupN * tiles_m), in_group = b % (kGroupN * tiles_m);
-        const int group_w = min(kGroupN, tiles_n - group * kGroupN);
-        n_base = (group * kGroupN + in_group % group_w) * BN;
-        m_base = (in_group / group_w) * BM;
-    };
-    auto rsrc_w_of = [&](int n_base) {
-        return PackedW ? __builtin_amdgcn_make_buffer_rsrc(
-                             const_cast<uint8_t *>(w + size_t(n_base / 16) * tiles_k * 1024), 0,
-                             min(BN, N - n_base) / 16 * tiles_k * 1024, 0x00020000)
-                       : __builtin_amdgcn_make_buffer_rsrc(
-                             const_cast<uint8_t *>(w + size_t(n_base) * K), 0,
-                             min(BN, N - n_base) * K, 0x00020000);
-    };
-    auto rsrc_x_of = [&](int m_base) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(x + size_t(m_base) * K), 0,
-                                                 min(BM, M - m_base) * K, 0x00020000);
-    };
-    const __amdgpu_buffer_rsrc_t rsrc_y = __builtin_amdgcn_make_buffer_rsrc(
-        y, 0, uint32_t(min(size_t(M) * N * 2, size_t(0x7fffffff))), 0x00020000);
-
-    const int lane_row = lane / CPR;
-    const int lane_chunk = (lane % CPR) ^ swizzle<BK>(wave * RPI + lane_row);
-    const uint32_t lane_voff = uint32_t(lane_row) * uint32_t(K) + uint32_t(lane_chunk * 16);
-    const uint32_t lane_voff_p =
-        uint32_t((lane_chunk / 4) * 1024 + (lane_chunk % 4) * 256 + lane_row * 16);
-    auto issue = [&](const __amdgpu_buffer_rsrc_t &rw, const __amdgpu_buffer_rsrc_t &rx,
-                     int stage, int k0) {
-        uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
-        const bool kin = KFull || k0 + lane_chunk * 16 < K;
-        const uint32_t voff = kin ? lane_voff + uint32_t(k0) : 0x80000000u;
-        const uint32_t voff_p = kin ? lane_voff_p : 0x80000000u;
-#pragma unroll
-        for (int i = 0; i < INSTS; ++i) {
-            const int row = (i * NW + wave) * RPI;
-            lds_ptr_t dst = (lds_ptr_t)(base + (i * NW + wave) * 1024);
-            if (PackedW && i < W_INSTS) {
-                const uint32_t soff = uint32_t((row / 16) * tiles_k * 1024 + (k0 / 64) * 1024);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, voff_p, soff, 0, 0);
-            } else {
-                const uint32_t soff = uint32_t(i < W_INSTS ? row : row - BN) * uint32_t(K);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(i < W_INSTS ? rw : rx, dst, 16, voff,
-                                                         soff, 0, 0);
-            }
-        }
-    };
-    constexpr int kScaleLoads = (BN + BM + 64 * NW - 1) / (64 * NW);
-    auto load_scales = [&](int n_base, int m_base, float (&v)[kScaleLoads]) {
-#pragma unroll
-        for (int l = 0; l < kScaleLoads; ++l) {
-            const int i = tid + l * 64 * NW;
-            v[l] = i < BN ? sw[min(n_base + i, N - 1)]
-                          : (i < BN + BM ? sx[min(m_base + i - BN, M - 1)] : 1.f);
-        }
-    };
-    auto store_scales = [&](float *scl, const float (&v)[kScaleLoads]) {
-#pragma unroll
-        for (int l = 0; l < kScaleLoads; ++l)
-            if (tid + l * 64 * NW < BN + BM) scl[tid + l * 64 * NW] = v[l];
-    };
-
-    int t = blockIdx.x;
-    if (t >= tiles) return;
-    int n_base, m_base;
-    coords(t, n_base, m_base);
-    __amdgpu_buffer_rsrc_t rsrc_w = rsrc_w_of(n_base), rsrc_x = rsrc_x_of(m_base);
-    {
-        float v[kScaleLoads];
-        load_scales(n_base, m_base, v);
-#pragma unroll
-        for (int s = 0; s < STAGES - 1; ++s)
-            if (s < stages) issue(rsrc_w, rsrc_x, s, s * BK);
-        store_scales(scl_base, v);
-    }
-    int buf = 0;
-    bool after_stores = false;  // the previous tile's stores follow this tile's prologue
-
-    const int a_row0 = wave_n * 16 * WTN + row16;
-    const int b_row0 = BN + wave_m * 16 * WTM + row16;
-    const int a_off = a_row0 * BK, b_off = b_row0 * BK;
-    const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
-    auto read = [&](int st, i32x4 (&a)[WTN], i32x4 (&bb)[WTM]) {
-        const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
-#pragma unroll
-        for (int j = 0; j < WTM; ++j)
-            bb[j] = *reinterpret_cast<const i32x4 *>(cur + b_off + j * 16 * BK + b_c0);
-#pragma unroll
-        for (int i = 0; i < WTN; ++i)
-            a[i] = *reinterpret_cast<const i32x4 *>(cur + a_off + i * 16 * BK + a_c0);
-    };
-    for (;;) {
-        i32x4 acc[WTN][WTM];
-#pragma unroll
-        for (int i = 0; i < WTN; ++i)
-#pragma unroll
-            for (int j = 0; j < WTM; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
-        auto mma = [&](const i32x4 (&a)[WTN], const i32x4 (&bb)[WTM], int i0, int i1) {
-#pragma unroll
-            for (int i = i0; i < i1; ++i)
-#pragma unroll
-                for (int j = 0; j < WTM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bb[j], acc[i][j], 0, 0, 0);
-        };
-        constexpr int kEarly = WTN / 4;
-        auto step = [&](int s, const i32x4 (&a)[WTN], const i32x4 (&bb)[WTM], i32x4 (&na)[WTN],
-                        i32x4 (&nb)[WTM]) {
-            if (s + STAGES - 1 < stages) issue(rsrc_w, rsrc_x, s + STAGES - 1, (s + STAGES - 1) * BK);
-            mma(a, bb, 0, kEarly);
-            if (s + STAGES - 1 < stages) {
-                // stage s+1 <= STAGES-2 was issued before the previous stores
-                if (after_stores && s + 1 <= STAGES - 2) wait_vmcnt<INSTS * (STAGES - 2) + kStores>();
-                else wait_vmcnt<INSTS * (STAGES - 2)>();
-            } else if (s + 1 < stages) {
-                wait_vmcnt<0>();
-            }
-            lds_barrier();
-            if (s + 1 < stages) read(s + 1, na, nb);
-            mma(a, bb, kEarly, WTN);
-        };
-        i32x4 a0[WTN], b0[WTM], a1[WTN], b1[WTM];
-        if (stages >= STAGES - 1) {
-            if (after_stores) wait_vmcnt<INSTS * (STAGES - 2) + kStores>();
-            else wait_vmcnt<INSTS * (STAGES - 2)>();
-        } else {
-            wait_vmcnt<0>();
-        }
-        lds_barrier();
-        read(0, a0, b0);
-        int s = 0;
-        for (; s + 1 < stages; s += 2) {
-            step(s, a0, b0, a1, b1);
-            step(s + 1, a1, b1, a0, b0);
-        }
-        if (s < stages) step(s, a0, b0, a1, b1);
-
-        // Next tile: its first stages go into the now free ring right away.
-        const int t_next = t + gridDim.x;
-        const bool has_next = t_next < tiles;
-        int nn = 0, nm = 0;
-        float nv[kScaleLoads];
-        if (has_next) {
-            coords(t_next, nn, nm);
-            rsrc_w = rsrc_w_of(nn);
-            rsrc_x = rsrc_x_of(nm);
-            load_scales(nn, nm, nv);
-#pragma unroll
-            for (int s2 = 0; s2 < STAGES - 1; ++s2)
-                if (s2 < stages) issue(rsrc_w, rsrc_x, s2, s2 * BK);
-        }
-        // Epilogue of tile t from registers: lane (row16, quad) of fragment
-        // (i, j) holds four consecutive channels of one token.
-        const float *scl = scl_base + buf * (BN + BM);
-#pragma unroll
-        for (int j = 0; j < WTM; ++j) {
-            const int m_l = wave_m * 16 * WTM + j * 16 + row16;
-            const float sxm = scl[BN + m_l];
-            const int m = m_base + m_l;
-#pragma unroll
-            for (int i = 0; i < WTN; ++i) {
-                const int n_l = wave_n * 16 * WTN + i * 16 + quad * 4;
-                const f32x4 swv = *reinterpret_cast<const f32x4 *>(scl + n_l);
-                float v[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float tt = float(acc[i][j][r]) * sxm;
-                    v[r] = tt * swv[r];
-                }
-                if constexpr (kFin) finish4<Out>(v, bias, n_base + n_l, N - 1, act);
-                const int n = n_base + n_l;
-                const uint32_t off = (m < M && n < N) ? uint32_t((size_t(m) * N + n) * 2) : 0x80000000u;
-                const uint32_t lo = pack2(v[0], v[1], Out{}), hi = pack2(v[2], v[3], Out{});
-                typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-                __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_y, off, 0, 0);
-            }
-        }
-        if (!has_next) break;
-        store_scales(scl_base + (buf ^ 1) * (BN + BM), nv);
-        buf ^= 1;
-        t = t_next;
-        n_base = nn;
-        m_base = nm;
-        after_stores = true;
-    }
-}
-
-template <int WN, int WM, int WTN, int WTM, int STAGES, class Out>
-int launch_persist(const GemmArgs &a, hipStream_t stream) {
-    constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
-    const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
-    const int tiles = tiles_n * tiles_m;
-    const size_t lds = size_t(STAGES) * (BN + BM) * 64 + size_t(2) * (BN + BM) * 4;
-    dim3 grid(unsigned(tiles < kPersistCUs ? tiles : kPersistCUs)), block(64 * WN * WM);
-#define QLIN_PERSIST(KF, PW)                                                                   \
-    hipLaunchKernelGGL((persist_gemm<WN, WM, WTN, WTM, STAGES, KF, Out, PW>), grid, block, lds, \
-                       stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K, tiles_m, tiles_n,     \
-                       a.bias, a.act)
-    if (a.K % 64 == 0) { if (a.packed) QLIN_PERSIST(true, true); else QLIN_PERSIST(true, false); }
-    else { if (a.packed) QLIN_PERSIST(false, true); else QLIN_PERSIST(false, false); }
-#undef QLIN_PERSIST
-    return 0;
-}
-
 template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, class Out>
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
@@ -1030,8 +790,6 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 4, 4, 128, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
-        if (p.channels == 256 && p.tokens == 256 && p.waves == 8 && p.staged == 1)
-            return launch_persist<2, 4, 8, 4, 4, Out>(a, s);
         // 256x128 with eight waves of 128x32.
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 2, 64, 4, false, Out>(a, s);

@@ -132,11 +132,16 @@ size_t skinny_workspace_bytes(const GemmArgs &, const GemmPath &);
 // LDS of a skinny launch (weight slab + cross-wave reduction buffer); a path
 // above kLdsBytes must not be launched.
 size_t skinny_lds_bytes(const GemmArgs &, const GemmPath &);
+// K bytes per wave range of a skinny launch: ceil(ceil(K/256) / (splits*8))
+// blocks of 256 (eight waves per workgroup; trailing ranges may be empty).
+int skinny_span(int K, int splits);
 constexpr size_t kLdsBytes = 160 * 1024;  // per workgroup on gfx950
 int launch_tiled(const GemmArgs &, const GemmPath &, hipStream_t);
 // Packed weight layout (weight_pack.hip): N % 16 == 0, bytes = N * ceil(K/64)*64.
 size_t packed_weight_bytes(int N, int K);
 void launch_pack_weights(const void *w, int N, int K, void *packed, hipStream_t);
 size_t tiled_workspace_bytes(const GemmArgs &, const GemmPath &);
+// Records `message` as qlin_last_error() of this thread; returns status.
+int set_error(int status, const char *message);
 
 }  // namespace qlin

@@ -27,6 +27,44 @@ int code(Type type) { return static_cast<int>(type); }
 
 }  // namespace
 
+// ---------------------------------------------------------------- Buffer
+Buffer::Buffer(size_t bytes) : size_(bytes) {
+    if (hipGetDevice(&device_) != hipSuccess) throw std::runtime_error("no HIP device");
+    if (bytes && hipMalloc(&data_, bytes) != hipSuccess)
+        throw std::runtime_error("device buffer allocation failed");
+}
+
+Buffer::~Buffer() {
+    if (data_) (void)hipFree(data_);
+}
+
+Buffer::Buffer(Buffer &&other) noexcept
+    : data_(other.data_), size_(other.size_), device_(other.device_) {
+    other.data_ = nullptr;
+    other.size_ = 0;
+}
+
+Buffer &Buffer::operator=(Buffer &&other) noexcept {
+    if (this != &other) {
+        if (data_) (void)hipFree(data_);
+        data_ = other.data_;
+        size_ = other.size_;
+        device_ = other.device_;
+        other.data_ = nullptr;
+        other.size_ = 0;
+    }
+    return *this;
+}
+
+// core/tensor_storage.h:35: a borrowed view at a byte offset, bounds-checked.
+TensorView Buffer::view(int rows, int columns, Type dtype, size_t offset, int stride) const {
+    const int ld = stride ? stride : columns;
+    const size_t span = rows && columns ? (size_t(rows - 1) * ld + columns) * bytes(dtype) : 0;
+    if (rows < 0 || columns < 0 || offset > size_ || span > size_ - offset)
+        throw std::invalid_argument("buffer view out of range");
+    return TensorView(static_cast<char *>(data_) + offset, rows, columns, dtype, stride, device_);
+}
+
 // ---------------------------------------------------------------- metadata
 // include/tts/quantization.h:8-29
 const char *quantization_name(Quantization quantization) {
@@ -175,6 +213,9 @@ void grouped_quant_gemm(KernelProblem problem, const void *input, const float *i
 }
 
 // ---------------------------------------------------------------- QuantizedGemm
+QuantizedGemm::QuantizedGemm(qlin_stream_t stream, void *, Buffer &workspace, Type format)
+    : QuantizedGemm(stream, workspace.data(), workspace.size(), format) {}
+
 QuantizedGemm::QuantizedGemm(qlin_stream_t stream, void *workspace, size_t workspace_bytes,
                              Type format)
     : stream_(stream), workspace_(workspace), workspace_bytes_(workspace_bytes), format_(format) {
@@ -188,7 +229,7 @@ QuantCacheStats QuantizedGemm::cache_stats() const {
     QuantCacheStats result{};
     result.selection = stats_;
     result.selection.entries = plans_.size();
-    result.prepared_plans = plans_.size();
+    result.prepared_plans = plans_.size() + finishes_.size();
     return result;
 }
 
@@ -278,18 +319,50 @@ bool finish_only(const ops::Epilogue &e) {
            !e.residual_rows && e.value_scale == 1 && e.output_scale == 1 &&
            !e.valid_rows_per_sequence && e.input_repeat == 1;
 }
+
+// The finish the GEMM epilogue runs: ReLU or tanh-GeLU (the reference's
+// simple_finish, ops/cuda/quantization.cpp:75-82), or a bias alone; -1 for
+// any other epilogue.
+int finish_activation(const ops::Epilogue &e) {
+    if (!finish_only(e)) return -1;
+    if (e.activation == ops::Activation::Relu) return QLIN_FINISH_RELU;
+    if (e.activation == ops::Activation::GeluTanh) return QLIN_FINISH_GELU_TANH;
+    if (e.activation == ops::Activation::Identity && e.bias.data) return QLIN_FINISH_NONE;
+    return -1;
+}
+
+// check_finish_bias (ops/cuda/quantization.cpp:83-87)
+void check_finish_bias(const ops::Epilogue &e, int channels, Type output_type) {
+    if (e.bias.data && (e.bias.type != output_type || !e.bias.dense() ||
+                        e.bias.numel() != size_t(channels)))
+        throw std::invalid_argument("quantized linear finish bias mismatch");
+}
 }  // namespace
+
+void QuantizedGemm::prepare_finish(int rows, int channels, int reduction, Type output_type,
+                                   const ops::Epilogue &finish, QuantizationGroups groups) {
+    if (finish_activation(finish) < 0) return;
+    check_finish_bias(finish, channels, output_type);
+    const Key key{row_capacity(rows), channels, reduction, output_type, groups.activation,
+                  groups.weight};
+    if (!plans_.count(key))
+        throw std::logic_error("quantized finish requires a prepared projection");
+    const FinishKey fk{key, finish.activation, finish.bias.data != nullptr};
+    if (finishes_.count(fk)) return;
+    if (sealed_) throw std::logic_error("prepared resource missing after initialization");
+    finishes_.insert(fk);
+}
 
 bool QuantizedGemm::linear_finish(RowScaledView input, RowScaledView weight, TensorView output,
                                   const ops::Epilogue &finish) {
     // The reference fuses ReLU / tanh-GeLU; a bias-only finish (identity
-    // activation) is fused here as well.
-    if (!finish_only(finish)) return false;
-    int act;
-    if (finish.activation == ops::Activation::Relu) act = QLIN_FINISH_RELU;
-    else if (finish.activation == ops::Activation::GeluTanh) act = QLIN_FINISH_GELU_TANH;
-    else if (finish.activation == ops::Activation::Identity && finish.bias.data) act = QLIN_FINISH_NONE;
-    else return false;
+    // activation) is fused here as well. Only prepared finishes run.
+    const int act = finish_activation(finish);
+    if (act < 0) return false;
+    const Key key{row_capacity(output.rows), output.cols, input.values.cols, output.type,
+                  input.group_size, weight.group_size};
+    if (!finishes_.count(FinishKey{key, finish.activation, finish.bias.data != nullptr}))
+        return false;
     input.validate();
     weight.validate();
     if (input.values.type != format_ || weight.values.type != format_ ||
@@ -297,10 +370,7 @@ bool QuantizedGemm::linear_finish(RowScaledView input, RowScaledView weight, Ten
         input.values.rows != output.rows || weight.values.rows != output.cols ||
         (output.type != Type::BF16 && output.type != Type::F16) || !output.dense())
         throw std::invalid_argument("quantized linear dimensions/type mismatch");
-    // check_finish_bias (ops/cuda/quantization.cpp:83-87)
-    if (finish.bias.data && (finish.bias.type != output.type || !finish.bias.dense() ||
-                             finish.bias.numel() != size_t(output.cols)))
-        throw std::invalid_argument("quantized linear finish bias mismatch");
+    check_finish_bias(finish, output.cols, output.type);
     const QuantizationGroups groups{input.group_size, weight.group_size, input.rotation_size};
     LinearPath path = planned(output.rows, output.cols, input.values.cols, output.type, groups);
     qlin_path c{static_cast<int>(path.kind), path.tokens, path.channels, path.splits, path.waves,
@@ -318,7 +388,9 @@ bool QuantizedGemm::normalized_linear(TensorView input, TensorView normalized,
                                       TensorView norm_weight, TensorView norm_bias, float epsilon,
                                       const ops::NormFusion &fusion, RowScaledView weight,
                                       TensorView output, const ops::Epilogue &epilogue,
-                                      RowScaledView encoded) {
+                                      RowScaledView encoded, const QkvProjectionOutput *writeback) {
+    // The QKV cache writeback belongs to the attention path (not built here).
+    if (writeback) return false;
     // The conditions of normalized_quantized_linear (sequence_norm.cu:522-545).
     if (weight.group_size || weight.rotation_size || encoded.group_size || encoded.rotation_size ||
         fusion.source_rows || weight.values.type != format_)
@@ -446,56 +518,113 @@ void matmul(RowScaledView input, RowScaledView weight, TensorView output) {
     context(output.device).linear(input, weight, output);
 }
 
-// ops/basic.cpp:48-53 (the finish-epilogue plan of the reference is not part
-// of this library).
+// ops/basic.cpp:48-53
 void prepare_quantized(TensorView weight, int rows, int output_channels, int input_channels,
-                       Type type, QuantizationGroups groups) {
-    context(weight.device).prepare(rows, output_channels, input_channels, type, groups);
+                       Type type, const Epilogue &epilogue, QuantizationGroups groups) {
+    QuantizedGemm &gemm = context(weight.device);
+    gemm.prepare(rows, output_channels, input_channels, type, groups);
+    gemm.prepare_finish(rows, output_channels, input_channels, type, epilogue, groups);
 }
 
-// ops/linear.cpp:71-90 (quantized weight, dense activation, no epilogue).
-// quantize_rows' checks, then both steps in QuantizedGemm::quantize_linear.
-void linear(TensorView input, RowScaledView weight, TensorView output, RowScaledView scratch) {
-    weight.validate();
-    scratch.validate();
-    if ((input.type != Type::BF16 && input.type != Type::F16) || input.rows < 1 ||
-        input.cols < 1 || !input.data || !scratch.values.data || !scratch.scales.data ||
-        input.rows != scratch.values.rows || input.cols != scratch.values.cols)
-        throw std::invalid_argument("quantization source/destination shape/type mismatch");
-    if (scratch.values.cols != weight.values.cols || output.rows != scratch.values.rows ||
-        output.cols != weight.values.rows || !output.dense())
-        throw std::invalid_argument("quantized linear dimensions/layout mismatch");
-    context(output.device).quantize_linear(input, scratch, weight, output);
+namespace {
+// check_linear_output (ops/linear.cpp:17-23)
+void check_linear_output(TensorView output, TensorView bias, const Epilogue &e) {
+    if (e.bias.data) throw std::invalid_argument("linear already owns its bias");
+    for (const TensorView &source : {bias, e.residual, e.gate, e.condition})
+        if (source.overlaps(output))
+            throw std::invalid_argument("linear epilogue source aliases its projection output");
 }
-// ops/linear.cpp:26-93, quantized weight and dense activation: quantize
-// into the scratch, then the GEMM with the fused finish; with a quantized
-// output, the fused finish + quantize_rows when the formats agree and the
-// epilogue is a finish, else the GEMM + pointwise_quantize.
-void linear(TensorView input, RowScaledView weight, TensorView bias, TensorView output,
-            Epilogue epilogue, RowScaledView scratch, RowScaledView quantized_output) {
-    weight.validate();
+
+bool plain_epilogue(const Epilogue &e) {
+    return e.activation == Activation::Identity && !e.bias.data && finish_only(e);
+}
+}  // namespace
+
+// ops/linear.cpp:24-93 with a quantized weight: quantize a dense input into
+// the scratch (one launch with the GEMM where the decode kernel quantizes its
+// own token rows), then the GEMM with the prepared fused finish; with a
+// quantized output, the fused finish + quantize_rows when the formats agree,
+// else the GEMM + pointwise_quantize.
+void linear(const LinearOperand &input, const LinearOperand &weight, TensorView bias,
+            TensorView output, Epilogue epilogue, RowScaledView scratch,
+            RowScaledView quantized_output) {
+    check_linear_output(output, bias, epilogue);
     epilogue.bias = bias;
-    quantize_rows(input, scratch);
-    if (scratch.values.cols != weight.values.cols || output.rows != scratch.values.rows ||
-        output.cols != weight.values.rows || !output.dense())
-        throw std::invalid_argument("quantized linear dimensions/layout mismatch");
+    const RowScaledView *matrix = std::get_if<RowScaledView>(&weight);
+    if (!matrix)
+        throw std::invalid_argument(
+            "dense (unquantized) linear is not part of the quantized linear library");
+    matrix->validate();
     QuantizedGemm &gemm = context(output.device);
+    RowScaledView activation;
+    if (const TensorView *dense = std::get_if<TensorView>(&input)) {
+        if (!quantized_output.values.data && plain_epilogue(epilogue)) {
+            scratch.validate();
+            if ((dense->type != Type::BF16 && dense->type != Type::F16) || dense->rows < 1 ||
+                dense->cols < 1 || !dense->data || !scratch.values.data ||
+                !scratch.scales.data || dense->rows != scratch.values.rows ||
+                dense->cols != scratch.values.cols)
+                throw std::invalid_argument("quantization source/destination shape/type mismatch");
+            if (scratch.values.cols != matrix->values.cols || output.rows != scratch.values.rows ||
+                output.cols != matrix->values.rows || !output.dense())
+                throw std::invalid_argument("quantized linear dimensions/layout mismatch");
+            gemm.quantize_linear(*dense, scratch, *matrix, output);
+            return;
+        }
+        quantize_rows(*dense, scratch);
+        activation = scratch;
+    } else {
+        activation = std::get<RowScaledView>(input);
+    }
+    if (activation.values.cols != matrix->values.cols || output.rows != activation.values.rows ||
+        output.cols != matrix->values.rows || !output.dense())
+        throw std::invalid_argument("quantized linear dimensions/layout mismatch");
     if (quantized_output.values.data) {
-        if (quantized_output.values.type == weight.values.type &&
-            gemm.linear_finish(scratch, weight, output, epilogue)) {
+        if (quantized_output.values.type == matrix->values.type &&
+            gemm.linear_finish(activation, *matrix, output, epilogue)) {
             quantize_rows(output, quantized_output);
             return;
         }
-        matmul(scratch, weight, output);
+        gemm.linear(activation, *matrix, output);
         pointwise_quantize(output, quantized_output, epilogue);
         return;
     }
-    if (epilogue.activation == Activation::Identity && !bias.data && finish_only(epilogue)) {
-        matmul(scratch, weight, output);
+    if (plain_epilogue(epilogue)) {
+        gemm.linear(activation, *matrix, output);
         return;
     }
-    if (!gemm.linear_finish(scratch, weight, output, epilogue))
-        throw std::invalid_argument("quantized linear epilogue is not a bias/ReLU/tanh-GeLU finish");
+    if (!gemm.linear_finish(activation, *matrix, output, epilogue))
+        throw std::invalid_argument(
+            "quantized linear epilogue is not a prepared bias/ReLU/tanh-GeLU finish");
+}
+
+// ops/linear.cpp:94-131 with a quantized weight.
+bool normalized_linear(TensorView input, const LinearOperand &weight, TensorView bias,
+                       TensorView normalized, TensorView output, TensorView norm_weight,
+                       TensorView norm_bias, float epsilon, const NormFusion &fusion,
+                       Epilogue e, const QkvProjectionOutput *writeback,
+                       RowScaledView quantized_output) {
+    check_linear_output(output, bias, e);
+    if (writeback && writeback->bias.data != bias.data)
+        throw std::invalid_argument("linear already owns its bias");
+    const RowScaledView *quantized = std::get_if<RowScaledView>(&weight);
+    if (!quantized || writeback) return false;
+    QuantizedGemm &gemm = context(input.device);
+    auto project = [&](const Epilogue &epilogue) {
+        return gemm.normalized_linear(input, normalized, norm_weight, norm_bias, epsilon, fusion,
+                                      *quantized, output, epilogue, {}, nullptr);
+    };
+    e.bias = bias;
+    if (quantized_output.values.data) {
+        if (quantized_output.values.type == quantized->values.type && project(e)) {
+            quantize_rows(output, quantized_output);
+        } else {
+            if (!project({})) return false;
+            pointwise_quantize(output, quantized_output, e);
+        }
+        return true;
+    }
+    return project(e);
 }
 
 namespace {

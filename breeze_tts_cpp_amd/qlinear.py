@@ -45,6 +45,19 @@ class Path:
                          self.staged)
 
 
+def grouped_partition(path: Path, K: int) -> tuple[int, int, int]:
+    """(splits, waves, span) of the K ranges a planned path sums separately
+    (the K-group oracle takes the same partition): a skinny launch splits K
+    into splits*8 wave ranges of ceil(ceil(K/256) / (splits*8)) 256-byte
+    blocks (trailing ranges may be empty); a tiled launch sums all of K in
+    one range."""
+    if path.kind == KIND_SKINNY:
+        blocks = -(-K // 256)
+        ranges = path.splits * path.waves
+        return path.splits, path.waves, -(-blocks // ranges) * 256
+    return 1, 1, K
+
+
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_workspace_bytes", "qlin_gemm", "qlin_linear", "qlin_quantized_norm",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
@@ -452,3 +465,4 @@ def linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int, group:
                               sw.data_ptr(), out.data_ptr(), rows, N, K, fmt, _TYPES[out.dtype],
                               group, group, rotation, ws_ptr, ws_bytes, _stream(stream)))
     return out
+

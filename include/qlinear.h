@@ -82,10 +82,11 @@ typedef struct qlin_path {
     int tokens;   /* token (M) tile */
     int channels; /* output-channel (N) tile */
     int splits;   /* grid-level K partitions (partials in workspace when > 1) */
-    int waves;    /* skinny: wave64s splitting K inside a workgroup;
-                     tiled: 1, or 8 for the eight-wave 256x256 INT8 tile */
-    int staged;   /* skinny: weight slabs staged global->LDS; 1 = per wave,
-                     2 = per workgroup (contiguous row runs per wave, one barrier) */
+    int waves;    /* skinny: 8 (wave64s splitting K inside a workgroup);
+                     tiled: 1, 2, 4 or 8 (the macro tile's wave layout) */
+    int staged;   /* skinny: 1 = each wave's weight slab staged global->LDS
+                     in one shot, 0 = weights loaded straight to registers;
+                     tiled: 0 */
 } qlin_path;
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -132,9 +133,9 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
  * planned). Two launches on `stream` (quantizer, GEMM), or one where the
  * path is an INT8 decode path with 16-token tiles, per-wave weight slabs and
  * K = 2048 with per-token scales, no rotation and a 16-byte-aligned source
- * with ld % 8 == 0: there the GEMM quantizes its own token rows and fills
- * (xq, sx) with the same bits. The first failing check's status is
- * returned. */
+ * with ld % 8 == 0, and neither y nor (xq, sx) overlaps x: there the GEMM
+ * quantizes its own token rows and fills (xq, sx) with the same bits. The
+ * first failing check's status is returned. */
 int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void *xq, float *sx,
                 const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,
                 int out_type, int input_group, int weight_group, int rotation, void *workspace,

@@ -16,19 +16,22 @@
 //   tts::launch_quantized_norm               <- ops/kernels/quant/quant_norm.h:5-7
 //   tts::launch_quantized_gated,
 //     quant_gated_supports_clusters          <- ops/kernels/quant/quant_gated.h:5-8
+//   tts::Buffer                              <- core/buffer.h:4 (Tensor::Storage, device subset)
+//   tts::QkvProjectionOutput                 <- core/qkv_projection.h:6-10 (fields only)
 //   tts::QuantizedGemm                       <- ops/cuda/quantization.h:15-42
 //     (normalized_linear                     <- ops/kernels/sequence/norm_projection.h:15)
 //   tts::QuantizationWorkspace               <- layers/quantization.h:9-49
+//   tts::ops::LinearOperand, linear,
+//     normalized_linear                      <- ops/linear.h:8-18 (quantized weights)
 //   tts::ops::quantize_rows / matmul /
-//     prepare_quantized / linear             <- ops/storage.h:12, ops/basic.h:11,25-26,
-//                                               ops/linear.h:11-13 (quantized branch)
+//     prepare_quantized                      <- ops/storage.h:12, ops/basic.h:11,25-26
 //   tts::ops::quantized_norm / quantized_gated <- ops/basic.h:33-35
 //
 // Errors: std::invalid_argument for shape/type/alignment/workspace problems,
 // std::runtime_error for device errors and missing kernel variants,
 // std::logic_error for unprepared shapes — as the reference throws.
-// Device pointers only; nothing here allocates device memory except
-// QuantizationWorkspace, which owns its buffers like the reference's.
+// Device pointers only; nothing here allocates device memory except Buffer
+// and QuantizationWorkspace, which own their memory like the reference's.
 #pragma once
 
 #include <cstddef>
@@ -36,8 +39,10 @@
 #include <map>
 #include <memory>
 #include <stdexcept>
+#include <set>
 #include <string>
 #include <tuple>
+#include <variant>
 
 #include "qlinear.h"
 
@@ -72,9 +77,44 @@ struct TensorView {
     }
     int ld() const { return stride ? stride : cols; }
     bool dense() const { return rows <= 1 || ld() == cols; }
+    // Whether the byte ranges the two views span intersect.
+    bool overlaps(const TensorView &other) const {
+        if (!data || !other.data || !numel() || !other.numel()) return false;
+        const auto begin = reinterpret_cast<uintptr_t>(data);
+        const auto other_begin = reinterpret_cast<uintptr_t>(other.data);
+        const uintptr_t end = begin + (size_t(rows - 1) * ld() + cols) * bytes(type);
+        const uintptr_t other_end =
+            other_begin + (size_t(other.rows - 1) * other.ld() + other.cols) * bytes(other.type);
+        return begin < other_end && other_begin < end;
+    }
     size_t numel() const { return size_t(rows) * size_t(cols); }
     size_t size() const { return numel() * bytes(type); }
     template <typename T> T *ptr() const { return static_cast<T *>(data); }
+};
+
+// Owned device memory (the reference's Buffer = Tensor::Storage, core/buffer.h,
+// core/tensor_storage.h:13-37, device subset): hipMalloc'ed on the current
+// device, released on destruction; views borrow it.
+class Buffer {
+  public:
+    Buffer() = default;
+    explicit Buffer(size_t bytes);
+    ~Buffer();
+    Buffer(const Buffer &) = delete;
+    Buffer &operator=(const Buffer &) = delete;
+    Buffer(Buffer &&other) noexcept;
+    Buffer &operator=(Buffer &&other) noexcept;
+    void *data() const { return data_; }
+    size_t size() const { return size_; }
+    int device() const { return device_; }
+    template <class Value> Value *ptr() const { return static_cast<Value *>(data_); }
+    TensorView view(int rows, int columns, Type dtype = Type::BF16, size_t offset = 0,
+                    int stride = 0) const;
+
+  private:
+    void *data_ = nullptr;
+    size_t size_ = 0;
+    int device_ = -1;
 };
 
 // ---------------------------------------------------------------- quantization metadata
@@ -168,6 +208,16 @@ struct NormFusion {
 };
 }  // namespace ops
 
+// The fused QKV-projection cache writeback target (reference
+// core/qkv_projection.h:6-10). The writeback kernel belongs to the attention
+// path, which this library does not include: the normalized projections
+// return false when given one, and the caller takes its unfused path.
+struct QkvProjectionOutput {
+    TensorView query, keys, values, bias;
+    const int *positions = nullptr;
+    int key_value_channels = 0, capacity = 0;
+};
+
 // ---------------------------------------------------------------- QuantizedGemm
 struct SelectionStats {
     size_t entries = 0, hits = 0, searches = 0;
@@ -182,6 +232,11 @@ struct QuantCacheStats {
 // (split-K partials), as the reference's CudaContext::gemm_workspace.
 class QuantizedGemm {
   public:
+    // The reference's constructor (ops/cuda/quantization.h:20-21): the BLAS
+    // handle is accepted and unused (every GEMM is this library's own);
+    // `workspace` receives the split-K partials and must outlive the object.
+    QuantizedGemm(qlin_stream_t stream, void *blas_handle, Buffer &workspace,
+                  Type format = Type::FP8);
     QuantizedGemm(qlin_stream_t stream, void *workspace, size_t workspace_bytes,
                   Type format = Type::FP8);
     QuantizedGemm(const QuantizedGemm &) = delete;
@@ -189,6 +244,13 @@ class QuantizedGemm {
     QuantCacheStats cache_stats() const;
     void prepare(int rows, int output_channels, int input_channels, Type output_type = Type::BF16,
                  QuantizationGroups groups = {});
+    // Registers the fused finish of a prepared projection (reference
+    // ops/cuda/quantization.cpp:395-455): a bias / ReLU / tanh-GeLU finish
+    // that linear_finish may then run in the GEMM's epilogue; any other
+    // epilogue is ignored. logic_error when the projection itself was not
+    // prepared.
+    void prepare_finish(int rows, int output_channels, int input_channels, Type output_type,
+                        const ops::Epilogue &finish, QuantizationGroups groups = {});
     void linear(RowScaledView input, RowScaledView weight, TensorView output);
     // ops::linear's quantize_rows + linear as one call (no reference
     // counterpart; qlin_linear): `scratch` receives the quantized input as
@@ -198,7 +260,8 @@ class QuantizedGemm {
                          TensorView output);
     // Fused bias + ReLU / tanh-GeLU finish (reference linear_finish,
     // ops/cuda/quantization.cpp:465-478), also bias-only: false when the
-    // epilogue is none of those (the caller then finishes separately).
+    // epilogue is none of those or its finish was not prepared (the caller
+    // then finishes separately).
     bool linear_finish(RowScaledView input, RowScaledView weight, TensorView output,
                        const ops::Epilogue &finish);
     // LayerNorm -> quantize -> GEMV in one launch for hidden sizes <= 512
@@ -208,7 +271,8 @@ class QuantizedGemm {
     bool normalized_linear(TensorView input, TensorView normalized, TensorView norm_weight,
                            TensorView norm_bias, float epsilon, const ops::NormFusion &fusion,
                            RowScaledView weight, TensorView output,
-                           const ops::Epilogue &epilogue = {}, RowScaledView encoded = {});
+                           const ops::Epilogue &epilogue = {}, RowScaledView encoded = {},
+                           const QkvProjectionOutput *writeback = nullptr);
     LinearPath planned(int rows, int output_channels, int input_channels,
                        Type output_type = Type::BF16, QuantizationGroups groups = {}) const;
     Type format() const { return format_; }
@@ -216,12 +280,14 @@ class QuantizedGemm {
 
   private:
     using Key = std::tuple<int, int, int, Type, int, int>;
+    using FinishKey = std::tuple<Key, ops::Activation, bool>;  // + bias present
     qlin_stream_t stream_;
     void *workspace_;
     size_t workspace_bytes_;
     Type format_;
     bool sealed_ = false;
     std::map<Key, LinearPath> plans_;
+    std::set<FinishKey> finishes_;
     SelectionStats stats_;
 };
 
@@ -257,6 +323,9 @@ void bind(int device, QuantizedGemm *gemm);
 QuantizedGemm &context(int device);
 
 void quantize_rows(TensorView input, RowScaledView output);
+// Operand of a projection (reference ops/linear.h:8): a dense 16-bit matrix,
+// or quantized values with row scales.
+using LinearOperand = std::variant<TensorView, RowScaledView>;
 // Pointwise epilogue -> row quantization (reference ops/sequence.h:38-42,
 // sequence_pointwise.cu:307-357); `multiprocessors` is accepted and unused.
 void pointwise_quantize(TensorView x, RowScaledView quantized, const Epilogue &e = {},
@@ -266,22 +335,38 @@ void pointwise_quantize(TensorView x, RowScaledView quantized, const Epilogue &e
 void layer_norm_quantize(TensorView x, RowScaledView quantized, TensorView weight, TensorView bias,
                          float eps, const NormFusion &fusion = {}, TensorView retained = {});
 void matmul(RowScaledView input, RowScaledView weight, TensorView output);
+// prepare + prepare_finish of the bound context (reference ops/basic.h:25-26,
+// ops/basic.cpp:48-53).
 void prepare_quantized(TensorView weight, int rows, int output_channels, int input_channels,
-                       Type type, QuantizationGroups groups = {});
-// Quantized branch of ops::linear: quantize `input` into `scratch`, then GEMM.
-void linear(TensorView input, RowScaledView weight, TensorView output, RowScaledView scratch);
+                       Type type, const Epilogue &epilogue = {}, QuantizationGroups groups = {});
 void quantized_norm(TensorView input, TensorView update, TensorView weight, RowScaledView output,
                     float epsilon, bool gemma = false, TensorView scale = {});
 void quantized_gated(TensorView input, RowScaledView output, int kind);
-// ops::linear's quantized branch with an epilogue (ops/linear.cpp:26-93):
-// bias + ReLU / tanh-GeLU is fused into the GEMM; with `quantized_output`
-// the output is also quantized for the next layer, through the fused finish
-// and quantize_rows, or the GEMM and pointwise_quantize for any other dense
-// epilogue. Without `quantized_output`, an epilogue beyond the fused finish
-// is rejected (the reference's non-quantized pointwise pass is not part of
-// this library).
-void linear(TensorView input, RowScaledView weight, TensorView bias, TensorView output,
-            Epilogue epilogue, RowScaledView scratch, RowScaledView quantized_output = {});
+// The reference's ops::linear (ops/linear.h:11-13, ops/linear.cpp:26-93) for
+// quantized weights. A dense `input` is quantized into `scratch` (one launch
+// with the GEMM on decode paths without an epilogue); a RowScaledView input
+// is used as is. A prepared bias + ReLU / tanh-GeLU finish runs in the
+// GEMM's epilogue; with `quantized_output` the output is also quantized for
+// the next layer, through the fused finish and quantize_rows, or the GEMM
+// and pointwise_quantize for any other dense epilogue. Without
+// `quantized_output`, an epilogue beyond a prepared fused finish is rejected
+// with invalid_argument, and so is a dense (TensorView) weight: the
+// reference's non-quantized pointwise pass and dense GEMMs are not part of
+// this library.
+void linear(const LinearOperand &input, const LinearOperand &weight, TensorView bias,
+            TensorView output, Epilogue epilogue = {}, RowScaledView scratch = {},
+            RowScaledView quantized_output = {});
+// The reference's ops::normalized_linear (ops/linear.h:14-18,
+// ops/linear.cpp:94-131) for quantized weights: LayerNorm -> quantize ->
+// GEMV in one launch (QuantizedGemm::normalized_linear), optionally followed
+// by the next layer's quantization. Returns false, leaving the caller's
+// unfused path responsible, for requests outside that kernel: a dense
+// weight, a QKV writeback, hidden sizes above 512, source-row gathers.
+bool normalized_linear(TensorView input, const LinearOperand &weight, TensorView bias,
+                       TensorView normalized, TensorView output, TensorView norm_weight,
+                       TensorView norm_bias, float epsilon, const NormFusion &fusion,
+                       Epilogue epilogue = {}, const QkvProjectionOutput *writeback = nullptr,
+                       RowScaledView quantized_output = {});
 }  // namespace ops
 
 }  // namespace tts

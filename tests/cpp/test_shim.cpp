@@ -31,6 +31,55 @@ static int failures = 0;
         }                                                                   \
     } while (0)
 
+// The projection calls of the reference's layers/linear.cpp, written as it
+// writes them (its members weight_ / bias_, layers/linear.h:12-14), so this
+// file compiles only where the header is a drop-in for those call sites.
+struct LayerCalls {
+    ops::LinearOperand weight_;
+    TensorView bias_;
+    // layers/linear.cpp:132-148 (prepare_range)
+    void prepare_range(TensorView matrix, int capacity, int output_channels, int input_channels,
+                       Type activation_type_, ops::Activation activation,
+                       QuantizationGroups layout) const {
+        ops::Epilogue finish;
+        finish.bias = bias_;
+        finish.activation = activation;
+        ops::prepare_quantized(matrix, capacity, output_channels, input_channels,
+                               activation_type_, finish, layout);
+    }
+    // layers/linear.cpp:179 (project with a quantized input)
+    void project(RowScaledView input, TensorView output) const {
+        ops::linear(input, weight_, {}, output);
+    }
+    // layers/linear.cpp:195
+    bool normalized_forward(TensorView input, TensorView normalized, TensorView output,
+                            TensorView norm_weight, TensorView norm_bias, float epsilon,
+                            const ops::NormFusion &fusion, ops::Epilogue epilogue,
+                            const QkvProjectionOutput *writeback) const {
+        return ops::normalized_linear(input, weight_, bias_, normalized, output, norm_weight,
+                                      norm_bias, epsilon, fusion, epilogue, writeback);
+    }
+    // layers/linear.cpp:207
+    bool normalized_quantized(TensorView input, TensorView normalized, TensorView output,
+                              TensorView norm_weight, TensorView norm_bias, float epsilon,
+                              const ops::NormFusion &fusion, ops::Epilogue epilogue,
+                              RowScaledView quantized_output) const {
+        return ops::normalized_linear(input, weight_, bias_, normalized, output, norm_weight,
+                                      norm_bias, epsilon, fusion, epilogue, nullptr,
+                                      quantized_output);
+    }
+    // layers/linear.cpp:212
+    void normalized_project(RowScaledView normalized_input, TensorView output,
+                            ops::Epilogue epilogue, RowScaledView quantized_output) const {
+        ops::linear(normalized_input, weight_, bias_, output, epilogue, {}, quantized_output);
+    }
+    // layers/linear.cpp:246 (apply)
+    void apply(TensorView input, TensorView output, TensorView bias, ops::Epilogue epilogue,
+               RowScaledView scratch, RowScaledView quantized_output = {}) const {
+        ops::linear(input, weight_, bias, output, epilogue, scratch, quantized_output);
+    }
+};
+
 template <class E> static bool throws(const std::function<void()> &f) {
     try {
         f();
@@ -139,6 +188,42 @@ static int host_tests() {
     }
     // ops without a bound context
     EXPECT(throws<std::logic_error>([&] { ops::matmul(x, w, TensorView(dummy, 30, 4096)); }));
+    // finishes are prepared on a prepared projection only
+    {
+        QuantizedGemm g(nullptr, nullptr, 0, Type::I8);
+        ops::Epilogue relu;
+        relu.activation = ops::Activation::Relu;
+        EXPECT(throws<std::logic_error>([&] { g.prepare_finish(30, 4096, 2048, Type::BF16, relu); }));
+        g.prepare(30, 4096, 2048);
+        g.prepare_finish(30, 4096, 2048, Type::BF16, relu);
+        ops::Epilogue silu;  // not a GEMM finish: ignored
+        silu.activation = ops::Activation::Silu;
+        g.prepare_finish(30, 4096, 2048, Type::BF16, silu);
+        EXPECT(g.cache_stats().prepared_plans == 2);
+    }
+    // ops::linear / ops::normalized_linear over LinearOperand
+    {
+        LayerCalls dense{TensorView(dummy, 64, 512), {}};
+        EXPECT(throws<std::invalid_argument>([&] {  // dense weights: not in this library
+            dense.apply(TensorView(dummy, 2, 512), TensorView(dummy, 2, 64), {}, {}, {});
+        }));
+        EXPECT(!dense.normalized_forward(TensorView(dummy, 2, 512), {}, TensorView(dummy, 2, 64),
+                                         {}, {}, 1e-5f, {}, {}, nullptr));
+        RowScaledView wq{TensorView(dummy, 64, 512, Type::I8), TensorView(dummy, 64, 1, Type::F32), 0, 0};
+        LayerCalls quantized{wq, {}};
+        QkvProjectionOutput writeback;
+        EXPECT(!quantized.normalized_forward(TensorView(dummy, 2, 512), {}, TensorView(dummy, 2, 64),
+                                             {}, {}, 1e-5f, {}, {}, &writeback));
+        ops::Epilogue owned;
+        owned.bias = TensorView(dummy, 1, 64);
+        EXPECT(throws<std::invalid_argument>([&] {  // ops::linear owns the bias
+            quantized.apply(TensorView(dummy, 2, 512), TensorView(dummy, 2, 64), {}, owned, {});
+        }));
+        EXPECT(throws<std::invalid_argument>([&] {  // bias aliases the output
+            quantized.apply(TensorView(dummy, 2, 512), TensorView(dummy, 2, 64),
+                            TensorView(dummy + 8, 1, 64), {}, {});
+        }));
+    }
     std::printf("host tests: %s\n", failures ? "FAILED" : "ok");
     return failures ? 1 : 0;
 }
@@ -168,55 +253,71 @@ static int gpu_test(const std::string &dir) {
     const QuantizationGroups groups = quantization_groups(q);
     auto x = read_file<uint16_t>(dir + "/x.bf16", size_t(M) * K);
     auto w = read_file<uint16_t>(dir + "/w.bf16", size_t(N) * K);
-    void *dx, *dw, *dwq, *dsw, *dy, *dws;
+    void *dx, *dw, *dwq, *dsw, *dy;
     const int wgroups = groups.weight ? (K + groups.weight - 1) / groups.weight : 1;
     HIP(hipMalloc(&dx, x.size() * 2));
     HIP(hipMalloc(&dw, w.size() * 2));
     HIP(hipMalloc(&dwq, size_t(N) * K));
     HIP(hipMalloc(&dsw, size_t(N) * wgroups * 4));
     HIP(hipMalloc(&dy, size_t(M) * N * 2));
-    const size_t ws_bytes = 8 << 20;  // the reference's gemm_workspace size
-    HIP(hipMalloc(&dws, ws_bytes));
     HIP(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice));
     HIP(hipMemcpy(dw, w.data(), w.size() * 2, hipMemcpyHostToDevice));
     hipStream_t stream;
     HIP(hipStreamCreate(&stream));
     {
-        QuantizedGemm gemm(reinterpret_cast<qlin_stream_t>(stream), dws, ws_bytes, fmt);
+        // The execution context as the reference's runtime builds it
+        // (runtime/cuda_context.cpp:61,72): an 8 MiB GEMM workspace Buffer.
+        Buffer gemm_workspace(8 << 20);
+        QuantizedGemm gemm(reinterpret_cast<qlin_stream_t>(stream), nullptr, gemm_workspace, fmt);
         ops::bind(0, &gemm);
         // Load time: weight quantization with the activation quantizer
-        // (io/weights.cpp:80-87), plan preparation, seal.
+        // (io/weights.cpp:80-87), plan preparation with the layer's finish
+        // (layers/linear.cpp:132-148), seal.
         RowScaledView wq{TensorView(dwq, N, K, fmt, 0, 0),
                          groups.weight ? TensorView(dsw, wgroups, N, Type::F32, 0, 0)
                                        : TensorView(dsw, N, 1, Type::F32, 0, 0),
                          groups.weight, groups.rotation};
         ops::quantize_rows(TensorView(dw, N, K, Type::BF16, 0, 0), wq);
-        ops::prepare_quantized(TensorView(dwq, N, K, fmt, 0, 0), M, N, K, Type::BF16, groups);
+        std::ifstream act_file(dir + "/finish.txt"), epi_file(dir + "/epilogue.txt"),
+            mode_file(dir + "/calls.txt");
+        int act = 0, activation = 0, use_residual = 0;
+        std::string calls;
+        const bool quantized_out = bool(epi_file >> activation >> use_residual);
+        const bool finish = !quantized_out && (act_file >> act) && act;
+        mode_file >> calls;
+        void *db = nullptr;
+        if (quantized_out || finish) {
+            auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
+            HIP(hipMalloc(&db, b.size() * 2));
+            HIP(hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice));
+        }
+        LayerCalls layer{wq, db ? TensorView(db, 1, N) : TensorView()};
+        const ops::Activation prepared = quantized_out ? static_cast<ops::Activation>(activation)
+                                         : finish ? (act == 1 ? ops::Activation::Relu
+                                                              : ops::Activation::GeluTanh)
+                                                  : ops::Activation::Identity;
+        layer.prepare_range(TensorView(dwq, N, K, fmt, 0, 0), row_capacity(M), N, K, Type::BF16,
+                            prepared, groups);
         gemm.seal();
         // Serving: dense bf16 activations through ops::linear.
         QuantizationWorkspace workspace(M, QuantizationWorkspace::Capacity::matrix(K, groups.activation));
         RowScaledView scratch = workspace.view(M, K, fmt, groups);
         scratch.values.device = scratch.scales.device = 0;
-        std::ifstream act_file(dir + "/finish.txt"), epi_file(dir + "/epilogue.txt");
-        int act = 0, activation = 0, use_residual = 0;
-        if (epi_file >> activation >> use_residual) {
+        if (quantized_out) {
             // ops::linear with a quantized output for the next layer
             // (ops/linear.cpp:35-78): bias + activation (+ residual), then codes.
-            auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
             auto r = read_file<uint16_t>(dir + "/residual.bf16", size_t(M) * N);
-            void *db, *dr, *dq, *dqs;
-            HIP(hipMalloc(&db, b.size() * 2));
+            void *dr, *dq, *dqs;
             HIP(hipMalloc(&dr, r.size() * 2));
             HIP(hipMalloc(&dq, size_t(M) * N));
             HIP(hipMalloc(&dqs, size_t(M) * 4));
-            HIP(hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice));
             HIP(hipMemcpy(dr, r.data(), r.size() * 2, hipMemcpyHostToDevice));
             ops::Epilogue e;
             e.activation = static_cast<ops::Activation>(activation);
             if (use_residual) e.residual = TensorView(dr, M, N, Type::BF16, 0, 0);
             RowScaledView next{TensorView(dq, M, N, fmt, 0, 0), TensorView(dqs, M, 1, Type::F32, 0, 0)};
-            ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq, TensorView(db, 1, N),
-                        TensorView(dy, M, N, Type::BF16, 0, 0), e, scratch, next);
+            layer.apply(TensorView(dx, M, K, Type::BF16, 0, 0), TensorView(dy, M, N, Type::BF16, 0, 0),
+                        layer.bias_, e, scratch, next);
             HIP(hipStreamSynchronize(stream));
             std::vector<uint8_t> qh(size_t(M) * N);
             std::vector<float> qsh(M);
@@ -224,23 +325,23 @@ static int gpu_test(const std::string &dir) {
             HIP(hipMemcpy(qsh.data(), dqs, qsh.size() * 4, hipMemcpyDeviceToHost));
             write_file(dir + "/next.u8", qh);
             write_file(dir + "/next_scales.f32", qsh);
-            for (void *p : {db, dr, dq, dqs}) (void)hipFree(p);
-        } else if (act_file >> act && act) {
+            for (void *p : {dr, dq, dqs}) (void)hipFree(p);
+        } else if (finish) {
             // ops::linear with a bias + activation epilogue (fused finish)
-            auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
-            void *db;
-            HIP(hipMalloc(&db, b.size() * 2));
-            HIP(hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice));
             ops::Epilogue e;
-            e.activation = act == 1 ? ops::Activation::Relu : ops::Activation::GeluTanh;
-            ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq, TensorView(db, 1, N),
-                        TensorView(dy, M, N, Type::BF16, 0, 0), e, scratch);
-            HIP(hipStreamSynchronize(stream));
-            (void)hipFree(db);
+            e.activation = prepared;
+            layer.apply(TensorView(dx, M, K, Type::BF16, 0, 0), TensorView(dy, M, N, Type::BF16, 0, 0),
+                        layer.bias_, e, scratch);
+        } else if (calls == "rowscaled") {
+            // A quantized input (layers/linear.cpp:179): quantize_rows, then
+            // ops::linear(input, weight_, {}, output).
+            ops::quantize_rows(TensorView(dx, M, K, Type::BF16, 0, 0), scratch);
+            layer.project(scratch, TensorView(dy, M, N, Type::BF16, 0, 0));
         } else {
-            ops::linear(TensorView(dx, M, K, Type::BF16, 0, 0), wq,
-                        TensorView(dy, M, N, Type::BF16, 0, 0), scratch);
+            layer.apply(TensorView(dx, M, K, Type::BF16, 0, 0), TensorView(dy, M, N, Type::BF16, 0, 0),
+                        {}, {}, scratch);
         }
+        if (db) (void)hipFree(db);
         HIP(hipStreamSynchronize(stream));
         std::vector<uint16_t> y(size_t(M) * N);
         std::vector<uint8_t> wqh(size_t(N) * K);
@@ -253,7 +354,7 @@ static int gpu_test(const std::string &dir) {
         write_file(dir + "/sw.f32", swh);
         ops::bind(0, nullptr);
     }
-    for (void *p : {dx, dw, dwq, dsw, dy, dws}) (void)hipFree(p);
+    for (void *p : {dx, dw, dwq, dsw, dy}) (void)hipFree(p);
     (void)hipStreamDestroy(stream);
     std::printf("gpu test %s M=%d N=%d K=%d: done\n", mode.c_str(), M, N, K);
     return 0;
@@ -320,14 +421,16 @@ static int producers_test(const std::string &dir) {
     return 0;
 }
 
-// ops::layer_norm_quantize (hidden 2048, K128 groups + rotation) and
-// QuantizedGemm::normalized_linear (LayerNorm + residual -> INT8 GEMV, k 512)
-// through the C++ interface.
+// ops::layer_norm_quantize (hidden 2048, K128 groups + rotation) feeding
+// ops::linear with a quantized input (layers/linear.cpp:212 form), and
+// ops::normalized_linear (LayerNorm + residual -> INT8 GEMV, k 512; the
+// layers/linear.cpp:195 and :207 forms) through the C++ interface.
 static int sequence_test(const std::string &dir) {
     int M;
     std::ifstream(dir + "/shape.txt") >> M;
-    const int H = 2048, k = 512, n = 384;
+    const int H = 2048, k = 512, n = 384, n2 = 256;
     auto x = read_file<uint16_t>(dir + "/x.bf16", size_t(M) * H);
+    auto w2 = read_file<uint16_t>(dir + "/w2.bf16", size_t(n2) * H);
     auto lw = read_file<uint16_t>(dir + "/lw.bf16", size_t(H));
     auto xs = read_file<uint16_t>(dir + "/xs.bf16", size_t(M) * k);
     auto rs = read_file<uint16_t>(dir + "/rs.bf16", size_t(M) * k);
@@ -345,6 +448,14 @@ static int sequence_test(const std::string &dir) {
     HIP(hipMalloc(&dy, size_t(M) * n * 2));
     HIP(hipMalloc(&dnorm, size_t(M) * k * 2));
     HIP(hipMalloc(&dgemm, 1 << 20));
+    void *dw2, *dw2q, *dsw2, *dy2, *dnq, *dnqs;
+    HIP(hipMalloc(&dw2, w2.size() * 2));
+    HIP(hipMalloc(&dw2q, size_t(n2) * H));
+    HIP(hipMalloc(&dsw2, size_t(H / 128) * n2 * 4));
+    HIP(hipMalloc(&dy2, size_t(M) * n2 * 2));
+    HIP(hipMalloc(&dnq, size_t(M) * n));
+    HIP(hipMalloc(&dnqs, size_t(M) * 4));
+    HIP(hipMemcpy(dw2, w2.data(), w2.size() * 2, hipMemcpyHostToDevice));
     HIP(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice));
     HIP(hipMemcpy(dlw, lw.data(), lw.size() * 2, hipMemcpyHostToDevice));
     HIP(hipMemcpy(dxs, xs.data(), xs.size() * 2, hipMemcpyHostToDevice));
@@ -359,15 +470,42 @@ static int sequence_test(const std::string &dir) {
                         128, 128};
         ops::layer_norm_quantize(TensorView(dx, M, H, Type::BF16, 0, 0), q,
                                  TensorView(dlw, 1, H, Type::BF16, 0, 0), TensorView(), 1e-5f);
+        // The K128 / H128 input feeds a projection with weights of the same
+        // layout (group_int8), ops::linear with a quantized input.
+        RowScaledView w2q{TensorView(dw2q, n2, H, Type::I8, 0, 0),
+                          TensorView(dsw2, H / 128, n2, Type::F32, 0, 0), 128, 128};
+        ops::quantize_rows(TensorView(dw2, n2, H, Type::BF16, 0, 0), w2q);
+        LayerCalls grouped{w2q, {}};
+        grouped.prepare_range(w2q.values, row_capacity(M), n2, H, Type::BF16,
+                              ops::Activation::Identity, {128, 128, 128});
+        grouped.normalized_project(q, TensorView(dy2, M, n2, Type::BF16, 0, 0), {}, {});
         RowScaledView wq{TensorView(dwq, n, k, Type::I8, 0, 0), TensorView(dsw, n, 1, Type::F32, 0, 0)};
         ops::quantize_rows(TensorView(dws, n, k, Type::BF16, 0, 0), wq);
         ops::NormFusion fusion;
         fusion.residual = TensorView(drs, M, k, Type::BF16, 0, 0);
-        const bool fused = gemm.normalized_linear(
+        LayerCalls small{wq, {}};
+        const bool fused = small.normalized_forward(
             TensorView(dxs, M, k, Type::BF16, 0, 0), TensorView(dnorm, M, k, Type::BF16, 0, 0),
-            TensorView(), TensorView(), 1e-5f, fusion, wq, TensorView(dy, M, n, Type::BF16, 0, 0));
+            TensorView(dy, M, n, Type::BF16, 0, 0), TensorView(), TensorView(), 1e-5f, fusion, {},
+            nullptr);
         EXPECT(fused);
+        // Again with the next layer's quantized input (same output y).
+        RowScaledView next{TensorView(dnq, M, n, Type::I8, 0, 0), TensorView(dnqs, M, 1, Type::F32, 0, 0)};
+        const bool fused_next = small.normalized_quantized(
+            TensorView(dxs, M, k, Type::BF16, 0, 0), TensorView(dnorm, M, k, Type::BF16, 0, 0),
+            TensorView(dy, M, n, Type::BF16, 0, 0), TensorView(), TensorView(), 1e-5f, fusion, {},
+            next);
+        EXPECT(fused_next);
         HIP(hipStreamSynchronize(stream));
+        std::vector<uint16_t> y2h(size_t(M) * n2);
+        std::vector<uint8_t> nqh(size_t(M) * n);
+        std::vector<float> nqsh(M);
+        HIP(hipMemcpy(y2h.data(), dy2, y2h.size() * 2, hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(nqh.data(), dnq, nqh.size(), hipMemcpyDeviceToHost));
+        HIP(hipMemcpy(nqsh.data(), dnqs, nqsh.size() * 4, hipMemcpyDeviceToHost));
+        write_file(dir + "/y2.bf16", y2h);
+        write_file(dir + "/next.u8", nqh);
+        write_file(dir + "/next.f32", nqsh);
         std::vector<uint8_t> qh(size_t(M) * H), wqh(size_t(n) * k);
         std::vector<float> qsh(size_t(H / 128) * M), swh(n);
         std::vector<uint16_t> yh(size_t(M) * n), nh(size_t(M) * k);
@@ -385,7 +523,9 @@ static int sequence_test(const std::string &dir) {
         write_file(dir + "/norm.bf16", nh);
         ops::bind(0, nullptr);
     }
-    for (void *p : {dx, dlw, dq, dqs, dxs, drs, dws, dwq, dsw, dy, dnorm, dgemm}) (void)hipFree(p);
+    for (void *p : {dx, dlw, dq, dqs, dxs, drs, dws, dwq, dsw, dy, dnorm, dgemm, dw2, dw2q, dsw2,
+                    dy2, dnq, dnqs})
+        (void)hipFree(p);
     (void)hipStreamDestroy(stream);
     std::printf("sequence test M=%d: %s\n", M, failures ? "FAILED" : "done");
     return failures ? 1 : 0;

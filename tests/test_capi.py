@@ -75,7 +75,9 @@ def test_gemm_validation():
     assert call(y=FAKE + 2) == -2
     bad = qlinear.Path(qlinear.KIND_SKINNY, 16, 16, 1, 3)
     assert call(path=bad) == -4
-    split = qlinear.Path(qlinear.KIND_SKINNY, 16, 16, 2, 1)
+    assert call(path=qlinear.Path(qlinear.KIND_SKINNY, 16, 16, 1, 4)) == -4  # eight waves only
+    assert call(path=qlinear.Path(qlinear.KIND_SKINNY, 48, 16, 1, 8)) == -4  # token tiles 16/32/64
+    split = qlinear.Path(qlinear.KIND_SKINNY, 16, 16, 2, 8)
     assert call(K=512, path=split) == -3     # split-K needs a workspace
     assert b"workspace" in L.qlin_last_error()
     assert call(K=512, path=split, ws=FAKE, wsb=10) == -3
@@ -105,7 +107,7 @@ def test_plan_and_workspace():
     p = qlinear.plan(32, 4096, 2048, I8)
     assert p.kind in (qlinear.KIND_SKINNY, qlinear.KIND_TILED)
     assert qlinear.workspace_bytes(p, 32, 4096, 2048, I8) >= 0
-    split = qlinear.Path(qlinear.KIND_SKINNY, 32, 16, 4, 2)
+    split = qlinear.Path(qlinear.KIND_SKINNY, 32, 16, 4, 8)
     assert qlinear.workspace_bytes(split, 32, 4096, 2048, I8) == 4 * 32 * 4096 * 4
     with pytest.raises(qlinear.QLinearError):
         qlinear.plan(0, 16, 16, I8)
@@ -257,3 +259,4 @@ def test_sequence_producer_validation():
     gather.source_rows = FAKE + 0x400000
     assert nl(fusion=gather) == -1
     assert nl(y=X + 2) == -1              # output overlaps the input
+

@@ -29,14 +29,19 @@ def test_host_interface():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("calls", ["dense", "rowscaled"])
 @pytest.mark.parametrize("mode,M,N,K", [("int8", 16, 2048, 2048), ("group_int8", 32, 512, 1024),
                                         ("int8", 300, 384, 512), ("fp8", 8, 256, 2048)])
-def test_linear_end_to_end(dev, orc, tmp_path, mode, M, N, K):
+def test_linear_end_to_end(dev, orc, tmp_path, mode, M, N, K, calls):
+    """Load (quantize_rows of the weights, prepare_quantized, seal) then
+    serve through ops::linear: a dense input as layers/linear.cpp:246 passes
+    it, or an input already quantized as layers/linear.cpp:179 does."""
     xb = synthetic.activations(M, K, seed=M)
     wb = synthetic.weights(N, K, seed=N)
     xb.tofile(tmp_path / "x.bf16")
     wb.tofile(tmp_path / "w.bf16")
     (tmp_path / "shape.txt").write_text(f"{M} {N} {K} {mode}\n")
+    (tmp_path / "calls.txt").write_text(f"{calls}\n")
     print(f"test_shim gpu {mode} M={M} N={N} K={K}", flush=True)
     r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
                        timeout=120)
@@ -56,8 +61,7 @@ def test_linear_end_to_end(dev, orc, tmp_path, mode, M, N, K):
     elif group:
         from breeze_tts_cpp_amd import qlinear
         p = qlinear.plan(M, N, K, fmt, group, group)
-        span = -(-K // 256) * 256 // (p.splits * p.waves) if p.kind == qlinear.KIND_SKINNY else K
-        splits, waves = (p.splits, p.waves) if p.kind == qlinear.KIND_SKINNY else (1, 1)
+        splits, waves, span = qlinear.grouped_partition(p, K)
         ref, _ = orc.gemm_grouped(xq, sx, wq_ref, sw_ref, fmt, group, group, splits, waves, span)
         assert np.array_equal(y, ref)
     else:
@@ -159,16 +163,19 @@ def test_linear_quantized_output_end_to_end(dev, orc, tmp_path, activation, use_
 @pytest.mark.gpu
 @pytest.mark.parametrize("M", [1, 32])
 def test_sequence_end_to_end(dev, orc, tmp_path, M):
-    """ops::layer_norm_quantize (K128 groups + H128 rotation) and
-    QuantizedGemm::normalized_linear (LayerNorm + residual -> INT8 GEMV)
-    through the C++ interface, against the oracle."""
+    """ops::layer_norm_quantize (K128 groups + H128 rotation) feeding
+    ops::linear with a quantized input (group_int8 projection), and
+    ops::normalized_linear (LayerNorm + residual -> INT8 GEMV), also with the
+    next layer's quantized output, through the C++ interface written as the
+    reference's layers/linear.cpp calls it, against the oracle."""
     rng = np.random.default_rng(M)
     x = synthetic.activations(M, 2048, seed=M)
     lw = synthetic.f32_to_bf16_bits(1.0 + 0.05 * rng.standard_normal(2048))
     xs = synthetic.activations(M, 512, seed=M + 1)
     rs = synthetic.activations(M, 512, seed=M + 2)
     ws = synthetic.weights(384, 512, seed=M)
-    for name, a in (("x", x), ("lw", lw), ("xs", xs), ("rs", rs), ("ws", ws)):
+    w2 = synthetic.weights(256, 2048, seed=M + 3)
+    for name, a in (("x", x), ("lw", lw), ("xs", xs), ("rs", rs), ("ws", ws), ("w2", w2)):
         a.tofile(tmp_path / f"{name}.bf16")
     (tmp_path / "shape.txt").write_text(f"{M}\n")
     print(f"test_shim sequence M={M}", flush=True)
@@ -183,3 +190,11 @@ def test_sequence_end_to_end(dev, orc, tmp_path, M):
     y, nrm, _, _, _ = orc.norm_linear(xs, wq, sw, I8, residual=rs)
     assert np.array_equal(np.fromfile(tmp_path / "norm.bf16", np.uint16).reshape(M, 512), nrm)
     assert np.array_equal(np.fromfile(tmp_path / "y.bf16", np.uint16).reshape(M, 384), y)
+    nq, nqs = orc.quantize_rows(y, I8)
+    assert np.array_equal(np.fromfile(tmp_path / "next.u8", np.uint8).reshape(M, 384), nq)
+    assert np.array_equal(np.fromfile(tmp_path / "next.f32", np.float32), nqs)
+    from breeze_tts_cpp_amd import qlinear
+    w2q, sw2 = orc.quantize_rows(w2, I8, group=128, rotation=128)
+    p = qlinear.plan(M, 256, 2048, I8, 128, 128)
+    ref2, _ = orc.gemm_grouped(q, s, w2q, sw2, I8, 128, 128, *qlinear.grouped_partition(p, 2048))
+    assert np.array_equal(np.fromfile(tmp_path / "y2.bf16", np.uint16).reshape(M, 256), ref2)

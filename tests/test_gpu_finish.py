@@ -27,13 +27,12 @@ def run_finish(dev, xq, sx, wq, sw, fmt, bias, act, path=None, out_dtype=torch.b
 
 def paths():
     from breeze_tts_cpp_amd.qlinear import Path, KIND_SKINNY, KIND_TILED
-    return [("skinny", None, 32), ("split", Path(KIND_SKINNY, 32, 16, 2, 2), 32),
+    return [("skinny", None, 32), ("split", Path(KIND_SKINNY, 32, 16, 2, 8), 32),
             ("tiled256x128", Path(KIND_TILED, 128, 256, 1, 1), 512),
             ("wide256x256", Path(KIND_TILED, 256, 256, 1, 4), 512),
             ("tiled8wave", Path(KIND_TILED, 256, 256, 1, 8), 512),
             ("tiled128x8wave", Path(KIND_TILED, 128, 128, 1, 8), 512),
-            ("tiled256x128x8wave", Path(KIND_TILED, 128, 256, 1, 8), 512),
-            ("persistent", Path(KIND_TILED, 256, 256, 1, 8, 1), 1024)]
+            ("tiled256x128x8wave", Path(KIND_TILED, 128, 256, 1, 8), 512)]
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])

@@ -42,8 +42,8 @@ def test_small_groups(dev, orc, fmt, ig, wg, M, N, K):
     torch.cuda.synchronize()
     got = bits(y)
     if fmt == I8:
-        span = -(-K // 256) * 256 // p.waves
-        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, 1, p.waves, span)
+        splits, waves, span = qlinear.grouped_partition(p, K)
+        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, splits, waves, span)
         assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
     else:
         ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, ig, wg)
@@ -58,7 +58,7 @@ def test_small_groups_unsupported_forms(dev, orc):
     xq, sx = orc.quantize_rows(synthetic.activations(M, K, seed=1), I8, group=32)
     wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=1), I8, group=32)
     args = [torch.from_numpy(a).to(dev) for a in (xq, sx, wq, sw)]
-    for path in (qlinear.Path(1, 16, 16, 2, 2, 0), qlinear.Path(2, 128, 128, 1, 8, 0)):
+    for path in (qlinear.Path(1, 16, 16, 2, 8, 0), qlinear.Path(2, 128, 128, 1, 8, 0)):
         with pytest.raises(qlinear.QLinearError):
             qlinear.gemm(*args, I8, input_group=32, weight_group=32, path=path,
                          workspace=torch.empty(1 << 20, dtype=torch.uint8, device=dev))
@@ -70,9 +70,11 @@ def test_small_groups_unsupported_forms(dev, orc):
 def test_staged_ragged_k(dev, orc, fmt, group, M, K):
     """Staged (LDS slab) decode paths with K not a multiple of 256: the last
     wave's range ends inside a 256-K block, so some of its activation pieces
-    lie past K. The slab wait counts the activation loads issued behind the
-    slab DMA; every one must be issued for the wait to cover the whole slab
-    (weight rows 14-15 of each tile came from the last DMA instruction)."""
+    lie past K. Regression test for a slab wait that counted the activation
+    loads issued behind the slab DMA: a wave that skipped out-of-range loads
+    came up short and read weight rows 14-15 of each tile before the last DMA
+    instruction landed. The kernel now waits for every load before it reads
+    the slab."""
     from breeze_tts_cpp_amd import qlinear
     N = 48
     print(f"staged ragged fmt={fmt} group={group} M={M} K={K}", flush=True)
@@ -85,8 +87,8 @@ def test_staged_ragged_k(dev, orc, fmt, group, M, K):
     torch.cuda.synchronize()
     got = bits(y)
     if fmt == I8 and group:
-        span = -(-K // 256) * 256 // p.waves
-        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, group, group, 1, p.waves, span)
+        splits, waves, span = qlinear.grouped_partition(p, K)
+        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, group, group, splits, waves, span)
         assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches, {p}"
     elif fmt == I8:
         ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw)

@@ -29,7 +29,7 @@ def test_core_path_in_a_graph(dev):
     wq8, sw8 = qlinear.row_quantize(bf(N, K, sc=0.05), FP8, group=128, rotation=128)
     packed = qlinear.pack_weights(wq)
     torch.cuda.synchronize()
-    split = Path(KIND_SKINNY, 32, 16, 2, 4)
+    split = Path(KIND_SKINNY, 32, 16, 2, 8)
     ws = torch.empty(qlinear.workspace_bytes(split, M, N, K, I8), dtype=torch.uint8, device=dev)
     outs = {k: torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             for k in ("planned", "split", "packed", "grouped")}

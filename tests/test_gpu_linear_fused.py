@@ -73,7 +73,7 @@ def test_fused_linear_planned(dev, orc, fmt, M, N, K):
 
 @pytest.mark.parametrize("tokens,channels,K", [(16, 16, 2048), (16, 32, 2048), (16, 48, 2048),
                                                (16, 32, 4096), (16, 16, 6144), (32, 16, 2048),
-                                               (32, 32, 2048), (32, 48, 2048), (48, 16, 2048)])
+                                               (32, 32, 2048), (32, 48, 2048), (64, 16, 2048)])
 def test_fused_linear_tiles(dev, orc, tokens, channels, K):
     """Every fused channel tile and K range, partial token and channel tiles;
     wider token tiles and K != 2048 take the two-launch form."""

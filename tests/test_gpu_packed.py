@@ -83,7 +83,7 @@ def test_packed_prefill(dev, orc, fmt, N, K):
                                      np.random.default_rng(N).choice(M, 28, replace=False)]))
     shapes = [(256, 256, 4), (256, 128, 2), (256, 128, 1), (256, 128, 8), (128, 128, 1), (128, 128, 8)]
     if fmt == I8:
-        shapes += [(256, 256, 8), (256, 256, 8, 1)]
+        shapes += [(256, 256, 8)]
     for channels, tokens, waves, *staged in shapes:
         p = Path(KIND_TILED, tokens, channels, 1, waves, *staged)
         print(f"packed prefill fmt={fmt} N={N} K={K} path={p}", flush=True)
@@ -117,6 +117,6 @@ def test_packed_rejects_split_and_staged(dev, orc):
     from breeze_tts_cpp_amd.qlinear import Path, KIND_SKINNY
     xq, sx, wq, sw = operands(orc, 32, 256, 2048, I8, seed=1)
     pw = qlinear.pack_weights(dev_u8(wq, dev))
-    for p in (Path(KIND_SKINNY, 32, 16, 2, 4), Path(KIND_SKINNY, 32, 16, 1, 8, 1)):
+    for p in (Path(KIND_SKINNY, 32, 16, 2, 8), Path(KIND_SKINNY, 32, 16, 1, 8, 1)):
         with pytest.raises(qlinear.QLinearError):
             qlinear.gemm(dev_u8(xq, dev), dev_f32(sx, dev), pw, dev_f32(sw, dev), I8, path=p)
