@@ -63,7 +63,7 @@ EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
            "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish", "qlin_norm_linear",
            "qlin_norm_fusion_init", "qlin_epilogue_init", "qlin_layer_norm_quantize",
-           "qlin_pointwise_quantize")
+           "qlin_pointwise_quantize", "qlin_linear_noalloc", "qlin_noalloc_scratch_bytes")
 
 
 def load():
@@ -88,6 +88,11 @@ def load():
     L.qlin_gemm.restype = i
     L.qlin_gemm.argtypes = [ctypes.POINTER(qlin_path), P, P, P, P, P, i, i, i, i, i, i, i, P, sz, P]
     L.qlin_linear.restype = i
+    L.qlin_linear_noalloc.restype = i
+    L.qlin_linear_noalloc.argtypes = [ctypes.POINTER(qlin_path), P, i, i, P, P, P, i, i, i, i, i,
+                                      i, i, i, P]
+    L.qlin_noalloc_scratch_bytes.restype = sz
+    L.qlin_noalloc_scratch_bytes.argtypes = []
     L.qlin_linear.argtypes = [ctypes.POINTER(qlin_path), P, i, i, P, P, P, P, P, i, i, i, i, i,
                               i, i, i, P, sz, P]
     L.qlin_quantized_norm.restype = i
@@ -466,3 +471,22 @@ def linear(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int, group:
                               group, group, rotation, ws_ptr, ws_bytes, _stream(stream)))
     return out
 
+
+def linear_noalloc(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int, group: int = 0,
+                   rotation: int = 0, out_dtype=torch.bfloat16, path: Path | None = None,
+                   out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """qlin_linear_noalloc: the same quantize + GEMM as `linear`, with the
+    scratch activation and split-K partials in the library's fixed device
+    array (nothing is allocated by the call itself)."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.dtype not in _TYPES:
+        raise ValueError("linear_noalloc expects a 2-D bf16/f16 tensor with unit column stride")
+    rows, K = x.shape
+    N = wq.shape[0]
+    if out is None:
+        out = torch.empty((rows, N), dtype=out_dtype, device=x.device)
+    p = (path or Path()).to_c()
+    _check(load().qlin_linear_noalloc(ctypes.byref(p), x.data_ptr(), x.stride(0), _TYPES[x.dtype],
+                                      wq.data_ptr(), sw.data_ptr(), out.data_ptr(), rows, N, K,
+                                      fmt, _TYPES[out.dtype], group, group, rotation,
+                                      _stream(stream)))
+    return out

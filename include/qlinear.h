@@ -28,6 +28,10 @@
  *                       <- no launcher of the reference: the packed weight layout that
  *                          follows its load-time quantization (io/weights.cpp:80-87);
  *                          qlin_gemm / qlin_linear on that layout
+ *   qlin_linear_noalloc, qlin_noalloc_scratch_bytes
+ *                       <- no counterpart in the reference: qlin_linear with its
+ *                          scratch in a fixed library-owned device array, for callers
+ *                          that cannot allocate
  *
  * Operand layouts (reference core/quantization.h:24-49):
  *   x  int8/e4m3 [rows, K] dense          sx f32 [rows] or [ceil(K/ig), rows]
@@ -312,6 +316,24 @@ int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
                             const qlin_epilogue *epilogue, void *retained, int rows, int cols,
                             void *values, float *scales, int fmt, int group, int rotation,
                             qlin_stream_t stream);
+
+/* Allocation-free quantized linear. No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments and results
+ * as qlin_linear (bit for bit), minus the scratch arguments: the activation
+ * codes, scales and split-K partials live in a fixed device array of
+ * QLIN_NOALLOC_SCRATCH_BYTES per GPU, held by the library until the process
+ * ends. Needs rows*K + 4*rows*ceil(K/input_group or K) + partials (each
+ * rounded up to 256 bytes) within that size, else QLIN_ERR_WORKSPACE. Calls no
+ * hipMalloc/hipFree; its first call on a device looks up the array's device
+ * address once. All calls on one device share the array: calls that overlap
+ * in time on one device (two streams or threads) race. */
+#define QLIN_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+size_t qlin_noalloc_scratch_bytes(void);
+int qlin_linear_noalloc(const qlin_path *path, const void *x, int ld, int src_type,
+                        const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,
+                        int out_type, int input_group, int weight_group, int rotation,
+                        qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -260,3 +260,12 @@ def test_sequence_producer_validation():
     assert nl(fusion=gather) == -1
     assert nl(y=X + 2) == -1              # output overlaps the input
 
+
+def test_noalloc_scratch_limit():
+    """qlin_linear_noalloc rejects a shape whose scratch exceeds its fixed
+    array before touching the device."""
+    L = qlinear.load()
+    assert L.qlin_noalloc_scratch_bytes() == 32 << 20
+    rc = L.qlin_linear_noalloc(None, FAKE, 16384, BF16, FAKE, FAKE, FAKE, 4096, 16, 16384, I8,
+                               BF16, 0, 0, 0, None)
+    assert rc == -3 and b"fixed" in L.qlin_last_error()
