@@ -115,11 +115,13 @@ def main():
                         "path": qlinear.plan(M_DECODE, N, K, I8)}
     for name in inputs:
         p = inputs[name]["path"]
-        assert qlinear.workspace_bytes(p, M_DECODE, *synthetic.PROJECTIONS[name], I8) == 0
+        need = qlinear.workspace_bytes(p, M_DECODE, *synthetic.PROJECTIONS[name], I8)
+        inputs[name]["ws"] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
 
     def linear(io, wt):
         qlinear.linear(io["x"], wt["wq"], wt["sw"], I8, path=io["path"],
-                       scratch=(io["xq"], io["sx"]), out=io["y"], stream=stream)
+                       scratch=(io["xq"], io["sx"]), out=io["y"], workspace=io["ws"],
+                       stream=stream)
 
     def step():
         for entry in layers:
@@ -162,41 +164,24 @@ def main():
                               for _, (N, K) in projections)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # ---- per projection: graph of the 16 layers' launches of one projection
-    # (distinct weights), timed with events on the launch stream: the GEMM on
-    # the quantized activations (the dominant kernel), and the whole linear.
-    def time_graph(launch):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            launch()
-        torch.cuda.synchronize()
-        for _ in range(3):
-            g.replay()
-        torch.cuda.synchronize()
-        reps = max(5, args.steps // 2)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            for _ in range(reps):
-                g.replay()
-            end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) * 1e3 / (reps * LAYERS)
-
+    # ---- per projection, per format and token count: graphs that rotate
+    # through >= 640 MB of distinct weights (so HBM, not the 256 MB Infinity
+    # Cache, serves them), timed with events on the launch stream: the GEMM on
+    # the quantized activations (the dominant kernel) and the whole linear.
     per_proj = {}
-    for name, (N, K) in projections:
-        io = inputs[name]
-        us = time_graph(lambda: [qlinear.gemm(io["xq"], io["sx"], entry[name]["wq"],
-                                              entry[name]["sw"], I8, path=io["path"],
-                                              out=io["y"], stream=stream)
-                                 for entry in layers])
-        us_linear = time_graph(lambda: [linear(io, entry[name]) for entry in layers])
-        b = gemm_bytes(M_DECODE, N, K)
-        p = io["path"]
-        per_proj[name] = {"N": N, "K": K, "us_per_launch": round(us, 3), "bytes": b,
-                          "GBps": round(b / (us * 1e-6) / 1e9, 1),
-                          "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                          "path": [p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged],
-                          "linear_us": round(us_linear, 3)}
+    sweep = {}
+    for mode, fmt, group, tokens in (("int8", I8, 0, M_DECODE), ("int8", I8, 0, 1),
+                                     ("int8", I8, 0, 8), ("int8", I8, 0, 64),
+                                     ("fp8", FP8, 0, M_DECODE),
+                                     ("group_int8", I8, 128, M_DECODE),
+                                     ("group_fp8", FP8, 128, M_DECODE)):
+        rows = decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, tokens,
+                            max(5, args.steps // 5))
+        if mode == "int8" and tokens == M_DECODE:
+            per_proj = rows
+        sweep[f"{mode} M={tokens}"] = {
+            n: {"gemm_us": r["us_per_launch"], "linear_us": r["linear_us"], "GBps": r["GBps"],
+                "frac_hbm": r["frac_hbm"], "path": r["path"]} for n, r in rows.items()}
     # the dominant kernel: the projection that moves the most bytes (gate_up)
     dominant = max(per_proj, key=lambda n: per_proj[n]["bytes"])
     d = per_proj[dominant]
@@ -227,17 +212,82 @@ def main():
                    "tokens": M_DECODE, "layers": LAYERS, "format": "int8",
                    "step_bytes": step_bytes},
         "decode_projections": per_proj,
+        "decode_sweep": sweep,
         "roofline": roofline,
     }
 
     if not args.no_prefill:
         result["prefill"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args)
+        result["prefill_m1024"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args,
+                                                M=1024)
         result["producers"] = bench_producers(torch, qlinear, synthetic, dev, stream, args)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args, value)
 
     print(json.dumps(result), flush=True)
+
+
+def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
+    """Per projection at M tokens: the GEMM alone and the linear (quantize +
+    GEMM, qlin_linear) over distinct weight copies totalling >= 640 MB, each
+    graph replayed `reps` times; microseconds per launch."""
+    rot = 128 if group else 0
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def time_graph(launch, per):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            launch()
+        torch.cuda.synchronize()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(reps):
+                g.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / (reps * per)
+
+    rows = {}
+    for name, (N, K) in synthetic.PROJECTIONS.items():
+        w = torch.from_numpy(synthetic.weights(N, K, seed=1000).view(np.int16)).view(
+            torch.bfloat16).to(dev)
+        x = torch.from_numpy(synthetic.activations(M, K, seed=0).view(np.int16)).view(
+            torch.bfloat16).to(dev)
+        with torch.cuda.stream(stream):
+            wq, sw = qlinear.row_quantize(w, fmt, group=group, rotation=rot, stream=stream)
+            xq, sx = qlinear.row_quantize(x, fmt, group=group, rotation=rot, stream=stream)
+        torch.cuda.synchronize()
+        del w
+        # distinct copies: the codes with one byte pattern flipped per copy
+        # (same sizes and scale layout; the data only has to be distinct)
+        copies = max(16, -(-(640 << 20) // (N * K)))
+        ws = [wq] + [torch.bitwise_xor(wq, (c * 37) & 0x7f) for c in range(1, copies)]
+        path = qlinear.plan(M, N, K, fmt, group, group)
+        need = qlinear.workspace_bytes(path, M, N, K, fmt, group, group)
+        wsp = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        xs, ss = torch.empty_like(xq), torch.empty_like(sx)
+        us = time_graph(lambda: [qlinear.gemm(xq, sx, wc, sw, fmt, input_group=group,
+                                              weight_group=group, path=path, out=y,
+                                              workspace=wsp, stream=stream) for wc in ws],
+                        len(ws))
+        us_linear = time_graph(lambda: [qlinear.linear(x, wc, sw, fmt, group, rot, path=path,
+                                                       scratch=(xs, ss), out=y, workspace=wsp,
+                                                       stream=stream) for wc in ws], len(ws))
+        b = gemm_bytes(M, N, K, group)
+        rows[name] = {"N": N, "K": K, "us_per_launch": round(us, 3), "bytes": b,
+                      "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                      "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                      "path": [path.kind, path.tokens, path.channels, path.splits, path.waves,
+                               path.staged],
+                      "linear_us": round(us_linear, 3), "weight_copies": copies}
+        del ws
+        torch.cuda.empty_cache()
+    return rows
 
 
 def measured_traffic(name):
@@ -253,7 +303,9 @@ def measured_traffic(name):
     found = None
     for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 3 and cells[0] == name:
+        # rows are labelled by projection, optionally followed by a note in
+        # parentheses ("qkv (one launch)"); the last matching row wins
+        if len(cells) >= 3 and cells[0].split(" (")[0] == name:
             try:
                 found = int(cells[-1].replace(",", ""))
             except ValueError:
@@ -292,7 +344,7 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
             torch.cuda.synchronize()
 
 
-def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
+def bench_prefill(torch, qlinear, synthetic, dev, stream, args, M=M_PREFILL):
     """M=4096 INT8, FP8, group_int8 and group_fp8 GEMMs over the four
     projections: TOPS = 2*M*N*K / kernel time. Per format, the four projections'
     graphs (10 GEMMs each) are built, warmed up together for about 30 replays
@@ -300,7 +352,6 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args):
     5 interleaved rounds of 3 replays; each projection reports its median."""
     import statistics
     out = {}
-    M = M_PREFILL
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps, rounds, per_round = 10, 5, 3
     modes = (("int8", qlinear.I8, 0), ("fp8", qlinear.FP8, 0), ("group_int8", qlinear.I8, 128),
@@ -449,7 +500,7 @@ def cpu_baseline(args, gpu_value):
     from breeze_tts_cpp_amd import synthetic
     from oracle import oracle
 
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads = args.cpu_threads or (os.cpu_count() or 1)
     jobs = []
     total_bytes = 0
     for name, (N, K) in synthetic.PROJECTIONS.items():

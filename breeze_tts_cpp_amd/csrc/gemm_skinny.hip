@@ -106,7 +106,7 @@ __device__ __forceinline__ void store_out(void *y, size_t index, float (&v)[4],
 // loads all NB blocks of its K range straight into registers up front, one
 // contiguous 1 KB piece per (16-row fragment, 64-K step).
 template <int Fmt, int MT, int NF, int WK, bool Grouped, bool Split, int NB = 0,
-          bool Packed = false, int FQ = 0, int GS = 128>
+          bool Packed = false, int FQ = 0, int GS = 128, bool XL = false>
 __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, void *__restrict__ partial, int M, int N,
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     static_assert(!FQ || (NB > 0 && !Packed && !Grouped && !Split && MT == 1 && NB == 1 && Fmt == I8),
                   "fused quantization: per-wave slab, activation blocks in registers");
     uint4 xraw[FQ ? NB : 1][MT][4][2];
-    if constexpr (FQ) {
+    if constexpr (FQ && !XL) {
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
@@ -195,15 +195,54 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             }
     }
 
+    // Dynamic LDS: the waves' weight slabs, then (XL) their activation
+    // tiles, then (FQ) the row absmax / scale exchange.
     extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
     constexpr int SNB = Packed ? 0 : NB;                        // staged slab blocks
     constexpr int kSlabBytes = 16 * NF * SNB * kBlockK;         // per wave
     constexpr int kRowBytes = SNB * kBlockK;
     constexpr int kRowGranules = kRowBytes / 16;
+    // XL: the wave's activation rows (16*MT tokens x its K range; 16-bit
+    // source rows for FQ) are staged through LDS like the weights.
+    static_assert(!XL || (SNB > 0 && !Split), "activation staging needs the weight slab");
+    constexpr int kXElem = FQ ? 2 : 1;
+    constexpr int kActRowBytes = kRowBytes * kXElem;
+    constexpr int kActBytes = XL ? 16 * MT * kActRowBytes : 0;  // per wave
     uint8_t *slab = wlds + wave * kSlabBytes;
+    uint8_t *xtile = wlds + WK * kSlabBytes + wave * kActBytes;
+    float *fq_amax = reinterpret_cast<float *>(wlds + WK * (kSlabBytes + kActBytes));
+    float *fq_scale = fq_amax + WK * MT * 16;
     const int slab_k0 = k_begin;
     if constexpr (SNB > 0) {
         typedef __attribute__((address_space(3))) void *lds_ptr_t;
+        if constexpr (XL) {
+            // Activation rows first (L2-resident, they land before the
+            // weights): each instruction moves 1 KB of consecutive (row,
+            // granule) positions, granule g of row r at slot g ^ (r & 15), as
+            // the weight slab. Bytes past the range read as zero (offset out
+            // of the buffer).
+            const int xrows = max(0, min(16 * MT, M - m0));
+            const uint8_t *xbase = FQ ? reinterpret_cast<const uint8_t *>(fq.src + size_t(m0) * fq.ld)
+                                      : x + size_t(m0) * K;
+            const uint32_t xstride = FQ ? uint32_t(fq.ld) * 2u : uint32_t(K);
+            const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t *>(xbase), 0, xrows * xstride, 0x00020000);
+            constexpr int kActGranules = kActRowBytes / 16;
+#pragma unroll
+            for (int i = 0; i < kActBytes / 1024; ++i) {
+                const int q = i * 64 + lane;
+                const int r = q / kActGranules, slot = q % kActGranules;
+                const int g = slot ^ (r & 15);
+                const int kb = k_begin * kXElem + g * 16;  // byte column
+                const uint32_t off = kb < k_end * kXElem ? uint32_t(r) * xstride + uint32_t(kb)
+                                                         : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(xtile + i * 1024), 16,
+                                                         off, 0, 0, 0);
+            }
+            // Keep the weight DMA behind it (FQ counts the slab's loads).
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const int rows_valid = max(0, min(16 * NF, N - n0));
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(w + size_t(n0) * K), 0, rows_valid * K, 0x00020000);
@@ -231,8 +270,13 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     constexpr int kSlotVals = MT * NF * 64 * 4;
     constexpr int kSlotStride = SNB > 0 ? kSlabBytes / int(sizeof(Red)) : kSlotVals;
     static_assert(SNB == 0 || kSlotVals * int(sizeof(Red)) <= kSlabBytes, "slot fits the slab");
-    __shared__ Red4 red_static[SNB > 0 || WK == 1 ? 1 : WK * kSlotVals / 4];
-    Red *red = SNB > 0 ? reinterpret_cast<Red *>(wlds) : reinterpret_cast<Red *>(red_static);
+    Red *red;
+    if constexpr (SNB > 0) {
+        red = reinterpret_cast<Red *>(wlds);
+    } else {
+        __shared__ Red4 red_static[WK == 1 ? 1 : WK * kSlotVals / 4];
+        red = reinterpret_cast<Red *>(red_static);
+    }
 
     // Grouped: fp32 running sums; per-channel: the raw accumulator.
     Acc acc[MT][NF];
@@ -262,9 +306,18 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // block waits for its own L2 round trip inside the loop.
     constexpr bool kPreX = NB > 0 && NB * MT <= 6 && !Packed;
     i32x4 wpre[1][NF][4];  // unused unless packed
-    i32x4 xpre[kPreX ? NB : 1][MT][4];
-    __shared__ float fq_amax[FQ ? WK : 1][FQ ? MT * 16 : 1];
-    __shared__ float fq_scale[FQ ? MT * 16 : 1];
+    i32x4 xpre[kPreX && (FQ || !XL) ? NB : 1][MT][4];
+    // XL: the activation fragments of block kb from the staged tile.
+    auto xfrag = [&](int kb, i32x4 (&b)[MT][4]) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int g = ((kb - slab_k0) + p * 64) / 16 + quad;
+                b[t][p] = *reinterpret_cast<const i32x4 *>(xtile + (t * 16 + row16) * kActRowBytes +
+                                                           ((g ^ row16) << 4));
+            }
+    };
     if constexpr (FQ) {
         // The per-token quantizer's arithmetic (row_quantize.hip
         // token_quantize; reference row_quantize.cu:24-87): row absmax over
@@ -272,8 +325,31 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         // through LDS), scale = quant_scale(amax), codes = encode(v * (1 /
         // scale)). Max is order-free, so the codes and scales are the
         // quantizer's bit for bit.
-        constexpr int ns = kSlabBytes / 1024;  // slab DMA loads, issued last
+        // Wait until at most the slab DMA's instructions are outstanding, so
+        // the activation rows are in while the slab is still in flight.
+        // Without XL this is a scheduling hint only (the compiler may order
+        // the loads differently; correctness rests on its own waits before
+        // xraw is used and on the vmcnt(0) before the slab is read). With XL
+        // it is the wait for the activation DMA, which was issued, in
+        // program order and unconditionally, before the slab's ns
+        // instructions, with no vector memory access after them.
+        constexpr int ns = kSlabBytes / 1024;
         __builtin_amdgcn_s_waitcnt((ns & 15) | ((ns >> 4) << 14) | (7 << 4) | (15 << 8));
+        if constexpr (XL) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int g = blk * 32 + p * 8 + quad * 2 + h;
+                            xraw[blk][t][p][h] = *reinterpret_cast<const uint4 *>(
+                                xtile + (t * 16 + row16) * kActRowBytes + ((g ^ row16) << 4));
+                        }
+        }
         // FQ 1: bf16 source, 2: f16 source.
         using Tin = std::conditional_t<FQ == 2, f16_t, bf16_t>;
         auto widen = [](uint32_t h) { return to_float(uint16_t(h), Tin{}); };
@@ -319,16 +395,16 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             }
             amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 16, 64));
             amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 32, 64));
-            if (quad == 0) fq_amax[wave][t * 16 + row16] = amax[t];
+            if (quad == 0) fq_amax[wave * MT * 16 + t * 16 + row16] = amax[t];
         }
         // A workgroup barrier that waits for LDS only: __syncthreads' fence
         // would also wait for the weight slab DMA still in flight.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            float a = fq_amax[0][t * 16 + row16];
+            float a = fq_amax[t * 16 + row16];
 #pragma unroll
-            for (int q = 1; q < WK; ++q) a = fmaxf(a, fq_amax[q][t * 16 + row16]);
+            for (int q = 1; q < WK; ++q) a = fmaxf(a, fq_amax[q * MT * 16 + t * 16 + row16]);
             const float step = quant_scale<Fmt>(a);
             const float inverse = 1.f / step;
             if (wave == 0 && quad == 0) fq_scale[t * 16 + row16] = step;
@@ -367,8 +443,10 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         }
         __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));  // slab in LDS
     } else if constexpr (kPreX) {
+        if constexpr (!XL) {
 #pragma unroll
-        for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
+            for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
+        }
         if constexpr (!Packed) {
             // The slab is in LDS once no load is outstanding. (A count of the
             // newer activation loads would not do: the compiler may order
@@ -532,7 +610,14 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) {
             const int kb = k_begin + blk * kBlockK;
-            if (kb < k_end) block(kb, xpre[blk], wpre[0]);
+            if (kb >= k_end) continue;
+            if constexpr (XL && !FQ) {
+                i32x4 b[MT][4];
+                xfrag(kb, b);
+                block(kb, b, wpre[0]);
+            } else {
+                block(kb, xpre[blk], wpre[0]);
+            }
         }
         if constexpr (FQ) {
             // Column tile 0 fills the scratch activation, after its MFMAs so
@@ -557,13 +642,14 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     } else {
         for (int kb = k_begin; kb < k_end; kb += kBlockK) {
             i32x4 b[MT][4];
-            load_x(kb, b);
+            if constexpr (!XL) load_x(kb, b);
             if constexpr (NB > 0) {
                 // The slab is in LDS once no load is outstanding.
                 if (kb == k_begin) {
                     __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));
                 }
             }
+            if constexpr (XL) xfrag(kb, b);
             block(kb, b, wpre[0]);
         }
     }
@@ -696,10 +782,14 @@ int span_of(int K, int splits) {
         a.bias, a.act, int(a.out_type == F16), a.fq
 
 template <int Fmt, int MT, int NF, bool Grouped, int NB, int GS = 128>
-int launch_slab(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
-    const size_t lds = size_t(kWaves) * 16 * NF * NB * kBlockK;
-    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, false, 0, GS>), grid,
-                       dim3(64 * kWaves), lds, stream, QLIN_SKINNY_ARGS);
+int launch_slab(const GemmArgs &a, dim3 grid, int span, int staged, hipStream_t stream) {
+    const size_t lds = size_t(kWaves) * 16 * (NF + (staged == 2 ? MT : 0)) * NB * kBlockK;
+    if (staged == 2)
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, false, 0, GS, true>),
+                           grid, dim3(64 * kWaves), lds, stream, QLIN_SKINNY_ARGS);
+    else
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, false, 0, GS>),
+                           grid, dim3(64 * kWaves), lds, stream, QLIN_SKINNY_ARGS);
     return 0;
 }
 
@@ -743,11 +833,11 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
     if (p.splits == 1) {
         // LDS-staged weight slabs: one-shot streaming of whole weight rows;
         // slab LDS per workgroup = 8 * 16*NF * span bytes.
-        if (p.staged == 1) {
+        if (p.staged == 1 || p.staged == 2) {
             switch (span / kBlockK) {
-            case 1: return launch_slab<Fmt, MT, NF, Grouped, 1, GS>(a, grid, span, stream);
-            case 2: return launch_slab<Fmt, MT, NF, Grouped, 2, GS>(a, grid, span, stream);
-            case 3: return launch_slab<Fmt, MT, NF, Grouped, 3, GS>(a, grid, span, stream);
+            case 1: return launch_slab<Fmt, MT, NF, Grouped, 1, GS>(a, grid, span, p.staged, stream);
+            case 2: return launch_slab<Fmt, MT, NF, Grouped, 2, GS>(a, grid, span, p.staged, stream);
+            case 3: return launch_slab<Fmt, MT, NF, Grouped, 3, GS>(a, grid, span, p.staged, stream);
             default: return -4;
             }
         }
@@ -784,7 +874,7 @@ int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 
 // Fused activation quantization (FQ): eight waves, per-wave slabs of NB
 // blocks, per-channel scales, no split.
-template <int Fmt, int MT, int NF, int NB>
+template <int Fmt, int MT, int NF, int NB, bool XL>
 int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     // Every workgroup quantizes its token rows again (the activation is
     // re-encoded once per column tile), which pays only while that ALU work
@@ -797,14 +887,16 @@ int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     if constexpr (MT == 1 && NB == 1 && Fmt == I8) {
         const int span = NB * kBlockK;
         dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
-        const size_t lds = size_t(kWaves) * 16 * NF * NB * kBlockK;
+        // slabs, (XL) 16-bit activation tiles, the absmax / scale exchange
+        const size_t lds = size_t(kWaves) * 16 * (NF + (XL ? 2 * MT : 0)) * NB * kBlockK +
+                           size_t(kWaves + 1) * MT * 16 * 4;
         if (a.fq.f16)
-            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 2>),
+            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 2, 128, XL>),
                                grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
                                a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
                                int(a.out_type == F16), a.fq);
         else
-            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 1>),
+            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 1, 128, XL>),
                                grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
                                a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
                                int(a.out_type == F16), a.fq);
@@ -815,10 +907,18 @@ int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
 template <int Fmt>
 int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if (p.tokens != 16 || a.K != kWaves * kBlockK) return -4;
+    if (p.staged == 2) {
+        switch (p.channels) {
+        case 16: return launch_fused_nb<Fmt, 1, 1, 1, true>(a, s);
+        case 32: return launch_fused_nb<Fmt, 1, 2, 1, true>(a, s);
+        case 48: return launch_fused_nb<Fmt, 1, 3, 1, true>(a, s);
+        default: return -4;
+        }
+    }
     switch (p.channels) {
-    case 16: return launch_fused_nb<Fmt, 1, 1, 1>(a, s);
-    case 32: return launch_fused_nb<Fmt, 1, 2, 1>(a, s);
-    case 48: return launch_fused_nb<Fmt, 1, 3, 1>(a, s);
+    case 16: return launch_fused_nb<Fmt, 1, 1, 1, false>(a, s);
+    case 32: return launch_fused_nb<Fmt, 1, 2, 1, false>(a, s);
+    case 48: return launch_fused_nb<Fmt, 1, 3, 1, false>(a, s);
     default: return -4;
     }
 }
@@ -854,9 +954,14 @@ size_t skinny_lds_bytes(const GemmArgs &a, const GemmPath &p) {
     const int mt = p.tokens / 16, nf = p.channels / 16;
     const int nb = span_of(a.K, p.splits < 1 ? 1 : p.splits) / kBlockK;
     const size_t slab = p.staged ? size_t(kWaves) * 16 * nf * nb * kBlockK : 0;
+    // staged 2: the activation tiles too (16-bit source rows when the GEMM
+    // quantizes its own input)
+    const size_t act = p.staged == 2 ? size_t(kWaves) * 16 * mt * nb * kBlockK * (a.fq.src ? 2 : 1) : 0;
     // Reduction slots reuse a staged slab; otherwise one static slot per wave.
-    const size_t red = p.staged ? 16 : size_t(kWaves) * mt * nf * 64 * 4 * 4;
-    return red + slab;
+    const size_t red = p.staged ? 0 : size_t(kWaves) * mt * nf * 64 * 4 * 4;
+    // the fused quantization's absmax / scale exchange
+    const size_t fq = a.fq.src ? size_t(kWaves + 1) * mt * 16 * 4 : 0;
+    return red + slab + act + fq;
 }
 
 int skinny_span(int K, int splits) { return span_of(K, splits); }
@@ -867,7 +972,7 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
 
 bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
     return a.fq.src && !a.packed && !a.bias && !a.act && !a.input_group && !a.weight_group &&
-           p.kind == KIND_SKINNY && p.splits == 1 && p.waves == kWaves && p.staged == 1 &&
+           p.kind == KIND_SKINNY && p.splits == 1 && p.waves == kWaves && (p.staged == 1 || p.staged == 2) &&
            a.fmt == I8 && a.K == kWaves * kBlockK && p.tokens == 16 &&
            (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
            skinny_lds_bytes(a, p) <= kLdsBytes;

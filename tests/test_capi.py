@@ -85,6 +85,12 @@ def test_gemm_validation():
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 4)) == -4          # no 4-wave 128x128 variant
     assert call(M=256, path=qlinear.Path(T, 128, 256, 1, 2), ig=128, wg=128) == -4  # K groups: no 32x32 tiles
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 2)) == -4
+    # grid limits are checked before any launch: token tiles on the skinny
+    # grid's z dimension (<= 65535), macro tiles on the tiled grid's x (< 2^31)
+    assert call(M=1 << 23, N=64, K=256, ig=32, wg=32) == -4
+    assert b"65535" in L.qlin_last_error()
+    assert call(M=1 << 30, N=1 << 30, K=16) == -4
+    assert b"macro tiles" in L.qlin_last_error()
 
 
 def test_prefill_plan_rules():

@@ -320,17 +320,21 @@ def test_tiled_grouped(dev, orc, fmt, M, N, K):
 @pytest.mark.parametrize("fmt", [I8, FP8])
 @pytest.mark.parametrize("grouped", [False, True])
 def test_staged_skinny_variants(dev, orc, fmt, grouped):
-    """Weight slabs staged through LDS: same results as the register path."""
+    """Weight slabs staged through LDS (staged 1), and activation tiles with
+    them (staged 2, where both fit in LDS): same results as the oracle, on
+    partial token tiles, ragged K and K ranges of 1-3 blocks."""
     from breeze_tts_cpp_amd.qlinear import Path, KIND_SKINNY
     g = 128 if grouped else 0
-    for M, N, K in ((32, 96, 2048), (5, 48, 4096), (64, 64, 6144), (17, 32, 2064)):
+    for M, N, K in ((32, 96, 2048), (5, 48, 4096), (64, 64, 6144), (17, 32, 2064), (40, 48, 4000)):
         rot = g if K % 128 == 0 else 0
         xq, sx, wq, sw = operands(orc, M, N, K, fmt, group=g, rotation=rot, seed=N + K)
-        blocks = -(-K // 256)
-        for channels in (16, 32, 48):
-            if -(-blocks // 8) > 3 or channels * -(-blocks // 8) * 8 * 256 > 160 * 1024:
+        nb = -(-(-(-K // 256)) // 8)
+        tokens = 64 if M > 32 else -(-M // 16) * 16
+        for channels, staged in ((16, 1), (32, 1), (48, 1), (16, 2), (32, 2), (48, 2)):
+            lds = 8 * 256 * nb * (channels + (tokens if staged == 2 else 0))
+            if nb > 3 or lds > 160 * 1024:
                 continue
-            p = Path(KIND_SKINNY, 64 if M > 32 else -(-M // 16) * 16, channels, 1, 8, 1)
+            p = Path(KIND_SKINNY, tokens, channels, 1, 8, staged)
             print(f"staged {p} M={M} N={N} K={K}", flush=True)
             y = gpu_gemm(dev, xq, sx, wq, sw, fmt, group=g, path=p)
             if grouped and fmt == I8:
