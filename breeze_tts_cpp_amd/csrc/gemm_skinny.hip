@@ -37,6 +37,21 @@ namespace {
 constexpr bool kFin = QLIN_FIN;
 constexpr int kBlockK = 256;  // K handled per main-loop iteration (4 pieces of 64)
 
+// f(std::integral_constant<int, I>{}) for I = B .. E-1, each I a constant
+// expression in f (for per-step s_waitcnt immediates).
+// s_waitcnt vmcnt(n) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int B, int E, class F> __device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 template <int Fmt> struct Mfma;
 template <> struct Mfma<I8> {
     using Acc = i32x4;
@@ -195,13 +210,35 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             }
     }
 
+    // Activation fragments of block kb: lane quad q holds K bytes [kb + 64p + 16q, +16).
+    auto load_x = [&](int kb, i32x4 (&b)[MT][4]) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int k = kb + p * 64;
+            const bool in = k + quad * 16 < k_end;
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                b[t][p] = (in && xvalid[t]) ? load16(xrow[t] + k) : i32x4{0, 0, 0, 0};
+        }
+    };
+    // With a staged slab of NB blocks, all of the wave's activation blocks are
+    // requested up front (when they fit in registers), ahead of the slab
+    // DMA, so no block waits for its own L2 round trip inside the loop.
+    constexpr bool kPreX = NB > 0 && NB * MT <= 6 && !Packed;
+    i32x4 wpre[1][NF][4];  // unused unless packed
+    i32x4 xpre[kPreX && (FQ || !XL) ? NB : 1][MT][4];
+    // Staged slabs are consumed chunk by chunk as they arrive (counted
+    // waits): the activation is then in LDS (XL), encoded from the 16-bit
+    // rows (FQ), or loaded into registers ahead of the slab (kPipeAct).
+    constexpr bool kPipeAct = NB > 0 && !Packed && !XL && !FQ && kPreX;
+    constexpr bool kPipe = NB > 0 && !Packed && (XL || FQ || kPipeAct);
+
     // Dynamic LDS: the waves' weight slabs, then (XL) their activation
     // tiles, then (FQ) the row absmax / scale exchange.
     extern __shared__ __attribute__((aligned(1024))) uint8_t wlds[];
     constexpr int SNB = Packed ? 0 : NB;                        // staged slab blocks
     constexpr int kSlabBytes = 16 * NF * SNB * kBlockK;         // per wave
     constexpr int kRowBytes = SNB * kBlockK;
-    constexpr int kRowGranules = kRowBytes / 16;
     // XL: the wave's activation rows (16*MT tokens x its K range; 16-bit
     // source rows for FQ) are staged through LDS like the weights.
     static_assert(!XL || (SNB > 0 && !Split), "activation staging needs the weight slab");
@@ -247,13 +284,27 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(w + size_t(n0) * K), 0, rows_valid * K, 0x00020000);
         const int k_stop = k_end;
+        // Chunk-major slab: chunk c = blk * NF + f holds weight rows
+        // [16f, 16f + 16) x K bytes [256 blk, +256) of the wave's range, 4 KB
+        // in 4 instructions of 4 whole 256-byte row runs; granule g of chunk
+        // row r sits at slot g ^ r. The MFMAs consume the chunks in
+        // instruction order while later ones are still arriving.
+        if constexpr (kPipeAct) {
+            // The activation blocks in registers, requested before the slab
+            // so that the chunk waits below count only slab instructions.
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int i = 0; i < kSlabBytes / 1024; ++i) {
-            const int q = i * 64 + lane;
-            const int r = q / kRowGranules, slot = q % kRowGranules;
-            const int g = slot ^ (r & 15);
-            const int k = slab_k0 + g * 16;
-            const uint32_t off = k < k_stop ? uint32_t(r) * uint32_t(K) + uint32_t(k) : 0x80000000u;
+            const int c = i / 4, blk = c / NF, f = c % NF;
+            const int r = (i % 4) * 4 + lane / 16, slot = lane % 16;
+            const int g = slot ^ r;
+            const int k = slab_k0 + blk * kBlockK + g * 16;
+            const uint32_t off = k < k_stop ? uint32_t(f * 16 + r) * uint32_t(K) + uint32_t(k)
+                                            : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rsrc, (lds_ptr_t)(slab + i * 1024), 16, off,
                 0, 0, 0);
@@ -290,23 +341,6 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             for (int r = 0; r < 4; ++r) facc[t][f][r] = 0.f;
         }
 
-    // Activation fragments of block kb: lane quad q holds K bytes [kb + 64p + 16q, +16).
-    auto load_x = [&](int kb, i32x4 (&b)[MT][4]) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int k = kb + p * 64;
-            const bool in = k + quad * 16 < k_end;
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                b[t][p] = (in && xvalid[t]) ? load16(xrow[t] + k) : i32x4{0, 0, 0, 0};
-        }
-    };
-    // With a staged slab of NB blocks, all of the wave's activation blocks are
-    // requested right behind the slab DMA (when they fit in registers), so no
-    // block waits for its own L2 round trip inside the loop.
-    constexpr bool kPreX = NB > 0 && NB * MT <= 6 && !Packed;
-    i32x4 wpre[1][NF][4];  // unused unless packed
-    i32x4 xpre[kPreX && (FQ || !XL) ? NB : 1][MT][4];
     // XL: the activation fragments of block kb from the staged tile.
     auto xfrag = [&](int kb, i32x4 (&b)[MT][4]) {
 #pragma unroll
@@ -441,21 +475,11 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     xpre[blk][t][p] = in ? codes : i32x4{0, 0, 0, 0};
                 }
         }
-        __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));  // slab in LDS
-    } else if constexpr (kPreX) {
-        if constexpr (!XL) {
-#pragma unroll
-            for (int blk = 0; blk < NB; ++blk) load_x(k_begin + blk * kBlockK, xpre[blk]);
-        }
-        if constexpr (!Packed) {
-            // The slab is in LDS once no load is outstanding. (A count of the
-            // newer activation loads would not do: the compiler may order
-            // them before the DMA, or skip a wave's out-of-range pieces.)
-            __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8));
-        }
     }
 
-    auto block = [&](int kb, const i32x4 (&b)[MT][4], const i32x4 (&wp)[NF][4]) {
+    // MFMAs of block kb for fragment fsel (all fragments when fsel < 0;
+    // fsel is a constant at every call, so the guards fold away).
+    auto block = [&](int kb, const i32x4 (&b)[MT][4], const i32x4 (&wp)[NF][4], int fsel) {
         i32x4 a[NF][4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -464,12 +488,13 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             (void)in;
 #pragma unroll
             for (int f = 0; f < NF; ++f) {
+                if (fsel >= 0 && f != fsel) continue;
                 if constexpr (Packed) {
                     a[f][p] = wp[f][p];
                 } else if constexpr (NB > 0) {
-                    const int r = f * 16 + row16;
-                    const int g = ((kb - slab_k0) + p * 64) / 16 + quad;
-                    a[f][p] = *reinterpret_cast<const i32x4 *>(slab + r * kRowBytes +
+                    const int chunk = ((kb - slab_k0) / kBlockK) * NF + f;
+                    const int g = p * 4 + quad;
+                    a[f][p] = *reinterpret_cast<const i32x4 *>(slab + chunk * 4096 + row16 * 256 +
                                                                ((g ^ row16) << 4));
                 } else {
                     a[f][p] = (in && wvalid[f]) ? load16(wrow[f] + k) : i32x4{0, 0, 0, 0};
@@ -483,8 +508,9 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 for (int t = 0; t < MT; ++t)
 #pragma unroll
                     for (int f = 0; f < NF; ++f)
-                        M_::run(acc[t][f], a[f][2 * h], a[f][2 * h + 1], b[t][2 * h],
-                                b[t][2 * h + 1]);
+                        if (fsel < 0 || f == fsel)
+                            M_::run(acc[t][f], a[f][2 * h], a[f][2 * h + 1], b[t][2 * h],
+                                    b[t][2 * h + 1]);
         } else if constexpr (GS == 128) {
             // Two 128-K groups per block, each reduced natively then scaled.
 #pragma unroll
@@ -498,6 +524,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 for (int f = 0; f < NF; ++f)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (fsel >= 0 && f != fsel) continue;
                         int n = n0 + f * 16 + quad * 4 + r;
                         swg[f][r] = (weight_group && n < N) ? sw[size_t(g_w) * N + n] : 1.f;
                     }
@@ -507,6 +534,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     float sxg = (input_group && m < M) ? sx[size_t(g_in) * M + m] : 1.f;
 #pragma unroll
                     for (int f = 0; f < NF; ++f) {
+                        if (fsel >= 0 && f != fsel) continue;
                         Acc p = Acc{0, 0, 0, 0};
                         M_::run(p, a[f][2 * h], a[f][2 * h + 1], b[t][2 * h], b[t][2 * h + 1]);
 #pragma unroll
@@ -536,6 +564,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 for (int f = 0; f < NF; ++f)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (fsel >= 0 && f != fsel) continue;
                         int n = n0 + f * 16 + quad * 4 + r;
                         swg[f][r] = (weight_group && n < N) ? sw[size_t(g_w) * N + n] : 1.f;
                     }
@@ -545,6 +574,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     float sxg = (input_group && m < M) ? sx[size_t(g_in) * M + m] : 1.f;
 #pragma unroll
                     for (int f = 0; f < NF; ++f) {
+                        if (fsel >= 0 && f != fsel) continue;
                         const Acc p = part(t, f);
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
@@ -603,22 +633,34 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
             for (int blk = 0; blk < NB; ++blk) {
                 const int kb = kc + blk * kBlockK;
-                if (kb < k_end) block(kb, xc[blk], wc[blk]);
+                if (kb < k_end) block(kb, xc[blk], wc[blk], -1);
             }
         }
     } else if constexpr (kPreX) {
-#pragma unroll
-        for (int blk = 0; blk < NB; ++blk) {
+        // Chunk c = blk * NF + f of the slab is complete once at most the
+        // 4 * (NB * NF - c - 1) slab instructions after it are outstanding:
+        // every vector memory operation older than the slab (scales,
+        // activation DMA or loads) completes first, and any issued later
+        // (K-group scales) only makes the count stricter.
+        static_assert(kPipe, "staged register-resident activations are consumed per chunk");
+        // K-group kernels consume whole blocks (their group scales are
+        // loaded per block; per fragment they would be loaded NF times).
+        constexpr int kStep = Grouped ? NF : 1;
+        i32x4 xb[MT][4];
+        static_for<0, NB * NF / kStep>([&](auto c_) {
+            constexpr int c = decltype(c_)::value * kStep;
+            constexpr int blk = c / NF, f = Grouped ? -1 : c % NF;
+            wait_vmcnt<4 * (NB * NF - c - kStep)>();
             const int kb = k_begin + blk * kBlockK;
-            if (kb >= k_end) continue;
-            if constexpr (XL && !FQ) {
-                i32x4 b[MT][4];
-                xfrag(kb, b);
-                block(kb, b, wpre[0]);
-            } else {
-                block(kb, xpre[blk], wpre[0]);
+            if (kb < k_end) {
+                if constexpr (XL && !FQ) {
+                    if constexpr (f <= 0) xfrag(kb, xb);
+                    block(kb, xb, wpre[0], f);
+                } else {
+                    block(kb, xpre[blk], wpre[0], f);
+                }
             }
-        }
+        });
         if constexpr (FQ) {
             // Column tile 0 fills the scratch activation, after its MFMAs so
             // that the stores do not delay the slab wait.
@@ -650,7 +692,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 }
             }
             if constexpr (XL) xfrag(kb, b);
-            block(kb, b, wpre[0]);
+            block(kb, b, wpre[0], -1);
         }
     }
 
