@@ -140,10 +140,11 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    against 45.3 us with four 32x32x64 waves.
     //  (Variants timed interleaved after a warm-up, median of 5 rounds: the
     //  clock settles upward under sustained MFMA load.)
-    //  - K groups (no wide-kernel variant), eight waves: INT8 256x128 (128x32
-    //    waves) for >= 256 tiles in full rounds (gate_up at 4096 230 us
-    //    against 326 us with four 128x64 waves), else 128x128 (64x32 waves);
-    //    FP8 128x128 (gate_up at 4096 265 us against 276 us on 256x128).
+    //  - K groups (no wide-kernel variant), eight waves, both formats:
+    //    256x128 (128x32 waves) for >= 256 tiles in full rounds (gate_up at
+    //    4096: INT8 193 us against 222 us on 128x128, FP8 193 us against
+    //    216 us), else 128x128 (64x32 waves): down at 1024 INT8 52 us
+    //    against 80 us on 256x128.
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;
@@ -168,7 +169,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         }
     } else {
         p.waves = 8;
-        if (fmt == QLIN_I8 && tiles_256x128 >= 256 && full) p.channels = 256;
+        if (tiles_256x128 >= 256 && full) p.channels = 256;
     }
     return p;
 }
@@ -243,6 +244,13 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");
+        if ((input_group || weight_group) && p.channels == 256 && p.waves != 8)
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group 256x128 tiled path has eight waves only");
+        // The K-group tiled kernel addresses its scale arrays through 32-bit
+        // buffer ranges.
+        if ((input_group || weight_group) &&
+            ((long(K) + 127) / 128) * (long(N) > rows ? long(N) : long(rows)) * 4 > INT32_MAX)
+            return fail(QLIN_ERR_UNSUPPORTED, "K-group scale arrays exceed 2 GiB");
         if (p.staged) return fail(QLIN_ERR_UNSUPPORTED, "tiled path staged must be 0");
         if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
             return fail(QLIN_ERR_UNSUPPORTED,

@@ -92,17 +92,26 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     constexpr int ROWS = BN + BM;
     constexpr int INSTS = ROWS / (RPI * NW);
     constexpr int W_INSTS = BN / (RPI * NW);
-    constexpr int STAGE_BYTES = ROWS * BK;
+    // K-group kernels: each stage slot also holds the stage's group scales
+    // (weight [BN] floats in its first KB, token [BM] floats in the second),
+    // copied by one extra DMA instruction of wave 0 (weights) and wave 1
+    // (tokens). Each gets a whole KB: a lane past the tile still writes
+    // (zeros) at its position.
+    constexpr int SCALE_BYTES = Grouped ? 2048 : 0;
+    constexpr int STAGE_BYTES = ROWS * BK + SCALE_BYTES;
     static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
+    static_assert(!Grouped || (BN * 4 <= 1024 && BM * 4 <= 1024 && NW >= 2),
+                  "one scale instruction per operand");
     // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
     constexpr bool kMF32 = Fmt == FP8 && !Grouped && BK == 64;
     // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
-    // exactly 64, the FP8 16x16x128 pipeline 128, the K-group pipeline one
-    // 128-wide group.
-    static_assert(Grouped ? BK == 128 : (Fmt == I8 ? BK == 64 : (BK == 64 || BK == 128)),
-                  "K bytes per stage");
-    static_assert(!Grouped || BK == 128, "one K group of 128 per stage");
+    // exactly 64, the FP8 16x16x128 pipeline 128; K groups are 128 wide (two
+    // INT8 stages or one FP8 stage).
+    static_assert(Fmt == I8 ? BK == 64 : (BK == 64 || BK == 128), "K bytes per stage");
+    static_assert(!Grouped || Fmt == I8 || BK == 128, "FP8 K groups use 128-byte stages");
+    constexpr int kGroupK = 128;
+    constexpr int SPG = kGroupK / BK;  // stages per K group
     using MMA = TileMma<Fmt>;
     using Acc = typename MMA::Acc;
 
@@ -135,6 +144,13 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                                                     0, min(BN, N - n_base) * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsrc_x = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(x + size_t(m_base) * K), 0, min(BM, M - m_base) * K, 0x00020000);
+    // K-group scales [ceil(K/g), N] and [ceil(K/g), M] (the host checks that
+    // both arrays stay below 2^31 bytes).
+    const int kgroups = (K + kGroupK - 1) / kGroupK;
+    const __amdgpu_buffer_rsrc_t rsrc_sw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(sw), 0, Grouped && weight_group ? kgroups * N * 4 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_sx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(sx), 0, Grouped && input_group ? kgroups * M * 4 : 0, 0x00020000);
 
     // Load instruction i of this wave fills stage rows [(i*NW + wave)*RPI, +RPI),
     // 1 KB of LDS in lane order: lane -> row += lane / CPR, physical chunk
@@ -168,6 +184,30 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                                                          voff, soff, 0, 0);
             }
         }
+        if constexpr (Grouped) {
+            // The stage's group scales: sw[g][n_base ..) by wave 0, sx[g][m_base ..)
+            // by wave 1 (lanes past the tile, or an operand without groups,
+            // read zero through an out-of-range offset).
+            const int g = k0 / kGroupK;
+            if (wave < 2) {
+                const bool wv = wave == 0;
+                const int grp = wv ? weight_group : input_group;
+                const int count = wv ? BN : BM;
+                const uint32_t off = (grp && lane * 4 < count)
+                                         ? uint32_t((size_t(g) * (wv ? N : M) + (wv ? n_base : m_base)) * 4 + lane * 16)
+                                         : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wv ? rsrc_sw : rsrc_sx,
+                                                         (lds_ptr_t)(base + ROWS * BK + (wv ? 0 : 1024)),
+                                                         16, off, 0, 0, 0);
+            }
+        }
+    };
+    // "Stage s+1 has landed" waits: waves 0 and 1 of a K-group kernel issue
+    // one more instruction per stage.
+    auto wait_ring = [&](auto outstanding_stages) {
+        constexpr int S = decltype(outstanding_stages)::value;
+        if (Grouped && wave < 2) wait_vmcnt<(INSTS + 1) * S>();
+        else wait_vmcnt<INSTS * S>();
     };
 
     Acc acc[(Grouped || kMF32) ? 1 : WTN][(Grouped || kMF32) ? 1 : WTM];
@@ -359,24 +399,24 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             step(s + 1, a1, b1, a0, b0);
         }
         if (s < stages) step(s, a0, b0, a1, b1);
-    } else {
+    } else if constexpr (Fmt == FP8) {
+        // FP8 K groups: one 128-K group per stage, stage-synchronous (the
+        // software-pipelined form below needs more registers than the i32x8
+        // FP8 fragments leave: it spilled and ran slower). Stages wait for
+        // themselves; the group scales are the stage slot's scale rows.
         for (int s = 0; s < stages; ++s) {
             // Stage s has landed once at most the newer stages are outstanding.
-            if (s + STAGES - 2 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
+            if (s + STAGES - 2 < stages) wait_ring(std::integral_constant<int, STAGES - 2>{});
             else wait_vmcnt<0>();
             __syncthreads();
             if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
             const uint8_t *cur = lds + (s % STAGES) * STAGE_BYTES;
+            const float *slot = reinterpret_cast<const float *>(cur + ROWS * BK);
             // One 128-wide K group per stage: r = fmaf(p, sxg*swg, r).
-            const int k = s * BK;
-            const int g_in = input_group ? k / input_group : 0;
-            const int g_w = weight_group ? k / weight_group : 0;
             float sxg[WTM];
 #pragma unroll
-            for (int j = 0; j < WTM; ++j) {
-                int m = min(m_base + wave_m * 16 * WTM + j * 16 + row16, M - 1);
-                sxg[j] = input_group ? sx[size_t(g_in) * M + m] : 1.f;
-            }
+            for (int j = 0; j < WTM; ++j)
+                sxg[j] = input_group ? slot[256 + wave_m * 16 * WTM + j * 16 + row16] : 1.f;
 #pragma unroll
             for (int i = 0; i < WTN; ++i) {
                 Acc part[WTM];
@@ -398,10 +438,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                 }
                 float swg[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int n = min(n_base + wave_n * 16 * WTN + i * 16 + quad * 4 + r, N - 1);
-                    swg[r] = weight_group ? sw[size_t(g_w) * N + n] : 1.f;
-                }
+                for (int r = 0; r < 4; ++r)
+                    swg[r] = weight_group ? slot[wave_n * 16 * WTN + i * 16 + quad * 4 + r] : 1.f;
 #pragma unroll
                 for (int j = 0; j < WTM; ++j)
 #pragma unroll
@@ -410,6 +448,104 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                             __builtin_fmaf(float(part[j][r]), sxg[j] * swg[r], facc[i][j][r]);
             }
         }
+    } else {
+        // K groups of 128: the per-channel software pipeline (fragments of
+        // stage s+1 read while stage s's MFMAs run), with the MFMAs of group
+        // g accumulated natively in part[g % 2] (exact int32 for INT8) and
+        // applied as facc = fmaf(p, sx_g * sw_g, facc), groups ascending,
+        // during the first stage of group g + 1, so that the conversion and
+        // fma of one group run under the next group's MFMAs. The group's
+        // scales come with its last stage (the stage slot's scale rows) and
+        // are held in registers until they are applied.
+        using Frag = std::conditional_t<Fmt == I8, i32x4, i32x8>;
+        const int a_off = a_row0 * BK, b_off = b_row0 * BK;
+        const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
+        const int a_c1 = ((4 + quad) ^ swizzle<BK>(a_row0)) * 16;
+        const int b_c1 = ((4 + quad) ^ swizzle<BK>(b_row0)) * 16;
+        auto read = [&](int st, Frag (&a)[WTN], Frag (&bb)[WTM]) {
+            const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
+            const uint8_t *pa = cur + a_off, *pb = cur + b_off;
+#pragma unroll
+            for (int j = 0; j < WTM; ++j) {
+                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c0);
+                if constexpr (Fmt == I8) {
+                    bb[j] = lo;
+                } else {
+                    const i32x4 hi = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c1);
+                    bb[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < WTN; ++i) {
+                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c0);
+                if constexpr (Fmt == I8) {
+                    a[i] = lo;
+                } else {
+                    const i32x4 hi = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c1);
+                    a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+        };
+        // One set of partials: group g's MFMAs accumulate natively (exact
+        // int32 for INT8) and the group is applied at its last stage. (A
+        // ping-pong set that defers the conversion to the next group's first
+        // stage needs registers the 8-wave tiles do not have: it spilled.)
+        // With two waves per SIMD the other wave's MFMAs run while one wave
+        // waits for its last MFMA result.
+        Acc part[WTN][WTM];
+        auto apply = [&](int st) {
+            const float *slot = reinterpret_cast<const float *>(lds + (st % STAGES) * STAGE_BYTES +
+                                                                ROWS * BK);
+            float xg[WTM];
+#pragma unroll
+            for (int j = 0; j < WTM; ++j)
+                xg[j] = input_group ? slot[256 + wave_m * 16 * WTM + j * 16 + row16] : 1.f;
+#pragma unroll
+            for (int i = 0; i < WTN; ++i) {
+                const f32x4 wg = weight_group ? *reinterpret_cast<const f32x4 *>(
+                                                    slot + wave_n * 16 * WTN + i * 16 + quad * 4)
+                                              : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+                for (int j = 0; j < WTM; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        facc[i][j][r] =
+                            __builtin_fmaf(float(part[i][j][r]), xg[j] * wg[r], facc[i][j][r]);
+            }
+        };
+        // One stage: MFMAs into part (from zero on the group's first stage),
+        // the group applied on its last stage from the scale rows of this
+        // stage's slot (read before the barrier: the next step's DMA refills
+        // the slot); then the ring wait, barrier and the next stage's
+        // fragment reads.
+        auto step = [&](int s, const Frag (&a)[WTN], const Frag (&bb)[WTM], Frag (&na)[WTN],
+                        Frag (&nb)[WTM]) {
+            const bool first = s % SPG == 0, last = s % SPG == SPG - 1 || s + 1 == stages;
+            if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
+#pragma unroll
+            for (int i = 0; i < WTN; ++i)
+#pragma unroll
+                for (int j = 0; j < WTM; ++j) {
+                    if (first) part[i][j] = Acc{0, 0, 0, 0};
+                    MMA::run(part[i][j], a[i], bb[j]);
+                }
+            if (last) apply(s);
+            if (s + STAGES - 1 < stages) wait_ring(std::integral_constant<int, STAGES - 2>{});
+            else if (s + 1 < stages) wait_vmcnt<0>();
+            lds_barrier();
+            if (s + 1 < stages) read(s + 1, na, nb);
+        };
+        Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
+        if (stages >= STAGES - 1) wait_ring(std::integral_constant<int, STAGES - 2>{});
+        else wait_vmcnt<0>();
+        lds_barrier();
+        read(0, a0, b0);
+        int s = 0;
+        for (; s + 1 < stages; s += 2) {
+            step(s, a0, b0, a1, b1);
+            step(s + 1, a1, b1, a0, b0);
+        }
+        if (s < stages) step(s, a0, b0, a1, b1);
     }
 
     // Epilogue. A lane holds C[n = 4*quad + r][m = row16] of each 16x16 tile:
@@ -760,8 +896,8 @@ template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Gr
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
     const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
-    const size_t lds = std::max(size_t(STAGES) * (BN + BM) * BK, size_t(BN) * BM * 2) +
-                       size_t(BN + BM) * 4;
+    const size_t stage = size_t(BN + BM) * BK + (Grouped ? 2048 : 0);
+    const size_t lds = std::max(size_t(STAGES) * stage, size_t(BN) * BM * 2) + size_t(BN + BM) * 4;
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
 #define QLIN_TILED(KF, PW)                                                                      \
     hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, KF, Out, PW>),   \
@@ -780,14 +916,14 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if constexpr (Grouped) {
         // No 256x256: the fp32 group accumulators would double the 128x128
         // register tile per wave and spill.
+        // INT8 in 64-byte stages (two per group), FP8 in 128-byte stages.
+        constexpr int GBK = Fmt == I8 ? 64 : 128;
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, true, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 2, GBK, GBK == 64 ? 4 : 3, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, true, Out>(a, s);
-        if (p.channels == 256 && p.tokens == 128)
-            return launch_shape<Fmt, 2, 2, 8, 4, 128, 3, true, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 4, 2, GBK, 4, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
-            return launch_shape<Fmt, 2, 2, 4, 4, 128, 4, true, Out>(a, s);
+            return launch_shape<Fmt, 2, 2, 4, 4, GBK, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
         // 256x128 with eight waves of 128x32.
