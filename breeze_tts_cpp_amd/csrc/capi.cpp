@@ -575,9 +575,6 @@ int check_row_output(int src_type, int rows, int cols, const void *values, const
     if (fmt != QLIN_I8 && fmt != QLIN_FP8)
         return fail(QLIN_ERR_INVALID, "quantized storage must be I8 or FP8");
     if (rows < 1 || cols < 1) return fail(QLIN_ERR_INVALID, "%s shape rows=%d cols=%d", what, rows, cols);
-    if (cols > qlin::kSequenceMaxCols)
-        return fail(QLIN_ERR_UNSUPPORTED, "%s supports cols <= %d (got %d)", what,
-                    qlin::kSequenceMaxCols, cols);
     if (!values || !scales) return fail(QLIN_ERR_INVALID, "%s output pointer is null", what);
     if (!valid_group(group))
         return fail(QLIN_ERR_INVALID, "quantization group must be 0, 32, 64 or 128 (got %d)", group);

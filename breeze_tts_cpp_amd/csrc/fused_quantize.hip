@@ -38,12 +38,12 @@ namespace {
 
 // One 256-thread workgroup per row; lane t holds columns [8t, 8t+8).
 // update_scale (optional) and gemma are uniform run-time choices.
-template <int Fmt, class T, bool Add, bool Rot, int G, bool Vec>
+template <int Fmt, class T, bool Add, bool Vec>
 __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
     uint16_t *__restrict__ x, const uint16_t *__restrict__ update,
     const uint16_t *__restrict__ update_scale, const uint16_t *__restrict__ weight,
     uint8_t *__restrict__ q, float *__restrict__ scales, int rows, int cols, float eps,
-    int gemma) {
+    int gemma, int group, int rot) {
     const int row = blockIdx.x, column = threadIdx.x * 8;
     uint16_t *xr = x + size_t(row) * cols;
     float v[1][8], w[8];
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[0][i] = round16<T>(round16<T>(v[0][i] * inv_norm) * w[i]);
     }
-    encode_row<Fmt, 1, Rot, G, Vec>(v, q, scales, row, rows, cols);
+    encode_row<Fmt, 1, Vec>(v, q, scales, row, rows, cols, group, rot);
 }
 
 template <int Kind> __device__ __forceinline__ float activate(float x) {
@@ -98,11 +98,11 @@ template <int Kind> __device__ __forceinline__ float activate(float x) {
 // Few rows (decode) use NT = 256 * chunks and one chunk per lane, so the
 // activation chains of a row run on more SIMDs at once.
 // The activation kind is a uniform run-time choice.
-template <int Fmt, class T, int Items, bool Rot, int G, bool Vec, int NT = kThreads>
+template <int Fmt, class T, int Items, bool Vec, int NT = kThreads>
 __global__ __launch_bounds__(NT) void gated_quantize(const uint16_t *__restrict__ input,
                                                      uint8_t *__restrict__ q,
                                                      float *__restrict__ scales, int rows,
-                                                     int width, int kind) {
+                                                     int width, int kind, int group, int rot) {
     const int row = blockIdx.x;
     const uint16_t *gate = input + size_t(row) * width * 2, *up = gate + width;
     float v[Items][8];
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(NT) void gated_quantize(const uint16_t *__restrict_
             for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(round16<T>(activate<0>(g[i])) * u[i]);
         }
     }
-    encode_row<Fmt, Items, Rot, G, Vec, NT>(v, q, scales, row, rows, width);
+    encode_row<Fmt, Items, Vec, NT>(v, q, scales, row, rows, width, group, rot);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -131,16 +131,9 @@ void launch_norm_enc(const NormQuantizeArgs &a, hipStream_t s) {
     auto *us = static_cast<const uint16_t *>(a.update_scale);
     auto *w = static_cast<const uint16_t *>(a.weight);
     auto *q = static_cast<uint8_t *>(a.values);
-#define QLIN_NORM(R, G)                                                                        \
-    hipLaunchKernelGGL((residual_rms_quantize<Fmt, T, Add, R, G, Vec>), dim3(a.rows),          \
-                       dim3(kThreads), 0, s, x, u, Add ? us : nullptr, w, q, a.scales, a.rows, \
-                       a.cols, a.eps, a.gemma)
-    if (a.group == 32) { if (a.rotation) QLIN_NORM(true, 32); else QLIN_NORM(false, 32); }
-    else if (a.group == 64) { if (a.rotation) QLIN_NORM(true, 64); else QLIN_NORM(false, 64); }
-    else if (a.group == 128) { if (a.rotation) QLIN_NORM(true, 128); else QLIN_NORM(false, 128); }
-    else if (a.rotation) QLIN_NORM(true, 0);
-    else QLIN_NORM(false, 0);
-#undef QLIN_NORM
+hipLaunchKernelGGL((residual_rms_quantize<Fmt, T, Add, Vec>), dim3(a.rows), dim3(kThreads), 0, s,
+                       x, u, Add ? us : nullptr, w, q, a.scales, a.rows, a.cols, a.eps, a.gemma,
+                       a.group, a.rotation ? 1 : 0);
 }
 
 template <int Fmt, class T, bool Vec>
@@ -153,15 +146,8 @@ template <int Fmt, class T, int Items, bool Vec, int NT = kThreads>
 void launch_gated_enc(const GatedQuantizeArgs &a, hipStream_t s) {
     auto *in = static_cast<const uint16_t *>(a.input);
     auto *q = static_cast<uint8_t *>(a.values);
-#define QLIN_GATED(R, G)                                                                       \
-    hipLaunchKernelGGL((gated_quantize<Fmt, T, Items, R, G, Vec, NT>), dim3(a.rows),           \
-                       dim3(NT), 0, s, in, q, a.scales, a.rows, a.width, a.kind)
-    if (a.group == 32) { if (a.rotation) QLIN_GATED(true, 32); else QLIN_GATED(false, 32); }
-    else if (a.group == 64) { if (a.rotation) QLIN_GATED(true, 64); else QLIN_GATED(false, 64); }
-    else if (a.group == 128) { if (a.rotation) QLIN_GATED(true, 128); else QLIN_GATED(false, 128); }
-    else if (a.rotation) QLIN_GATED(true, 0);
-    else QLIN_GATED(false, 0);
-#undef QLIN_GATED
+hipLaunchKernelGGL((gated_quantize<Fmt, T, Items, Vec, NT>), dim3(a.rows), dim3(NT), 0, s, in,
+                       q, a.scales, a.rows, a.width, a.kind, a.group, a.rotation ? 1 : 0);
 }
 
 // Rows at or below this count run one 2048-column chunk per lane (NT = 256 *

@@ -64,7 +64,7 @@ struct LayerNormQuantizeArgs {
     float eps;
     qlin_norm_fusion f;
     void *retained;     // [rows, cols] or null
-    int rows, cols;     // cols <= 16384
+    int rows, cols;
     void *values;
     float *scales;
     int fmt, group, rotation;
@@ -74,12 +74,11 @@ struct PointwiseQuantizeArgs {
     int x_rows, src_type;
     qlin_epilogue e;
     void *retained;     // [rows, cols] or null
-    int rows, cols;     // cols <= 16384
+    int rows, cols;
     void *values;
     float *scales;
     int fmt, group, rotation;
 };
-constexpr int kSequenceMaxCols = 16384;
 void launch_norm_linear(const NormLinearArgs &, hipStream_t);
 void launch_layer_norm_quantize(const LayerNormQuantizeArgs &, hipStream_t);
 void launch_pointwise_quantize(const PointwiseQuantizeArgs &, hipStream_t);

@@ -121,33 +121,45 @@ template <int NT = kThreads> __device__ __forceinline__ float block_max(float v)
     return r;
 }
 
+// One lane's 8 columns [column, column+8) of a K-group encoding (group 32,
+// 64 or 128, so the group spans group/8 adjacent lanes): the group's amax by
+// lane shuffles, its scale written by the group's first lane, the codes.
+template <int Fmt, bool Vec>
+__device__ __forceinline__ void encode_group8(const float (&v)[8], uint8_t *__restrict__ dst,
+                                              float *__restrict__ scales, int row, int rows,
+                                              int cols, int column, int group) {
+    const int lanes = group / 8;
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int d = 1; d < lanes; d *= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    const float step = quant_scale<Fmt>(amax);
+    if (column < cols && (column % group) == 0) scales[size_t(column / group) * rows + row] = step;
+    store8<Fmt, Vec>(dst, column, cols, v, 1.f / step);
+}
+
 // Encode a row held in registers by NT threads (v[it][i] = column
-// (it*NT + t)*8 + i; columns past `cols` hold 0): optional H128 rotation, then
-// per-(row, G) scales ([ceil(cols/G), rows]) when G > 0, else one per-token
-// scale ([rows]). The reference's rotated_quantize / encode_group / token
-// paths (quant_device.cuh:63-88,145-195, row_quantize.cu:24-165). Groups and
-// rotation blocks stay inside one wave for any NT (multiples of 64).
-template <int Fmt, int Items, bool Rot, int G, bool Vec, int NT = kThreads>
+// (it*NT + t)*8 + i; columns past `cols` hold 0): optional H128 rotation
+// (`rot`), then per-(row, group) scales ([ceil(cols/group), rows]) for group
+// 32, 64 or 128, else (group 0) one per-token scale ([rows]). The reference's
+// rotated_quantize / encode_group / token paths (quant_device.cuh:63-88,
+// 145-195, row_quantize.cu:24-165). Groups and rotation blocks stay inside one
+// wave for any NT (multiples of 64). `group` and `rot` are uniform across the
+// workgroup, so their branches never diverge.
+template <int Fmt, int Items, bool Vec, int NT = kThreads>
 __device__ __forceinline__ void encode_row(float (&v)[Items][8], uint8_t *__restrict__ q,
                                            float *__restrict__ scales, int row, int rows,
-                                           int cols) {
+                                           int cols, int group, int rot) {
     uint8_t *dst = q + size_t(row) * cols;
-    if constexpr (Rot) {
+    if (rot) {
 #pragma unroll
         for (int it = 0; it < Items; ++it) rotate8(v[it], (it * NT + threadIdx.x) * 8);
     }
-    if constexpr (G > 0) {
+    if (group) {
 #pragma unroll
-        for (int it = 0; it < Items; ++it) {
-            const int column = (it * NT + threadIdx.x) * 8;
-            float amax = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[it][i]));
-            amax = group_max<G / 8>(amax);
-            const float step = quant_scale<Fmt>(amax);
-            if (column < cols && (column % G) == 0) scales[size_t(column / G) * rows + row] = step;
-            store8<Fmt, Vec>(dst, column, cols, v[it], 1.f / step);
-        }
+        for (int it = 0; it < Items; ++it)
+            encode_group8<Fmt, Vec>(v[it], dst, scales, row, rows, cols,
+                                    (it * NT + threadIdx.x) * 8, group);
     } else {
         float amax = 0.f;
 #pragma unroll

@@ -148,50 +148,31 @@ __device__ __forceinline__ void load8_or(const uint16_t *row, int column, int co
 }
 
 // ---------------------------------------------------------------- LayerNorm -> quant
-template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
-__global__ __launch_bounds__(kThreads) void layer_norm_quantize(
-    const uint16_t *__restrict__ x, int x_rows, const uint16_t *__restrict__ nw,
-    const uint16_t *__restrict__ nb, float eps, qlin_norm_fusion f, uint16_t *__restrict__ retained,
-    int rows, int cols, uint8_t *__restrict__ q, float *__restrict__ scales) {
-    __shared__ float cache[Items * kChunk];
-    __shared__ float red[8];
-    const int out_row = blockIdx.x, t = threadIdx.x;
-    const int row = f.source_rows ? f.source_rows[out_row] : out_row;
-    float v[Items][8];
-    if (row < 0 || row >= x_rows) {
-        // An out-of-range source row: NaN outputs, unit scales, codes of NaN
-        // (norm_kernel's first branch, sequence_norm.cu:73-81).
-#pragma unroll
-        for (int it = 0; it < Items; ++it)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = __builtin_nanf("");
-#pragma unroll
-        for (int it = 0; it < Items; ++it) {
-            const int column = (it * kThreads + t) * 8;
-            if (retained) store16x8<T, Vec>(retained + size_t(out_row) * cols, column, cols, v[it]);
-            store8<Fmt, Vec>(q + size_t(out_row) * cols, column, cols, v[it], 1.f);
-        }
-        const int groups = G ? (cols + G - 1) / G : 1;
-        for (int g = t; g < groups; g += kThreads) scales[size_t(g) * rows + out_row] = 1.f;
-        return;
+// The operands of one LayerNorm row (NormRow, sequence_norm.cu:29-57) and its
+// two 8-column steps: the fused input (projection bias, gate, residual) and
+// the normalized output (weight, bias, scale, shift), each with the
+// reference's 16-bit rounding points. Columns past `cols` come out as 0.
+template <class T, bool Vec> struct LayerNormRow {
+    const uint16_t *xr, *pb, *gate, *res, *nw, *nb, *scale, *shift;
+    uint16_t *raw;
+    int cols;
+
+    __device__ LayerNormRow(const uint16_t *x, int x_rows, const uint16_t *norm_weight,
+                            const uint16_t *norm_bias, const qlin_norm_fusion &f, int row,
+                            int out_row, int cols_)
+        : nw(norm_weight), nb(norm_bias), cols(cols_) {
+        const int sequence = row / f.rows_per_sequence;
+        xr = x + size_t(row) * cols;
+        pb = row_of(f.projection_bias, 1, 0, cols);
+        gate = row_of(f.gate, f.gate_rows, sequence, cols);
+        res = row_of(f.residual, x_rows, row, cols);
+        scale = row_of(f.scale, f.scale_rows, sequence, cols);
+        shift = row_of(f.shift, f.shift_rows, sequence, cols);
+        raw = f.raw ? static_cast<uint16_t *>(f.raw) + size_t(out_row) * cols : nullptr;
     }
-    const int sequence = row / f.rows_per_sequence;
-    const uint16_t *xr = x + size_t(row) * cols;
-    const uint16_t *pb = row_of(f.projection_bias, 1, 0, cols);
-    const uint16_t *gate = row_of(f.gate, f.gate_rows, sequence, cols);
-    const uint16_t *res = row_of(f.residual, x_rows, row, cols);
-    const uint16_t *scale = row_of(f.scale, f.scale_rows, sequence, cols);
-    const uint16_t *shift = row_of(f.shift, f.shift_rows, sequence, cols);
-    uint16_t *raw = f.raw ? static_cast<uint16_t *>(f.raw) + size_t(out_row) * cols : nullptr;
-#pragma unroll
-    for (int it = 0; it < Items; ++it) {
-        const int column = (it * kThreads + t) * 8;
-        if (column >= cols) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
-            continue;
-        }
-        // An absent operand adds 0 (exact; -0 becomes +0 as the reference's).
+
+    // An absent operand adds 0 (exact; -0 becomes +0 as the reference's).
+    __device__ __forceinline__ void input8(int column, float (&v)[8]) const {
         float a[8], b[8];
         load8<T, Vec>(xr, column, cols, a);
         if (pb) {
@@ -216,11 +197,83 @@ __global__ __launch_bounds__(kThreads) void layer_norm_quantize(
             for (int i = 0; i < 8; ++i) a[i] += 0.f;
         }
 #pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = Vec || column + i < cols ? a[i] : 0.f;
+    }
+
+    __device__ __forceinline__ void output8(int column, float (&v)[8], float mean, float inv) const {
+        float w[8], b[8];
+        load8_or<T, Vec>(nw, column, cols, w, 1.f);
+        load8_or<T, Vec>(nb, column, cols, b, 0.f);
+#pragma unroll
         for (int i = 0; i < 8; ++i) {
-            v[it][i] = Vec || column + i < cols ? a[i] : 0.f;
-            if (Vec || column + i < cols) cache[column + i] = v[it][i];
+            float u = (v[i] - mean) * inv;
+            if (nw) u = u * w[i];
+            v[i] = round16<T>(u + b[i]);
         }
-        if (raw) store16x8<T, Vec>(raw, column, cols, v[it]);
+        if (scale) {
+            load8<T, Vec>(scale, column, cols, w);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = round16<T>(v[i] * round16<T>(1.f + w[i]));
+        }
+        if (shift) {
+            load8<T, Vec>(shift, column, cols, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = round16<T>(v[i] + b[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] += 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = Vec || column + i < cols ? v[i] : 0.f;
+    }
+};
+
+// An out-of-range source row: NaN outputs, unit scales, codes of NaN
+// (norm_kernel's first branch, sequence_norm.cu:73-81).
+template <int Fmt, class T, bool Vec>
+__device__ void nan_row(uint16_t *retained, uint8_t *q, float *scales, int out_row, int rows,
+                        int cols, int group) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_nanf("");
+    for (int column = threadIdx.x * 8; column < cols; column += kChunk) {
+        if (retained) store16x8<T, Vec>(retained + size_t(out_row) * cols, column, cols, v);
+        store8<Fmt, Vec>(q + size_t(out_row) * cols, column, cols, v, 1.f);
+    }
+    const int groups = group ? (cols + group - 1) / group : 1;
+    for (int g = threadIdx.x; g < groups; g += kThreads) scales[size_t(g) * rows + out_row] = 1.f;
+}
+
+// Rows of up to Items * 2048 columns, held in registers (and in LDS for the
+// statistics' column order).
+template <int Fmt, class T, int Items, bool Vec>
+__global__ __launch_bounds__(kThreads) void layer_norm_quantize(
+    const uint16_t *__restrict__ x, int x_rows, const uint16_t *__restrict__ nw,
+    const uint16_t *__restrict__ nb, float eps, qlin_norm_fusion f, uint16_t *__restrict__ retained,
+    int rows, int cols, uint8_t *__restrict__ q, float *__restrict__ scales, int group, int rot) {
+    __shared__ float cache[Items * kChunk];
+    __shared__ float red[8];
+    const int out_row = blockIdx.x, t = threadIdx.x;
+    const int row = f.source_rows ? f.source_rows[out_row] : out_row;
+    if (row < 0 || row >= x_rows) {
+        nan_row<Fmt, T, Vec>(retained, q, scales, out_row, rows, cols, group);
+        return;
+    }
+    const LayerNormRow<T, Vec> r(x, x_rows, nw, nb, f, row, out_row, cols);
+    float v[Items][8];
+#pragma unroll
+    for (int it = 0; it < Items; ++it) {
+        const int column = (it * kThreads + t) * 8;
+        if (column >= cols) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
+            continue;
+        }
+        r.input8(column, v[it]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (Vec || column + i < cols) cache[column + i] = v[it][i];
+        if (r.raw) store16x8<T, Vec>(r.raw, column, cols, v[it]);
     }
     __syncthreads();
     // Thread t's columns t, t + 256, ... in order (the reference's per-thread
@@ -245,62 +298,191 @@ __global__ __launch_bounds__(kThreads) void layer_norm_quantize(
     for (int it = 0; it < Items; ++it) {
         const int column = (it * kThreads + t) * 8;
         if (column >= cols) continue;
-        float w[8], b[8];
-        load8_or<T, Vec>(nw, column, cols, w, 1.f);
-        load8_or<T, Vec>(nb, column, cols, b, 0.f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float u = (v[it][i] - mean) * inv;
-            if (nw) u = u * w[i];
-            v[it][i] = round16<T>(u + b[i]);
-        }
-        if (scale) {
-            load8<T, Vec>(scale, column, cols, w);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(v[it][i] * round16<T>(1.f + w[i]));
-        }
-        if (shift) {
-            load8<T, Vec>(shift, column, cols, b);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = round16<T>(v[it][i] + b[i]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] += 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[it][i] = Vec || column + i < cols ? v[it][i] : 0.f;
+        r.output8(column, v[it], mean, inv);
         if (retained) store16x8<T, Vec>(retained + size_t(out_row) * cols, column, cols, v[it]);
     }
-    encode_row<Fmt, Items, Rot, G, Vec>(v, q, scales, out_row, rows, cols);
+    encode_row<Fmt, Items, Vec>(v, q, scales, out_row, rows, cols, group, rot);
+}
+
+// Rows of any length, streamed in 2048-column chunks that are re-read from
+// global memory for each pass, as the reference's uncached norm_kernel loops
+// re-run NormRow::load (sequence_norm.cu:93-99,113-118,156-188): the sum, the
+// squared deviations, then the output; per-token scales take one more pass
+// for the amax before the codes. Every pass computes the same values, in the
+// same per-thread column order as the register-resident kernel. The 16-bit
+// raw and retained rows are written only by the last pass, so that they may
+// alias the inputs.
+template <int Fmt, class T, bool Vec>
+__global__ __launch_bounds__(kThreads) void layer_norm_quantize_long(
+    const uint16_t *__restrict__ x, int x_rows, const uint16_t *__restrict__ nw,
+    const uint16_t *__restrict__ nb, float eps, qlin_norm_fusion f, uint16_t *retained, int rows,
+    int cols, uint8_t *__restrict__ q, float *__restrict__ scales, int group, int rot) {
+    __shared__ float cache[kChunk];
+    __shared__ float red[8];
+    const int out_row = blockIdx.x, t = threadIdx.x;
+    const int row = f.source_rows ? f.source_rows[out_row] : out_row;
+    if (row < 0 || row >= x_rows) {
+        nan_row<Fmt, T, Vec>(retained, q, scales, out_row, rows, cols, group);
+        return;
+    }
+    const LayerNormRow<T, Vec> r(x, x_rows, nw, nb, f, row, out_row, cols);
+    uint16_t *kept = retained ? retained + size_t(out_row) * cols : nullptr;
+    uint8_t *dst = q + size_t(out_row) * cols;
+    const int chunks = (cols + kChunk - 1) / kChunk;
+    // Passes 1 and 2: the statistics, each chunk staged through LDS so that
+    // thread t adds the chunk's columns t, t + 256, ... in order.
+    float mean = 0.f, sum = 0.f;
+    for (int pass = 0; pass < 2; ++pass) {
+        sum = 0.f;
+        for (int ch = 0; ch < chunks; ++ch) {
+            const int column = (ch * kThreads + t) * 8;
+            float v[8];
+            r.input8(column, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cache[t * 8 + i] = v[i];
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (ch * kChunk + t + j * kThreads < cols) {
+                    const float value = cache[t + j * kThreads];
+                    if (pass == 0) sum += value;
+                    else {
+                        const float d = value - mean;
+                        sum = __builtin_fmaf(d, d, sum);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (pass == 0) mean = block_sum_256(sum, red) / float(cols);
+    }
+    const float inv = rsqrt_rn(block_sum_256(sum, red) / float(cols) + eps);
+    float inverse = 0.f;
+    if (!group) {
+        float amax = 0.f;
+        for (int ch = 0; ch < chunks; ++ch) {
+            const int column = (ch * kThreads + t) * 8;
+            float v[8];
+            r.input8(column, v);
+            r.output8(column, v, mean, inv);
+            if (rot) rotate8(v, column);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        }
+        const float step = quant_scale<Fmt>(block_max_256(amax, red));
+        if (t == 0) scales[out_row] = step;
+        inverse = 1.f / step;
+    }
+    for (int ch = 0; ch < chunks; ++ch) {
+        const int column = (ch * kThreads + t) * 8;
+        float v[8];
+        r.input8(column, v);
+        if (r.raw) store16x8<T, Vec>(r.raw, column, cols, v);
+        r.output8(column, v, mean, inv);
+        if (kept) store16x8<T, Vec>(kept, column, cols, v);
+        if (rot) rotate8(v, column);
+        if (group) encode_group8<Fmt, Vec>(v, dst, scales, out_row, rows, cols, column, group);
+        else store8<Fmt, Vec>(dst, column, cols, v, inverse);
+    }
 }
 
 // ---------------------------------------------------------------- pointwise -> quant
-template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+// The operands of one pointwise-epilogue row and its 8-column step
+// (sequence_pointwise.cu:149-260): bias, gate, the scaled or indexed
+// residual, condition, then (after the optional raw store) the output scale
+// and activation, with the reference's 16-bit rounding points. Columns past
+// `cols` come out as 0; a masked row is all 0.
+template <class T, bool Vec> struct PointwiseRow {
+    const uint16_t *xr, *bias, *gate, *cond, *res;
+    uint16_t *raw;
+    int cols, activation;
+    float value_scale, residual_scale, output_scale, alpha;
+    bool masked, skip_nan, scaled_residual, scaled_output, rounded_act;
+
+    __device__ PointwiseRow(const uint16_t *x, int x_rows, const qlin_epilogue &e, int row,
+                            int cols_)
+        : cols(cols_), activation(e.activation), value_scale(e.value_scale),
+          residual_scale(e.residual_scale), output_scale(e.output_scale), alpha(e.alpha) {
+        masked = e.valid_rows_per_sequence && row % e.rows_per_sequence >= e.valid_rows_per_sequence;
+        const int sequence = row / e.rows_per_sequence;
+        xr = row_of(x, x_rows, row / e.input_repeat, cols);
+        bias = row_of(e.bias, 1, 0, cols);
+        gate = row_of(e.gate, e.gate_rows, sequence, cols);
+        cond = row_of(e.condition, e.condition_rows, sequence, cols);
+        const int r = e.residual_index ? e.residual_index[row] : row;
+        skip_nan = e.residual && r >= e.residual_rows;
+        res = e.residual && r >= 0 && !skip_nan ? row_of(e.residual, e.residual_rows, r, cols)
+                                                : nullptr;
+        raw = e.raw ? static_cast<uint16_t *>(e.raw) + size_t(row) * cols : nullptr;
+        // Steps that leave a 16-bit value unchanged skip their rounding:
+        // without a residual, value_scale 1 and a positive finite
+        // residual_scale the residual step is v + 0 (exact; it turns -0 into
+        // +0 as the reference's does); output_scale 1 multiplies exactly;
+        // identity and ReLU return a 16-bit value.
+        scaled_residual = res || skip_nan || e.value_scale != 1.f ||
+                          !(e.residual_scale > 0.f && e.residual_scale <= 3.4e38f);
+        scaled_output = e.output_scale != 1.f;
+        rounded_act = e.activation != QLIN_ACT_IDENTITY && e.activation != QLIN_ACT_RELU;
+    }
+
+    // The row's 8 values at `column`; the raw row is stored when `store_raw`.
+    __device__ __forceinline__ void value8(int column, float (&v)[8], bool store_raw) const {
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.f;
+            if (store_raw && raw) store16x8<T, Vec>(raw, column, cols, v);
+            return;
+        }
+        float a[8], b[8];
+        load8<T, Vec>(xr, column, cols, a);
+        if (bias) {
+            load8<T, Vec>(bias, column, cols, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] += 0.f;
+        }
+        if (gate) {
+            load8<T, Vec>(gate, column, cols, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * b[i]);
+        }
+        if (scaled_residual) {
+            load8_or<T, Vec>(res, column, cols, b, skip_nan ? __builtin_nanf("") : 0.f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                a[i] = round16<T>(__builtin_fmaf(value_scale, a[i], residual_scale * b[i]));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] += 0.f;
+        }
+        if (cond) {
+            load8<T, Vec>(cond, column, cols, b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
+        }
+        if (store_raw && raw) store16x8<T, Vec>(raw, column, cols, a);
+        if (scaled_output) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * output_scale);
+        }
+        activate8(a, activation, alpha);
+        if (rounded_act) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = Vec || column + i < cols ? a[i] : 0.f;
+    }
+};
+
+template <int Fmt, class T, int Items, bool Vec>
 __global__ __launch_bounds__(kThreads) void pointwise_quantize(
     const uint16_t *__restrict__ x, int x_rows, qlin_epilogue e, uint16_t *__restrict__ retained,
-    int rows, int cols, uint8_t *__restrict__ q, float *__restrict__ scales) {
+    int rows, int cols, uint8_t *__restrict__ q, float *__restrict__ scales, int group, int rot) {
     const int row = blockIdx.x, t = threadIdx.x;
-    const bool masked =
-        e.valid_rows_per_sequence && row % e.rows_per_sequence >= e.valid_rows_per_sequence;
-    const int sequence = row / e.rows_per_sequence;
-    const uint16_t *xr = row_of(x, x_rows, row / e.input_repeat, cols);
-    const uint16_t *bias = row_of(e.bias, 1, 0, cols);
-    const uint16_t *gate = row_of(e.gate, e.gate_rows, sequence, cols);
-    const uint16_t *cond = row_of(e.condition, e.condition_rows, sequence, cols);
-    const int r = e.residual_index ? e.residual_index[row] : row;
-    const bool skip_nan = e.residual && r >= e.residual_rows;
-    const uint16_t *res = e.residual && r >= 0 && !skip_nan
-                              ? row_of(e.residual, e.residual_rows, r, cols) : nullptr;
-    uint16_t *raw = e.raw ? static_cast<uint16_t *>(e.raw) + size_t(row) * cols : nullptr;
-    // Steps that leave a 16-bit value unchanged skip their rounding: without
-    // a residual, value_scale 1 and a positive finite residual_scale the
-    // residual step is v + 0 (exact; it turns -0 into +0 as the reference's
-    // does); output_scale 1 multiplies exactly; identity and ReLU return a
-    // 16-bit value.
-    const bool scaled_residual = res || skip_nan || e.value_scale != 1.f ||
-                                 !(e.residual_scale > 0.f && e.residual_scale <= 3.4e38f);
-    const bool scaled_output = e.output_scale != 1.f;
-    const bool rounded_act = e.activation != QLIN_ACT_IDENTITY && e.activation != QLIN_ACT_RELU;
+    const PointwiseRow<T, Vec> r(x, x_rows, e, row, cols);
     float v[Items][8];
 #pragma unroll
     for (int it = 0; it < Items; ++it) {
@@ -310,56 +492,49 @@ __global__ __launch_bounds__(kThreads) void pointwise_quantize(
             for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
             continue;
         }
-        if (masked) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = 0.f;
-            if (raw) store16x8<T, Vec>(raw, column, cols, v[it]);
-        } else {
-            float a[8], b[8];
-            load8<T, Vec>(xr, column, cols, a);
-            if (bias) {
-                load8<T, Vec>(bias, column, cols, b);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] += 0.f;
-            }
-            if (gate) {
-                load8<T, Vec>(gate, column, cols, b);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * b[i]);
-            }
-            if (scaled_residual) {
-                load8_or<T, Vec>(res, column, cols, b, skip_nan ? __builtin_nanf("") : 0.f);
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    a[i] = round16<T>(__builtin_fmaf(e.value_scale, a[i], e.residual_scale * b[i]));
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] += 0.f;
-            }
-            if (cond) {
-                load8<T, Vec>(cond, column, cols, b);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] + b[i]);
-            }
-            if (raw) store16x8<T, Vec>(raw, column, cols, a);
-            if (scaled_output) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i] * e.output_scale);
-            }
-            activate8(a, e.activation, e.alpha);
-            if (rounded_act) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = round16<T>(a[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = Vec || column + i < cols ? a[i] : 0.f;
-        }
+        r.value8(column, v[it], true);
         if (retained) store16x8<T, Vec>(retained + size_t(row) * cols, column, cols, v[it]);
     }
-    encode_row<Fmt, Items, Rot, G, Vec>(v, q, scales, row, rows, cols);
+    encode_row<Fmt, Items, Vec>(v, q, scales, row, rows, cols, group, rot);
+}
+
+// Rows of any length in 2048-column chunks: per-token scales take an amax
+// pass before the pass that writes codes, raw and retained rows (so that
+// those may alias the inputs); K-group scales need the one pass only.
+template <int Fmt, class T, bool Vec>
+__global__ __launch_bounds__(kThreads) void pointwise_quantize_long(
+    const uint16_t *__restrict__ x, int x_rows, qlin_epilogue e, uint16_t *retained, int rows,
+    int cols, uint8_t *__restrict__ q, float *__restrict__ scales, int group, int rot) {
+    __shared__ float red[8];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const PointwiseRow<T, Vec> r(x, x_rows, e, row, cols);
+    uint16_t *kept = retained ? retained + size_t(row) * cols : nullptr;
+    uint8_t *dst = q + size_t(row) * cols;
+    const int chunks = (cols + kChunk - 1) / kChunk;
+    float inverse = 0.f;
+    if (!group) {
+        float amax = 0.f;
+        for (int ch = 0; ch < chunks; ++ch) {
+            const int column = (ch * kThreads + t) * 8;
+            float v[8];
+            r.value8(column, v, false);
+            if (rot) rotate8(v, column);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        }
+        const float step = quant_scale<Fmt>(block_max_256(amax, red));
+        if (t == 0) scales[row] = step;
+        inverse = 1.f / step;
+    }
+    for (int ch = 0; ch < chunks; ++ch) {
+        const int column = (ch * kThreads + t) * 8;
+        float v[8];
+        r.value8(column, v, true);
+        if (kept) store16x8<T, Vec>(kept, column, cols, v);
+        if (rot) rotate8(v, column);
+        if (group) encode_group8<Fmt, Vec>(v, dst, scales, row, rows, cols, column, group);
+        else store8<Fmt, Vec>(dst, column, cols, v, inverse);
+    }
 }
 
 // ---------------------------------------------------------------- LayerNorm -> GEMV
@@ -483,51 +658,51 @@ __global__ __launch_bounds__(256) void norm_project(
 
 // ---------------------------------------------------------------- launchers
 // The row-quantizer variants (format x 16-bit type x items per lane x
-// group/rotation mode x vector access) compile in four parallel parts, one
+// vector access) compile in four parallel parts, one
 // per (family, format): QLIN_SEQ_PART names the part's launcher,
 // QLIN_SEQ_FAMILY is 0 (LayerNorm) or 1 (pointwise), QLIN_SEQ_FMT the format.
 // The build without QLIN_SEQ_PART holds the dispatchers and norm_project.
 #ifdef QLIN_SEQ_PART
-template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+template <int Fmt, class T, int Items, bool Vec>
 void launch_one(const LayerNormQuantizeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((layer_norm_quantize<Fmt, T, Items, Rot, G, Vec>), dim3(a.rows),
-                       dim3(kThreads), 0, s, static_cast<const uint16_t *>(a.x), a.x_rows,
-                       static_cast<const uint16_t *>(a.norm_weight),
-                       static_cast<const uint16_t *>(a.norm_bias), a.eps, a.f,
-                       static_cast<uint16_t *>(a.retained), a.rows, a.cols,
-                       static_cast<uint8_t *>(a.values), a.scales);
+    const int rot = a.rotation ? 1 : 0;
+    auto *x = static_cast<const uint16_t *>(a.x);
+    auto *nw = static_cast<const uint16_t *>(a.norm_weight);
+    auto *nb = static_cast<const uint16_t *>(a.norm_bias);
+    auto *kept = static_cast<uint16_t *>(a.retained);
+    auto *q = static_cast<uint8_t *>(a.values);
+    if constexpr (Items == 0)
+        hipLaunchKernelGGL((layer_norm_quantize_long<Fmt, T, Vec>), dim3(a.rows), dim3(kThreads),
+                           0, s, x, a.x_rows, nw, nb, a.eps, a.f, kept, a.rows, a.cols, q,
+                           a.scales, a.group, rot);
+    else
+        hipLaunchKernelGGL((layer_norm_quantize<Fmt, T, Items, Vec>), dim3(a.rows), dim3(kThreads),
+                           0, s, x, a.x_rows, nw, nb, a.eps, a.f, kept, a.rows, a.cols, q,
+                           a.scales, a.group, rot);
 }
 
-template <int Fmt, class T, int Items, bool Rot, int G, bool Vec>
+template <int Fmt, class T, int Items, bool Vec>
 void launch_one(const PointwiseQuantizeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((pointwise_quantize<Fmt, T, Items, Rot, G, Vec>), dim3(a.rows),
-                       dim3(kThreads), 0, s, static_cast<const uint16_t *>(a.x), a.x_rows, a.e,
-                       static_cast<uint16_t *>(a.retained), a.rows, a.cols,
-                       static_cast<uint8_t *>(a.values), a.scales);
-}
-
-template <int Fmt, class T, int Items, bool Vec, class Args>
-void by_mode(const Args &a, hipStream_t s) {
-    if (a.group == 32) {
-        if (a.rotation) launch_one<Fmt, T, Items, true, 32, Vec>(a, s);
-        else launch_one<Fmt, T, Items, false, 32, Vec>(a, s);
-    } else if (a.group == 64) {
-        if (a.rotation) launch_one<Fmt, T, Items, true, 64, Vec>(a, s);
-        else launch_one<Fmt, T, Items, false, 64, Vec>(a, s);
-    } else if (a.group == 128) {
-        if (a.rotation) launch_one<Fmt, T, Items, true, 128, Vec>(a, s);
-        else launch_one<Fmt, T, Items, false, 128, Vec>(a, s);
-    } else {
-        launch_one<Fmt, T, Items, false, 0, Vec>(a, s);
-    }
+    const int rot = a.rotation ? 1 : 0;
+    auto *x = static_cast<const uint16_t *>(a.x);
+    auto *kept = static_cast<uint16_t *>(a.retained);
+    auto *q = static_cast<uint8_t *>(a.values);
+    if constexpr (Items == 0)
+        hipLaunchKernelGGL((pointwise_quantize_long<Fmt, T, Vec>), dim3(a.rows), dim3(kThreads), 0,
+                           s, x, a.x_rows, a.e, kept, a.rows, a.cols, q, a.scales, a.group, rot);
+    else
+        hipLaunchKernelGGL((pointwise_quantize<Fmt, T, Items, Vec>), dim3(a.rows), dim3(kThreads),
+                           0, s, x, a.x_rows, a.e, kept, a.rows, a.cols, q, a.scales, a.group, rot);
 }
 
 template <int Fmt, class T, bool Vec, class Args>
 void by_items(const Args &a, hipStream_t s) {
-    // Items: 1, 2 or 8 chunks of 2048 columns (cols <= 16384).
-    if (a.cols > 2 * kChunk) by_mode<Fmt, T, 8, Vec>(a, s);
-    else if (a.cols > kChunk) by_mode<Fmt, T, 2, Vec>(a, s);
-    else by_mode<Fmt, T, 1, Vec>(a, s);
+    // Items: 1, 2 or 8 register-resident chunks of 2048 columns, or (0) the
+    // streaming kernel for rows longer than 16384 columns.
+    if (a.cols > 8 * kChunk) launch_one<Fmt, T, 0, Vec>(a, s);
+    else if (a.cols > 2 * kChunk) launch_one<Fmt, T, 8, Vec>(a, s);
+    else if (a.cols > kChunk) launch_one<Fmt, T, 2, Vec>(a, s);
+    else launch_one<Fmt, T, 1, Vec>(a, s);
 }
 #endif
 

@@ -299,7 +299,8 @@ int qlin_norm_linear(const void *x, const qlin_norm_fusion *fusion, const void *
  * of `rows` output rows (x has x_rows rows; x_rows == rows unless
  * fusion->source_rows is given), optionally stored to `retained` [rows, cols],
  * then quantized as qlin_row_quantize (per token, or K groups with optional
- * H128 rotation; rotation requires a group). 1 <= cols <= 16384. */
+ * H128 rotation; rotation requires a group). cols >= 1; rows longer than
+ * 16384 columns are streamed (re-read per pass) instead of held on chip. */
 int qlin_layer_norm_quantize(const void *x, int x_rows, int src_type, const void *norm_weight,
                              const void *norm_bias, float eps, const qlin_norm_fusion *fusion,
                              void *retained, int rows, int cols, void *values, float *scales,
@@ -311,7 +312,7 @@ int qlin_layer_norm_quantize(const void *x, int x_rows, int src_type, const void
  * the qlin_epilogue result of each element of x (x_rows * input_repeat ==
  * rows), optionally stored to `retained` [rows, cols], quantized as
  * qlin_row_quantize (rotation requires a group). epilogue may be NULL
- * (identity). 1 <= cols <= 16384. */
+ * (identity). cols >= 1; rows longer than 16384 columns are streamed. */
 int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
                             const qlin_epilogue *epilogue, void *retained, int rows, int cols,
                             void *values, float *scales, int fmt, int group, int rotation,

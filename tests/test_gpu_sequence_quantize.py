@@ -3,7 +3,8 @@ the oracle: qlin_layer_norm_quantize (reference layer_norm_quantize,
 ops/kernels/sequence/sequence_norm.cu:65-200,412-440) and
 qlin_pointwise_quantize (reference pointwise_quantize, sequence_pointwise.cu:
 149-260,325-357). Codes, scales, retained and raw rows bit-exact in every
-encoding mode, for bf16/f16, ragged and vector row widths up to 16384, with
+encoding mode, for bf16/f16, ragged and vector row widths up to 16384 held in
+registers and past it streamed (16391 ... 24576), with
 every fusion, the source-row gather and every activation."""
 import numpy as np
 import pytest
@@ -32,7 +33,7 @@ def same_codes(got, want):
 
 @pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, BF16), (torch.float16, F16)])
 @pytest.mark.parametrize("fmt", [I8, FP8])
-@pytest.mark.parametrize("cols", [7, 136, 1000, 2048, 6144, 16384])
+@pytest.mark.parametrize("cols", [7, 136, 1000, 2048, 6144, 16384, 16392, 20007, 24576])
 def test_layer_norm_quantize_parity(dev, orc, dtype, src_type, fmt, cols):
     from breeze_tts_cpp_amd import qlinear
     rows, rps = 6, 3
@@ -69,12 +70,13 @@ def test_layer_norm_quantize_parity(dev, orc, dtype, src_type, fmt, cols):
             assert np.array_equal(sd.cpu().numpy(), s)
 
 
+@pytest.mark.parametrize("cols", [2048, 17408])
 @pytest.mark.parametrize("fmt", [I8, FP8])
-def test_layer_norm_quantize_gather(dev, orc, fmt):
+def test_layer_norm_quantize_gather(dev, orc, fmt, cols):
     """source_rows: gathered rows, and NaN rows with unit scales for sources
     outside the input."""
     from breeze_tts_cpp_amd import qlinear
-    x_rows, cols = 5, 2048
+    x_rows = 5
     g = torch.Generator().manual_seed(fmt)
     x, res = mk(g, torch.bfloat16, x_rows, cols, sc=2.0), mk(g, torch.bfloat16, x_rows, cols)
     src = np.array([4, 0, -1, 2, 5, 2, 1], np.int32)
@@ -97,7 +99,7 @@ def test_layer_norm_quantize_gather(dev, orc, fmt):
 
 @pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, BF16), (torch.float16, F16)])
 @pytest.mark.parametrize("fmt", [I8, FP8])
-@pytest.mark.parametrize("cols", [9, 256, 1000, 4096, 12288])
+@pytest.mark.parametrize("cols", [9, 256, 1000, 4096, 12288, 16391, 20480])
 def test_pointwise_quantize_parity(dev, orc, dtype, src_type, fmt, cols):
     from breeze_tts_cpp_amd import qlinear
     x_rows, repeat, rps, valid = 4, 2, 4, 3
@@ -137,12 +139,14 @@ def test_pointwise_quantize_parity(dev, orc, dtype, src_type, fmt, cols):
             assert np.array_equal(sd.cpu().numpy(), s)
 
 
-def test_pointwise_quantize_in_place(dev, orc):
-    """retained may replace x row for row (ops::linear's output reuse)."""
+@pytest.mark.parametrize("cols", [2048, 18432])
+def test_pointwise_quantize_in_place(dev, orc, cols):
+    """retained may replace x row for row (ops::linear's output reuse), also
+    for streamed rows."""
     from breeze_tts_cpp_amd import qlinear
     g = torch.Generator().manual_seed(9)
-    x = mk(g, torch.bfloat16, 32, 2048, sc=2.0)
-    b = mk(g, torch.bfloat16, 2048, sc=0.3)
+    x = mk(g, torch.bfloat16, 32, cols, sc=2.0)
+    b = mk(g, torch.bfloat16, cols, sc=0.3)
     q, s, out, _ = orc.pointwise_quantize(x, I8, bias=b, activation=1)
     xd = dev16(x, torch.bfloat16, dev)
     b_d = dev16(b, torch.bfloat16, dev)  # alive across the call
