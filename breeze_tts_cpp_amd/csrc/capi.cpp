@@ -50,10 +50,7 @@ qlin::GemmPath to_internal(const qlin_path &p) {
 // LDS-tiled MFMA GEMM.
 qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_group) {
     qlin_path p{};
-    // K groups of 32 / 64 have partials only in the skinny kernel, which
-    // also serves more than 64 rows in 64-token tiles.
-    const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
-    if (rows <= 64 || small_group) {
+    if (rows <= 64) {
         // Decode: the weights are streamed once and each CU's share of them
         // bounds the time, so the grid is sized to about one workgroup per
         // CU (256 on MI355X). Rules measured on the BASELINE projections at
@@ -144,7 +141,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    256x128 (128x32 waves) for >= 256 tiles in full rounds (gate_up at
     //    4096: INT8 193 us against 222 us on 128x128, FP8 193 us against
     //    216 us), else 128x128 (64x32 waves): down at 1024 INT8 52 us
-    //    against 80 us on 256x128.
+    //    against 80 us on 256x128. Groups of 32 / 64 follow the same rule
+    //    for INT8 (qkv at 4096, G 32: 219 us against 267 us); FP8 takes
+    //    128x128 (255 us against 428 us).
     p.kind = QLIN_KIND_TILED;
     p.splits = 1;
     p.waves = 1;
@@ -169,7 +168,8 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         }
     } else {
         p.waves = 8;
-        if (tiles_256x128 >= 256 && full) p.channels = 256;
+        const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
+        if (tiles_256x128 >= 256 && full && !(small_group && fmt == QLIN_FP8)) p.channels = 256;
     }
     return p;
 }
@@ -252,9 +252,11 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             ((long(K) + 127) / 128) * (long(N) > rows ? long(N) : long(rows)) * 4 > INT32_MAX)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group scale arrays exceed 2 GiB");
         if (p.staged) return fail(QLIN_ERR_UNSUPPORTED, "tiled path staged must be 0");
-        if ((input_group && input_group != 128) || (weight_group && weight_group != 128))
-            return fail(QLIN_ERR_UNSUPPORTED,
-                        "tiled K-group GEMM supports group size 128 (32/64: skinny path)");
+        const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
+        if (small_group && p.waves != 8)
+            return fail(QLIN_ERR_UNSUPPORTED, "tiled K groups of 32/64 have eight-wave tiles only");
+        if (small_group && fmt == QLIN_FP8 && p.channels != 128)
+            return fail(QLIN_ERR_UNSUPPORTED, "FP8 tiled K groups of 32/64 have 128x128 tiles only");
         return ok();
     }
     return fail(QLIN_ERR_UNSUPPORTED, "unknown path kind %d", p.kind);

@@ -80,7 +80,7 @@ __device__ __forceinline__ void lds_barrier() {
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, bool KFull,
-          class Out, bool PackedW = false>
+          class Out, bool PackedW = false, int GS = 128>
 __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     const uint8_t *__restrict__ x, const float *__restrict__ sx, const uint8_t *__restrict__ w,
     const float *__restrict__ sw, void *__restrict__ y, int M, int N, int K, int tiles_m,
@@ -96,19 +96,23 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // (weight [BN] floats in its first KB, token [BM] floats in the second),
     // copied by one extra DMA instruction of wave 0 (weights) and wave 1
     // (tokens). Each gets a whole KB: a lane past the tile still writes
-    // (zeros) at its position.
-    constexpr int SCALE_BYTES = Grouped ? 2048 : 0;
+    // (zeros) at its position. Groups of GS = 32 / 64 (the smaller of the two
+    // operands' group sizes) read their scales from global memory instead.
+    constexpr bool kScaleDma = Grouped && GS == 128;
+    constexpr int SCALE_BYTES = kScaleDma ? 2048 : 0;
     constexpr int STAGE_BYTES = ROWS * BK + SCALE_BYTES;
     static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
-    static_assert(!Grouped || (BN * 4 <= 1024 && BM * 4 <= 1024 && NW >= 2),
+    static_assert(!kScaleDma || (BN * 4 <= 1024 && BM * 4 <= 1024 && NW >= 2),
                   "one scale instruction per operand");
+    static_assert(GS == 128 || (Grouped && BK == 128 && !PackedW && (GS == 32 || GS == 64)),
+                  "K groups of 32 / 64 use 128-byte stages of row-major weights");
     // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
     constexpr bool kMF32 = Fmt == FP8 && !Grouped && BK == 64;
     // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
     // exactly 64, the FP8 16x16x128 pipeline 128; K groups are 128 wide (two
     // INT8 stages or one FP8 stage).
-    static_assert(Fmt == I8 ? BK == 64 : (BK == 64 || BK == 128), "K bytes per stage");
+    static_assert(Fmt == I8 ? (BK == 64 || GS < 128) : (BK == 64 || BK == 128), "K bytes per stage");
     static_assert(!Grouped || Fmt == I8 || BK == 128, "FP8 K groups use 128-byte stages");
     constexpr int kGroupK = 128;
     constexpr int SPG = kGroupK / BK;  // stages per K group
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                                                          voff, soff, 0, 0);
             }
         }
-        if constexpr (Grouped) {
+        if constexpr (kScaleDma) {
             // The stage's group scales: sw[g][n_base ..) by wave 0, sx[g][m_base ..)
             // by wave 1 (lanes past the tile, or an operand without groups,
             // read zero through an out-of-range offset).
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // one more instruction per stage.
     auto wait_ring = [&](auto outstanding_stages) {
         constexpr int S = decltype(outstanding_stages)::value;
-        if (Grouped && wave < 2) wait_vmcnt<(INSTS + 1) * S>();
+        if (kScaleDma && wave < 2) wait_vmcnt<(INSTS + 1) * S>();
         else wait_vmcnt<INSTS * S>();
     };
 
@@ -399,6 +403,82 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             step(s + 1, a1, b1, a0, b0);
         }
         if (s < stages) step(s, a0, b0, a1, b1);
+    } else if constexpr (GS < kGroupK) {
+        // K groups of GS = 32 / 64 (the reference grouped_gemm's GroupSize,
+        // the smaller of the two operands' group sizes), stage-synchronous
+        // over 128-byte stages. Sub-group g of a stage covers K bytes
+        // [g*GS, (g+1)*GS) of it: its MFMAs accumulate natively from zero and
+        // are applied as facc = fmaf(p, sx * sw, facc), sub-groups ascending.
+        // The 16-byte fragment chunk c of a lane covers K [16c, 16c+16)
+        // (INT8: chunk 4h + quad of 64-K sub-step h; FP8: chunks quad and
+        // 4 + quad in registers 0-3 and 4-7); the sub-group's MFMAs run on B
+        // fragments with the chunks of other sub-groups zeroed. The scales
+        // are read from global memory (L2): sx[k / input_group][m],
+        // sw[k / weight_group][n] at the sub-group's first K.
+        constexpr int SUB = BK / GS;
+        for (int s = 0; s < stages; ++s) {
+            if (s + STAGES - 2 < stages) wait_ring(std::integral_constant<int, STAGES - 2>{});
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
+            const uint8_t *cur = lds + (s % STAGES) * STAGE_BYTES;
+            // Not unrolled: unrolled sub-groups hoist every scale load and spill.
+#pragma unroll 1
+            for (int g = 0; g < SUB; ++g) {
+                const int k = s * BK + g * GS;
+                if (!KFull && k >= K) break;
+                float sxg[WTM];
+#pragma unroll
+                for (int j = 0; j < WTM; ++j) {
+                    const int m = min(m_base + wave_m * 16 * WTM + j * 16 + row16, M - 1);
+                    sxg[j] = input_group ? sx[size_t(k / input_group) * M + m] : 1.f;
+                }
+                const float *swr = sw + size_t(weight_group ? k / weight_group : 0) * N;
+                // Chunk c belongs to sub-group c * 16 / GS.
+                auto keep = [&](int c) { return c * 16 / GS == g; };
+#pragma unroll
+                for (int i = 0; i < WTN; ++i) {
+                    Acc part[WTM];
+#pragma unroll
+                    for (int j = 0; j < WTM; ++j) part[j] = Acc{0, 0, 0, 0};
+                    if constexpr (Fmt == I8) {
+                        const int hs = g * GS / 64;  // the 64-K sub-step holding g
+                        const i32x4 af = frag16(cur, a_row0 + i * 16, hs);
+#pragma unroll
+                        for (int j = 0; j < WTM; ++j) {
+                            i32x4 bf = frag16(cur, b_row0 + j * 16, hs);
+                            if (!keep(hs * 4 + quad)) bf = i32x4{0, 0, 0, 0};
+                            MMA::run(part[j], af, bf);
+                        }
+                    } else {
+                        const i32x8 af = frag32(cur, a_row0 + i * 16);
+                        const bool k0 = keep(quad), k1 = keep(4 + quad);
+#pragma unroll
+                        for (int j = 0; j < WTM; ++j) {
+                            i32x8 bf = frag32(cur, b_row0 + j * 16);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                bf[e] = k0 ? bf[e] : 0;
+                                bf[4 + e] = k1 ? bf[4 + e] : 0;
+                            }
+                            MMA::run(part[j], af, bf);
+                        }
+                    }
+                    float swg[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = min(n_base + wave_n * 16 * WTN + i * 16 + quad * 4 + r, N - 1);
+                        swg[r] = weight_group ? swr[n] : 1.f;
+                    }
+#pragma unroll
+                    for (int j = 0; j < WTM; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            facc[i][j][r] = __builtin_fmaf(float(part[j][r]), sxg[j] * swg[r],
+                                                           facc[i][j][r]);
+                }
+            }
+        }
     } else if constexpr (Fmt == FP8) {
         // FP8 K groups: one 128-K group per stage, stage-synchronous (the
         // software-pipelined form below needs more registers than the i32x8
@@ -892,21 +972,42 @@ int launch_wide(const GemmArgs &a, hipStream_t stream) {
     return 0;
 }
 
-template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, class Out>
+template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, class Out,
+          int GS = 128>
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
     const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
-    const size_t stage = size_t(BN + BM) * BK + (Grouped ? 2048 : 0);
+    const size_t stage = size_t(BN + BM) * BK + (Grouped && GS == 128 ? 2048 : 0);
     const size_t lds = std::max(size_t(STAGES) * stage, size_t(BN) * BM * 2) + size_t(BN + BM) * 4;
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
 #define QLIN_TILED(KF, PW)                                                                      \
-    hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, KF, Out, PW>),   \
+    hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, KF, Out, PW, GS>), \
                        grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,      \
                        tiles_m, tiles_n, a.input_group, a.weight_group, a.bias, a.act)
-    if (a.K % BK == 0) { if (a.packed) QLIN_TILED(true, true); else QLIN_TILED(true, false); }
-    else { if (a.packed) QLIN_TILED(false, true); else QLIN_TILED(false, false); }
+    if constexpr (GS < 128) {
+        // Small K groups: row-major weights only.
+        if (a.packed) return -4;
+        if (a.K % BK == 0) QLIN_TILED(true, false);
+        else QLIN_TILED(false, false);
+    } else {
+        if (a.K % BK == 0) { if (a.packed) QLIN_TILED(true, true); else QLIN_TILED(true, false); }
+        else { if (a.packed) QLIN_TILED(false, true); else QLIN_TILED(false, false); }
+    }
 #undef QLIN_TILED
     return 0;
+}
+
+// K groups of 32 / 64 (GS, the smaller of the two operands' sizes) on
+// 128-byte stages, eight waves: 256x128 (128x32 waves, INT8 only: the FP8
+// tile spills) or 128x128 (64x32).
+template <int Fmt, class Out, int GS>
+int dispatch_small_groups(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    if constexpr (Fmt == I8)
+        if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, true, Out, GS>(a, s);
+    if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
+        return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, true, Out, GS>(a, s);
+    return -4;
 }
 
 // Macro tiles (weight rows x tokens): 256x256 with eight waves of 128x64;
@@ -967,7 +1068,11 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 
 template <int Fmt, class Out>
 int dispatch_grouped(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    if (a.input_group || a.weight_group) return dispatch_shape<Fmt, true, Out>(a, p, s);
+    const int g = a.input_group && a.weight_group ? std::min(a.input_group, a.weight_group)
+                                                  : a.input_group + a.weight_group;
+    if (g == 32) return dispatch_small_groups<Fmt, Out, 32>(a, p, s);
+    if (g == 64) return dispatch_small_groups<Fmt, Out, 64>(a, p, s);
+    if (g) return dispatch_shape<Fmt, true, Out>(a, p, s);
     return dispatch_shape<Fmt, false, Out>(a, p, s);
 }
 

@@ -50,12 +50,12 @@ def grouped_partition(path: Path, K: int) -> tuple[int, int, int]:
     (the K-group oracle takes the same partition): a skinny launch splits K
     into splits*8 wave ranges of ceil(ceil(K/256) / (splits*8)) 256-byte
     blocks (trailing ranges may be empty); a tiled launch sums all of K in
-    one range."""
+    one range (given as K rounded up to 128, a whole number of groups)."""
     if path.kind == KIND_SKINNY:
         blocks = -(-K // 256)
         ranges = path.splits * path.waves
         return path.splits, path.waves, -(-blocks // ranges) * 256
-    return 1, 1, K
+    return 1, 1, -(-K // 128) * 128
 
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",

@@ -121,8 +121,9 @@ size_t qlin_workspace_bytes(const qlin_path *path, int rows, int N, int K, int f
  * qlin_plan). input_group / weight_group: 0 = per-row scales, 32 / 64 / 128 =
  * K-group scales (group_int8 / group_fp8 use 128); partials are taken per the
  * smaller of the two group sizes (reference quant_grouped.cu:185-202). Groups
- * of 32 / 64 run on the skinny path only (planned for any rows; a tiled,
- * split-K or packed-weight path returns QLIN_ERR_UNSUPPORTED). Shape rules of the reference make_plan
+ * of 32 / 64 run on the skinny path up to 64 rows and on eight-wave tiled
+ * paths above (INT8 256x128 or 128x128, FP8 128x128); split-K and
+ * packed-weight paths return QLIN_ERR_UNSUPPORTED for them. Shape rules of the reference make_plan
  * (ops/cuda/quantization.cpp:210-222): K % 16 == 0, N % 16 == 0, and for
  * INT8 K <= 131071. */
 int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void *w,

@@ -85,9 +85,11 @@ def test_gemm_validation():
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 4)) == -4          # no 4-wave 128x128 variant
     assert call(M=256, path=qlinear.Path(T, 128, 256, 1, 2), ig=128, wg=128) == -4  # K groups: no 32x32 tiles
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 2)) == -4
+    assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 1), ig=32, wg=32) == -4  # small groups: 8 waves
+    assert call(M=256, fmt=FP8, path=qlinear.Path(T, 128, 256, 1, 8), ig=64, wg=64) == -4  # FP8: 128x128
     # grid limits are checked before any launch: token tiles on the skinny
     # grid's z dimension (<= 65535), macro tiles on the tiled grid's x (< 2^31)
-    assert call(M=1 << 23, N=64, K=256, ig=32, wg=32) == -4
+    assert call(M=1 << 23, N=64, K=256, path=qlinear.Path(qlinear.KIND_SKINNY, 64, 16, 1, 8)) == -4
     assert b"65535" in L.qlin_last_error()
     assert call(M=1 << 30, N=1 << 30, K=16) == -4
     assert b"macro tiles" in L.qlin_last_error()
@@ -107,6 +109,7 @@ def test_prefill_plan_rules():
     assert tile(1024, "gate_up", FP8) == (128, 128, 8)   # 384 256x128 tiles: 1.5 rounds
     assert tile(4096, "qkv", I8, 128) == (256, 128, 8) and tile(4096, "qkv", FP8, 128) == (256, 128, 8)
     assert tile(1024, "gate_up", I8, 128) == (128, 128, 8) and tile(1024, "gate_up", FP8, 128) == (128, 128, 8)
+    assert tile(4096, "qkv", I8, 32) == (256, 128, 8) and tile(4096, "qkv", FP8, 64) == (128, 128, 8)
 
 
 def test_plan_and_workspace():

@@ -5,7 +5,8 @@ weight scales (a 32-column partial of a 128-column activation group takes
 that group's scale) and fma-accumulated in ascending K order
 (quant_grouped.cu:85-146). INT8 bit-exact against the oracle's grouped
 GEMM with the planned wave split; FP8 within rel-L2 1e-2 of the exact
-product. More than 64 rows run in 64-token skinny tiles."""
+product. Up to 64 rows run on the skinny (decode) kernel; more rows on the
+tiled kernel's small-group variant (both eight-wave tiles)."""
 import numpy as np
 import pytest
 import torch
@@ -28,37 +29,73 @@ def quantize(orc, b, fmt, group):
 @pytest.mark.parametrize("ig,wg", [(32, 32), (64, 64), (128, 32), (32, 128), (64, 128),
                                    (128, 64), (0, 64), (32, 0)])
 @pytest.mark.parametrize("M,N,K", [(8, 256, 2048), (32, 4096, 2048), (100, 272, 1536),
-                                   (3, 48, 4000)])
+                                   (3, 48, 4000), (200, 528, 1008), (300, 256, 2048)])
 def test_small_groups(dev, orc, fmt, ig, wg, M, N, K):
     from breeze_tts_cpp_amd import qlinear
     print(f"small groups fmt={fmt} ig={ig} wg={wg} M={M} N={N} K={K}", flush=True)
     xq, sx = quantize(orc, synthetic.activations(M, K, seed=M + ig), fmt, ig)
     wq, sw = quantize(orc, synthetic.weights(N, K, seed=N + wg), fmt, wg)
+    planned = qlinear.plan(M, N, K, fmt, ig, wg)
+    assert planned.kind == (qlinear.KIND_SKINNY if M <= 64 else qlinear.KIND_TILED)
+    assert planned.splits == 1
+    paths = [planned]
+    if M > 64:  # the eight-wave tiles of the small-group variant
+        paths = [qlinear.Path(qlinear.KIND_TILED, 128, 128, 1, 8, 0)]
+        if fmt == I8:
+            paths.append(qlinear.Path(qlinear.KIND_TILED, 128, 256, 1, 8, 0))
+    for p in paths:
+        y = qlinear.gemm(torch.from_numpy(xq).to(dev), torch.from_numpy(sx).to(dev),
+                         torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev), fmt,
+                         input_group=ig, weight_group=wg, path=p)
+        torch.cuda.synchronize()
+        got = bits(y)
+        if fmt == I8:
+            splits, waves, span = qlinear.grouped_partition(p, K)
+            ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, splits, waves, span)
+            assert np.array_equal(got, ref), f"{p}: {np.count_nonzero(got != ref)} mismatches"
+        else:
+            ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, ig, wg)
+            f = synthetic.bf16_bits_to_f32(got).astype(np.float64)
+            assert np.linalg.norm(f - ideal) / np.linalg.norm(ideal) <= 1e-2, p
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("ig,wg", [(32, 32), (64, 128)])
+def test_small_groups_prefill_projection(dev, orc, fmt, ig, wg):
+    """A BASELINE-sized prefill projection (qkv 4096x2048 at M = 1024) with
+    32/64 groups through the planned tiled path, checked on sampled rows."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N, K = 1024, 4096, 2048
+    print(f"small groups prefill fmt={fmt} ig={ig} wg={wg}", flush=True)
+    xq, sx = quantize(orc, synthetic.activations(M, K, seed=5), fmt, ig)
+    wq, sw = quantize(orc, synthetic.weights(N, K, seed=6), fmt, wg)
     p = qlinear.plan(M, N, K, fmt, ig, wg)
-    assert p.kind == qlinear.KIND_SKINNY and p.splits == 1
+    assert p.kind == qlinear.KIND_TILED
     y = qlinear.gemm(torch.from_numpy(xq).to(dev), torch.from_numpy(sx).to(dev),
                      torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev), fmt,
                      input_group=ig, weight_group=wg, path=p)
     torch.cuda.synchronize()
-    got = bits(y)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(3).choice(M, 24)]))
+    got = bits(y)[rows]
+    xs = xq[rows]
+    sxs = np.ascontiguousarray(sx[:, rows]) if ig else sx[rows]
     if fmt == I8:
-        splits, waves, span = qlinear.grouped_partition(p, K)
-        ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, splits, waves, span)
+        ref, _ = orc.gemm_grouped(xs, sxs, wq, sw, fmt, ig, wg)
         assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
     else:
-        ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, ig, wg)
+        ideal = orc.gemm_grouped_ideal(xs, sxs, wq, sw, fmt, ig, wg)
         f = synthetic.bf16_bits_to_f32(got).astype(np.float64)
         assert np.linalg.norm(f - ideal) / np.linalg.norm(ideal) <= 1e-2
 
 
 def test_small_groups_unsupported_forms(dev, orc):
-    """Split-K, packed weights and the tiled kernel decline 32/64 groups."""
+    """Split-K skinny paths and four-wave tiled paths decline 32/64 groups."""
     from breeze_tts_cpp_amd import qlinear
     M, N, K = 8, 64, 1024
     xq, sx = orc.quantize_rows(synthetic.activations(M, K, seed=1), I8, group=32)
     wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=1), I8, group=32)
     args = [torch.from_numpy(a).to(dev) for a in (xq, sx, wq, sw)]
-    for path in (qlinear.Path(1, 16, 16, 2, 8, 0), qlinear.Path(2, 128, 128, 1, 8, 0)):
+    for path in (qlinear.Path(1, 16, 16, 2, 8, 0), qlinear.Path(2, 128, 128, 1, 1, 0)):
         with pytest.raises(qlinear.QLinearError):
             qlinear.gemm(*args, I8, input_group=32, weight_group=32, path=path,
                          workspace=torch.empty(1 << 20, dtype=torch.uint8, device=dev))
