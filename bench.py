@@ -39,6 +39,11 @@ M_DECODE = 32
 M_PREFILL = 4096
 
 
+def progress(message):
+    """One progress line on stderr (the JSON result goes to stdout)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {message}", file=sys.stderr, flush=True)
+
+
 def gemm_bytes(M, N, K, group=0):
     scales = 4 * N * K // group + 4 * M * K // group if group else 4 * N + 4 * M
     return N * K + M * K + scales + 2 * M * N
@@ -148,6 +153,7 @@ def main():
     for n in inputs:
         assert torch.equal(inputs[n]["y"], eager[n]), f"graph replay differs from eager ({n})"
 
+    progress("decode step")
     for _ in range(args.warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -175,13 +181,16 @@ def main():
                                      ("fp8", FP8, 0, M_DECODE),
                                      ("group_int8", I8, 128, M_DECODE),
                                      ("group_fp8", FP8, 128, M_DECODE)):
+        progress(f"decode sweep {mode} M={tokens}")
         rows = decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, tokens,
                             max(5, args.steps // 5))
         if mode == "int8" and tokens == M_DECODE:
             per_proj = rows
         sweep[f"{mode} M={tokens}"] = {
             n: {"gemm_us": r["us_per_launch"], "linear_us": r["linear_us"], "GBps": r["GBps"],
-                "frac_hbm": r["frac_hbm"], "path": r["path"]} for n, r in rows.items()}
+                "frac_hbm": r["frac_hbm"], "stream_us": r["stream_us"],
+                "frac_of_stream": r["frac_of_stream"], "path": r["path"]}
+            for n, r in rows.items()}
     # the dominant kernel: the projection that moves the most bytes (gate_up)
     dominant = max(per_proj, key=lambda n: per_proj[n]["bytes"])
     d = per_proj[dominant]
@@ -189,7 +198,8 @@ def main():
                 "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(d["GBps"] / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(dominant),
-                "bytes_per_launch": d["bytes"]}
+                "bytes_per_launch": d["bytes"],
+                "stream_ceiling_us": d["stream_us"], "frac_of_stream": d["frac_of_stream"]}
 
     result = {
         "metric": "INT8/FP8 GEMM TOPS @M=4096 + HBM GB/s @M=32, % of MI355X roofline",
@@ -217,12 +227,16 @@ def main():
     }
 
     if not args.no_prefill:
+        progress("prefill M=4096")
         result["prefill"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args)
+        progress("prefill M=1024")
         result["prefill_m1024"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args,
                                                 M=1024)
+        progress("producers")
         result["producers"] = bench_producers(torch, qlinear, synthetic, dev, stream, args)
 
     if not args.no_cpu:
+        progress("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args, value)
 
     print(json.dumps(result), flush=True)
@@ -278,13 +292,19 @@ def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
         us_linear = time_graph(lambda: [qlinear.linear(x, wc, sw, fmt, group, rot, path=path,
                                                        scratch=(xs, ss), out=y, workspace=wsp,
                                                        stream=stream) for wc in ws], len(ws))
+        # the streaming-read ceiling: the same weight copies read once each
+        # by the plain 16-byte-load kernel (qlin_stream_read), same replay
+        us_stream = time_graph(lambda: [qlinear.stream_read(wc, stream=stream) for wc in ws],
+                               len(ws))
         b = gemm_bytes(M, N, K, group)
         rows[name] = {"N": N, "K": K, "us_per_launch": round(us, 3), "bytes": b,
                       "GBps": round(b / (us * 1e-6) / 1e9, 1),
                       "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                       "path": [path.kind, path.tokens, path.channels, path.splits, path.waves,
                                path.staged],
-                      "linear_us": round(us_linear, 3), "weight_copies": copies}
+                      "linear_us": round(us_linear, 3), "weight_copies": copies,
+                      "stream_us": round(us_stream, 3),
+                      "frac_of_stream": round(us_stream / us, 4)}
         del ws
         torch.cuda.empty_cache()
     return rows
@@ -315,14 +335,27 @@ def measured_traffic(name):
 
 def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections):
     """Kernels for counter passes, in this order: one 64 MiB copy (known
-    traffic: 64 MiB read + 64 MiB written), 5 rounds of each projection's
-    16-layer decode linear (qlin_linear, fused at M=32), then one M=4096 INT8
-    and FP8 GEMM per projection."""
+    traffic: 64 MiB read + 64 MiB written), the streaming-read kernel over 16
+    copies of each projection's weight bytes (two passes), 5 rounds of each projection's
+    16-layer decode linear (qlin_linear, fused at M=32), then one M=4096 INT8,
+    FP8, group_int8 and group_fp8 GEMM per projection."""
     src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
+    # the streaming-read ceiling kernel over each projection's weight bytes,
+    # 16 distinct copies each (so they come from HBM)
+    for name, (N, K) in projections:
+        copies = [torch.empty(N * K, dtype=torch.uint8, device=dev).fill_(c) for c in range(16)]
+        torch.cuda.synchronize()
+        # two passes: the first also pays for writing the fills' dirty lines
+        # back from the caches; the second is the measurement
+        for _ in range(2):
+            for buf in copies:
+                qlinear.stream_read(buf, stream=stream)
+            torch.cuda.synchronize()
+        del copies
     for name, (N, K) in projections:
         io = inputs[name]
         for _ in range(5):
@@ -332,15 +365,17 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
                                stream=stream)
     torch.cuda.synchronize()
     M = M_PREFILL
-    for fmt in (qlinear.I8, qlinear.FP8):
+    for fmt, group in ((qlinear.I8, 0), (qlinear.FP8, 0), (qlinear.I8, 128), (qlinear.FP8, 128)):
+        rot = 128 if group else 0
         for name, (N, K) in projections:
             x = torch.from_numpy(synthetic.activations(M, K, seed=1).view(np.int16)).view(
                 torch.bfloat16).to(dev)
             w = torch.from_numpy(synthetic.weights(N, K, seed=1).view(np.int16)).view(
                 torch.bfloat16).to(dev)
-            xq, sx = qlinear.row_quantize(x, fmt, stream=stream)
-            wq, sw = qlinear.row_quantize(w, fmt, stream=stream)
-            qlinear.gemm(xq, sx, wq, sw, fmt, stream=stream)
+            xq, sx = qlinear.row_quantize(x, fmt, group=group, rotation=rot, stream=stream)
+            wq, sw = qlinear.row_quantize(w, fmt, group=group, rotation=rot, stream=stream)
+            qlinear.gemm(xq, sx, wq, sw, fmt, input_group=group, weight_group=group,
+                         stream=stream)
             torch.cuda.synchronize()
 
 

@@ -1,0 +1,50 @@
+// qlin_stream_read: the streaming-read ceiling that the decode GEMMs are
+// measured against. No counterpart in the reference: a measurement helper
+// for bench.py. It reads `bytes` of device memory once with 16-byte loads
+// (512 workgroups of 512 threads, 4 loads in flight per lane, each workgroup
+// a contiguous share), xor-reduces what it read and stores to `sink` only on
+// an impossible value, so nothing but the reads reach memory.
+#include <hip/hip_runtime.h>
+
+#include "qlin_internal.hpp"
+
+namespace {
+
+constexpr int kWorkgroups = 512, kThreads = 512, kUnroll = 4;
+
+__global__ __launch_bounds__(kThreads) void stream_read(const uint4 *__restrict__ src, long per_wg,
+                                                        long total, unsigned *sink) {
+    const long first = long(blockIdx.x) * per_wg;
+    const long last = blockIdx.x + 1 == gridDim.x ? total : first + per_wg;
+    unsigned acc = 0;
+    for (long i = first + threadIdx.x; i < last; i += long(kThreads) * kUnroll) {
+        uint4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const long j = i + long(u) * kThreads;
+            v[u] = j < last ? src[j] : uint4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u && sink) sink[blockIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" int qlin_stream_read(const void *src, size_t bytes, unsigned *sink,
+                                qlin_stream_t stream) {
+    if (!src || bytes == 0 || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+        return qlin::set_error(QLIN_ERR_INVALID,
+                               "qlin_stream_read: src must be 16-byte aligned, bytes a nonzero "
+                               "multiple of 16");
+    const long total = long(bytes / 16);
+    const long per_wg = (total + kWorkgroups - 1) / kWorkgroups;
+    const int wgs = int((total + per_wg - 1) / per_wg);
+    hipLaunchKernelGGL(stream_read, dim3(wgs), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), static_cast<const uint4 *>(src),
+                       per_wg, total, sink);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? QLIN_OK
+                           : qlin::set_error(QLIN_ERR_HIP, "qlin_stream_read: launch failed");
+}

@@ -276,3 +276,13 @@ def test_noalloc_scratch_limit():
     rc = L.qlin_linear_noalloc(None, FAKE, 16384, BF16, FAKE, FAKE, FAKE, 4096, 16, 16384, I8,
                                BF16, 0, 0, 0, None)
     assert rc == -3 and b"fixed" in L.qlin_last_error()
+
+
+def test_stream_read_validation():
+    """The streaming-read ceiling kernel rejects unaligned or ragged buffers
+    before launching."""
+    L = qlinear.load()
+    assert L.qlin_stream_read(FAKE + 8, 1 << 20, None, None) == -1
+    assert L.qlin_stream_read(FAKE, (1 << 20) + 4, None, None) == -1
+    assert L.qlin_stream_read(FAKE, 0, None, None) == -1
+    assert L.qlin_stream_read(None, 1 << 20, None, None) == -1
