@@ -188,7 +188,7 @@ def main():
             per_proj = rows
         sweep[f"{mode} M={tokens}"] = {
             n: {"gemm_us": r["us_per_launch"], "linear_us": r["linear_us"], "GBps": r["GBps"],
-                "frac_hbm": r["frac_hbm"], "stream_us": r["stream_us"],
+                "frac_hbm": r["frac_hbm"], "stream_us": r["stream_us"], "warm_us": r["warm_us"],
                 "frac_of_stream": r["frac_of_stream"], "path": r["path"]}
             for n, r in rows.items()}
     # the dominant kernel: the projection that moves the most bytes (gate_up)
@@ -245,7 +245,9 @@ def main():
 def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
     """Per projection at M tokens: the GEMM alone and the linear (quantize +
     GEMM, qlin_linear) over distinct weight copies totalling >= 640 MB, each
-    graph replayed `reps` times; microseconds per launch."""
+    graph replayed `reps` times; microseconds per launch. Also the GEMM warm
+    (one weight copy, cache-resident) and the streaming-read ceiling over the
+    same copies."""
     rot = 128 if group else 0
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -292,6 +294,12 @@ def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
         us_linear = time_graph(lambda: [qlinear.linear(x, wc, sw, fmt, group, rot, path=path,
                                                        scratch=(xs, ss), out=y, workspace=wsp,
                                                        stream=stream) for wc in ws], len(ws))
+        # warm (cache-resident): the first copy 16 times in a row, so L2 and
+        # the Infinity Cache serve the weights after the first launch
+        us_warm = time_graph(lambda: [qlinear.gemm(xq, sx, ws[0], sw, fmt, input_group=group,
+                                                   weight_group=group, path=path, out=y,
+                                                   workspace=wsp, stream=stream)
+                                      for _ in range(16)], 16)
         # the streaming-read ceiling: the same weight copies read once each
         # by the plain 16-byte-load kernel (qlin_stream_read), same replay
         us_stream = time_graph(lambda: [qlinear.stream_read(wc, stream=stream) for wc in ws],
@@ -303,7 +311,7 @@ def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
                       "path": [path.kind, path.tokens, path.channels, path.splits, path.waves,
                                path.staged],
                       "linear_us": round(us_linear, 3), "weight_copies": copies,
-                      "stream_us": round(us_stream, 3),
+                      "stream_us": round(us_stream, 3), "warm_us": round(us_warm, 3),
                       "frac_of_stream": round(us_stream / us, 4)}
         del ws
         torch.cuda.empty_cache()
