@@ -140,7 +140,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //  - K groups (no wide-kernel variant), eight waves, both formats:
     //    256x128 (128x32 waves) for >= 256 tiles in full rounds (gate_up at
     //    4096: INT8 193 us against 222 us on 128x128, FP8 193 us against
-    //    216 us), else 128x128 (64x32 waves): down at 1024 INT8 52 us
+    //    216 us), else 128x128 (64x32 waves): down at 1024 INT8 44 us
     //    against 80 us on 256x128. Groups of 32 / 64 follow the same rule
     //    for INT8 (qkv at 4096, G 32: 219 us against 267 us); FP8 takes
     //    128x128 (255 us against 428 us).

@@ -94,12 +94,14 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     constexpr int W_INSTS = BN / (RPI * NW);
     // K-group kernels: each stage slot also holds the stage's group scales
     // (weight [BN] floats in its first KB, token [BM] floats in the second),
-    // copied by one extra DMA instruction of wave 0 (weights) and wave 1
-    // (tokens). Each gets a whole KB: a lane past the tile still writes
-    // (zeros) at its position. Groups of GS = 32 / 64 (the smaller of the two
-    // operands' group sizes) read their scales from global memory instead.
+    // copied by one extra DMA instruction per wave: wave 0 the weight scales,
+    // wave 1 the token scales, the other waves nothing (out-of-range offsets
+    // into a third, unused KB), so that the issue has no branch. Each gets a
+    // whole KB: a lane past the tile still writes (zeros) at its position.
+    // Groups of GS = 32 / 64 (the smaller of the two operands' group sizes)
+    // read their scales from global memory instead.
     constexpr bool kScaleDma = Grouped && GS == 128;
-    constexpr int SCALE_BYTES = kScaleDma ? 2048 : 0;
+    constexpr int SCALE_BYTES = kScaleDma ? 3072 : 0;
     constexpr int STAGE_BYTES = ROWS * BK + SCALE_BYTES;
     static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
     static_assert(!kScaleDma || (BN * 4 <= 1024 && BM * 4 <= 1024 && NW >= 2),
@@ -169,6 +171,14 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // group go in the uniform offset.
     const uint32_t lane_voff_p =
         uint32_t((lane_chunk / 4) * 1024 + (lane_chunk % 4) * 256 + lane_row * 16);
+    // The scale DMA's per-lane offset (host-checked: both scale arrays stay
+    // below 2^31 bytes): group g's row starts at g * scale_stride.
+    const bool scale_wv = wave == 0, scale_xv = wave == 1;
+    const bool scale_live = Grouped && (scale_wv || scale_xv) &&
+                            (scale_wv ? weight_group : input_group) &&
+                            lane * 4 < (scale_wv ? BN : BM);
+    const uint32_t scale_stride = uint32_t((scale_wv ? N : M) * 4);
+    const uint32_t scale_lane = uint32_t((scale_wv ? n_base : m_base) * 4 + lane * 16);
     auto issue = [&](int stage, int k0) {
         uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
         const bool kin = KFull || k0 + lane_chunk * 16 < K;
@@ -191,27 +201,21 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         if constexpr (kScaleDma) {
             // The stage's group scales: sw[g][n_base ..) by wave 0, sx[g][m_base ..)
             // by wave 1 (lanes past the tile, or an operand without groups,
-            // read zero through an out-of-range offset).
-            const int g = k0 / kGroupK;
-            if (wave < 2) {
-                const bool wv = wave == 0;
-                const int grp = wv ? weight_group : input_group;
-                const int count = wv ? BN : BM;
-                const uint32_t off = (grp && lane * 4 < count)
-                                         ? uint32_t((size_t(g) * (wv ? N : M) + (wv ? n_base : m_base)) * 4 + lane * 16)
-                                         : 0x80000000u;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wv ? rsrc_sw : rsrc_sx,
-                                                         (lds_ptr_t)(base + ROWS * BK + (wv ? 0 : 1024)),
-                                                         16, off, 0, 0, 0);
-            }
+            // read zero through an out-of-range offset); waves 2.. write zeros
+            // into the slot's third KB.
+            const uint32_t g = uint32_t(k0 / kGroupK);
+            const uint32_t off = scale_live ? g * scale_stride + scale_lane : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                scale_wv ? rsrc_sw : rsrc_sx,
+                (lds_ptr_t)(base + ROWS * BK + (scale_wv ? 0 : scale_xv ? 1024 : 2048)), 16, off, 0,
+                0, 0);
         }
     };
-    // "Stage s+1 has landed" waits: waves 0 and 1 of a K-group kernel issue
-    // one more instruction per stage.
+    // "Stage s+1 has landed" waits: the waves of a K-group kernel issue one
+    // more instruction per stage.
     auto wait_ring = [&](auto outstanding_stages) {
         constexpr int S = decltype(outstanding_stages)::value;
-        if (kScaleDma && wave < 2) wait_vmcnt<(INSTS + 1) * S>();
-        else wait_vmcnt<INSTS * S>();
+        wait_vmcnt<(INSTS + (kScaleDma ? 1 : 0)) * S>();
     };
 
     Acc acc[(Grouped || kMF32) ? 1 : WTN][(Grouped || kMF32) ? 1 : WTM];
@@ -566,10 +570,134 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                 }
             }
         };
+      // Two banks of partials (INT8 tiles of at most 8 MFMA tiles per wave,
+      // i.e. 128x128 with eight 64x32 waves): group g accumulates in bank
+      // g % 2, and its conversion and fma run during group g+1's first stage,
+      // interleaved with that stage's MFMAs of the other bank, so one wave's
+      // VALU and MFMA work overlap. Larger wave tiles have no registers for
+      // the second bank (it spilled on 256x128) and apply each group at its
+      // last stage instead.
+      constexpr bool kTwoBanks = Fmt == I8 && WTN * WTM <= 8 && SPG == 2;
+      if constexpr (kTwoBanks) {
+        Acc pp[2][WTN][WTM];
+        float xg[WTM];
+        f32x4 wg[WTN];
+        // Scales of group g from its last stage's slot (read before that
+        // step's barrier: the next step's DMA refills the slot).
+        auto load_scales = [&](int st) {
+            const float *slot = reinterpret_cast<const float *>(lds + (st % STAGES) * STAGE_BYTES +
+                                                                ROWS * BK);
+#pragma unroll
+            for (int j = 0; j < WTM; ++j)
+                xg[j] = input_group ? slot[256 + wave_m * 16 * WTM + j * 16 + row16] : 1.f;
+#pragma unroll
+            for (int i = 0; i < WTN; ++i)
+                wg[i] = weight_group ? *reinterpret_cast<const f32x4 *>(slot + wave_n * 16 * WTN +
+                                                                         i * 16 + quad * 4)
+                                     : f32x4{1.f, 1.f, 1.f, 1.f};
+        };
+        auto apply = [&](auto bank_) {
+            constexpr int B = decltype(bank_)::value;
+#pragma unroll
+            for (int i = 0; i < WTN; ++i)
+#pragma unroll
+                for (int j = 0; j < WTM; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        facc[i][j][r] = __builtin_fmaf(float(pp[B][i][j][r]), xg[j] * wg[i][r],
+                                                       facc[i][j][r]);
+        };
+        // One stage into bank B. In the main loop every flag is a compile-time
+        // constant and every stage-bound check is known to pass (Check =
+        // false), so the step has no branches and the compiler interleaves
+        // the previous group's conversion and fma with this stage's MFMAs;
+        // the first group and the last stages run with run-time checks.
+        auto step = [&](int s, auto bank_, auto first_, auto last_, auto apply_, auto check_,
+                        const Frag (&a)[WTN], const Frag (&bb)[WTM], Frag (&na)[WTN],
+                        Frag (&nb)[WTM]) {
+            constexpr int B = decltype(bank_)::value;
+            constexpr bool Check = decltype(check_)::value;
+            const bool first = Check ? s % SPG == 0 : decltype(first_)::value;
+            const bool last = Check ? (s % SPG == SPG - 1 || s + 1 == stages) : decltype(last_)::value;
+            const bool apply_prev = Check ? (first && s > 0) : decltype(apply_)::value;
+            // Without checks and with the previous group to apply, each MFMA
+            // of this bank is followed by the 12 VALU operations (convert,
+            // scale product, fma for 4 elements) of the other bank's same
+            // tile, in that order.
+            constexpr bool kInterleave = !Check && decltype(apply_)::value;
+#pragma unroll
+            for (int i = 0; i < WTN; ++i)
+#pragma unroll
+                for (int j = 0; j < WTM; ++j) {
+                    if (first) pp[B][i][j] = Acc{0, 0, 0, 0};
+                    MMA::run(pp[B][i][j], a[i], bb[j]);
+                    if constexpr (kInterleave) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            facc[i][j][r] = __builtin_fmaf(float(pp[1 - B][i][j][r]),
+                                                           xg[j] * wg[i][r], facc[i][j][r]);
+                    }
+                }
+            if constexpr (kInterleave) {
+#pragma unroll
+                for (int k = 0; k < WTN * WTM; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // twelve VALU
+                }
+                // Keep the updated accumulators in this step (not moved to a
+                // loop boundary, away from the MFMAs they interleave with).
+#pragma unroll
+                for (int i = 0; i < WTN; ++i)
+#pragma unroll
+                    for (int j = 0; j < WTM; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(facc[i][j][r]));
+            } else if (apply_prev) {
+                apply(std::integral_constant<int, 1 - B>{});
+            }
+            // The next DMA after this stage's MFMAs: its control flow would
+            // otherwise split the MFMA / VALU region.
+            if (!Check || s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
+            if (last) load_scales(s);
+            if (!Check || s + STAGES - 1 < stages) wait_ring(std::integral_constant<int, STAGES - 2>{});
+            else if (s + 1 < stages) wait_vmcnt<0>();
+            lds_barrier();
+            if (!Check || s + 1 < stages) read(s + 1, na, nb);
+        };
+        using B0 = std::integral_constant<int, 0>;
+        using B1 = std::integral_constant<int, 1>;
+        using T = std::true_type;
+        using F = std::false_type;
+        Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
+        if (stages >= STAGES - 1) wait_ring(std::integral_constant<int, STAGES - 2>{});
+        else wait_vmcnt<0>();
+        lds_barrier();
+        read(0, a0, b0);
+        // Group 0 (bank 0), checked.
+        step(0, B0{}, F{}, F{}, F{}, T{}, a0, b0, a1, b1);
+        if (1 < stages) step(1, B0{}, F{}, F{}, F{}, T{}, a1, b1, a0, b0);
+        // Groups 1, 2, ... in pairs (banks 1, 0) while all four stages and
+        // their DMAs lie inside K.
+        int s = 2;
+        for (; s + 3 + STAGES - 1 < stages; s += 4) {
+            step(s, B1{}, T{}, F{}, T{}, F{}, a0, b0, a1, b1);
+            step(s + 1, B1{}, F{}, T{}, F{}, F{}, a1, b1, a0, b0);
+            step(s + 2, B0{}, T{}, F{}, T{}, F{}, a0, b0, a1, b1);
+            step(s + 3, B0{}, F{}, T{}, F{}, F{}, a1, b1, a0, b0);
+        }
+        // The remaining stages (at most STAGES + 2), checked; s is even here,
+        // so stage s opens a group of bank 1.
+        for (; s < stages; s += 4) {
+            step(s, B1{}, F{}, F{}, F{}, T{}, a0, b0, a1, b1);
+            if (s + 1 < stages) step(s + 1, B1{}, F{}, F{}, F{}, T{}, a1, b1, a0, b0);
+            if (s + 2 < stages) step(s + 2, B0{}, F{}, F{}, F{}, T{}, a0, b0, a1, b1);
+            if (s + 3 < stages) step(s + 3, B0{}, F{}, F{}, F{}, T{}, a1, b1, a0, b0);
+        }
+        if (((stages - 1) / SPG) % 2 == 0) apply(B0{});
+        else apply(B1{});
+      } else {
         // One set of partials: group g's MFMAs accumulate natively (exact
-        // int32 for INT8) and the group is applied at its last stage. (A
-        // ping-pong set that defers the conversion to the next group's first
-        // stage needs registers the 8-wave tiles do not have: it spilled.)
+        // int32 for INT8) and the group is applied at its last stage.
         // With two waves per SIMD the other wave's MFMAs run while one wave
         // waits for its last MFMA result.
         Acc part[WTN][WTM];
@@ -626,6 +754,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             step(s + 1, a1, b1, a0, b0);
         }
         if (s < stages) step(s, a0, b0, a1, b1);
+      }
     }
 
     // Epilogue. A lane holds C[n = 4*quad + r][m = row16] of each 16x16 tile:
@@ -977,7 +1106,7 @@ template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Gr
 int launch_shape(const GemmArgs &a, hipStream_t stream) {
     constexpr int BN = 16 * WTN * WN, BM = 16 * WTM * WM;
     const int tiles_n = (a.N + BN - 1) / BN, tiles_m = (a.M + BM - 1) / BM;
-    const size_t stage = size_t(BN + BM) * BK + (Grouped && GS == 128 ? 2048 : 0);
+    const size_t stage = size_t(BN + BM) * BK + (Grouped && GS == 128 ? 3072 : 0);
     const size_t lds = std::max(size_t(STAGES) * stage, size_t(BN) * BM * 2) + size_t(BN + BM) * 4;
     dim3 grid(unsigned(tiles_n * tiles_m)), block(64 * WN * WM);
 #define QLIN_TILED(KF, PW)                                                                      \

@@ -110,6 +110,7 @@ def test_prefill_plan_rules():
     assert tile(4096, "qkv", I8, 128) == (256, 128, 8) and tile(4096, "qkv", FP8, 128) == (256, 128, 8)
     assert tile(1024, "gate_up", I8, 128) == (128, 128, 8) and tile(1024, "gate_up", FP8, 128) == (128, 128, 8)
     assert tile(4096, "qkv", I8, 32) == (256, 128, 8) and tile(4096, "qkv", FP8, 64) == (128, 128, 8)
+    assert tile(4096, "down", I8, 128) == (256, 128, 8) and tile(1024, "down", I8, 128) == (128, 128, 8)
 
 
 def test_plan_and_workspace():
