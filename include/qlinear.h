@@ -342,8 +342,10 @@ int qlin_linear_noalloc(const qlin_path *path, const void *x, int ld, int src_ty
 /* Streaming-read ceiling (measurement helper; no counterpart in the
  * reference). Reads `bytes` (a nonzero multiple of 16) at 16-byte aligned
  * `src` once with 16-byte loads, 512 workgroups of 512 threads; writes
- * nothing except, never in practice, to `sink` (may be NULL). bench.py times
- * it over the decode weight sizes as the ceiling for the decode GEMMs. */
+ * nothing except, never in practice, to `sink` (NULL, or room for 512
+ * unsigned values: a workgroup stores its xor only if it equals one fixed
+ * constant, which keeps the loads live). bench.py times it over the decode
+ * weight sizes as the ceiling for the decode GEMMs. */
 int qlin_stream_read(const void *src, size_t bytes, unsigned *sink, qlin_stream_t stream);
 
 #ifdef __cplusplus
