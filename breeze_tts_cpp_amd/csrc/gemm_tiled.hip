@@ -533,51 +533,31 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             }
         }
     } else {
-        // K groups of 128: the per-channel software pipeline (fragments of
-        // stage s+1 read while stage s's MFMAs run), with the MFMAs of group
-        // g accumulated natively in part[g % 2] (exact int32 for INT8) and
-        // applied as facc = fmaf(p, sx_g * sw_g, facc), groups ascending,
-        // during the first stage of group g + 1, so that the conversion and
-        // fma of one group run under the next group's MFMAs. The group's
-        // scales come with its last stage (the stage slot's scale rows) and
-        // are held in registers until they are applied.
-        using Frag = std::conditional_t<Fmt == I8, i32x4, i32x8>;
+        // INT8 K groups of 128: the per-channel software pipeline (fragments
+        // of stage s+1 read while stage s's MFMAs run). Each group's MFMAs
+        // accumulate natively (exact int32) and the group is applied as
+        // facc = fmaf(p, sx_g * sw_g, facc), groups ascending. The group's
+        // scales come with its last stage (the stage slot's scale rows).
+        static_assert(Fmt == I8 && BK == 64, "the pipelined K-group path is INT8 on 64-byte stages");
+        using Frag = i32x4;
         const int a_off = a_row0 * BK, b_off = b_row0 * BK;
         const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
-        const int a_c1 = ((4 + quad) ^ swizzle<BK>(a_row0)) * 16;
-        const int b_c1 = ((4 + quad) ^ swizzle<BK>(b_row0)) * 16;
         auto read = [&](int st, Frag (&a)[WTN], Frag (&bb)[WTM]) {
             const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
             const uint8_t *pa = cur + a_off, *pb = cur + b_off;
 #pragma unroll
-            for (int j = 0; j < WTM; ++j) {
-                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c0);
-                if constexpr (Fmt == I8) {
-                    bb[j] = lo;
-                } else {
-                    const i32x4 hi = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c1);
-                    bb[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
-            }
+            for (int j = 0; j < WTM; ++j) bb[j] = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c0);
 #pragma unroll
-            for (int i = 0; i < WTN; ++i) {
-                const i32x4 lo = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c0);
-                if constexpr (Fmt == I8) {
-                    a[i] = lo;
-                } else {
-                    const i32x4 hi = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c1);
-                    a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
-            }
+            for (int i = 0; i < WTN; ++i) a[i] = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c0);
         };
-      // Two banks of partials (INT8 tiles of at most 8 MFMA tiles per wave,
-      // i.e. 128x128 with eight 64x32 waves): group g accumulates in bank
-      // g % 2, and its conversion and fma run during group g+1's first stage,
-      // interleaved with that stage's MFMAs of the other bank, so one wave's
-      // VALU and MFMA work overlap. Larger wave tiles have no registers for
-      // the second bank (it spilled on 256x128) and apply each group at its
-      // last stage instead.
-      constexpr bool kTwoBanks = Fmt == I8 && WTN * WTM <= 8 && SPG == 2;
+      // Two banks of partials (tiles of at most 8 MFMA tiles per wave, i.e.
+      // 128x128 with eight 64x32 waves): group g accumulates in bank g % 2,
+      // and its conversion and fma are spread over group g+1's first stage,
+      // one MFMA of the other bank between every 12 of them (gfx950 overlaps
+      // VALU and MFMA work only a little, so this gains 5-13%, not the whole
+      // rescale). Larger wave tiles have no registers for the second bank
+      // (it spilled on 256x128) and apply each group at its last stage.
+      constexpr bool kTwoBanks = WTN * WTM <= 8 && SPG == 2;
       if constexpr (kTwoBanks) {
         Acc pp[2][WTN][WTM];
         float xg[WTM];
@@ -1139,14 +1119,18 @@ int dispatch_small_groups(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     return -4;
 }
 
-// Macro tiles (weight rows x tokens): 256x256 with eight waves of 128x64;
-// 256x128 (waves of 128x64) and 128x128 (64x64) with four.
+// Macro tiles (weight rows x tokens) and waves per path: 256x256 with eight
+// waves of 128x64 (waves 8) or four of 128x128 on 32x32 MFMAs (wide_gemm,
+// waves 4); 256x128 with eight waves of 128x32 (8), one workgroup of four
+// 128x64 waves (1) or two 128x128 waves (2); 128x128 with eight waves of
+// 64x32 (8) or four of 64x64 (1).
 template <int Fmt, bool Grouped, class Out>
 int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if constexpr (Grouped) {
         // No 256x256: the fp32 group accumulators would double the 128x128
-        // register tile per wave and spill.
-        // INT8 in 64-byte stages (two per group), FP8 in 128-byte stages.
+        // register tile per wave and spill. INT8 in 64-byte stages (two per
+        // group; the 8-wave 128x128 tile runs two accumulator banks), FP8 in
+        // 128-byte stages.
         constexpr int GBK = Fmt == I8 ? 64 : 128;
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 2, GBK, GBK == 64 ? 4 : 3, true, Out>(a, s);
