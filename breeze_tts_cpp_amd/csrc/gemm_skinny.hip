@@ -81,6 +81,28 @@ __device__ __forceinline__ i32x4 load16(const uint8_t *p) {
     return *reinterpret_cast<const i32x4 *>(p);
 }
 
+// Four 16-byte LDS reads by explicit ds_read_b128 instructions and their
+// wait, in one statement. The compiler's wait insertion treats any LDS read
+// as possibly reading what an outstanding global->LDS copy writes and then
+// waits for every outstanding vector load; reads of a region whose copy the
+// caller has already waited for (counted vmcnt) go through this path so that
+// later copies, still in flight, are not waited for. The wait is inside the
+// statement because the compiler does not know these reads are pending: no
+// instruction may consume the results before it.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
+    typedef __attribute__((address_space(3))) const uint8_t *lds_cptr_t;
+    return uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_t)p));
+}
+__device__ __forceinline__ void lds_read16x4(const uint8_t *p0, const uint8_t *p1,
+                                             const uint8_t *p2, const uint8_t *p3, i32x4 &v0,
+                                             i32x4 &v1, i32x4 &v2, i32x4 &v3) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\t"
+        "ds_read_b128 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+        : "v"(lds_addr(p0)), "v"(lds_addr(p1)), "v"(lds_addr(p2)), "v"(lds_addr(p3)));
+}
+
 template <class Out>
 __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4]) {
     uint2 packed;
@@ -186,7 +208,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // range, requested before the weight slab so that they land first. Lane
     // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
     // row m0 + 16t + row16: exactly the codes its MFMA B fragments need.
-    static_assert(!FQ || (NB > 0 && !Packed && !Grouped && !Split && MT == 1 && NB == 1 && Fmt == I8),
+    static_assert(!FQ || (NB > 0 && !Packed && !Grouped && !Split && NB * MT <= 3),
                   "fused quantization: per-wave slab, activation blocks in registers");
     uint4 xraw[FQ ? NB : 1][MT][4][2];
     if constexpr (FQ && !XL) {
@@ -344,13 +366,13 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // XL: the activation fragments of block kb from the staged tile.
     auto xfrag = [&](int kb, i32x4 (&b)[MT][4]) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const int g = ((kb - slab_k0) + p * 64) / 16 + quad;
-                b[t][p] = *reinterpret_cast<const i32x4 *>(xtile + (t * 16 + row16) * kActRowBytes +
-                                                           ((g ^ row16) << 4));
-            }
+        for (int t = 0; t < MT; ++t) {
+            const uint8_t *row = xtile + (t * 16 + row16) * kActRowBytes;
+            const int g0 = (kb - slab_k0) / 16 + quad;
+            lds_read16x4(row + ((g0 ^ row16) << 4), row + (((g0 + 4) ^ row16) << 4),
+                         row + (((g0 + 8) ^ row16) << 4), row + (((g0 + 12) ^ row16) << 4),
+                         b[t][0], b[t][1], b[t][2], b[t][3]);
+        }
     };
     if constexpr (FQ) {
         // The per-token quantizer's arithmetic (row_quantize.hip
@@ -376,13 +398,20 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
                 for (int t = 0; t < MT; ++t)
 #pragma unroll
-                    for (int p = 0; p < 4; ++p)
+                    for (int p = 0; p < 4; p += 2) {
+                        // granules of pieces p and p + 1, halves 0 and 1
+                        const uint8_t *row = xtile + (t * 16 + row16) * kActRowBytes;
+                        const int g = blk * 32 + p * 8 + quad * 2;
+                        i32x4 r[4];
+                        lds_read16x4(row + ((g ^ row16) << 4), row + (((g + 1) ^ row16) << 4),
+                                     row + (((g + 8) ^ row16) << 4), row + (((g + 9) ^ row16) << 4),
+                                     r[0], r[1], r[2], r[3]);
 #pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            const int g = blk * 32 + p * 8 + quad * 2 + h;
-                            xraw[blk][t][p][h] = *reinterpret_cast<const uint4 *>(
-                                xtile + (t * 16 + row16) * kActRowBytes + ((g ^ row16) << 4));
-                        }
+                        for (int q = 0; q < 4; ++q)
+                            xraw[blk][t][p + q / 2][q % 2] =
+                                uint4{uint32_t(r[q][0]), uint32_t(r[q][1]), uint32_t(r[q][2]),
+                                      uint32_t(r[q][3])};
+                    }
         }
         // FQ 1: bf16 source, 2: f16 source.
         using Tin = std::conditional_t<FQ == 2, f16_t, bf16_t>;
@@ -662,14 +691,17 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             }
         });
         if constexpr (FQ) {
-            // Column tile 0 fills the scratch activation, after its MFMAs so
-            // that the stores do not delay the slab wait.
-            if (blockIdx.x == 0) {
+            // The scratch activation is filled after the MFMAs, so that the
+            // stores do not delay the slab waits, and spread over column
+            // tiles so that no workgroup carries all of it: wave w's K range
+            // of this token tile is written by column tile w % (column
+            // tiles), the scales by column tile 0.
+            if (int(blockIdx.x) == wave % int(gridDim.x)) {
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     const int m = m0 + t * 16 + row16;
                     if (!xvalid[t]) continue;
-                    if (wave == 0 && quad == 0) fq.sx[m] = fq_scale[t * 16 + row16];
+                    if (blockIdx.x == 0 && wave == 0 && quad == 0) fq.sx[m] = fq_scale[t * 16 + row16];
 #pragma unroll
                     for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
@@ -919,50 +951,51 @@ int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 template <int Fmt, int MT, int NF, int NB, bool XL>
 int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     // Every workgroup quantizes its token rows again (the activation is
-    // re-encoded once per column tile), which pays only while that ALU work
-    // is small. Measured on MI355X (graphs of 16 launches over distinct
-    // weights), single launch against quantizer + GEMM: INT8 K = 2048 with
-    // 16-token tiles qkv 5.7-6.9 us vs 6.7-7.7, o_proj 5.4-6.6 vs 5.9-7.0,
-    // gate_up (M <= 16) 8.5-8.6 vs 9.6-9.9; a 32-token tile (gate_up M = 32)
-    // 12.0 vs 11.8; K = 6144 (down) 14.1 vs 9.8; FP8 (integer e4m3 encoder,
-    // ~15 VALU ops per value) 13-26 us vs 6.4-12.
-    if constexpr (MT == 1 && NB == 1 && Fmt == I8) {
-        const int span = NB * kBlockK;
-        dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
-        // slabs, (XL) 16-bit activation tiles, the absmax / scale exchange
-        const size_t lds = size_t(kWaves) * 16 * (NF + (XL ? 2 * MT : 0)) * NB * kBlockK +
-                           size_t(kWaves + 1) * MT * 16 * 4;
-        if (a.fq.f16)
-            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 2, 128, XL>),
-                               grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
-                               a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
-                               int(a.out_type == F16), a.fq);
-        else
-            hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 1, 128, XL>),
-                               grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
-                               a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
-                               int(a.out_type == F16), a.fq);
-        return 0;
-    }
-    return -4;
+    // re-encoded once per column tile). That ALU work overlaps the weight
+    // slab's DMA: the encoding waits only for the 16-bit activation loads,
+    // issued ahead of the slab.
+    const int span = NB * kBlockK;
+    dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
+    // slabs, (XL) 16-bit activation tiles, the absmax / scale exchange
+    const size_t lds = size_t(kWaves) * 16 * (NF + (XL ? 2 * MT : 0)) * NB * kBlockK +
+                       size_t(kWaves + 1) * MT * 16 * 4;
+    if (a.fq.f16)
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 2, 128, XL>),
+                           grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
+                           a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
+                           int(a.out_type == F16), a.fq);
+    else
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 1, 128, XL>),
+                           grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
+                           a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
+                           int(a.out_type == F16), a.fq);
+    return 0;
 }
-template <int Fmt>
-int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    if (p.tokens != 16 || a.K != kWaves * kBlockK) return -4;
-    if (p.staged == 2) {
-        switch (p.channels) {
-        case 16: return launch_fused_nb<Fmt, 1, 1, 1, true>(a, s);
-        case 32: return launch_fused_nb<Fmt, 1, 2, 1, true>(a, s);
-        case 48: return launch_fused_nb<Fmt, 1, 3, 1, true>(a, s);
-        default: return -4;
-        }
-    }
+template <int Fmt, int MT, int NB, bool XL>
+int launch_fused_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.channels) {
-    case 16: return launch_fused_nb<Fmt, 1, 1, 1, false>(a, s);
-    case 32: return launch_fused_nb<Fmt, 1, 2, 1, false>(a, s);
-    case 48: return launch_fused_nb<Fmt, 1, 3, 1, false>(a, s);
+    case 16: return launch_fused_nb<Fmt, MT, 1, NB, XL>(a, s);
+    case 32: return launch_fused_nb<Fmt, MT, 2, NB, XL>(a, s);
+    case 48: return launch_fused_nb<Fmt, MT, 3, NB, XL>(a, s);
     default: return -4;
     }
+}
+// Variants (skinny_fused_supported lists them): INT8, 16-token tiles, one
+// 256-column block of K per wave (staged 2: the 16-bit activation rows
+// through LDS; staged 1: in registers). Measured on MI355X (graphs of
+// launches over distinct weights, bf16 source): qkv at M = 32 6.2 us against
+// 6.7 us for quantizer + GEMM, o_proj 5.5 against 5.9. The kernel also
+// takes 32-token tiles and two or three blocks per wave, but every
+// workgroup re-encodes its rows, and there the encoding no longer hides
+// under the weight stream: gate_up at M = 32 (32-token tile) 11.4 us
+// against 10.2, down (three blocks) 13.9 against 10.2, FP8 (integer e4m3
+// encoder) 13.7 against 7.3 for qkv.
+template <int Fmt>
+int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
+    if constexpr (Fmt != I8) return -4;
+    if (p.tokens != 16 || span_of(a.K, 1) != kBlockK) return -4;
+    if (p.staged == 2) return launch_fused_nf<Fmt, 1, 1, true>(a, p, s);
+    return launch_fused_nf<Fmt, 1, 1, false>(a, p, s);
 }
 
 template <int Fmt, bool Grouped, int GS = 128>
@@ -1013,11 +1046,17 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
 }
 
 bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
-    return a.fq.src && !a.packed && !a.bias && !a.act && !a.input_group && !a.weight_group &&
-           p.kind == KIND_SKINNY && p.splits == 1 && p.waves == kWaves && (p.staged == 1 || p.staged == 2) &&
-           a.fmt == I8 && a.K == kWaves * kBlockK && p.tokens == 16 &&
-           (p.channels == 16 || p.channels == 32 || p.channels == 48) &&
-           skinny_lds_bytes(a, p) <= kLdsBytes;
+    if (!a.fq.src || a.packed || a.bias || a.act || a.input_group || a.weight_group ||
+        a.fmt != I8 || p.kind != KIND_SKINNY || p.splits != 1 || p.waves != kWaves ||
+        (p.staged != 1 && p.staged != 2) || p.tokens != 16 ||
+        (p.channels != 16 && p.channels != 32 && p.channels != 48) ||
+        span_of(a.K, 1) != kBlockK)
+        return false;
+    // slabs, (staged 2) the 16-bit activation tiles, the absmax exchange
+    const size_t lds = size_t(kWaves) * p.channels * kBlockK +
+                       (p.staged == 2 ? size_t(kWaves) * 16 * 2 * kBlockK : 0) +
+                       size_t(kWaves + 1) * p.tokens * 4;
+    return lds <= size_t(kLdsBytes);
 }
 
 #endif

@@ -1,10 +1,12 @@
-"""qlin_linear's one-launch decode form: for per-token scales on a decode
-INT8 path with 16-token tiles, per-wave weight slabs and K = 2048, the GEMM
-quantizes its own token rows (the arithmetic of the per-token quantizer, reference
-row_quantize.cu:24-87) instead of a separate quantizer launch. Checked
-against the two-launch form on the same inputs (qlin_row_quantize +
-qlin_gemm with the same path): output bits identical for INT8 and FP8, and
-the scratch activation (codes and scales) equal to the oracle's quantizer."""
+"""qlin_linear's one-launch decode form: for per-token INT8 scales on a
+decode path with 16-token tiles, per-wave weight slabs and one 256-column
+block of K per wave (K <= 2048), the GEMM quantizes its own token rows (the
+arithmetic of the per-token quantizer, reference row_quantize.cu:24-87)
+instead of a separate quantizer launch. Checked against the two-launch form
+on the same inputs (qlin_row_quantize + qlin_gemm with the same path):
+output bits identical for INT8 and FP8 (FP8 and every other path take the
+two-launch form), and the scratch activation (codes and scales) equal to
+the oracle's quantizer."""
 import numpy as np
 import pytest
 import torch
@@ -32,12 +34,18 @@ def lds_bytes(path, K, fused=False):
     return 8 * 256 * nb * (path.channels + act) + (9 * path.tokens * 4 if fused else 0)
 
 
-def fused_eligible(path, M, K):
-    """The library's rule for the fused form (per-token, planned skinny path
-    with per-wave slabs, eight waves, no split, 16-token tiles, K == 2048,
-    within LDS; INT8 only)."""
-    return (path.kind == 1 and path.splits == 1 and path.waves == 8 and path.staged in (1, 2)
-            and path.tokens == 16 and K == 2048 and lds_bytes(path, K, True) <= 160 * 1024)
+def fused_eligible(path, M, K, fmt=I8):
+    """The library's rule for the fused form: INT8 per-token scales on a
+    planned skinny path with per-wave slabs, eight waves, no split, 16-token
+    tiles, one 256-column block of K per wave (the activation tile in LDS for
+    staged 2), within LDS."""
+    nb = -(-(-(-K // 256)) // 8)
+    if not (fmt == I8 and path.kind == 1 and path.splits == 1 and path.waves == 8
+            and path.staged in (1, 2) and path.tokens == 16 and path.channels in (16, 32, 48)
+            and nb == 1):
+        return False
+    lds = 8 * 256 * path.channels + (8 * 16 * 2 * 256 if path.staged == 2 else 0) + 9 * 16 * 4
+    return lds <= 160 * 1024
 
 
 def run_pair(dev, orc, xb, fmt, N, K, path=None, src=torch.bfloat16, out=torch.bfloat16, ld=None,
@@ -80,24 +88,27 @@ def test_fused_linear_planned(dev, orc, fmt, M, N, K):
     run_pair(dev, orc, synthetic.activations(M, K, seed=M + N), fmt, N, K)
 
 
+@pytest.mark.parametrize("fmt", [I8, FP8])
 @pytest.mark.parametrize("staged", [1, 2])
 @pytest.mark.parametrize("tokens,channels,K", [(16, 16, 2048), (16, 32, 2048), (16, 48, 2048),
-                                               (16, 32, 4096), (16, 16, 6144), (32, 16, 2048),
-                                               (32, 32, 2048), (32, 48, 2048), (64, 16, 2048)])
-def test_fused_linear_tiles(dev, orc, tokens, channels, K, staged):
-    """Every fused channel tile and K range, partial token and channel tiles,
-    weight slabs with and without the activation tiles in LDS; wider token
-    tiles, K != 2048 and activation tiles beyond LDS take the two-launch
-    form."""
+                                               (16, 32, 4096), (16, 48, 4096), (16, 16, 6144),
+                                               (16, 48, 6144), (16, 32, 5120), (32, 16, 2048),
+                                               (32, 32, 2048), (32, 48, 2048), (16, 32, 1024),
+                                               (32, 32, 4096), (64, 16, 2048)])
+def test_fused_linear_tiles(dev, orc, fmt, tokens, channels, K, staged):
+    """Every fused channel tile (K 2048 and the short wave ranges of K 1024),
+    partial token and channel tiles, weight slabs with and without the
+    activation tiles in LDS; the paths the fused form does not cover (wider
+    token tiles, several blocks per wave, FP8) take the two-launch form,
+    checked the same way."""
     from breeze_tts_cpp_amd import qlinear
     M, N = 29, 16 * 37
     path = qlinear.Path(1, tokens, channels, 1, 8, staged)
     if lds_bytes(path, K) > 160 * 1024:
         pytest.skip("no variant: the staged tiles exceed LDS")
-    assert fused_eligible(path, M, K) == (tokens == 16 and K == 2048 and
-                                          lds_bytes(path, K, True) <= 160 * 1024)
-    print(f"fused tile {tokens}x{channels} K={K}", flush=True)
-    run_pair(dev, orc, synthetic.activations(M, K, seed=tokens * channels + K), I8, N, K, path=path)
+    print(f"fused tile fmt={fmt} {tokens}x{channels} K={K} staged={staged} "
+          f"fused={fused_eligible(path, M, K, fmt)}", flush=True)
+    run_pair(dev, orc, synthetic.activations(M, K, seed=tokens * channels + K), fmt, N, K, path=path)
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])
