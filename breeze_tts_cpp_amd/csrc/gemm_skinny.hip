@@ -204,6 +204,36 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             pre_w[k][r] = (live && !(Grouped && weight_group)) ? sw[n + r] : 1.f;
     }
 
+    // K groups of 128 on a staged slab: every group scale of this wave's K
+    // range (two groups per 256-column block) is requested here, ahead of the
+    // slab, instead of when its block's MFMAs run after the slab has landed.
+    constexpr bool kPreScale = Grouped && GS == 128 && NB > 0 && NB * MT <= 6 && !Packed;
+    float pre_sw[kPreScale ? NB : 1][2][NF][4];
+    float pre_sx[kPreScale ? NB : 1][2][MT];
+    if constexpr (kPreScale) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = k_begin + blk * kBlockK + h * 128;
+                const bool kin = k < k_end;
+                const int g = k / 128;
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = n0 + f * 16 + quad * 4 + r;
+                        pre_sw[blk][h][f][r] =
+                            (kin && weight_group && n < N) ? sw[size_t(g) * N + n] : 1.f;
+                    }
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const int m = m0 + t * 16 + row16;
+                    pre_sx[blk][h][t] = (kin && input_group && m < M) ? sx[size_t(g) * M + m] : 1.f;
+                }
+            }
+    }
+
     // FQ: the 16-bit activation fragments of every block of this wave's K
     // range, requested before the weight slab so that they land first. Lane
     // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
@@ -548,6 +578,8 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 if (k >= k_end) break;
                 const int g_in = input_group ? k / input_group : 0;
                 const int g_w = weight_group ? k / weight_group : 0;
+                // with kPreScale, blk is a constant once the block loop is unrolled
+                const int blk = kPreScale ? (kb - k_begin) / kBlockK : 0;
                 float swg[NF][4];
 #pragma unroll
                 for (int f = 0; f < NF; ++f)
@@ -555,12 +587,15 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     for (int r = 0; r < 4; ++r) {
                         if (fsel >= 0 && f != fsel) continue;
                         int n = n0 + f * 16 + quad * 4 + r;
-                        swg[f][r] = (weight_group && n < N) ? sw[size_t(g_w) * N + n] : 1.f;
+                        if constexpr (kPreScale) swg[f][r] = pre_sw[blk][h][f][r];
+                        else swg[f][r] = (weight_group && n < N) ? sw[size_t(g_w) * N + n] : 1.f;
                     }
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     int m = m0 + t * 16 + row16;
-                    float sxg = (input_group && m < M) ? sx[size_t(g_in) * M + m] : 1.f;
+                    float sxg;
+                    if constexpr (kPreScale) sxg = pre_sx[blk][h][t];
+                    else sxg = (input_group && m < M) ? sx[size_t(g_in) * M + m] : 1.f;
 #pragma unroll
                     for (int f = 0; f < NF; ++f) {
                         if (fsel >= 0 && f != fsel) continue;
