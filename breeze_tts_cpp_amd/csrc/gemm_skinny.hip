@@ -1087,6 +1087,10 @@ bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
         (p.channels != 16 && p.channels != 32 && p.channels != 48) ||
         span_of(a.K, 1) != kBlockK)
         return false;
+    // One round of workgroups (256 CUs, one workgroup each): over two rounds
+    // the re-encoding no longer hides under the weight stream (qkv at M = 64,
+    // 512 workgroups: 10.1 us against 9.0 us for quantizer + GEMM).
+    if (long((a.N + p.channels - 1) / p.channels) * ((a.M + 15) / 16) > 256) return false;
     // slabs, (staged 2) the 16-bit activation tiles, the absmax exchange
     const size_t lds = size_t(kWaves) * p.channels * kBlockK +
                        (p.staged == 2 ? size_t(kWaves) * 16 * 2 * kBlockK : 0) +

@@ -34,15 +34,17 @@ def lds_bytes(path, K, fused=False):
     return 8 * 256 * nb * (path.channels + act) + (9 * path.tokens * 4 if fused else 0)
 
 
-def fused_eligible(path, M, K, fmt=I8):
+def fused_eligible(path, M, N, K, fmt=I8):
     """The library's rule for the fused form: INT8 per-token scales on a
     planned skinny path with per-wave slabs, eight waves, no split, 16-token
     tiles, one 256-column block of K per wave (the activation tile in LDS for
-    staged 2), within LDS."""
+    staged 2), at most 256 workgroups, within LDS."""
     nb = -(-(-(-K // 256)) // 8)
     if not (fmt == I8 and path.kind == 1 and path.splits == 1 and path.waves == 8
             and path.staged in (1, 2) and path.tokens == 16 and path.channels in (16, 32, 48)
             and nb == 1):
+        return False
+    if -(-N // path.channels) * -(-M // 16) > 256:
         return False
     lds = 8 * 256 * path.channels + (8 * 16 * 2 * 256 if path.staged == 2 else 0) + 9 * 16 * 4
     return lds <= 160 * 1024
@@ -107,7 +109,7 @@ def test_fused_linear_tiles(dev, orc, fmt, tokens, channels, K, staged):
     if lds_bytes(path, K) > 160 * 1024:
         pytest.skip("no variant: the staged tiles exceed LDS")
     print(f"fused tile fmt={fmt} {tokens}x{channels} K={K} staged={staged} "
-          f"fused={fused_eligible(path, M, K, fmt)}", flush=True)
+          f"fused={fused_eligible(path, M, N, K, fmt)}", flush=True)
     run_pair(dev, orc, synthetic.activations(M, K, seed=tokens * channels + K), fmt, N, K, path=path)
 
 
