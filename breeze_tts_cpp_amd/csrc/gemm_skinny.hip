@@ -453,6 +453,14 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         constexpr uint32_t kInfBits = FQ == 2 ? 0x7c00u : 0x7f80u;
         typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
         float amax[MT];
+        // FP8: per token tile, this lane's values are all finite. Then every
+        // v * inverse is below 464 in magnitude, where the hardware
+        // conversion equals encode_fp8 (encode_fp8x4): with the row's absmax
+        // a finite, scale = max(a / 448, FLT_MIN) and inverse = 1 / scale
+        // (both rounded to nearest) keep |v * inverse| <= 448 * (1 + 2^-24)^3
+        // for |v| <= a (or |v| * 2^126 < 448 exactly); with a = Inf the
+        // inverse is 0.
+        bool finite[MT];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             u16x2 top = {0, 0};
@@ -470,6 +478,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                                 top, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
                     }
             const uint32_t bits = top.x > top.y ? top.x : top.y;
+            finite[t] = bits < kInfBits;
             if (bits <= kInfBits) {
                 amax[t] = widen(bits);
             } else {
@@ -520,11 +529,12 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                                     widen(wd[2 * j + 1] >> 16) * inverse));
                                 continue;
                             }
-                            const uint32_t c0 = encode<Fmt>(widen(wd[2 * j] & 0xffffu) * inverse);
-                            const uint32_t c1 = encode<Fmt>(widen(wd[2 * j] >> 16) * inverse);
-                            const uint32_t c2 = encode<Fmt>(widen(wd[2 * j + 1] & 0xffffu) * inverse);
-                            const uint32_t c3 = encode<Fmt>(widen(wd[2 * j + 1] >> 16) * inverse);
-                            codes[2 * h + j] = int(c0 | (c1 << 8) | (c2 << 16) | (c3 << 24));
+                            const float v0 = widen(wd[2 * j] & 0xffffu) * inverse;
+                            const float v1 = widen(wd[2 * j] >> 16) * inverse;
+                            const float v2 = widen(wd[2 * j + 1] & 0xffffu) * inverse;
+                            const float v3 = widen(wd[2 * j + 1] >> 16) * inverse;
+                            codes[2 * h + j] = int(finite[t] ? encode_fp8x4_inrange(v0, v1, v2, v3)
+                                                             : encode_fp8x4(v0, v1, v2, v3));
                         }
                     }
                     // Columns past the range (or rows past M) encode zeros,
@@ -1015,19 +1025,18 @@ int launch_fused_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     default: return -4;
     }
 }
-// Variants (skinny_fused_supported lists them): INT8, 16-token tiles, one
-// 256-column block of K per wave (staged 2: the 16-bit activation rows
-// through LDS; staged 1: in registers). Measured on MI355X (graphs of
-// launches over distinct weights, bf16 source): qkv at M = 32 6.2 us against
-// 6.7 us for quantizer + GEMM, o_proj 5.5 against 5.9. The kernel also
-// takes 32-token tiles and two or three blocks per wave, but every
+// Variants (skinny_fused_supported lists them): INT8 and FP8, 16-token
+// tiles, one 256-column block of K per wave (staged 2: the 16-bit activation
+// rows through LDS; staged 1: in registers). Measured on MI355X (graphs of
+// launches over distinct weights, bf16 source, M = 32) against quantizer +
+// GEMM: INT8 qkv 6.1 us against 6.7, o_proj 5.4 against 5.9; FP8 (hardware
+// e4m3 conversion) qkv 6.1 against 7.3, o_proj 5.5 against 6.7. The kernel
+// also takes 32-token tiles and two or three blocks per wave, but every
 // workgroup re-encodes its rows, and there the encoding no longer hides
-// under the weight stream: gate_up at M = 32 (32-token tile) 11.4 us
-// against 10.2, down (three blocks) 13.9 against 10.2, FP8 (integer e4m3
-// encoder) 13.7 against 7.3 for qkv.
+// under the weight stream: gate_up at M = 32 (32-token tile) 11.4 us against
+// 10.2, down (three blocks) 13.9 against 10.2.
 template <int Fmt>
 int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
-    if constexpr (Fmt != I8) return -4;
     if (p.tokens != 16 || span_of(a.K, 1) != kBlockK) return -4;
     if (p.staged == 2) return launch_fused_nf<Fmt, 1, 1, true>(a, p, s);
     return launch_fused_nf<Fmt, 1, 1, false>(a, p, s);
@@ -1082,7 +1091,7 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
 
 bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
     if (!a.fq.src || a.packed || a.bias || a.act || a.input_group || a.weight_group ||
-        a.fmt != I8 || p.kind != KIND_SKINNY || p.splits != 1 || p.waves != kWaves ||
+        p.kind != KIND_SKINNY || p.splits != 1 || p.waves != kWaves ||
         (p.staged != 1 && p.staged != 2) || p.tokens != 16 ||
         (p.channels != 16 && p.channels != 32 && p.channels != 48) ||
         span_of(a.K, 1) != kBlockK)

@@ -41,8 +41,17 @@ template <int Fmt, bool Vec>
 __device__ __forceinline__ void store8(uint8_t *row, int column, int cols, const float (&v)[8],
                                        float inverse) {
     uint32_t code[8];
+    if constexpr (Fmt == FP8 && Vec) {
+        const uint32_t lo = encode_fp8x4(v[0] * inverse, v[1] * inverse, v[2] * inverse,
+                                         v[3] * inverse);
+        const uint32_t hi = encode_fp8x4(v[4] * inverse, v[5] * inverse, v[6] * inverse,
+                                         v[7] * inverse);
+        if (column < cols) *reinterpret_cast<uint2 *>(row + column) = uint2{lo, hi};
+        return;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = encode<Fmt>(v[i] * inverse);
+        for (int i = 0; i < 8; ++i) code[i] = encode<Fmt>(v[i] * inverse);
+    }
     if constexpr (Vec) {
         if (column < cols) {
             uint2 packed;

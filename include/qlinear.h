@@ -138,7 +138,7 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
  * rotation) into the scratch activation (xq [rows, K], sx), as
  * qlin_row_quantize, then y = D(xq . w^T) as qlin_gemm with `path` (NULL =
  * planned). Two launches on `stream` (quantizer, GEMM), or one where the
- * path is an INT8 decode path with 16-token tiles, per-wave weight slabs, one
+ * path is an INT8 or FP8 decode path with 16-token tiles, per-wave weight slabs, one
  * 256-column block of K per wave (K <= 2048) and at most 256 workgroups, with
  * per-token scales, no rotation and a 16-byte-aligned source with ld % 8 ==
  * 0, and neither y nor (xq, sx) overlaps x: there the GEMM quantizes its own

@@ -1,12 +1,12 @@
-"""qlin_linear's one-launch decode form: for per-token INT8 scales on a
-decode path with 16-token tiles, per-wave weight slabs and one 256-column
+"""qlin_linear's one-launch decode form: for per-token INT8 or FP8 scales on
+a decode path with 16-token tiles, per-wave weight slabs and one 256-column
 block of K per wave (K <= 2048), the GEMM quantizes its own token rows (the
 arithmetic of the per-token quantizer, reference row_quantize.cu:24-87)
 instead of a separate quantizer launch. Checked against the two-launch form
 on the same inputs (qlin_row_quantize + qlin_gemm with the same path):
-output bits identical for INT8 and FP8 (FP8 and every other path take the
-two-launch form), and the scratch activation (codes and scales) equal to
-the oracle's quantizer."""
+output bits identical, and the scratch activation (codes and scales) equal
+to the oracle's quantizer; paths outside the form take the two launches and
+are checked the same way."""
 import numpy as np
 import pytest
 import torch
@@ -35,12 +35,12 @@ def lds_bytes(path, K, fused=False):
 
 
 def fused_eligible(path, M, N, K, fmt=I8):
-    """The library's rule for the fused form: INT8 per-token scales on a
+    """The library's rule for the fused form: per-token scales on a
     planned skinny path with per-wave slabs, eight waves, no split, 16-token
     tiles, one 256-column block of K per wave (the activation tile in LDS for
     staged 2), at most 256 workgroups, within LDS."""
     nb = -(-(-(-K // 256)) // 8)
-    if not (fmt == I8 and path.kind == 1 and path.splits == 1 and path.waves == 8
+    if not (path.kind == 1 and path.splits == 1 and path.waves == 8
             and path.staged in (1, 2) and path.tokens == 16 and path.channels in (16, 32, 48)
             and nb == 1):
         return False
@@ -133,8 +133,9 @@ def test_fused_linear_f16_strided_special_rows(dev, orc, fmt):
     run_pair(dev, orc, xb, fmt, N, K, src=torch.bfloat16, out=torch.bfloat16, ld=K + 8)
 
 
+@pytest.mark.parametrize("fmt", [I8, FP8])
 @pytest.mark.parametrize("src", [torch.bfloat16, torch.float16])
-def test_fused_linear_nan_inf_rows(dev, orc, src):
+def test_fused_linear_nan_inf_rows(dev, orc, src, fmt):
     """Rows with a NaN among finite values, +Inf, -Inf and all NaN: the fused
     form's absmax (a packed 16-bit max of the sign-cleared bits, redone with
     fmaxf where a lane holds a NaN pattern) gives the same scratch codes,
@@ -149,8 +150,8 @@ def test_fused_linear_nan_inf_rows(dev, orc, src):
     xb[6] = nan
     xb[8, 2000] = inf | np.uint16(0x8000)
     xb[10, 1] = np.uint16(0x7f81)  # a signalling-NaN pattern
-    print(f"fused nan/inf rows src={src}", flush=True)
-    run_pair(dev, orc, xb, I8, N, K, src=src, out=src, oracle=False)
+    print(f"fused nan/inf rows src={src} fmt={fmt}", flush=True)
+    run_pair(dev, orc, xb, fmt, N, K, src=src, out=src, oracle=False)
 
 
 def test_fused_linear_repeated_calls(dev, orc):
