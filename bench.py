@@ -322,9 +322,10 @@ def measured_traffic(name):
     """HBM bytes per launch of the decode linear for projection `name`, from the
     committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (profiles/hbm_traffic_decode_linear.md, copy-kernel calibrated: a row per
-    projection, the last column the scaled bytes per dispatch; the last row for
-    a projection is the current measurement); None when that summary has no
-    row for it."""
+    projection in its first table, the last column the scaled bytes per
+    dispatch; the later streaming-read table, whose rows carry the same
+    projection names, is not read); None when that summary has no row for
+    it."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_decode_linear.md")
     if not os.path.exists(path):
         return None
@@ -332,12 +333,14 @@ def measured_traffic(name):
     for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         # rows are labelled by projection, optionally followed by a note in
-        # parentheses ("qkv (one launch)"); the last matching row wins
+        # parentheses ("qkv (one launch)"); the first matching row is the
+        # decode linear's
         if len(cells) >= 3 and cells[0].split(" (")[0] == name:
             try:
                 found = int(cells[-1].replace(",", ""))
             except ValueError:
                 found = None
+            break
     return found
 
 
