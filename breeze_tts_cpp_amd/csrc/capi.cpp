@@ -171,6 +171,17 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
         if (tiles_256x128 >= 256 && full && !(small_group && fmt == QLIN_FP8)) p.channels = 256;
     }
+    // A 128x128 grid of at most 128 tiles fills half the GPU or less; 128x64
+    // tiles (four 64x32 waves; FP8 per-channel eight 64x16 waves) double the
+    // workgroups: o_proj / down at M = 1024 (128 tiles of 128x128), INT8
+    // 18.7 / 36.6 us against 17.9 / 31.7, FP8 19.6 / 38.7 against 18.2 /
+    // 32.9, group_int8 22.0 / 46.4 against 20.7 / 41.3 (random operands).
+    const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
+    const long tiles_128 = long((N + 127) / 128) * ((rows + 127) / 128);
+    if (p.channels == 128 && p.tokens == 128 && tiles_128 <= 128 && !small_group) {
+        p.tokens = 64;
+        p.waves = fmt == QLIN_FP8 && !grouped ? 8 : 4;
+    }
     return p;
 }
 
@@ -220,10 +231,10 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
     }
     if (p.kind == QLIN_KIND_TILED) {
         if (!((p.channels == 256 && (p.tokens == 256 || p.tokens == 128)) ||
-              (p.channels == 128 && p.tokens == 128)))
+              (p.channels == 128 && (p.tokens == 128 || p.tokens == 64))))
             return fail(QLIN_ERR_UNSUPPORTED,
-                        "tiled path channels x tokens must be 256x256, 256x128 or 128x128 (got %dx%d)", p.channels,
-                        p.tokens);
+                        "tiled path channels x tokens must be 256x256, 256x128, 128x128 or 128x64 (got %dx%d)",
+                        p.channels, p.tokens);
         if (p.splits != 1)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled path has no split-K variant");
         // Macro tiles run along the grid's x dimension (below 2^31).
@@ -236,11 +247,14 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         // (1) or eight of 64x32 (8).
         const bool wave_ok = (p.channels == 256 && p.tokens == 256) ? (p.waves == 8 || p.waves == 4)
                              : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2 || p.waves == 8)
-                                                                       : (p.waves == 1 || p.waves == 8);
+                             : p.tokens == 64 ? (p.waves == 4 || (p.waves == 8 && fmt == QLIN_FP8 &&
+                                                                  !input_group && !weight_group))
+                                              : (p.waves == 1 || p.waves == 8);
         if (!wave_ok)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,
                         p.tokens, p.waves);
-        if (p.waves != 1 && p.waves != 8 && p.tokens != 256 && (input_group || weight_group))
+        if (p.waves != 1 && p.waves != 8 && p.tokens != 256 && p.tokens != 64 &&
+            (input_group || weight_group))
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 32x32-tile variant");
         if ((input_group || weight_group) && p.tokens == 256)
             return fail(QLIN_ERR_UNSUPPORTED, "K-group tiled path has no 256-token tile");

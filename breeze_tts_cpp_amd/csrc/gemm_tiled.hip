@@ -1138,6 +1138,8 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 2, GBK, 4, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, GBK, 4, true, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 64 && p.waves == 4)
+            return launch_shape<Fmt, 2, 2, 4, 2, GBK, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
         // 256x128 with eight waves of 128x32.
@@ -1156,6 +1158,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 2, 64, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
+        // 128x64: four waves of 64x32.
+        if (p.channels == 128 && p.tokens == 64 && p.waves == 4)
+            return launch_shape<Fmt, 2, 2, 4, 2, 64, 4, false, Out>(a, s);
         return -4;
     } else {
         // 256x128 with eight waves of 128x32.
@@ -1175,6 +1180,12 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
+        // 128x64: four waves of 64x32 (32x32x64 MFMA) or eight of 64x16
+        // (16x16x128 MFMA over 128-byte K stages).
+        if (p.channels == 128 && p.tokens == 64 && p.waves == 4)
+            return launch_shape<Fmt, 2, 2, 4, 2, 64, 4, false, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 64 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, false, Out>(a, s);
         return -4;
     }
 }
