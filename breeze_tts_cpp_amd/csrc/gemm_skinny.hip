@@ -717,13 +717,16 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         // activation DMA or loads) completes first, and any issued later
         // (K-group scales) only makes the count stricter.
         static_assert(kPipe, "staged register-resident activations are consumed per chunk");
-        // K-group kernels consume whole blocks (their group scales are
-        // loaded per block; per fragment they would be loaded NF times).
-        constexpr int kStep = Grouped ? NF : 1;
+        // K groups of 32 / 64 consume whole blocks (their group scales are
+        // loaded per block; per fragment they would be loaded NF times);
+        // 128-group scales are prefetched, so those kernels go chunk by
+        // chunk like the per-channel ones.
+        constexpr bool kWhole = Grouped && !kPreScale;
+        constexpr int kStep = kWhole ? NF : 1;
         i32x4 xb[MT][4];
         static_for<0, NB * NF / kStep>([&](auto c_) {
             constexpr int c = decltype(c_)::value * kStep;
-            constexpr int blk = c / NF, f = Grouped ? -1 : c % NF;
+            constexpr int blk = c / NF, f = kWhole ? -1 : c % NF;
             wait_vmcnt<4 * (NB * NF - c - kStep)>();
             const int kb = k_begin + blk * kBlockK;
             if (kb < k_end) {
