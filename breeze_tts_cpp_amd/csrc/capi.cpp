@@ -481,8 +481,8 @@ int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void
     // ops::linear, quantized branch (reference ops/linear.cpp:51-71):
     // quantize_rows into the scratch activation, then the GEMM.
     if (!xq || !sx) return fail(QLIN_ERR_INVALID, "linear needs the scratch activation (xq, sx)");
-    // Decode shapes with per-token scales: one launch in which the GEMM
-    // quantizes its own token rows (and fills the scratch as the quantizer
+    // Decode shapes with per-token scales or activation groups of 128 (no
+    // rotation): one launch in which the GEMM quantizes its own token rows (and fills the scratch as the quantizer
     // would), when the planned path has a fused variant. In that launch some
     // workgroups still read x while others write y and the scratch, so an
     // output or scratch overlapping x takes the two-launch form, which
@@ -498,8 +498,11 @@ int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void
         rows >= 1 && N >= 1 && K >= 1 && ld >= 1 && x && y &&
         !overlaps(span_of(x, size_t(rows) * ld * 2), span_of(y, size_t(rows) * N * 2)) &&
         !overlaps(span_of(x, size_t(rows) * ld * 2), span_of(xq, size_t(rows) * K)) &&
-        !overlaps(span_of(x, size_t(rows) * ld * 2), span_of(sx, size_t(rows) * 4));
-    if (!input_group && !rotation && (src_type == QLIN_BF16 || src_type == QLIN_F16) && x &&
+        !overlaps(span_of(x, size_t(rows) * ld * 2),
+                  span_of(sx, size_t(rows) * 4 *
+                                  (input_group > 0 ? size_t(K + input_group - 1) / input_group : 1)));
+    if ((!input_group || input_group == 128) && !rotation &&
+        (src_type == QLIN_BF16 || src_type == QLIN_F16) && x &&
         aligned(x, 16) && ld % 8 == 0 && ld >= K && rows >= 1 && aligned(xq, 16) &&
         aligned(sx, 4) && disjoint) {
         const qlin::FusedSource fq{static_cast<const uint16_t *>(x), ld, src_type == QLIN_F16 ? 1 : 0,

@@ -81,6 +81,18 @@ __device__ __forceinline__ i32x4 load16(const uint8_t *p) {
     return *reinterpret_cast<const i32x4 *>(p);
 }
 
+// The value of lane l ^ S (S = 16 or 32) by gfx950's v_permlane16_swap /
+// v_permlane32_swap (one VALU instruction; a shuffle goes through LDS). With
+// both operands x, the swap leaves the partner's value in the first result
+// for lanes with bit S set and in the second for the others.
+template <int S> __device__ __forceinline__ float lane_xor(float v) {
+    static_assert(S == 16 || S == 32, "row swaps");
+    const unsigned u = __float_as_uint(v);
+    const auto r = S == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float((threadIdx.x & S) ? r[0] : r[1]);
+}
+
 // Four 16-byte LDS reads by explicit ds_read_b128 instructions and their
 // wait, in one statement. The compiler's wait insertion treats any LDS read
 // as possibly reading what an outstanding global->LDS copy writes and then
@@ -229,7 +241,8 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     const int m = m0 + t * 16 + row16;
-                    pre_sx[blk][h][t] = (kin && input_group && m < M) ? sx[size_t(g) * M + m] : 1.f;
+                    // (FQ: computed from the 16-bit rows below)
+                    pre_sx[blk][h][t] = (kin && input_group && m < M && !FQ) ? sx[size_t(g) * M + m] : 1.f;
                 }
             }
     }
@@ -238,7 +251,8 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
     // range, requested before the weight slab so that they land first. Lane
     // (row16, quad) of token tile t holds K columns [kb + 64p + 16q, +16) of
     // row m0 + 16t + row16: exactly the codes its MFMA B fragments need.
-    static_assert(!FQ || (NB > 0 && !Packed && !Grouped && !Split && NB * MT <= 3),
+    static_assert(!FQ || (NB > 0 && !Packed && !Split && NB * MT <= 3 &&
+                          (!Grouped || (GS == 128 && NB == 1))),
                   "fused quantization: per-wave slab, activation blocks in registers");
     uint4 xraw[FQ ? NB : 1][MT][4][2];
     if constexpr (FQ && !XL) {
@@ -404,6 +418,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                          b[t][0], b[t][1], b[t][2], b[t][3]);
         }
     };
+    float fq_group_scale[MT][2];  // FQ, K groups: this wave's two group scales per token tile
     if constexpr (FQ) {
         // The per-token quantizer's arithmetic (row_quantize.hip
         // token_quantize; reference row_quantize.cu:24-87): row absmax over
@@ -446,103 +461,169 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         // FQ 1: bf16 source, 2: f16 source.
         using Tin = std::conditional_t<FQ == 2, f16_t, bf16_t>;
         auto widen = [](uint32_t h) { return to_float(uint16_t(h), Tin{}); };
-        // |v| of a 16-bit float orders as its sign-cleared bits, so the
-        // absmax is a packed unsigned 16-bit max of the bits; a NaN (bits
-        // above the infinity pattern) makes the lane redo its values with
-        // fmaxf, which ignores NaN as the quantizer's reduction does.
-        constexpr uint32_t kInfBits = FQ == 2 ? 0x7c00u : 0x7f80u;
-        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-        float amax[MT];
-        // FP8: per token tile, this lane's values are all finite. Then every
-        // v * inverse is below 464 in magnitude, where the hardware
-        // conversion equals encode_fp8 (encode_fp8x4): with the row's absmax
-        // a finite, scale = max(a / 448, FLT_MIN) and inverse = 1 / scale
-        // (both rounded to nearest) keep |v * inverse| <= 448 * (1 + 2^-24)^3
-        // for |v| <= a (or |v| * 2^126 < 448 exactly); with a = Inf the
-        // inverse is 0.
-        bool finite[MT];
+        if constexpr (Grouped) {
+            // K groups of 128, not rotated (reference group_token_quantize,
+            // row_quantize.cu:145-165, with encode_group,
+            // quant_device.cuh:63-88): a wave's 256-column block is two whole
+            // groups, so no other wave is involved. Lane (row16, quad) holds,
+            // per group g, columns 64p' + 16 quad + 8h + i (pieces p = 2g +
+            // p', halves h, elements i): the group amax (fmaxf, order-free)
+            // over the lane's 32 values and lanes xor 16, 32, scale =
+            // quant_scale(amax), codes = encode(v * (1 / scale)), bit for bit
+            // the group quantizer's. (With the H128 rotation, re-encoding in
+            // every workgroup costs more than the separate quantizer: qkv at
+            // M = 32 took 11.9 us in one launch against 8.5 us in two.)
+            static_assert(NB == 1, "two 128-groups per wave");
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            u16x2 top = {0, 0};
-#pragma unroll
-            for (int blk = 0; blk < NB; ++blk)
+            for (int t = 0; t < MT; ++t) {
+                float v[4][2][8];
 #pragma unroll
                 for (int p = 0; p < 4; ++p)
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
-                                                xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
+                        const uint32_t wd[4] = {xraw[0][t][p][h].x, xraw[0][t][p][h].y,
+                                                xraw[0][t][p][h].z, xraw[0][t][p][h].w};
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            top = __builtin_elementwise_max(
-                                top, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
+                        for (int i = 0; i < 4; ++i) {
+                            v[p][h][2 * i] = widen(wd[i] & 0xffffu);
+                            v[p][h][2 * i + 1] = widen(wd[i] >> 16);
+                        }
                     }
-            const uint32_t bits = top.x > top.y ? top.x : top.y;
-            finite[t] = bits < kInfBits;
-            if (bits <= kInfBits) {
-                amax[t] = widen(bits);
-            } else {
-                amax[t] = 0.f;
 #pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    float a = 0.f;
+#pragma unroll
+                    for (int p = 2 * g; p < 2 * g + 2; ++p)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[p][h][i]));
+                    a = fmaxf(a, lane_xor<16>(a));
+                    a = fmaxf(a, lane_xor<32>(a));
+                    const float step = quant_scale<Fmt>(a);
+                    const float inverse = 1.f / step;
+                    fq_group_scale[t][g] = step;
+#pragma unroll
+                    for (int p = 2 * g; p < 2 * g + 2; ++p) {
+                        i32x4 codes;
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j) {
+                                const float *e = &v[p][h][4 * j];
+                                if constexpr (Fmt == I8)
+                                    codes[2 * h + j] = int(encode_i8x4(e[0] * inverse, e[1] * inverse,
+                                                                       e[2] * inverse, e[3] * inverse));
+                                else
+                                    codes[2 * h + j] = int(encode_fp8x4(e[0] * inverse, e[1] * inverse,
+                                                                        e[2] * inverse, e[3] * inverse));
+                            }
+                        const int k = k_begin + p * 64 + quad * 16;
+                        const bool in = k < k_end && xvalid[t];
+                        xpre[0][t][p] = in ? codes : i32x4{0, 0, 0, 0};
+                    }
+                    if constexpr (kPreScale) pre_sx[0][g][t] = step;
+                }
+            }
+        } else {
+            // |v| of a 16-bit float orders as its sign-cleared bits, so the
+            // absmax is a packed unsigned 16-bit max of the bits; a NaN (bits
+            // above the infinity pattern) makes the lane redo its values with
+            // fmaxf, which ignores NaN as the quantizer's reduction does.
+            constexpr uint32_t kInfBits = FQ == 2 ? 0x7c00u : 0x7f80u;
+            typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+            float amax[MT];
+            // FP8: per token tile, this lane's values are all finite. Then every
+            // v * inverse is below 464 in magnitude, where the hardware
+            // conversion equals encode_fp8 (encode_fp8x4): with the row's absmax
+            // a finite, scale = max(a / 448, FLT_MIN) and inverse = 1 / scale
+            // (both rounded to nearest) keep |v * inverse| <= 448 * (1 + 2^-24)^3
+            // for |v| <= a (or |v| * 2^126 < 448 exactly); with a = Inf the
+            // inverse is 0.
+            bool finite[MT];
+    #pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                u16x2 top = {0, 0};
+    #pragma unroll
                 for (int blk = 0; blk < NB; ++blk)
+    #pragma unroll
                     for (int p = 0; p < 4; ++p)
+    #pragma unroll
                         for (int h = 0; h < 2; ++h) {
                             const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
                                                     xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
-                            for (int i = 0; i < 4; ++i) {
-                                amax[t] = fmaxf(amax[t], fabsf(widen(wd[i] & 0xffffu)));
-                                amax[t] = fmaxf(amax[t], fabsf(widen(wd[i] >> 16)));
-                            }
+    #pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                top = __builtin_elementwise_max(
+                                    top, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
                         }
-            }
-            amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 16, 64));
-            amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 32, 64));
-            if (quad == 0) fq_amax[wave * MT * 16 + t * 16 + row16] = amax[t];
-        }
-        // A workgroup barrier that waits for LDS only: __syncthreads' fence
-        // would also wait for the weight slab DMA still in flight.
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            float a = fq_amax[t * 16 + row16];
-#pragma unroll
-            for (int q = 1; q < WK; ++q) a = fmaxf(a, fq_amax[q * MT * 16 + t * 16 + row16]);
-            const float step = quant_scale<Fmt>(a);
-            const float inverse = 1.f / step;
-            if (wave == 0 && quad == 0) fq_scale[t * 16 + row16] = step;
-#pragma unroll
-            for (int blk = 0; blk < NB; ++blk)
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    i32x4 codes;
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
-                                                xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            if constexpr (Fmt == I8) {
-                                codes[2 * h + j] = int(encode_i8x4(
-                                    widen(wd[2 * j] & 0xffffu) * inverse,
-                                    widen(wd[2 * j] >> 16) * inverse,
-                                    widen(wd[2 * j + 1] & 0xffffu) * inverse,
-                                    widen(wd[2 * j + 1] >> 16) * inverse));
-                                continue;
+                const uint32_t bits = top.x > top.y ? top.x : top.y;
+                finite[t] = bits < kInfBits;
+                if (bits <= kInfBits) {
+                    amax[t] = widen(bits);
+                } else {
+                    amax[t] = 0.f;
+    #pragma unroll
+                    for (int blk = 0; blk < NB; ++blk)
+                        for (int p = 0; p < 4; ++p)
+                            for (int h = 0; h < 2; ++h) {
+                                const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
+                                                        xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
+                                for (int i = 0; i < 4; ++i) {
+                                    amax[t] = fmaxf(amax[t], fabsf(widen(wd[i] & 0xffffu)));
+                                    amax[t] = fmaxf(amax[t], fabsf(widen(wd[i] >> 16)));
+                                }
                             }
-                            const float v0 = widen(wd[2 * j] & 0xffffu) * inverse;
-                            const float v1 = widen(wd[2 * j] >> 16) * inverse;
-                            const float v2 = widen(wd[2 * j + 1] & 0xffffu) * inverse;
-                            const float v3 = widen(wd[2 * j + 1] >> 16) * inverse;
-                            codes[2 * h + j] = int(finite[t] ? encode_fp8x4_inrange(v0, v1, v2, v3)
-                                                             : encode_fp8x4(v0, v1, v2, v3));
-                        }
-                    }
-                    // Columns past the range (or rows past M) encode zeros,
-                    // as the zero-filled plain activation loads.
-                    const int k = k_begin + blk * kBlockK + p * 64 + quad * 16;
-                    const bool in = k < k_end && xvalid[t];
-                    xpre[blk][t][p] = in ? codes : i32x4{0, 0, 0, 0};
                 }
+                amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 16, 64));
+                amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 32, 64));
+                if (quad == 0) fq_amax[wave * MT * 16 + t * 16 + row16] = amax[t];
+            }
+            // A workgroup barrier that waits for LDS only: __syncthreads' fence
+            // would also wait for the weight slab DMA still in flight.
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    #pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                float a = fq_amax[t * 16 + row16];
+    #pragma unroll
+                for (int q = 1; q < WK; ++q) a = fmaxf(a, fq_amax[q * MT * 16 + t * 16 + row16]);
+                const float step = quant_scale<Fmt>(a);
+                const float inverse = 1.f / step;
+                if (wave == 0 && quad == 0) fq_scale[t * 16 + row16] = step;
+    #pragma unroll
+                for (int blk = 0; blk < NB; ++blk)
+    #pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        i32x4 codes;
+    #pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
+                                                    xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
+    #pragma unroll
+                            for (int j = 0; j < 2; ++j) {
+                                if constexpr (Fmt == I8) {
+                                    codes[2 * h + j] = int(encode_i8x4(
+                                        widen(wd[2 * j] & 0xffffu) * inverse,
+                                        widen(wd[2 * j] >> 16) * inverse,
+                                        widen(wd[2 * j + 1] & 0xffffu) * inverse,
+                                        widen(wd[2 * j + 1] >> 16) * inverse));
+                                    continue;
+                                }
+                                const float v0 = widen(wd[2 * j] & 0xffffu) * inverse;
+                                const float v1 = widen(wd[2 * j] >> 16) * inverse;
+                                const float v2 = widen(wd[2 * j + 1] & 0xffffu) * inverse;
+                                const float v3 = widen(wd[2 * j + 1] >> 16) * inverse;
+                                codes[2 * h + j] = int(finite[t] ? encode_fp8x4_inrange(v0, v1, v2, v3)
+                                                                 : encode_fp8x4(v0, v1, v2, v3));
+                            }
+                        }
+                        // Columns past the range (or rows past M) encode zeros,
+                        // as the zero-filled plain activation loads.
+                        const int k = k_begin + blk * kBlockK + p * 64 + quad * 16;
+                        const bool in = k < k_end && xvalid[t];
+                        xpre[blk][t][p] = in ? codes : i32x4{0, 0, 0, 0};
+                    }
+            }
         }
     }
 
@@ -749,7 +830,15 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                 for (int t = 0; t < MT; ++t) {
                     const int m = m0 + t * 16 + row16;
                     if (!xvalid[t]) continue;
-                    if (blockIdx.x == 0 && wave == 0 && quad == 0) fq.sx[m] = fq_scale[t * 16 + row16];
+                    if constexpr (Grouped) {
+                        // scales [K/128, M]: this wave's two groups
+                        if (quad == 0)
+                            for (int g = 0; g < 2; ++g)
+                                if (k_begin + g * 128 < k_end)
+                                    fq.sx[size_t(k_begin / 128 + g) * M + m] = fq_group_scale[t][g];
+                    } else {
+                        if (blockIdx.x == 0 && wave == 0 && quad == 0) fq.sx[m] = fq_scale[t * 16 + row16];
+                    }
 #pragma unroll
                     for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
@@ -821,7 +910,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         const int m = m0 + t * 16 + (l & 15);
         const int n = n0 + f * 16 + (l >> 4) * 4;
         if (m >= M || n >= N) continue;
-        if constexpr (FQ) pre_x[k] = fq_scale[t * 16 + (l & 15)];
+        if constexpr (FQ && !Grouped) pre_x[k] = fq_scale[t * 16 + (l & 15)];
         Red sum[4];
         total(tf, l, t, f, sum);
         float v[4];
@@ -996,35 +1085,37 @@ int dispatch_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 
 // Fused activation quantization (FQ): eight waves, per-wave slabs of NB
 // blocks, per-channel scales, no split.
-template <int Fmt, int MT, int NF, int NB, bool XL>
+template <int Fmt, int MT, int NF, int NB, bool XL, bool G>
 int launch_fused_nb(const GemmArgs &a, hipStream_t stream) {
     // Every workgroup quantizes its token rows again (the activation is
     // re-encoded once per column tile). That ALU work overlaps the weight
     // slab's DMA: the encoding waits only for the 16-bit activation loads,
-    // issued ahead of the slab.
+    // issued ahead of the slab. G: K groups of 128 (activation groups of 128;
+    // weight groups of 128 or per-channel weight scales).
     const int span = NB * kBlockK;
     dim3 grid((a.N + 16 * NF - 1) / (16 * NF), 1, (a.M + 16 * MT - 1) / (16 * MT));
     // slabs, (XL) 16-bit activation tiles, the absmax / scale exchange
     const size_t lds = size_t(kWaves) * 16 * (NF + (XL ? 2 * MT : 0)) * NB * kBlockK +
                        size_t(kWaves + 1) * MT * 16 * 4;
+    const int ig = G ? 128 : 0, wg = G ? a.weight_group : 0;
     if (a.fq.f16)
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 2, 128, XL>),
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, G, false, NB, false, 2, 128, XL>),
                            grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
-                           a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
+                           a.y, nullptr, a.M, a.N, a.K, span, ig, wg, nullptr, 0,
                            int(a.out_type == F16), a.fq);
     else
-        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, false, false, NB, false, 1, 128, XL>),
+        hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, G, false, NB, false, 1, 128, XL>),
                            grid, dim3(64 * kWaves), lds, stream, nullptr, nullptr, a.w, a.sw,
-                           a.y, nullptr, a.M, a.N, a.K, span, 0, 0, nullptr, 0,
+                           a.y, nullptr, a.M, a.N, a.K, span, ig, wg, nullptr, 0,
                            int(a.out_type == F16), a.fq);
     return 0;
 }
-template <int Fmt, int MT, int NB, bool XL>
+template <int Fmt, int MT, int NB, bool XL, bool G>
 int launch_fused_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     switch (p.channels) {
-    case 16: return launch_fused_nb<Fmt, MT, 1, NB, XL>(a, s);
-    case 32: return launch_fused_nb<Fmt, MT, 2, NB, XL>(a, s);
-    case 48: return launch_fused_nb<Fmt, MT, 3, NB, XL>(a, s);
+    case 16: return launch_fused_nb<Fmt, MT, 1, NB, XL, G>(a, s);
+    case 32: return launch_fused_nb<Fmt, MT, 2, NB, XL, G>(a, s);
+    case 48: return launch_fused_nb<Fmt, MT, 3, NB, XL, G>(a, s);
     default: return -4;
     }
 }
@@ -1041,8 +1132,12 @@ int launch_fused_nf(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
 template <int Fmt>
 int launch_fused(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if (p.tokens != 16 || span_of(a.K, 1) != kBlockK) return -4;
-    if (p.staged == 2) return launch_fused_nf<Fmt, 1, 1, true>(a, p, s);
-    return launch_fused_nf<Fmt, 1, 1, false>(a, p, s);
+    if (a.input_group) {
+        if (p.staged == 2) return launch_fused_nf<Fmt, 1, 1, true, true>(a, p, s);
+        return launch_fused_nf<Fmt, 1, 1, false, true>(a, p, s);
+    }
+    if (p.staged == 2) return launch_fused_nf<Fmt, 1, 1, true, false>(a, p, s);
+    return launch_fused_nf<Fmt, 1, 1, false, false>(a, p, s);
 }
 
 template <int Fmt, bool Grouped, int GS = 128>
@@ -1093,7 +1188,11 @@ size_t skinny_workspace_bytes(const GemmArgs &a, const GemmPath &p) {
 }
 
 bool skinny_fused_supported(const GemmArgs &a, const GemmPath &p) {
-    if (!a.fq.src || a.packed || a.bias || a.act || a.input_group || a.weight_group ||
+    // per-token scales, or activation groups of 128 with weight groups of 128
+    // or per-channel weight scales (the caller takes unrotated sources only)
+    const bool per_token = !a.input_group && !a.weight_group;
+    const bool grouped = a.input_group == 128 && (a.weight_group == 0 || a.weight_group == 128);
+    if (!a.fq.src || a.packed || a.bias || a.act || !(per_token || grouped) ||
         p.kind != KIND_SKINNY || p.splits != 1 || p.waves != kWaves ||
         (p.staged != 1 && p.staged != 2) || p.tokens != 16 ||
         (p.channels != 16 && p.channels != 32 && p.channels != 48) ||

@@ -91,15 +91,15 @@ void launch_pointwise_quantize_fp8(const PointwiseQuantizeArgs &, bool vec, hipS
 // Kernel families; numbering is part of the C ABI (qlin_path.kind).
 enum Kind : int { KIND_AUTO = 0, KIND_SKINNY = 1, KIND_TILED = 2 };
 
-// Fused per-token quantization of the 16-bit activation inside the decode
-// GEMM (qlin_linear): the GEMM reads src [M, ld] instead of x, encodes it as
-// the per-token quantizer does and, in the workgroups of output-column tile 0,
-// stores the codes and scales to xq [M, K] / sx [M].
+// Fused quantization of the 16-bit activation inside the decode GEMM
+// (qlin_linear): the GEMM reads src [M, ld] instead of x, encodes it as the
+// per-token or the 128-group (unrotated) quantizer does, and stores
+// the codes and scales to xq [M, K] / sx.
 struct FusedSource {
     const uint16_t *src = nullptr;
     int ld = 0, f16 = 0;
     uint8_t *xq = nullptr;
-    float *sx = nullptr;
+    float *sx = nullptr;  // [M], or [K/128, M] for K groups of 128
 };
 
 struct GemmArgs {

@@ -140,9 +140,10 @@ int qlin_gemm(const qlin_path *path, const void *x, const float *sx, const void 
  * planned). Two launches on `stream` (quantizer, GEMM), or one where the
  * path is an INT8 or FP8 decode path with 16-token tiles, per-wave weight slabs, one
  * 256-column block of K per wave (K <= 2048) and at most 256 workgroups, with
- * per-token scales, no rotation and a 16-byte-aligned source with ld % 8 ==
- * 0, and neither y nor (xq, sx) overlaps x: there the GEMM quantizes its own
- * token rows and fills (xq, sx) with the same bits. The first failing
+ * per-token scales or activation groups of 128 (weight groups of 128 or per
+ * channel), no rotation and a 16-byte-aligned source with ld % 8 == 0, and
+ * neither y nor (xq, sx) overlaps x: there the GEMM quantizes its own token
+ * rows and fills (xq, sx) with the same bits. The first failing
  * check's status is returned. */
 int qlin_linear(const qlin_path *path, const void *x, int ld, int src_type, void *xq, float *sx,
                 const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,

@@ -171,3 +171,86 @@ def test_fused_linear_repeated_calls(dev, orc):
         xr, sr = orc.quantize_rows(xb, I8)
         assert np.array_equal(xq[:M].cpu().numpy(), xr) and np.array_equal(sx[:M].cpu().numpy(), sr)
         assert np.array_equal(bits(y), orc.epilogue_i8(orc.gemm_i8_acc(xr, wq), sr, sw))
+
+
+def run_group_pair(dev, orc, xb, fmt, N, K, rotation, weight_group=128, path=None,
+                   src=torch.bfloat16, oracle=True):
+    """qlin_linear with activation groups of 128 (optionally H128-rotated)
+    against quantizer + GEMM on the same path: scratch codes, [K/128, M]
+    scales and output bits identical; the scratch also equals the oracle's
+    group quantizer for bf16 sources."""
+    from breeze_tts_cpp_amd import qlinear
+    M = xb.shape[0]
+    wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=N + K + 7), fmt, group=weight_group,
+                               rotation=rotation)
+    wq_d, sw_d = torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev)
+    x = dev16(xb, src, dev)
+    groups = -(-K // 128)
+    xq_f = torch.full((M, K), 0x5a, dtype=torch.uint8, device=dev)
+    sx_f = torch.full((groups, M), -1.0, dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    qlinear.load().qlin_linear(  # activation groups 128, weight groups weight_group
+        __import__("ctypes").byref((path or qlinear.Path()).to_c()), x.data_ptr(), x.stride(0),
+        {torch.bfloat16: BF16, torch.float16: F16}[src], xq_f.data_ptr(), sx_f.data_ptr(),
+        wq_d.data_ptr(), sw_d.data_ptr(), out.data_ptr(), M, N, K, fmt, BF16, 128, weight_group,
+        rotation, None, 0, None)
+    xq_s, sx_s = qlinear.row_quantize(x, fmt, group=128, rotation=rotation)
+    y_s = qlinear.gemm(xq_s, sx_s, wq_d, sw_d, fmt, input_group=128, weight_group=weight_group,
+                       path=path)
+    torch.cuda.synchronize()
+    assert np.array_equal(xq_f.cpu().numpy(), xq_s.cpu().numpy()), "scratch codes differ"
+    assert np.array_equal(sx_f.cpu().numpy().reshape(-1), sx_s.cpu().numpy().reshape(-1)), \
+        "scratch scales differ"
+    assert np.array_equal(bits(out), bits(y_s)), \
+        f"{np.count_nonzero(bits(out) != bits(y_s))} outputs differ from the two-launch form"
+    if oracle and src == torch.bfloat16:
+        xr, sr = orc.quantize_rows(xb, fmt, group=128, rotation=rotation)
+        assert np.array_equal(xq_f.cpu().numpy(), xr)
+        assert np.array_equal(sx_f.cpu().numpy().reshape(-1), np.asarray(sr).reshape(-1))
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("rotation", [0, 128])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 2048), (32, 4096, 2048), (32, 2048, 2048),
+                                   (17, 2048, 1024), (32, 12288, 2048), (32, 2048, 6144)])
+def test_fused_group_linear_planned(dev, orc, fmt, rotation, M, N, K):
+    """K-group decode linears on the planned path: one launch for unrotated
+    groups where the path has 16-token tiles over one 256-column block per
+    wave (qkv, o_proj); two launches otherwise (rotated groups, as group_int8
+    / group_fp8 use, and gate_up, down); both checked."""
+    print(f"fused group linear fmt={fmt} rot={rotation} M={M} N={N} K={K}", flush=True)
+    run_group_pair(dev, orc, synthetic.activations(M, K, seed=M + N + rotation), fmt, N, K, rotation)
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("staged", [1, 2])
+@pytest.mark.parametrize("channels", [16, 32, 48])
+def test_fused_group_linear_tiles(dev, orc, fmt, staged, channels):
+    """Every fused channel tile, activation tile in LDS or in registers,
+    partial token and channel tiles; weights with per-channel scales as well
+    as 128-groups."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N, K = 29, 16 * 37, 2048
+    path = qlinear.Path(1, 16, channels, 1, 8, staged)
+    print(f"fused group tile fmt={fmt} 16x{channels} staged={staged}", flush=True)
+    xb = synthetic.activations(M, K, seed=channels + staged)
+    run_group_pair(dev, orc, xb, fmt, N, K, 0, path=path)
+    run_group_pair(dev, orc, xb, fmt, N, K, 0, weight_group=0, path=path)
+
+
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float16])
+def test_fused_group_linear_special_rows(dev, orc, src):
+    """Zero, NaN, Inf and huge values and an all-zero group through the
+    grouped one-launch form against the two-launch form (the oracle is not
+    consulted for these rows)."""
+    M, N, K = 16, 2048, 2048
+    xb = synthetic.activations(M, K, seed=33)
+    xb[1] = 0
+    xb[2, 5] = np.uint16(0x7fc0)
+    xb[3, 300] = np.uint16(0x7f80)
+    xb[4, 1000] = synthetic.f32_to_bf16_bits(np.float32(3.0e4)).item()
+    xb[5, 128:256] = 0
+    for fmt in (I8, FP8):
+        for rotation in (0, 128):
+            print(f"fused group special rows src={src} fmt={fmt} rot={rotation}", flush=True)
+            run_group_pair(dev, orc, xb, fmt, N, K, rotation, src=src, oracle=False)
