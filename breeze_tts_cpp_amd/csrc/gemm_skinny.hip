@@ -541,18 +541,18 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             // for |v| <= a (or |v| * 2^126 < 448 exactly); with a = Inf the
             // inverse is 0.
             bool finite[MT];
-    #pragma unroll
+#pragma unroll
             for (int t = 0; t < MT; ++t) {
                 u16x2 top = {0, 0};
-    #pragma unroll
+#pragma unroll
                 for (int blk = 0; blk < NB; ++blk)
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < 4; ++p)
-    #pragma unroll
+#pragma unroll
                         for (int h = 0; h < 2; ++h) {
                             const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
                                                     xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
-    #pragma unroll
+#pragma unroll
                             for (int i = 0; i < 4; ++i)
                                 top = __builtin_elementwise_max(
                                     top, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                     amax[t] = widen(bits);
                 } else {
                     amax[t] = 0.f;
-    #pragma unroll
+#pragma unroll
                     for (int blk = 0; blk < NB; ++blk)
                         for (int p = 0; p < 4; ++p)
                             for (int h = 0; h < 2; ++h) {
@@ -582,24 +582,24 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
             // A workgroup barrier that waits for LDS only: __syncthreads' fence
             // would also wait for the weight slab DMA still in flight.
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    #pragma unroll
+#pragma unroll
             for (int t = 0; t < MT; ++t) {
                 float a = fq_amax[t * 16 + row16];
-    #pragma unroll
+#pragma unroll
                 for (int q = 1; q < WK; ++q) a = fmaxf(a, fq_amax[q * MT * 16 + t * 16 + row16]);
                 const float step = quant_scale<Fmt>(a);
                 const float inverse = 1.f / step;
                 if (wave == 0 && quad == 0) fq_scale[t * 16 + row16] = step;
-    #pragma unroll
+#pragma unroll
                 for (int blk = 0; blk < NB; ++blk)
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < 4; ++p) {
                         i32x4 codes;
-    #pragma unroll
+#pragma unroll
                         for (int h = 0; h < 2; ++h) {
                             const uint32_t wd[4] = {xraw[blk][t][p][h].x, xraw[blk][t][p][h].y,
                                                     xraw[blk][t][p][h].z, xraw[blk][t][p][h].w};
-    #pragma unroll
+#pragma unroll
                             for (int j = 0; j < 2; ++j) {
                                 if constexpr (Fmt == I8) {
                                     codes[2 * h + j] = int(encode_i8x4(
