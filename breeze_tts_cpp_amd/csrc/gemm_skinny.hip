@@ -81,18 +81,6 @@ __device__ __forceinline__ i32x4 load16(const uint8_t *p) {
     return *reinterpret_cast<const i32x4 *>(p);
 }
 
-// The value of lane l ^ S (S = 16 or 32) by gfx950's v_permlane16_swap /
-// v_permlane32_swap (one VALU instruction; a shuffle goes through LDS). With
-// both operands x, the swap leaves the partner's value in the first result
-// for lanes with bit S set and in the second for the others.
-template <int S> __device__ __forceinline__ float lane_xor(float v) {
-    static_assert(S == 16 || S == 32, "row swaps");
-    const unsigned u = __float_as_uint(v);
-    const auto r = S == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
-                           : __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    return __uint_as_float((threadIdx.x & S) ? r[0] : r[1]);
-}
-
 // Four 16-byte LDS reads by explicit ds_read_b128 instructions and their
 // wait, in one statement. The compiler's wait insertion treats any LDS read
 // as possibly reading what an outstanding global->LDS copy writes and then
@@ -575,8 +563,8 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                                 }
                             }
                 }
-                amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 16, 64));
-                amax[t] = fmaxf(amax[t], __shfl_xor(amax[t], 32, 64));
+                amax[t] = fmaxf(amax[t], lane_xor<16>(amax[t]));
+                amax[t] = fmaxf(amax[t], lane_xor<32>(amax[t]));
                 if (quad == 0) fq_amax[wave * MT * 16 + t * 16 + row16] = amax[t];
             }
             // A workgroup barrier that waits for LDS only: __syncthreads' fence

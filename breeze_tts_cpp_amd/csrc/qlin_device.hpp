@@ -246,10 +246,41 @@ __device__ __noinline__ void finish4(float (&v)[4], const uint16_t *bias, int n,
 }
 
 // ---------------------------------------------------------------- wave64 reductions
-// Max over a power-of-two lane group of width W (aligned), via xor shuffles.
+// The value held by lane (lane ^ S), S a power of two up to 32, without an
+// LDS round trip: S = 1, 2 by a DPP quad permutation, 4 by two row rotations
+// and a select, 8 by a row rotation, 16 / 32 by gfx950's row swaps
+// (v_permlane16_swap / v_permlane32_swap, which with both operands x leave
+// the partner's value in the first result for lanes with bit S set and in
+// the second for the others).
+template <int S> __device__ __forceinline__ float lane_xor(float v) {
+    const int u = __float_as_int(v);
+    if constexpr (S == 1) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    } else if constexpr (S == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    } else if constexpr (S == 4) {
+        // row_ror:n moves data n lanes up a 16-lane row: lane l reads l - n
+        const int from_below = __builtin_amdgcn_update_dpp(0, u, 0x124, 0xF, 0xF, false);  // l - 4
+        const int from_above = __builtin_amdgcn_update_dpp(0, u, 0x12C, 0xF, 0xF, false);  // l + 4
+        return __int_as_float((threadIdx.x & 4) ? from_below : from_above);
+    } else if constexpr (S == 8) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x128, 0xF, 0xF, false));  // row_ror:8
+    } else {
+        static_assert(S == 16 || S == 32, "lane distance");
+        const auto r = S == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __int_as_float(int((threadIdx.x & S) ? r[0] : r[1]));
+    }
+}
+
+// Max over a power-of-two lane group of width W (aligned).
 template <int W> __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int d = 1; d < W; d *= 2) v = fmaxf(v, __shfl_xor(v, d, 64));
+    if constexpr (W > 1) v = fmaxf(v, lane_xor<1>(v));
+    if constexpr (W > 2) v = fmaxf(v, lane_xor<2>(v));
+    if constexpr (W > 4) v = fmaxf(v, lane_xor<4>(v));
+    if constexpr (W > 8) v = fmaxf(v, lane_xor<8>(v));
+    if constexpr (W > 16) v = fmaxf(v, lane_xor<16>(v));
+    if constexpr (W > 32) v = fmaxf(v, lane_xor<32>(v));
     return v;
 }
 

@@ -9,6 +9,8 @@
 #pragma once
 #include "qlin_device.hpp"
 
+#include <type_traits>
+
 namespace qlin {
 namespace {
 
@@ -106,14 +108,18 @@ __device__ __forceinline__ void rotate8(float (&v)[8], int column) {
             }
     }
     const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int span = 1; span < 16; span *= 2) {
+    auto stage = [&](auto span_, auto xchg) {
+        constexpr int span = decltype(span_)::value;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            float other = __shfl_xor(v[i], span, 64);
+            const float other = xchg(v[i]);
             v[i] = (lane & span) ? other - v[i] : v[i] + other;
         }
-    }
+    };
+    stage(std::integral_constant<int, 1>{}, [](float x) { return lane_xor<1>(x); });
+    stage(std::integral_constant<int, 2>{}, [](float x) { return lane_xor<2>(x); });
+    stage(std::integral_constant<int, 4>{}, [](float x) { return lane_xor<4>(x); });
+    stage(std::integral_constant<int, 8>{}, [](float x) { return lane_xor<8>(x); });
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] *= 0.08838834764831845f;
 }
@@ -141,7 +147,10 @@ __device__ __forceinline__ void encode_group8(const float (&v)[8], uint8_t *__re
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    for (int d = 1; d < lanes; d *= 2) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    if (lanes > 1) amax = fmaxf(amax, lane_xor<1>(amax));
+    if (lanes > 2) amax = fmaxf(amax, lane_xor<2>(amax));
+    if (lanes > 4) amax = fmaxf(amax, lane_xor<4>(amax));
+    if (lanes > 8) amax = fmaxf(amax, lane_xor<8>(amax));
     const float step = quant_scale<Fmt>(amax);
     if (column < cols && (column % group) == 0) scales[size_t(column / group) * rows + row] = step;
     store8<Fmt, Vec>(dst, column, cols, v, 1.f / step);
