@@ -36,6 +36,9 @@ CASES = [
     (3, 128),
     (5, 4096),
     (64, 2048),
+    # one 8-column piece per lane over 512..1024 threads (decode-sized rows)
+    (7, 2056), (9, 8192), (3, 7000),
+    (600, 6144),  # many rows: 256 threads of three pieces
 ]
 
 
@@ -51,7 +54,7 @@ def test_token_quant(dev, orc, fmt, rows, cols):
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])
-@pytest.mark.parametrize("rows,cols", [(4, 2048), (8, 6144), (2, 128), (3, 20480)])
+@pytest.mark.parametrize("rows,cols", [(4, 2048), (8, 6144), (2, 128), (3, 20480), (5, 8192)])
 def test_rotated_token_quant(dev, orc, fmt, rows, cols):
     print(f"rotated_token_quant fmt={fmt} rows={rows} cols={cols}", flush=True)
     bits = synthetic.activations(rows, cols, seed=cols + 1)
