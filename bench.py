@@ -54,6 +54,80 @@ def quant_bytes(M, K, group=0):
 
 
 
+def bench_decoder_layer(torch, qlinear, synthetic, dev, stream, layers, args):
+    """The same 16 layers' weights in the reference decoder's call order
+    (decoder.h:242,271-275,292) at M=32, INT8: residual + RMSNorm -> quant
+    (qlin_quantized_norm) -> qkv GEMM; o_proj as a linear (quantize + GEMM);
+    residual + RMSNorm -> quant -> gate_up GEMM; SiLU(gate)*up -> quant
+    (qlin_quantized_gated) -> down GEMM. Attention itself is outside the path
+    (its output is a fixed synthetic tensor). One captured graph of the 16
+    layers, timed like the step; bytes = the GEMMs' operands and outputs plus
+    each producer's algorithmic bytes."""
+    M, H, W = M_DECODE, 2048, 6144
+    I8 = qlinear.I8
+
+    def bf(rows, cols, seed):
+        return torch.from_numpy(synthetic.activations(rows, cols, seed=seed).view(np.int16)).view(
+            torch.bfloat16).to(dev)
+
+    residual, attn = bf(M, H, 11), bf(M, H, 12)
+    norm_w = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    buf = {
+        "xq_h": torch.empty((M, H), dtype=torch.uint8, device=dev),
+        "sx": torch.empty((M,), dtype=torch.float32, device=dev),
+        "xq_w": torch.empty((M, W), dtype=torch.uint8, device=dev),
+        "qkv": torch.empty((M, 4096), dtype=torch.bfloat16, device=dev),
+        "o": torch.empty((M, H), dtype=torch.bfloat16, device=dev),
+        "gu": torch.empty((M, 2 * W), dtype=torch.bfloat16, device=dev),
+        "down": torch.empty((M, H), dtype=torch.bfloat16, device=dev),
+    }
+    paths = {n: qlinear.plan(M, N, K, I8) for n, (N, K) in synthetic.PROJECTIONS.items()}
+
+    def layer(entry):
+        qlinear.quantized_norm(residual, norm_w, I8, update=buf["down"], values=buf["xq_h"],
+                               scales=buf["sx"], stream=stream)
+        qlinear.gemm(buf["xq_h"], buf["sx"], entry["qkv"]["wq"], entry["qkv"]["sw"], I8,
+                     path=paths["qkv"], out=buf["qkv"], stream=stream)
+        qlinear.linear(attn, entry["o_proj"]["wq"], entry["o_proj"]["sw"], I8,
+                       path=paths["o_proj"], scratch=(buf["xq_h"], buf["sx"]), out=buf["o"],
+                       stream=stream)
+        qlinear.quantized_norm(residual, norm_w, I8, update=buf["o"], values=buf["xq_h"],
+                               scales=buf["sx"], stream=stream)
+        qlinear.gemm(buf["xq_h"], buf["sx"], entry["gate_up"]["wq"], entry["gate_up"]["sw"], I8,
+                     path=paths["gate_up"], out=buf["gu"], stream=stream)
+        qlinear.quantized_gated(buf["gu"], I8, kind=0, values=buf["xq_w"], scales=buf["sx"],
+                                stream=stream)
+        qlinear.gemm(buf["xq_w"], buf["sx"], entry["down"]["wq"], entry["down"]["sw"], I8,
+                     path=paths["down"], out=buf["down"], stream=stream)
+
+    buf["down"].zero_()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for entry in layers:
+            layer(entry)
+    torch.cuda.synchronize()
+    for _ in range(max(3, args.warmup)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    gemms = sum(gemm_bytes(M, N, K) for _, (N, K) in synthetic.PROJECTIONS.items())
+    norm = 7 * M * H + 2 * H + 4 * M
+    gated = 5 * M * W + 4 * M
+    layer_bytes = gemms + quant_bytes(M, H) + 2 * norm + gated
+    return {"ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / len(layers), 2),
+            "GBps": round(layer_bytes * len(layers) / (ms * 1e-3) / 1e9, 1),
+            "layer_bytes": layer_bytes,
+            "sequence": "norm->quant, qkv GEMM, o_proj linear, norm->quant, gate_up GEMM, "
+                        "SiLU*up->quant, down GEMM"}
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +244,9 @@ def main():
                               for _, (N, K) in projections)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
+    progress("decoder layer")
+    decoder_layer = bench_decoder_layer(torch, qlinear, synthetic, dev, stream, layers, args)
+
     # ---- per projection, per format and token count: graphs that rotate
     # through >= 640 MB of distinct weights (so HBM, not the 256 MB Infinity
     # Cache, serves them), timed with events on the launch stream: the GEMM on
@@ -222,6 +299,7 @@ def main():
                    "tokens": M_DECODE, "layers": LAYERS, "format": "int8",
                    "step_bytes": step_bytes},
         "decode_projections": per_proj,
+        "decoder_layer": decoder_layer,
         "decode_sweep": sweep,
         "roofline": roofline,
     }
