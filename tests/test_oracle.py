@@ -331,3 +331,82 @@ def test_cpu_baseline_equals_oracle_pipeline(orc):
     xq, sx = orc.quantize_rows(bits_x, I8, group=128, rotation=128)
     ref, _ = orc.gemm_grouped(xq, sx, wq, sw, I8, 128, 128)
     assert np.array_equal(y, ref)
+
+
+# ---------------------------------------------------------------- evaluation orders
+def _butterflies_f32(v, strides):
+    v = v.astype(np.float32).copy()
+    for span in strides:
+        for i in range(128):
+            if not i & span:
+                a, b = v[i], v[i | span]
+                v[i], v[i | span] = a + b, a - b
+    return v
+
+
+def test_rotation_stride_order_is_observable_and_ascending(orc):
+    """The H128 transform is order-free in exact arithmetic, so the fp32 result
+    pins the butterfly order only where the orders round differently. The
+    reference runs strides 1, 2, ..., 64 with the sum on the lower index and a
+    separate multiply by 1/sqrt(128) afterwards (quant_device.cuh:96-125).
+    On random blocks the descending order and a scale folded into the sign
+    step differ from that in fp32; the oracle must give the ascending result on
+    every block and differ from each alternative on some block."""
+    rng = np.random.default_rng(21)
+    inv = np.float32(0.08838834764831845)
+    differs_desc = differs_folded = 0
+    for c0 in range(0, 20 * 128, 128):
+        x = (rng.standard_normal(128) * 3).astype(np.float32)
+        signed = x * orc.rotation_signs(c0 + 128)[c0:]
+        asc = _butterflies_f32(signed, [1, 2, 4, 8, 16, 32, 64]) * inv
+        desc = _butterflies_f32(signed, [64, 32, 16, 8, 4, 2, 1]) * inv
+        folded = _butterflies_f32(signed * inv, [1, 2, 4, 8, 16, 32, 64])
+        y = orc.rotate128(x, c0)
+        assert np.array_equal(y, asc), c0
+        differs_desc += not np.array_equal(y, desc)
+        differs_folded += not np.array_equal(y, folded)
+    assert differs_desc > 0 and differs_folded > 0
+
+
+def _round_f32(q):
+    """Correctly rounded (ties to even) float32 of an exact Fraction."""
+    from fractions import Fraction
+    c = np.float32(float(q))
+    best = None
+    for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        d = abs(Fraction(float(cand)) - q)
+        key = (d, int(np.array(cand).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, cand)
+    return best[1]
+
+
+def test_grouped_accumulation_is_one_fma_per_group(orc):
+    """Group partials accumulate as r = fmaf(p, sa*sb, r): the scale product is
+    rounded first and the product-plus-sum is rounded once (quant_grouped.cu:144,
+    compiled with nvcc's default contraction). Evaluated exactly with
+    fractions, that differs from the uncontracted round(round(p*s) + r) and from
+    fmaf(p*sa, sb, r) on many random two-group dot products; the oracle must
+    give the contracted value every time."""
+    from fractions import Fraction
+    rng = np.random.default_rng(22)
+    seen_unfused = seen_other_assoc = 0
+    for _ in range(200):
+        xq = rng.integers(-127, 128, (1, 256)).astype(np.int8)
+        wq = rng.integers(-127, 128, (1, 256)).astype(np.int8)
+        sx = rng.uniform(0.001, 0.1, (2, 1)).astype(np.float32)
+        sw = rng.uniform(1e-4, 1e-2, (2, 1)).astype(np.float32)
+        _, yf = orc.gemm_grouped(xq.view(np.uint8), sx, wq.view(np.uint8), sw, I8, 128, 128)
+        p = [int(xq[0, g * 128:(g + 1) * 128].astype(np.int64) @ wq[0, g * 128:(g + 1) * 128].astype(np.int64))
+             for g in range(2)]
+        s = [np.float32(sx[g, 0] * sw[g, 0]) for g in range(2)]
+        r0 = _round_f32(Fraction(p[0]) * Fraction(float(s[0])))
+        fused = _round_f32(Fraction(p[1]) * Fraction(float(s[1])) + Fraction(float(r0)))
+        assert yf[0, 0] == fused
+        unfused = np.float32(_round_f32(Fraction(p[1]) * Fraction(float(s[1]))) + r0)
+        seen_unfused += unfused != fused
+        ps = [_round_f32(Fraction(p[g]) * Fraction(float(sx[g, 0]))) for g in range(2)]
+        r0b = _round_f32(Fraction(float(ps[0])) * Fraction(float(sw[0, 0])))
+        other = _round_f32(Fraction(float(ps[1])) * Fraction(float(sw[1, 0])) + Fraction(float(r0b)))
+        seen_other_assoc += other != fused
+    assert seen_unfused > 0 and seen_other_assoc > 0, (seen_unfused, seen_other_assoc)
