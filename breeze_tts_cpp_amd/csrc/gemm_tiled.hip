@@ -79,6 +79,17 @@ __device__ __forceinline__ void lds_barrier() {
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
+// Unit scales: the stage-slot scale DMA of an operand without K groups copies
+// these, so the group rescale reads its slot unconditionally (1 * s and s * 1
+// are exact).
+#define QLIN_ONES4 1.f, 1.f, 1.f, 1.f
+#define QLIN_ONES16 QLIN_ONES4, QLIN_ONES4, QLIN_ONES4, QLIN_ONES4
+#define QLIN_ONES64 QLIN_ONES16, QLIN_ONES16, QLIN_ONES16, QLIN_ONES16
+__device__ const float kUnitScales[256] = {QLIN_ONES64, QLIN_ONES64, QLIN_ONES64, QLIN_ONES64};
+#undef QLIN_ONES64
+#undef QLIN_ONES16
+#undef QLIN_ONES4
+
 template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, bool KFull,
           class Out, bool PackedW = false, int GS = 128>
 __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
@@ -153,10 +164,15 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // K-group scales [ceil(K/g), N] and [ceil(K/g), M] (the host checks that
     // both arrays stay below 2^31 bytes).
     const int kgroups = (K + kGroupK - 1) / kGroupK;
+    // An operand without groups reads the 1 KB of unit scales instead, at
+    // every group.
+    const bool w_groups = Grouped && weight_group, x_groups = Grouped && input_group;
     const __amdgpu_buffer_rsrc_t rsrc_sw = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(sw), 0, Grouped && weight_group ? kgroups * N * 4 : 0, 0x00020000);
+        const_cast<float *>(w_groups ? sw : kUnitScales), 0, w_groups ? kgroups * N * 4 : 1024,
+        0x00020000);
     const __amdgpu_buffer_rsrc_t rsrc_sx = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(sx), 0, Grouped && input_group ? kgroups * M * 4 : 0, 0x00020000);
+        const_cast<float *>(x_groups ? sx : kUnitScales), 0, x_groups ? kgroups * M * 4 : 1024,
+        0x00020000);
 
     // Load instruction i of this wave fills stage rows [(i*NW + wave)*RPI, +RPI),
     // 1 KB of LDS in lane order: lane -> row += lane / CPR, physical chunk
@@ -174,11 +190,11 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // The scale DMA's per-lane offset (host-checked: both scale arrays stay
     // below 2^31 bytes): group g's row starts at g * scale_stride.
     const bool scale_wv = wave == 0, scale_xv = wave == 1;
-    const bool scale_live = Grouped && (scale_wv || scale_xv) &&
-                            (scale_wv ? weight_group : input_group) &&
-                            lane * 4 < (scale_wv ? BN : BM);
-    const uint32_t scale_stride = uint32_t((scale_wv ? N : M) * 4);
-    const uint32_t scale_lane = uint32_t((scale_wv ? n_base : m_base) * 4 + lane * 16);
+    const bool scale_groups = scale_wv ? w_groups : x_groups;
+    const bool scale_live = Grouped && (scale_wv || scale_xv) && lane * 4 < (scale_wv ? BN : BM);
+    const uint32_t scale_stride = scale_groups ? uint32_t((scale_wv ? N : M) * 4) : 0u;
+    const uint32_t scale_lane =
+        uint32_t((scale_groups ? (scale_wv ? n_base : m_base) * 4 : 0) + lane * 16);
     auto issue = [&](int stage, int k0) {
         uint8_t *base = lds + (stage % STAGES) * STAGE_BYTES;
         const bool kin = KFull || k0 + lane_chunk * 16 < K;
@@ -200,9 +216,9 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         }
         if constexpr (kScaleDma) {
             // The stage's group scales: sw[g][n_base ..) by wave 0, sx[g][m_base ..)
-            // by wave 1 (lanes past the tile, or an operand without groups,
-            // read zero through an out-of-range offset); waves 2.. write zeros
-            // into the slot's third KB.
+            // by wave 1 (unit scales for an operand without groups; lanes past
+            // the tile read zero through an out-of-range offset); waves 2..
+            // write zeros into the slot's third KB.
             const uint32_t g = uint32_t(k0 / kGroupK);
             const uint32_t off = scale_live ? g * scale_stride + scale_lane : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -500,7 +516,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             float sxg[WTM];
 #pragma unroll
             for (int j = 0; j < WTM; ++j)
-                sxg[j] = input_group ? slot[256 + wave_m * 16 * WTM + j * 16 + row16] : 1.f;
+                sxg[j] = slot[256 + wave_m * 16 * WTM + j * 16 + row16];
 #pragma unroll
             for (int i = 0; i < WTN; ++i) {
                 Acc part[WTM];
@@ -523,7 +539,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                 float swg[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    swg[r] = weight_group ? slot[wave_n * 16 * WTN + i * 16 + quad * 4 + r] : 1.f;
+                    swg[r] = slot[wave_n * 16 * WTN + i * 16 + quad * 4 + r];
 #pragma unroll
                 for (int j = 0; j < WTM; ++j)
 #pragma unroll
@@ -569,12 +585,11 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                                                                 ROWS * BK);
 #pragma unroll
             for (int j = 0; j < WTM; ++j)
-                xg[j] = input_group ? slot[256 + wave_m * 16 * WTM + j * 16 + row16] : 1.f;
+                xg[j] = slot[256 + wave_m * 16 * WTM + j * 16 + row16];
 #pragma unroll
             for (int i = 0; i < WTN; ++i)
-                wg[i] = weight_group ? *reinterpret_cast<const f32x4 *>(slot + wave_n * 16 * WTN +
-                                                                         i * 16 + quad * 4)
-                                     : f32x4{1.f, 1.f, 1.f, 1.f};
+                wg[i] = *reinterpret_cast<const f32x4 *>(slot + wave_n * 16 * WTN + i * 16 +
+                                                         quad * 4);
         };
         auto apply = [&](auto bank_) {
             constexpr int B = decltype(bank_)::value;
@@ -687,12 +702,11 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             float xg[WTM];
 #pragma unroll
             for (int j = 0; j < WTM; ++j)
-                xg[j] = input_group ? slot[256 + wave_m * 16 * WTM + j * 16 + row16] : 1.f;
+                xg[j] = slot[256 + wave_m * 16 * WTM + j * 16 + row16];
 #pragma unroll
             for (int i = 0; i < WTN; ++i) {
-                const f32x4 wg = weight_group ? *reinterpret_cast<const f32x4 *>(
-                                                    slot + wave_n * 16 * WTN + i * 16 + quad * 4)
-                                              : f32x4{1.f, 1.f, 1.f, 1.f};
+                const f32x4 wg =
+                    *reinterpret_cast<const f32x4 *>(slot + wave_n * 16 * WTN + i * 16 + quad * 4);
 #pragma unroll
                 for (int j = 0; j < WTM; ++j)
 #pragma unroll
