@@ -409,7 +409,10 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
             else if (s + 1 < stages) wait_vmcnt<0>();
             lds_barrier();
-            if (s + 1 < stages) read(s + 1, na, nb);
+            // FP8 reads the next fragments unconditionally (after the last
+            // stage, a ring slot whose fragments go unused): a conditional
+            // read makes the compiler copy every i32x8 fragment at each stage.
+            if (Fmt == FP8 || s + 1 < stages) read(s + 1, na, nb);
             mma(a, bb, kEarly, WTN);
         };
         Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
@@ -1011,23 +1014,33 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
                     acc[i][j0 + j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                         fa[i], fb[j], acc[i][j0 + j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
         };
-        i32x8 fa[4], fb0[2], fb1[2];
-        if (stages >= STAGES) wait_vmcnt<INSTS * (STAGES - 1)>();
-        else wait_vmcnt<0>();
-        lds_barrier();
-        read0(0, fa, fb0);
-        for (int s = 0; s < stages; ++s) {
+        // Stage s uses A fragments fa (read during stage s-1); the next
+        // stage's go to the other set, so that the loop, unrolled by two,
+        // carries no fragment copies between iterations.
+        i32x8 fa0[4], fa1[4], fb0[2], fb1[2];
+        auto step = [&](int s, const i32x8 (&fa)[4], i32x8 (&na)[4]) {
             read1(s, fb1);
             mma(fa, fb0, 0);
-            // fa is still needed by the second half: the next stage's A
-            // fragments are read after it.
             if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
             else wait_vmcnt<0>();
             lds_barrier();
             if (s + STAGES < stages) issue(s + STAGES, (s + STAGES) * BK);
             mma(fa, fb1, 2);
-            if (s + 1 < stages) read0(s + 1, fa, fb0);
+            // Unconditional (after the last stage it reads a ring slot whose
+            // fragments go unused): a conditional read here makes the
+            // compiler copy every fragment register at each stage.
+            read0(s + 1, na, fb0);
+        };
+        if (stages >= STAGES) wait_vmcnt<INSTS * (STAGES - 1)>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        read0(0, fa0, fb0);
+        int s = 0;
+        for (; s + 1 < stages; s += 2) {
+            step(s, fa0, fa1);
+            step(s + 1, fa1, fa0);
         }
+        if (s < stages) step(s, fa0, fa1);
     }
 
     // Epilogue: scale, round, transpose through LDS (the ring is free after
