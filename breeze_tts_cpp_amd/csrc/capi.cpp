@@ -126,8 +126,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     // last round is at least 90% occupied.
     //  - INT8 per-channel, all with eight waves: 256x256 (128x64 waves) when
     //    it has >= 192 tiles (qkv/gate_up at 4096, gate_up at 1024); else
-    //    256x128 (128x32 waves) for >= 256 tiles in full rounds: down at 4096
-    //    57.6 us against 68.6 us on 128x128; else 128x128 (64x32 waves): qkv
+    //    256x128 (128x32 waves, 128-byte K stages) for >= 256 tiles in full
+    //    rounds: down at 4096 54 us against 68 us on 128x128; else 128x128
+    //    (64x32 waves): qkv
     //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
     //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
     //    when it has >= 256 tiles; else 256x128 (one workgroup of 128x64
@@ -172,15 +173,16 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         if (tiles_256x128 >= 256 && full && !(small_group && fmt == QLIN_FP8)) p.channels = 256;
     }
     // A 128x128 grid of at most 128 tiles fills half the GPU or less; 128x64
-    // tiles (four 64x32 waves; FP8 per-channel eight 64x16 waves) double the
-    // workgroups: o_proj / down at M = 1024 (128 tiles of 128x128), INT8
-    // 18.7 / 36.6 us against 17.9 / 31.7, FP8 19.6 / 38.7 against 18.2 /
-    // 32.9, group_int8 22.0 / 46.4 against 20.7 / 41.3 (random operands).
+    // tiles (per-channel: eight 64x16 waves over 128-byte K stages; K groups:
+    // four 64x32 waves) double the workgroups: o_proj / down at M = 1024 (128
+    // tiles of 128x128), INT8 18.2 / 36.9 us against 17.2 / 25.4 (four 64x32
+    // waves: 16.9 / 32.2), FP8 19.6 / 38.7 against 18.2 / 32.9, group_int8
+    // 22.0 / 46.4 against 20.7 / 41.3 (random operands).
     const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
     const long tiles_128 = long((N + 127) / 128) * ((rows + 127) / 128);
     if (p.channels == 128 && p.tokens == 128 && tiles_128 <= 128 && !small_group) {
         p.tokens = 64;
-        p.waves = fmt == QLIN_FP8 && !grouped ? 8 : 4;
+        p.waves = grouped ? 4 : 8;
     }
     return p;
 }
@@ -247,8 +249,8 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         // (1) or eight of 64x32 (8).
         const bool wave_ok = (p.channels == 256 && p.tokens == 256) ? (p.waves == 8 || p.waves == 4)
                              : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2 || p.waves == 8)
-                             : p.tokens == 64 ? (p.waves == 4 || (p.waves == 8 && fmt == QLIN_FP8 &&
-                                                                  !input_group && !weight_group))
+                             : p.tokens == 64 ? (p.waves == 4 || (p.waves == 8 && !input_group &&
+                                                                  !weight_group))
                                               : (p.waves == 1 || p.waves == 8);
         if (!wave_ok)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,

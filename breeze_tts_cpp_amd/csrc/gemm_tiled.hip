@@ -47,6 +47,13 @@ template <> struct TileMma<I8> {
     __device__ static void run(Acc &c, const i32x4 &a, const i32x4 &b) {
         c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
     }
+    // A 128-byte stage: K [0, 64) in registers 0-3, [64, 128) in 4-7.
+    __device__ static void run(Acc &c, const i32x8 &a, const i32x8 &b) {
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(i32x4{a[0], a[1], a[2], a[3]},
+                                                  i32x4{b[0], b[1], b[2], b[3]}, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(i32x4{a[4], a[5], a[6], a[7]},
+                                                  i32x4{b[4], b[5], b[6], b[7]}, c, 0, 0, 0);
+    }
 };
 template <> struct TileMma<FP8> {
     using Acc = f32x4;
@@ -125,7 +132,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
     // exactly 64, the FP8 16x16x128 pipeline 128; K groups are 128 wide (two
     // INT8 stages or one FP8 stage).
-    static_assert(Fmt == I8 ? (BK == 64 || GS < 128) : (BK == 64 || BK == 128), "K bytes per stage");
+    static_assert(Fmt == I8 ? (BK == 64 || GS < 128 || !Grouped) : (BK == 64 || BK == 128),
+                  "K bytes per stage");
     static_assert(!Grouped || Fmt == I8 || BK == 128, "FP8 K groups use 128-byte stages");
     constexpr int kGroupK = 128;
     constexpr int SPG = kGroupK / BK;  // stages per K group
@@ -356,14 +364,15 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         }
         if (s < stages) step(s, a0, b0, a1, b1);
     } else if constexpr (!Grouped) {
-        // Software pipeline, one MFMA sub-step per stage (INT8: BK = 64,
-        // FP8: BK = 128). Iteration s: issue the global loads of stage
+        // Software pipeline, one stage per step (INT8: BK = 64, one 64-K
+        // MFMA per tile, or BK = 128, two; FP8: BK = 128, one 128-K MFMA).
+        // Iteration s: issue the global loads of stage
         // s+STAGES-1; run the first MFMA rows of stage s; wait for stage s+1
         // and barrier; read stage s+1 fragments into the other register set
         // while the remaining MFMAs of stage s run. The barrier also retires
         // every wave's reads of buffer s % STAGES, which iteration s+1 refills.
-        static_assert(Fmt == FP8 || BK == 64, "INT8 pipeline uses 64-byte stages");
-        using Frag = std::conditional_t<Fmt == I8, i32x4, i32x8>;
+        static_assert(BK == 64 ? Fmt == I8 : BK == 128, "per-channel stage size");
+        using Frag = std::conditional_t<BK == 64, i32x4, i32x8>;
         const int a_off = a_row0 * BK, b_off = b_row0 * BK;
         const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
         const int a_c1 = ((4 + quad) ^ swizzle<BK>(a_row0)) * 16;
@@ -374,7 +383,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 #pragma unroll
             for (int j = 0; j < WTM; ++j) {
                 const i32x4 lo = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c0);
-                if constexpr (Fmt == I8) {
+                if constexpr (BK == 64) {
                     bb[j] = lo;
                 } else {
                     const i32x4 hi = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c1);
@@ -384,7 +393,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 #pragma unroll
             for (int i = 0; i < WTN; ++i) {
                 const i32x4 lo = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c0);
-                if constexpr (Fmt == I8) {
+                if constexpr (BK == 64) {
                     a[i] = lo;
                 } else {
                     const i32x4 hi = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c1);
@@ -409,10 +418,11 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
             else if (s + 1 < stages) wait_vmcnt<0>();
             lds_barrier();
-            // FP8 reads the next fragments unconditionally (after the last
-            // stage, a ring slot whose fragments go unused): a conditional
-            // read makes the compiler copy every i32x8 fragment at each stage.
-            if (Fmt == FP8 || s + 1 < stages) read(s + 1, na, nb);
+            // i32x8 fragments (128-byte stages) are read unconditionally
+            // (after the last stage, a ring slot whose fragments go unused):
+            // a conditional read makes the compiler copy every one of them at
+            // each stage.
+            if (BK == 128 || s + 1 < stages) read(s + 1, na, nb);
             mma(a, bb, kEarly, WTN);
         };
         Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
@@ -1169,9 +1179,11 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 4, 2, GBK, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
-        // 256x128 with eight waves of 128x32.
+        // 256x128 with eight waves of 128x32 over 128-byte K stages (two
+        // MFMAs per tile and stage, half the barriers of 64-byte stages:
+        // down at 4096 54 us against 59 us, o_proj 28 against 29).
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 2, 64, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
@@ -1185,9 +1197,12 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 2, 64, 4, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
-        // 128x64: four waves of 64x32.
+        // 128x64: four waves of 64x32, or eight of 64x16 over 128-byte K
+        // stages (down at 1024 25 us against 32 us).
         if (p.channels == 128 && p.tokens == 64 && p.waves == 4)
             return launch_shape<Fmt, 2, 2, 4, 2, 64, 4, false, Out>(a, s);
+        if (p.channels == 128 && p.tokens == 64 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, false, Out>(a, s);
         return -4;
     } else {
         // 256x128 with eight waves of 128x32.
