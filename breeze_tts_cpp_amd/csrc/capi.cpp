@@ -131,9 +131,10 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    (64x32 waves): qkv
     //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
     //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
-    //    when it has >= 256 tiles; else 256x128 (one workgroup of 128x64
-    //    waves) for >= 256 tiles in full rounds: o_proj at 4096 26.1 us
-    //    against 28.5 us on 128x128; else 128x128 with eight 64x32 waves on
+    //    when it has >= 256 tiles; else 256x128 (eight 128x32 waves,
+    //    16x16x128 MFMA over 128-byte stages) for >= 256 tiles in full
+    //    rounds: o_proj at 4096 27.7 us against 30.2 us with four 128x64
+    //    waves on 32x32x64 and 30.4 on 128x128; else 128x128 with eight 64x32 waves on
     //    the 16x16x128 MFMA over 128-byte K stages: down at 1024 35.5 us
     //    against 45.3 us with four 32x32x64 waves.
     //  (Variants timed interleaved after a warm-up, median of 5 rounds: the
@@ -164,6 +165,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
             p.waves = 4;
         } else if (tiles_256x128 >= 256 && full) {
             p.channels = 256;
+            p.waves = 8;
         } else {
             p.waves = 8;
         }

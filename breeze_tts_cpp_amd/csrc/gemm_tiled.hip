@@ -1205,9 +1205,11 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, false, Out>(a, s);
         return -4;
     } else {
-        // 256x128 with eight waves of 128x32.
+        // 256x128 with eight waves of 128x32 on the 16x16x128 MFMA over
+        // 128-byte K stages (down at 4096 54 us against 60 us for one
+        // workgroup of four 128x64 waves on 32x32x64).
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 2, 64, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
