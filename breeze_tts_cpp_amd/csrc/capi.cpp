@@ -130,8 +130,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    rounds: down at 4096 54 us against 68 us on 128x128; else 128x128
     //    (64x32 waves): qkv
     //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
-    //  - FP8 per-channel: 256x256 with four 128x128 waves (32x32x64 MFMA)
-    //    when it has >= 256 tiles; else 256x128 (eight 128x32 waves,
+    //  - FP8 per-channel: 256x256 with eight 128x64 waves (32x32x64 MFMA)
+    //    when it has >= 256 tiles (gate_up at 4096 114 us against 116 us
+    //    with four 128x128 waves); else 256x128 (eight 128x32 waves,
     //    16x16x128 MFMA over 128-byte stages) for >= 256 tiles in full
     //    rounds: o_proj at 4096 27.7 us against 30.2 us with four 128x64
     //    waves on 32x32x64 and 30.4 on 128x128; else 128x128 with eight 64x32 waves on
@@ -162,7 +163,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     } else if (!grouped) {
         if (tiles_256 >= 256) {
             p.channels = p.tokens = 256;
-            p.waves = 4;
+            p.waves = 8;
         } else if (tiles_256x128 >= 256 && full) {
             p.channels = 256;
             p.waves = 8;

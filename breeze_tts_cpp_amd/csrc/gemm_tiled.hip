@@ -349,7 +349,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             if (s + STAGES - 1 < stages) wait_vmcnt<INSTS * (STAGES - 2)>();
             else if (s + 1 < stages) wait_vmcnt<0>();
             lds_barrier();
-            if (s + 1 < stages) read(s + 1, na, nb);
+            // Unconditional: see the 16x16 pipeline below.
+            read(s + 1, na, nb);
             mma(a, bb, kEarly, NA);
         };
         i32x8 a0[NA], b0[NBF], a1[NA], b1[NBF];

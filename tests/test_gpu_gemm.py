@@ -236,9 +236,7 @@ def _tiled_paths(grouped=False, fmt=I8):
     if not grouped:
         shapes = [(256, 128, 1)] + shapes
         # 32x32-MFMA kernels: four waves of 128x128, two waves of 128x128
-        shapes = [(256, 256, 4), (256, 128, 2)] + shapes
-        if fmt == I8:
-            shapes = [(256, 256, 8)] + shapes
+        shapes = [(256, 256, 8), (256, 256, 4), (256, 128, 2)] + shapes
     for channels, tokens, waves in shapes:
         yield Path(KIND_TILED, tokens, channels, 1, waves)
 
