@@ -176,16 +176,16 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         if (tiles_256x128 >= 256 && full && !(small_group && fmt == QLIN_FP8)) p.channels = 256;
     }
     // A 128x128 grid of at most 128 tiles fills half the GPU or less; 128x64
-    // tiles (per-channel: eight 64x16 waves over 128-byte K stages; K groups:
-    // four 64x32 waves) double the workgroups: o_proj / down at M = 1024 (128
-    // tiles of 128x128), INT8 18.2 / 36.9 us against 17.2 / 25.4 (four 64x32
-    // waves: 16.9 / 32.2), FP8 19.6 / 38.7 against 18.2 / 32.9, group_int8
-    // 22.0 / 46.4 against 20.7 / 41.3 (random operands).
+    // tiles (eight 64x16 waves over 128-byte K stages) double the
+    // workgroups: o_proj / down at M = 1024 (128 tiles of 128x128), INT8
+    // 18.2 / 36.9 us against 17.2 / 25.4 (four 64x32 waves: 16.9 / 32.2),
+    // FP8 19.6 / 38.7 against 18.2 / 32.9, group_int8 22.0 / 46.4 against
+    // 17.4 / 31.6 (four 64x32 waves: 20.0 / 38.8; random operands).
     const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
     const long tiles_128 = long((N + 127) / 128) * ((rows + 127) / 128);
     if (p.channels == 128 && p.tokens == 128 && tiles_128 <= 128 && !small_group) {
         p.tokens = 64;
-        p.waves = grouped ? 4 : 8;
+        p.waves = 8;
     }
     return p;
 }
@@ -252,8 +252,7 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         // (1) or eight of 64x32 (8).
         const bool wave_ok = (p.channels == 256 && p.tokens == 256) ? (p.waves == 8 || p.waves == 4)
                              : (p.channels == 256 && p.tokens == 128) ? (p.waves == 1 || p.waves == 2 || p.waves == 8)
-                             : p.tokens == 64 ? (p.waves == 4 || (p.waves == 8 && !input_group &&
-                                                                  !weight_group))
+                             : p.tokens == 64 ? (p.waves == 4 || p.waves == 8)
                                               : (p.waves == 1 || p.waves == 8);
         if (!wave_ok)
             return fail(QLIN_ERR_UNSUPPORTED, "tiled %dx%d path has no %d-wave variant", p.channels,

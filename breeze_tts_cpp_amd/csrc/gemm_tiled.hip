@@ -132,8 +132,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
     // exactly 64, the FP8 16x16x128 pipeline 128; K groups are 128 wide (two
     // INT8 stages or one FP8 stage).
-    static_assert(Fmt == I8 ? (BK == 64 || GS < 128 || !Grouped) : (BK == 64 || BK == 128),
-                  "K bytes per stage");
+    static_assert(BK == 64 || BK == 128, "K bytes per stage");
     static_assert(!Grouped || Fmt == I8 || BK == 128, "FP8 K groups use 128-byte stages");
     constexpr int kGroupK = 128;
     constexpr int SPG = kGroupK / BK;  // stages per K group
@@ -568,17 +567,30 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         // accumulate natively (exact int32) and the group is applied as
         // facc = fmaf(p, sx_g * sw_g, facc), groups ascending. The group's
         // scales come with its last stage (the stage slot's scale rows).
-        static_assert(Fmt == I8 && BK == 64, "the pipelined K-group path is INT8 on 64-byte stages");
-        using Frag = i32x4;
+        // 64-byte stages (two per group) or 128-byte stages (one group per
+        // stage, two MFMAs per tile; the 128x64 eight-wave tile).
+        static_assert(Fmt == I8, "the pipelined K-group path is INT8");
+        using Frag = std::conditional_t<BK == 64, i32x4, i32x8>;
         const int a_off = a_row0 * BK, b_off = b_row0 * BK;
         const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
+        const int a_c1 = ((4 + quad) ^ swizzle<BK>(a_row0)) * 16;
+        const int b_c1 = ((4 + quad) ^ swizzle<BK>(b_row0)) * 16;
+        auto frag = [&](const uint8_t *p, int c0, int c1) {
+            const i32x4 lo = *reinterpret_cast<const i32x4 *>(p + c0);
+            if constexpr (BK == 64) {
+                return lo;
+            } else {
+                const i32x4 hi = *reinterpret_cast<const i32x4 *>(p + c1);
+                return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+        };
         auto read = [&](int st, Frag (&a)[WTN], Frag (&bb)[WTM]) {
             const uint8_t *cur = lds + (st % STAGES) * STAGE_BYTES;
             const uint8_t *pa = cur + a_off, *pb = cur + b_off;
 #pragma unroll
-            for (int j = 0; j < WTM; ++j) bb[j] = *reinterpret_cast<const i32x4 *>(pb + j * 16 * BK + b_c0);
+            for (int j = 0; j < WTM; ++j) bb[j] = frag(pb + j * 16 * BK, b_c0, b_c1);
 #pragma unroll
-            for (int i = 0; i < WTN; ++i) a[i] = *reinterpret_cast<const i32x4 *>(pa + i * 16 * BK + a_c0);
+            for (int i = 0; i < WTN; ++i) a[i] = frag(pa + i * 16 * BK, a_c0, a_c1);
         };
       // Two banks of partials (tiles of at most 8 MFMA tiles per wave, i.e.
       // 128x128 with eight 64x32 waves): group g accumulates in bank g % 2,
@@ -749,7 +761,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             if (s + STAGES - 1 < stages) wait_ring(std::integral_constant<int, STAGES - 2>{});
             else if (s + 1 < stages) wait_vmcnt<0>();
             lds_barrier();
-            if (s + 1 < stages) read(s + 1, na, nb);
+            // i32x8 fragments: unconditional, as in the per-channel pipeline.
+            if (BK == 128 || s + 1 < stages) read(s + 1, na, nb);
         };
         Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
         if (stages >= STAGES - 1) wait_ring(std::integral_constant<int, STAGES - 2>{});
@@ -1178,6 +1191,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 4, 4, GBK, 4, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 64 && p.waves == 4)
             return launch_shape<Fmt, 2, 2, 4, 2, GBK, 4, true, Out>(a, s);
+        // 128x64 with eight 64x16 waves, one group per 128-byte stage.
+        if (p.channels == 128 && p.tokens == 64 && p.waves == 8)
+            return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
         // 256x128 with eight waves of 128x32 over 128-byte K stages (two

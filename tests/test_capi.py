@@ -86,7 +86,7 @@ def test_gemm_validation():
     assert call(M=256, path=qlinear.Path(T, 128, 256, 1, 2), ig=128, wg=128) == -4  # K groups: no 32x32 tiles
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 2)) == -4
     assert call(M=256, path=qlinear.Path(T, 64, 128, 1, 1)) == -4           # 128x64: 4 / 8 waves
-    assert call(M=256, path=qlinear.Path(T, 64, 128, 1, 8), ig=128, wg=128) == -4  # 8 waves: per-channel only
+    assert call(M=256, path=qlinear.Path(T, 64, 128, 1, 8), ig=32, wg=32) == -4  # small groups: no 128x64
     assert call(M=256, path=qlinear.Path(T, 64, 128, 1, 4), ig=32, wg=32) == -4
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 1), ig=32, wg=32) == -4  # small groups: 8 waves
     assert call(M=256, fmt=FP8, path=qlinear.Path(T, 128, 256, 1, 8), ig=64, wg=64) == -4  # FP8: 128x128
@@ -116,7 +116,7 @@ def test_prefill_plan_rules():
     assert tile(4096, "down", I8, 128) == (256, 128, 8) and tile(1024, "gate_up", I8, 64) == (128, 128, 8)
     # half-GPU 128x128 grids (o_proj / down at 1024: 128 tiles) take 128x64 tiles
     assert tile(1024, "down", I8) == (128, 64, 8) and tile(1024, "o_proj", FP8) == (128, 64, 8)
-    assert tile(1024, "down", I8, 128) == (128, 64, 4) and tile(1024, "o_proj", FP8, 128) == (128, 64, 4)
+    assert tile(1024, "down", I8, 128) == (128, 64, 8) and tile(1024, "o_proj", FP8, 128) == (128, 64, 8)
     assert tile(1024, "down", I8, 32) == (128, 128, 8)  # small groups: no 128x64 tile
 
 

@@ -230,9 +230,7 @@ def test_end_to_end_linear(dev, orc):
 def _tiled_paths(grouped=False, fmt=I8):
     """Every instantiated macro tile (channels x tokens, waves) for the mode."""
     from breeze_tts_cpp_amd.qlinear import Path, KIND_TILED
-    shapes = [(128, 128, 1), (256, 128, 8), (128, 128, 8), (128, 64, 4)]
-    if not grouped:
-        shapes = [(128, 64, 8)] + shapes  # 128-byte stages
+    shapes = [(128, 128, 1), (256, 128, 8), (128, 128, 8), (128, 64, 4), (128, 64, 8)]
     if not grouped:
         shapes = [(256, 128, 1)] + shapes
         # 32x32-MFMA kernels: four waves of 128x128, two waves of 128x128
