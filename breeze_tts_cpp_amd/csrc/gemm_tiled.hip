@@ -1179,14 +1179,19 @@ template <int Fmt, bool Grouped, class Out>
 int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
     if constexpr (Grouped) {
         // No 256x256: the fp32 group accumulators would double the 128x128
-        // register tile per wave and spill. INT8 in 64-byte stages (two per
-        // group; the 8-wave 128x128 tile runs two accumulator banks), FP8 in
-        // 128-byte stages.
+        // register tile per wave and spill. FP8 in 128-byte stages; INT8 in
+        // 128-byte stages on the 8-wave 128x128 and 128x64 tiles, 64-byte
+        // stages (two per group) elsewhere: its 256x128 tile spilled on
+        // 128-byte stages, and the 4-wave 128x64 tile runs two accumulator
+        // banks.
         constexpr int GBK = Fmt == I8 ? 64 : 128;
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 2, GBK, GBK == 64 ? 4 : 3, true, Out>(a, s);
+        // 128x128 with eight 64x32 waves, one group per 128-byte stage (qkv
+        // at 1024 23.7 us against 25.0 us for INT8's two-bank 64-byte-stage
+        // pipeline, which the four-wave 128x64 tile keeps).
         if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 4, 2, GBK, 4, true, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, GBK, 4, true, Out>(a, s);
         if (p.channels == 128 && p.tokens == 64 && p.waves == 4)
