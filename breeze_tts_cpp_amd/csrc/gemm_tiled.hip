@@ -512,11 +512,12 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                 }
             }
         }
-    } else if constexpr (Fmt == FP8) {
-        // FP8 K groups: one 128-K group per stage, stage-synchronous (the
-        // software-pipelined form below needs more registers than the i32x8
-        // FP8 fragments leave: it spilled and ran slower). Stages wait for
-        // themselves; the group scales are the stage slot's scale rows.
+    } else if constexpr (Fmt == FP8 && WTN * WTM > 8) {
+        // FP8 K groups on 128x32 waves: one 128-K group per stage,
+        // stage-synchronous (the software-pipelined form below needs a second
+        // set of i32x8 fragments that these waves have no registers for: it
+        // spilled and ran slower). Stages wait for themselves; the group
+        // scales are the stage slot's scale rows.
         for (int s = 0; s < stages; ++s) {
             // Stage s has landed once at most the newer stages are outstanding.
             if (s + STAGES - 2 < stages) wait_ring(std::integral_constant<int, STAGES - 2>{});
@@ -562,14 +563,15 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             }
         }
     } else {
-        // INT8 K groups of 128: the per-channel software pipeline (fragments
-        // of stage s+1 read while stage s's MFMAs run). Each group's MFMAs
-        // accumulate natively (exact int32) and the group is applied as
-        // facc = fmaf(p, sx_g * sw_g, facc), groups ascending. The group's
-        // scales come with its last stage (the stage slot's scale rows).
-        // 64-byte stages (two per group) or 128-byte stages (one group per
-        // stage, two MFMAs per tile; the 128x64 eight-wave tile).
-        static_assert(Fmt == I8, "the pipelined K-group path is INT8");
+        // K groups of 128: the per-channel software pipeline (fragments of
+        // stage s+1 read while stage s's MFMAs run). Each group's MFMAs
+        // accumulate natively (exact int32 for INT8; fp32 from zero for FP8)
+        // and the group is applied as facc = fmaf(p, sx_g * sw_g, facc),
+        // groups ascending. The group's scales come with its last stage (the
+        // stage slot's scale rows). INT8 on 64-byte stages (two per group) or
+        // 128-byte stages (one group per stage, two MFMAs per tile); FP8 on
+        // 128-byte stages with wave tiles of at most 8 MFMA tiles.
+        static_assert(Fmt == I8 || BK == 128, "FP8 K groups use 128-byte stages");
         using Frag = std::conditional_t<BK == 64, i32x4, i32x8>;
         const int a_off = a_row0 * BK, b_off = b_row0 * BK;
         const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16, b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
