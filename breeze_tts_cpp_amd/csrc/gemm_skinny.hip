@@ -103,6 +103,14 @@ __device__ __forceinline__ void lds_read16x4(const uint8_t *p0, const uint8_t *p
         : "v"(lds_addr(p0)), "v"(lds_addr(p1)), "v"(lds_addr(p2)), "v"(lds_addr(p3)));
 }
 
+// Cache policy of the weight slab DMA: non-temporal (the buffer
+// instruction's nt bit). Decode weights are read once per step, so keeping
+// them out of the caches' retained lines measured 4-6% faster per decode GEMM
+// (gate_up INT8 M = 32: 7.50 -> 7.09 us) than the default policy; sc0 alone
+// changed nothing. (Non-temporal output stores measured slower: o_proj
+// 3.36 -> 3.57 us.)
+constexpr int kWeightAux = 2;
+
 template <class Out>
 __device__ __forceinline__ void store4(void *y, size_t index, const float (&v)[4]) {
     uint2 packed;
@@ -361,7 +369,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                                             : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rsrc, (lds_ptr_t)(slab + i * 1024), 16, off,
-                0, 0, 0);
+                0, 0, kWeightAux);
         }
     }
 

@@ -97,6 +97,17 @@ __device__ const float kUnitScales[256] = {QLIN_ONES64, QLIN_ONES64, QLIN_ONES64
 #undef QLIN_ONES16
 #undef QLIN_ONES4
 
+// One 16-byte piece of a bf16/f16 output row, stored non-temporally: a
+// prefill GEMM writes its whole output at the end of each tile (all CUs at
+// once in one-round grids), and streaming it past the caches measured 5-8%
+// faster over the four M = 4096 projections than plain stores. (The
+// operand DMA keeps the default policy: non-temporal loads of the weight
+// tiles, which other tiles re-read through L2, measured 10-20% slower.)
+__device__ __forceinline__ void store_out16(uint16_t *dst, const uint4 &val) {
+    __builtin_nontemporal_store(i32x4{int(val.x), int(val.y), int(val.z), int(val.w)},
+                                reinterpret_cast<i32x4 *>(dst));
+}
+
 template <int Fmt, int WN, int WM, int WTN, int WTM, int BK, int STAGES, bool Grouped, bool KFull,
           class Out, bool PackedW = false, int GS = 128>
 __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
@@ -857,7 +868,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         if (m >= M || n >= N) continue;
         uint16_t *dst = static_cast<uint16_t *>(y) + size_t(m) * N + n;
         if (vec16) {
-            *reinterpret_cast<uint4 *>(dst) = val;
+            store_out16(dst, val);
         } else {
             reinterpret_cast<uint2 *>(dst)[0] = make_uint2(val.x, val.y);
             reinterpret_cast<uint2 *>(dst)[1] = make_uint2(val.z, val.w);
@@ -1110,7 +1121,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
         if (m >= M || n >= N) continue;
         uint16_t *dst = static_cast<uint16_t *>(y) + size_t(m) * N + n;
         if (vec16) {
-            *reinterpret_cast<uint4 *>(dst) = val;
+            store_out16(dst, val);
         } else {
             reinterpret_cast<uint2 *>(dst)[0] = make_uint2(val.x, val.y);
             reinterpret_cast<uint2 *>(dst)[1] = make_uint2(val.z, val.w);

@@ -1,6 +1,6 @@
 // qlin_stream_read: the streaming-read ceiling that the decode GEMMs are
 // measured against. No counterpart in the reference: a measurement helper
-// for bench.py. It reads `bytes` of device memory once with 16-byte loads
+// for bench.py. It reads `bytes` of device memory once with 16-byte non-temporal loads
 // (512 workgroups of 512 threads, 4 loads in flight per lane, each workgroup
 // a contiguous share), xor-reduces what it read and stores to `sink` only on
 // an impossible value, so nothing but the reads reach memory.
@@ -9,6 +9,8 @@
 #include "qlin_internal.hpp"
 
 namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWorkgroups = 512, kThreads = 512, kUnroll = 4;
 
@@ -22,7 +24,11 @@ __global__ __launch_bounds__(kThreads) void stream_read(const uint4 *__restrict_
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const long j = i + long(u) * kThreads;
-            v[u] = j < last ? src[j] : uint4{0, 0, 0, 0};
+                        v[u] = uint4{0, 0, 0, 0};
+            if (j < last) {
+                const i32x4 t = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(src + j));
+                v[u] = uint4{unsigned(t[0]), unsigned(t[1]), unsigned(t[2]), unsigned(t[3])};
+            }
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
