@@ -45,6 +45,39 @@ qlin::GemmPath to_internal(const qlin_path &p) {
     return {p.kind, p.tokens, p.channels, p.splits, p.waves, p.staged};
 }
 
+// The skinny path's staging for a tiling (tokens, channels, waves = 8): 1
+// when each wave's weight slab (at most three 256-byte K blocks) is copied
+// global->LDS in one shot, 2 when its activation rows fit beside it, else 0.
+int skinny_staging(int rows, int N, int K, int fmt, int input_group, int weight_group,
+                   qlin_path p) {
+    p.waves = 8;
+    const int nb = qlin::skinny_span(K, 1) / 256;
+    p.staged = nb <= 3 && long(p.channels) * nb * 8 * 256 <= 160 * 1024 ? 1 : 0;
+    qlin::GemmArgs a{};
+    a.M = rows;
+    a.N = N;
+    a.K = K;
+    a.fmt = fmt;
+    a.input_group = input_group;
+    a.weight_group = weight_group;
+    if (p.staged && qlin::skinny_lds_bytes(a, to_internal(p)) > qlin::kLdsBytes) p.staged = 0;
+    if (p.staged) {
+        p.staged = 2;
+        if (qlin::skinny_lds_bytes(a, to_internal(p)) > qlin::kLdsBytes) p.staged = 1;
+    }
+    return p.staged;
+}
+
+bool skinny_stages(int rows, int N, int K, int fmt, int input_group, int weight_group, int tokens,
+                   int channels) {
+    qlin_path p{};
+    p.kind = QLIN_KIND_SKINNY;
+    p.tokens = tokens;
+    p.channels = channels;
+    p.splits = 1;
+    return skinny_staging(rows, N, K, fmt, input_group, weight_group, p) > 0;
+}
+
 // Path selection for gfx950 (256 CUs, 8 XCDs). Decode shapes stream the
 // weights once through the skinny kernel; larger token counts use the
 // LDS-tiled MFMA GEMM.
@@ -70,14 +103,31 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
             p.tokens = 64;
             p.channels = 32;
         } else if (rows > 16 && long(N) * K < (16L << 20)) {
-            const int token_tiles = (rows + 15) / 16;
+            // 16-token tiles first, then 32; the first tiling with <= 256
+            // workgroups whose weight slab can be staged in LDS, else the
+            // first with <= 256 workgroups. Measured at M = 64 (INT8, weights
+            // from HBM): qkv 32x32 4.62 us against 6.87 us on 16x32 (512
+            // workgroups), down 32x16 (staged) 9.42 us against 11.24 us on
+            // 16x32 (its 3-block slab does not fit).
             p.tokens = 16;
             p.channels = 32;
-            for (int channels : {16, 32, 48})
-                if (long((N + channels - 1) / channels) * token_tiles <= 256) {
-                    p.channels = channels;
-                    break;
+            bool found = false, found_staged = false;
+            for (int tokens : {16, 32}) {
+                if (found_staged) break;
+                for (int channels : {16, 32, 48}) {
+                    if (long((N + channels - 1) / channels) * ((rows + tokens - 1) / tokens) > 256)
+                        continue;
+                    const bool stages = skinny_stages(rows, N, K, fmt, input_group, weight_group,
+                                                      tokens, channels);
+                    if (!found || (stages && !found_staged)) {
+                        p.tokens = tokens;
+                        p.channels = channels;
+                        found = true;
+                        found_staged = stages;
+                    }
+                    if (found_staged) break;
                 }
+            }
         } else {
             // Token tiles of 16, 32 or 64 rows that divide the rows rounded
             // up to 16 (48 rows count as one padded 64-row tile).
@@ -104,20 +154,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         // of 16 rows. Measured at M = 32 (weights from HBM): qkv 5.05 ->
         // 4.65 us, o_proj 4.24 -> 3.64 us.
         p.waves = 8;
-        const int nb = qlin::skinny_span(K, 1) / 256;
-        p.staged = nb <= 3 && long(p.channels) * nb * 8 * 256 <= 160 * 1024 ? 1 : 0;
-        qlin::GemmArgs a{};
-        a.M = rows;
-        a.N = N;
-        a.K = K;
-        a.fmt = fmt;
-        a.input_group = input_group;
-        a.weight_group = weight_group;
-        if (p.staged && qlin::skinny_lds_bytes(a, to_internal(p)) > qlin::kLdsBytes) p.staged = 0;
-        if (p.staged) {
-            p.staged = 2;
-            if (qlin::skinny_lds_bytes(a, to_internal(p)) > qlin::kLdsBytes) p.staged = 1;
-        }
+        p.staged = skinny_staging(rows, N, K, fmt, input_group, weight_group, p);
         return p;
     }
     // Prefill: the macro tile by measured MI355X rules (BASELINE projections

@@ -140,6 +140,21 @@ def test_decode_grid_plans():
         assert p.staged
 
 
+@pytest.mark.parametrize("fmt,group", [(I8, 0), (qlinear.FP8, 0), (I8, 128), (qlinear.FP8, 128)])
+def test_decode_grid_plans_m64(fmt, group):
+    """At M=64 the weights under 16 MB take the first tiling (16-token tiles
+    before 32, fewest weight rows first) that fits 256 workgroups and stages
+    its slab in LDS: qkv moves to 32x32 (16x32 would need 512 workgroups),
+    down to 32x16 (the 16x32 slab of K=6144 does not fit), o_proj keeps
+    16x32."""
+    want = {(4096, 2048): (32, 32), (2048, 2048): (16, 32), (2048, 6144): (32, 16)}
+    for (N, K), (tokens, channels) in want.items():
+        p = qlinear.plan(64, N, K, fmt, group, group)
+        assert p.kind == qlinear.KIND_SKINNY
+        assert (p.tokens, p.channels) == (tokens, channels), (N, K, p)
+        assert (N // p.channels) * (64 // p.tokens) == 256 and p.staged, (N, K, p)
+
+
 def test_linear_validation():
     """qlin_linear checks its quantize half, then its GEMM half."""
     L = qlinear.load()
