@@ -80,6 +80,13 @@ template <> struct Mfma<FP8> {
 __device__ __forceinline__ i32x4 load16(const uint8_t *p) {
     return *reinterpret_cast<const i32x4 *>(p);
 }
+// Packed-layout weight pieces (read once per step) are loaded non-temporally:
+// M = 32 INT8 packed GEMMs measured 4-7% faster (gate_up 9.52 -> 8.81 us).
+// The unstaged row-major register path keeps plain loads (gate_up 11.86 ->
+// 12.81 us with non-temporal ones).
+__device__ __forceinline__ i32x4 load16_packed(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(p));
+}
 
 // Four 16-byte LDS reads by explicit ds_read_b128 instructions and their
 // wait, in one statement. The compiler's wait insertion treats any LDS read
@@ -776,7 +783,7 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
 #pragma unroll
                     for (int f = 0; f < NF; ++f)
                         wc[blk][f][p] = (k < k_end && wvalid[f])
-                                            ? load16(wrow[f] + size_t(k / 64) * 1024)
+                                            ? load16_packed(wrow[f] + size_t(k / 64) * 1024)
                                             : i32x4{0, 0, 0, 0};
                 }
 #pragma unroll
