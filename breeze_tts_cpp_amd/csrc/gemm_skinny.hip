@@ -398,6 +398,25 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         red = reinterpret_cast<Red *>(red_static);
     }
 
+    // INT8 K groups of 128 on a staged slab accumulate in the reference's
+    // order (quant_grouped.cu:112-146, one K range): r = fmaf(p_g, sx_g *
+    // sw_g, r) over every group of K in ascending order, starting from 0.
+    // Each wave keeps the exact int32 partial p_g of each of its groups in
+    // registers (gp); after the main loop the partials and the group scales
+    // go through LDS and the epilogue runs the whole chain per output.
+    constexpr bool kRO = Grouped && Fmt == I8 && GS == 128 && kPreScale && WK > 1 && !Split;
+    Acc gp[kRO ? NB : 1][2][kRO ? MT : 1][kRO ? NF : 1];
+    if constexpr (kRO) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int f = 0; f < NF; ++f) gp[blk][h][t][f] = Acc{0, 0, 0, 0};
+    }
+
     // Grouped: fp32 running sums; per-channel: the raw accumulator.
     Acc acc[MT][NF];
     float facc[MT][NF][4];
@@ -695,6 +714,10 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
                         if (fsel >= 0 && f != fsel) continue;
                         Acc p = Acc{0, 0, 0, 0};
                         M_::run(p, a[f][2 * h], a[f][2 * h + 1], b[t][2 * h], b[t][2 * h + 1]);
+                        if constexpr (kRO) {
+                            gp[blk][h][t][f] = p;
+                            continue;
+                        }
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             facc[t][f][r] =
@@ -868,6 +891,107 @@ __global__ __launch_bounds__(64 * WK) void skinny_gemm(
         }
     }
 
+
+    if constexpr (kRO) {
+        // The reference-order chain. Per pass of kTP token tiles, the waves
+        // put their groups' terms in LDS (the slab and activation tiles are
+        // no longer read): PS[group][unit][r] = (float(p_g), sx_g * sw_g)
+        // for unit = (tile, fragment, lane) of the MFMA layout, the scale
+        // product computed as the reference does (activation scale times
+        // weight scale, quant_grouped.cu:133) and the int32 partial
+        // converted exactly (|p| < 2^22). Group g of the workgroup is wave
+        // g / (2 NB), block (g / 2) % NB, half g % 2: ascending K. Then one
+        // thread per output runs r = fmaf(p_g, s_g, r) over every group.
+        constexpr int kGL = WK * 2 * NB;
+        constexpr int kAvail = WK * (kSlabBytes + kActBytes);
+        constexpr int kTP = kGL * MT * NF * 2048 <= kAvail ? MT
+                            : (MT % 2 == 0 && kGL * (MT / 2) * NF * 2048 <= kAvail) ? MT / 2
+                                                                                   : 1;
+        static_assert(kGL * kTP * NF * 2048 <= kAvail, "chain terms fit the slab");
+        constexpr int kUP = kTP * NF * 64;
+        constexpr int kPasses = MT / kTP, kIters = (kUP * 4 + 64 * WK - 1) / (64 * WK);
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        f32x2 *PS = reinterpret_cast<f32x2 *>(wlds);
+        // LDS-only barrier (builtins, so that the compiler's wait insertion
+        // does not also wait for outstanding global memory operations).
+        auto lds_barrier = [] {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+        };
+        float res[kPasses][kIters];
+#pragma unroll
+        for (int pass = 0; pass < kPasses; ++pass) {
+            const int t0 = pass * kTP;
+            // Every wave is done with the slab (first pass) or with the
+            // previous pass's terms.
+            lds_barrier();
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int g = wave * 2 * NB + blk * 2 + h;
+#pragma unroll
+                    for (int tl = 0; tl < kTP; ++tl)
+#pragma unroll
+                        for (int f = 0; f < NF; ++f) {
+                            f32x2 *dst = PS + (g * kUP + (tl * NF + f) * 64 + lane) * 4;
+                            const Acc &p = gp[blk][h][t0 + tl][f];
+                            const float sxg = pre_sx[blk][h][t0 + tl];
+                            f32x4 lo = {float(p[0]), sxg * pre_sw[blk][h][f][0], float(p[1]),
+                                        sxg * pre_sw[blk][h][f][1]};
+                            f32x4 hi = {float(p[2]), sxg * pre_sw[blk][h][f][2], float(p[3]),
+                                        sxg * pre_sw[blk][h][f][3]};
+                            reinterpret_cast<f32x4 *>(dst)[0] = lo;
+                            reinterpret_cast<f32x4 *>(dst)[1] = hi;
+                        }
+                }
+            lds_barrier();
+            // One output per thread and iteration; the four lanes of a unit
+            // are adjacent. The results stay in registers until every pass
+            // is done, so no store is waited for between passes.
+#pragma unroll
+            for (int it = 0; it < kIters; ++it) {
+                const int o = threadIdx.x + it * 64 * WK;
+                float sum = 0.f;
+                if (o < kUP * 4) {
+#pragma unroll
+                    for (int g = 0; g < kGL; ++g) {
+                        const f32x2 ps = PS[g * kUP * 4 + o];
+                        sum = __builtin_fmaf(ps[0], ps[1], sum);
+                    }
+                }
+                res[pass][it] = sum;
+            }
+        }
+#pragma unroll
+        for (int pass = 0; pass < kPasses; ++pass)
+#pragma unroll
+            for (int it = 0; it < kIters; ++it) {
+                const int o = threadIdx.x + it * 64 * WK;
+                if (kUP * 4 % (64 * WK) != 0 && o >= kUP * 4) break;  // whole waves
+                const int unit = o >> 2, r = o & 3;
+                const int tl = unit >> 6, l = unit & 63;
+                const int t = pass * kTP + tl / NF, f = tl % NF;
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = __shfl(res[pass][it], (lane & ~3) | q);
+                const int m = m0 + t * 16 + (l & 15), n = n0 + f * 16 + (l >> 4) * 4;
+                if (r == 0 && m < M && n < N) {
+                    // Outer scales of an operand without groups
+                    // (quant_grouped.cu:161-165; 1 * 1 is exact), loaded
+                    // only then: a load here would also wait for the
+                    // previous iteration's store.
+                    if (!input_group || !weight_group) {
+                        const float ox = input_group ? 1.f : sx[m];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            v[q] = v[q] * (ox * (weight_group ? 1.f : sw[n + q]));
+                    }
+                    store_out(y, size_t(m) * N + n, v, bias, n, N - 1, act, out_f16);
+                }
+            }
+        return;
+    }
 
     if constexpr (WK > 1) {
         Red *slot = red + wave * kSlotStride;

@@ -45,16 +45,27 @@ class Path:
                          self.staged)
 
 
-def grouped_partition(path: Path, K: int) -> tuple[int, int, int]:
+def grouped_partition(path: Path, K: int, fmt: int = I8, input_group: int = 128,
+                      weight_group: int = 128, packed: bool = False) -> tuple[int, int, int]:
     """(splits, waves, span) of the K ranges a planned path sums separately
-    (the K-group oracle takes the same partition): a skinny launch splits K
-    into splits*8 wave ranges of ceil(ceil(K/256) / (splits*8)) 256-byte
-    blocks (trailing ranges may be empty); a tiled launch sums all of K in
-    one range (given as K rounded up to 128, a whole number of groups)."""
+    (the K-group oracle takes the same partition).
+
+    A tiled launch sums all of K in one range (given as K rounded up to 128,
+    a whole number of groups), and so does an INT8 skinny launch with K
+    groups of 128 on a staged slab of at most 6 (blocks x token tiles) and no
+    split: it runs the reference's single chain over every group of K
+    (quant_grouped.cu:112-146). Any other skinny launch splits K into
+    splits*8 wave ranges of ceil(ceil(K/256) / (splits*8)) 256-byte blocks
+    (trailing ranges may be empty), each summed on its own."""
     if path.kind == KIND_SKINNY:
         blocks = -(-K // 256)
         ranges = path.splits * path.waves
-        return path.splits, path.waves, -(-blocks // ranges) * 256
+        span_blocks = -(-blocks // ranges)
+        groups = [g for g in (input_group, weight_group) if g]
+        if (fmt == I8 and groups and min(groups) == 128 and not packed and path.splits == 1
+                and path.staged in (1, 2) and span_blocks * (path.tokens // 16) <= 6):
+            return 1, 1, -(-K // 128) * 128
+        return path.splits, path.waves, span_blocks * 256
     return 1, 1, -(-K // 128) * 128
 
 
@@ -63,7 +74,7 @@ EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
            "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish", "qlin_norm_linear",
            "qlin_norm_fusion_init", "qlin_epilogue_init", "qlin_layer_norm_quantize",
-           "qlin_pointwise_quantize", "qlin_linear_noalloc", "qlin_noalloc_scratch_bytes",
+           "qlin_pointwise_quantize", "qlin_pointwise", "qlin_linear_noalloc", "qlin_noalloc_scratch_bytes",
            "qlin_stream_read")
 
 
@@ -123,6 +134,8 @@ def load():
                                            i, P]
     L.qlin_pointwise_quantize.restype = i
     L.qlin_pointwise_quantize.argtypes = [P, i, i, P, P, i, i, P, P, i, i, i, P]
+    L.qlin_pointwise.restype = i
+    L.qlin_pointwise.argtypes = [P, i, i, P, P, i, i, P]
     L.qlin_quantized_gated.restype = i
     L.qlin_quantized_gated.argtypes = [P, i, i, i, i, P, P, i, i, i, P]
     _lib = L
@@ -346,6 +359,25 @@ def pointwise_quantize(x: torch.Tensor, fmt: int, epilogue: qlin_epilogue | None
         _ptr(retained), rows, cols, values.data_ptr(), scales.data_ptr(), fmt, group, rotation,
         _stream(stream)))
     return values, scales
+
+
+def pointwise(x: torch.Tensor, epilogue: qlin_epilogue | None = None,
+              out: torch.Tensor | None = None, rows: int | None = None, stream=None):
+    """Dense pointwise epilogue (qlin_pointwise): out = epilogue(x) in x's
+    16-bit type; out may be x. Returns out."""
+    if x.dim() != 2 or not x.is_contiguous() or x.dtype not in _TYPES:
+        raise ValueError("pointwise expects a dense 2-D bf16/f16 input")
+    x_rows, cols = x.shape
+    if rows is None:
+        rows = x_rows * (epilogue.input_repeat if epilogue is not None else 1)
+    if out is None:
+        out = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+    if out.shape != (rows, cols) or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError("pointwise output must be dense [rows, cols] in the input type")
+    _check(load().qlin_pointwise(
+        x.data_ptr(), x_rows, _TYPES[x.dtype], None if epilogue is None else ctypes.byref(epilogue),
+        out.data_ptr(), rows, cols, _stream(stream)))
+    return out
 
 
 def plan(rows: int, N: int, K: int, fmt: int, input_group: int = 0, weight_group: int = 0) -> Path:

@@ -50,7 +50,7 @@ def test_small_groups(dev, orc, fmt, ig, wg, M, N, K):
         torch.cuda.synchronize()
         got = bits(y)
         if fmt == I8:
-            splits, waves, span = qlinear.grouped_partition(p, K)
+            splits, waves, span = qlinear.grouped_partition(p, K, fmt, ig, wg)
             ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, splits, waves, span)
             assert np.array_equal(got, ref), f"{p}: {np.count_nonzero(got != ref)} mismatches"
         else:
@@ -124,7 +124,7 @@ def test_staged_ragged_k(dev, orc, fmt, group, M, K):
     torch.cuda.synchronize()
     got = bits(y)
     if fmt == I8 and group:
-        splits, waves, span = qlinear.grouped_partition(p, K)
+        splits, waves, span = qlinear.grouped_partition(p, K, fmt, group, group)
         ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, group, group, splits, waves, span)
         assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches, {p}"
     elif fmt == I8:
