@@ -774,18 +774,12 @@ int qlin_layer_norm_quantize(const void *x, int x_rows, int src_type, const void
     return check_launch("layer norm quantize launch");
 }
 
-int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
-                            const qlin_epilogue *epilogue, void *retained, int rows, int cols,
-                            void *values, float *scales, int fmt, int group, int rotation,
-                            qlin_stream_t stream) {
-    // validate_pointwise_quantize (reference sequence_pointwise.cu:307-324) and
-    // check_epilogue (sequence_internal.cuh:154-178).
-    qlin_epilogue e;
-    qlin_epilogue_init(&e);
-    if (epilogue) e = *epilogue;
-    if (int st = check_row_output(src_type, rows, cols, values, scales, fmt, group, rotation,
-                                  "pointwise quantize"))
-        return st;
+namespace {
+// validate_pointwise_quantize (reference sequence_pointwise.cu:307-324) and
+// check_epilogue (sequence_internal.cuh:154-178); with values == NULL (the
+// dense pointwise, sequence_pointwise.cu:281-287) only the row outputs.
+int check_pointwise(const void *x, int x_rows, const qlin_epilogue &e, const void *retained,
+                    int rows, int cols, const void *values, const float *scales, int group) {
     if (!x || x_rows < 1 || e.input_repeat < 1 || int64_t(x_rows) * e.input_repeat != rows ||
         (e.input_repeat > 1 && retained && retained == x))
         return fail(QLIN_ERR_INVALID, "invalid quantized pointwise input/repetition");
@@ -828,10 +822,43 @@ int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
             (o.p != e.residual || e.residual_index))
             return fail(QLIN_ERR_INVALID, "quantized sequence output has unsafe row alias");
     }
+    return QLIN_OK;
+}
+}  // namespace
+
+int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
+                            const qlin_epilogue *epilogue, void *retained, int rows, int cols,
+                            void *values, float *scales, int fmt, int group, int rotation,
+                            qlin_stream_t stream) {
+    qlin_epilogue e;
+    qlin_epilogue_init(&e);
+    if (epilogue) e = *epilogue;
+    if (int st = check_row_output(src_type, rows, cols, values, scales, fmt, group, rotation,
+                                  "pointwise quantize"))
+        return st;
+    if (int st = check_pointwise(x, x_rows, e, retained, rows, cols, values, scales, group))
+        return st;
     qlin::PointwiseQuantizeArgs a{x, x_rows, src_type, e, retained, rows, cols, values, scales,
                                   fmt, group, rotation};
     qlin::launch_pointwise_quantize(a, reinterpret_cast<hipStream_t>(stream));
     return check_launch("pointwise quantize launch");
+}
+
+int qlin_pointwise(const void *x, int x_rows, int src_type, const qlin_epilogue *epilogue,
+                   void *y, int rows, int cols, qlin_stream_t stream) {
+    qlin_epilogue e;
+    qlin_epilogue_init(&e);
+    if (epilogue) e = *epilogue;
+    if (src_type != QLIN_BF16 && src_type != QLIN_F16)
+        return fail(QLIN_ERR_INVALID, "pointwise input must be BF16 or F16");
+    if (rows < 1 || cols < 1 || !y)
+        return fail(QLIN_ERR_INVALID, "pointwise output rows=%d cols=%d", rows, cols);
+    if (int st = check_pointwise(x, x_rows, e, y, rows, cols, nullptr, nullptr, 0)) return st;
+    // The quantizing kernel with no codes: the epilogue's rows only.
+    qlin::PointwiseQuantizeArgs a{x, x_rows, src_type, e, y, rows, cols, nullptr, nullptr,
+                                  QLIN_I8, 0, 0};
+    qlin::launch_pointwise_quantize(a, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("pointwise launch");
 }
 
 int qlin_quantized_gated(const void *input, int src_type, int rows, int width, int kind,

@@ -495,7 +495,8 @@ __global__ __launch_bounds__(kThreads) void pointwise_quantize(
         r.value8(column, v[it], true);
         if (retained) store16x8<T, Vec>(retained + size_t(row) * cols, column, cols, v[it]);
     }
-    encode_row<Fmt, Items, Vec>(v, q, scales, row, rows, cols, group, rot);
+    // q == nullptr: the dense pointwise (rows only, no codes).
+    if (q) encode_row<Fmt, Items, Vec>(v, q, scales, row, rows, cols, group, rot);
 }
 
 // Rows of any length in 2048-column chunks: per-token scales take an amax
@@ -509,8 +510,18 @@ __global__ __launch_bounds__(kThreads) void pointwise_quantize_long(
     const int row = blockIdx.x, t = threadIdx.x;
     const PointwiseRow<T, Vec> r(x, x_rows, e, row, cols);
     uint16_t *kept = retained ? retained + size_t(row) * cols : nullptr;
-    uint8_t *dst = q + size_t(row) * cols;
     const int chunks = (cols + kChunk - 1) / kChunk;
+    if (!q) {
+        // The dense pointwise: one pass writing the rows.
+        for (int ch = 0; ch < chunks; ++ch) {
+            const int column = (ch * kThreads + t) * 8;
+            float v[8];
+            r.value8(column, v, true);
+            if (kept) store16x8<T, Vec>(kept, column, cols, v);
+        }
+        return;
+    }
+    uint8_t *dst = q + size_t(row) * cols;
     float inverse = 0.f;
     if (!group) {
         float amax = 0.f;

@@ -593,9 +593,11 @@ void linear(const LinearOperand &input, const LinearOperand &weight, TensorView 
         gemm.linear(activation, *matrix, output);
         return;
     }
-    if (!gemm.linear_finish(activation, *matrix, output, epilogue))
-        throw std::invalid_argument(
-            "quantized linear epilogue is not a prepared bias/ReLU/tanh-GeLU finish");
+    if (gemm.linear_finish(activation, *matrix, output, epilogue)) return;
+    // Not a prepared fused finish: the GEMM, then the dense epilogue in place
+    // (ops/linear.cpp:68-82).
+    gemm.linear(activation, *matrix, output);
+    pointwise(output, output, epilogue);
 }
 
 // ops/linear.cpp:94-131 with a quantized weight.
@@ -679,6 +681,27 @@ void pointwise_quantize(TensorView x, RowScaledView q, const Epilogue &e, Tensor
                                   code(q.values.type), q.group_size, q.rotation_size,
                                   context(x.device).stream()),
           "pointwise quantize");
+}
+
+void pointwise(TensorView x, TensorView y, const Epilogue &e) {
+    // check_output / check_epilogue (sequence_pointwise.cu:283-287).
+    if ((y.type != Type::BF16 && y.type != Type::F16) || !y.dense() || !x.dense())
+        throw std::invalid_argument("sequence output requires dense F16/BF16 rows");
+    if (!x.data || e.input_repeat < 1 || x.type != y.type || x.cols != y.cols ||
+        int64_t(x.rows) * e.input_repeat != y.rows || (e.input_repeat > 1 && x.data == y.data))
+        throw std::invalid_argument("invalid pointwise input/repetition");
+    if (e.bias.data && (e.bias.type != y.type || e.bias.numel() != size_t(y.cols)))
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    check_operand(e.residual, y.type, y.cols, "invalid indexed residual");
+    check_operand(e.raw, y.type, y.cols, "sequence operation shape/type mismatch");
+    check_operand(e.gate, y.type, y.cols, "invalid epilogue gate");
+    check_operand(e.condition, y.type, y.cols, "invalid epilogue condition");
+    if (e.raw.data && e.raw.rows != y.rows)
+        throw std::invalid_argument("sequence operation shape/type mismatch");
+    const qlin_epilogue c = to_c(e);
+    check(qlin_pointwise(x.data, x.rows, code(x.type), &c, y.data, y.rows, y.cols,
+                         context(y.device).stream()),
+          "pointwise");
 }
 
 void layer_norm_quantize(TensorView x, RowScaledView q, TensorView weight, TensorView bias,

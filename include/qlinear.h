@@ -323,6 +323,15 @@ int qlin_pointwise_quantize(const void *x, int x_rows, int src_type,
                             void *values, float *scales, int fmt, int group, int rotation,
                             qlin_stream_t stream);
 
+/* Dense pointwise epilogue (the reference's ops::pointwise,
+ * ops/kernels/sequence/sequence_pointwise.cu:281-287, ops/sequence.h:34),
+ * which ops::linear applies to a dense output after the GEMM when the
+ * epilogue is not a fused finish (ops/linear.cpp:79-82): y[r, :] = the
+ * qlin_epilogue result of x's rows, as the rows qlin_pointwise_quantize
+ * retains. y may be x (input_repeat 1). */
+int qlin_pointwise(const void *x, int x_rows, int src_type, const qlin_epilogue *epilogue,
+                   void *y, int rows, int cols, qlin_stream_t stream);
+
 /* Allocation-free quantized linear. No counterpart in the reference: it is
  * for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same arguments and results

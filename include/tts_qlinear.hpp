@@ -182,7 +182,8 @@ enum class Activation { Identity, Relu, LeakyRelu, Silu, Gelu, GeluTanh, Mish, T
 // The reference's ops::Epilogue (ops/sequence.h:8-27) without the packed /
 // indirect addressing (packed, condition_sources, output_rows), which only
 // its non-quantized pointwise consumers use. The quantized GEMM's fused
-// finish covers bias + ReLU / tanh-GeLU; pointwise_quantize covers all of it.
+// finish covers bias + ReLU / tanh-GeLU; pointwise and pointwise_quantize
+// cover all of it.
 struct Epilogue {
     TensorView bias, residual;
     float value_scale = 1;
@@ -330,6 +331,9 @@ using LinearOperand = std::variant<TensorView, RowScaledView>;
 // sequence_pointwise.cu:307-357); `multiprocessors` is accepted and unused.
 void pointwise_quantize(TensorView x, RowScaledView quantized, const Epilogue &e = {},
                         TensorView retained = {}, int multiprocessors = 0);
+// Dense pointwise epilogue (reference ops/sequence.h:34,
+// sequence_pointwise.cu:281-287): y = e(x) in x's 16-bit type; y may be x.
+void pointwise(TensorView x, TensorView y, const Epilogue &e = {});
 // LayerNorm -> row quantization (reference ops/sequence.h:63-65,
 // sequence_norm.cu:412-440).
 void layer_norm_quantize(TensorView x, RowScaledView quantized, TensorView weight, TensorView bias,
@@ -349,10 +353,10 @@ void quantized_gated(TensorView input, RowScaledView output, int kind);
 // GEMM's epilogue; with `quantized_output` the output is also quantized for
 // the next layer, through the fused finish and quantize_rows, or the GEMM
 // and pointwise_quantize for any other dense epilogue. Without
-// `quantized_output`, an epilogue beyond a prepared fused finish is rejected
-// with invalid_argument, and so is a dense (TensorView) weight: the
-// reference's non-quantized pointwise pass and dense GEMMs are not part of
-// this library.
+// `quantized_output`, an epilogue that is not a prepared fused finish runs
+// as the GEMM followed by pointwise(output, output, e), as the reference
+// does (ops/linear.cpp:79-82). A dense (TensorView) weight is rejected with
+// invalid_argument: dense GEMMs are not part of this library.
 void linear(const LinearOperand &input, const LinearOperand &weight, TensorView bias,
             TensorView output, Epilogue epilogue = {}, RowScaledView scratch = {},
             RowScaledView quantized_output = {});

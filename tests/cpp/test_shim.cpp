@@ -5,6 +5,9 @@
 //                         launch_row_quantize (load-time path), runs
 //                         ops::linear and writes DIR/y.bf16 plus the
 //                         quantized weights DIR/{wq.u8,sw.f32}.
+//                         DIR/dense.txt (ACTIVATION RESIDUAL) selects a dense
+//                         output with an epilogue that is no prepared finish
+//                         (bias.bf16, residual.bf16).
 //   test_shim producers DIR : ops::quantized_norm (residual update, RMSNorm)
 //                         on DIR/{x,u,w}.bf16 and ops::quantized_gated (SiLU)
 //                         on DIR/g.bf16 (shape.txt: M WIDTH GROUP), writing
@@ -280,13 +283,15 @@ static int gpu_test(const std::string &dir) {
         ops::quantize_rows(TensorView(dw, N, K, Type::BF16, 0, 0), wq);
         std::ifstream act_file(dir + "/finish.txt"), epi_file(dir + "/epilogue.txt"),
             mode_file(dir + "/calls.txt");
-        int act = 0, activation = 0, use_residual = 0;
+        std::ifstream dense_file(dir + "/dense.txt");
+        int act = 0, activation = 0, use_residual = 0, dense_act = 0, dense_residual = 0;
         std::string calls;
         const bool quantized_out = bool(epi_file >> activation >> use_residual);
         const bool finish = !quantized_out && (act_file >> act) && act;
+        const bool dense_epilogue = bool(dense_file >> dense_act >> dense_residual);
         mode_file >> calls;
         void *db = nullptr;
-        if (quantized_out || finish) {
+        if (quantized_out || finish || dense_epilogue) {
             auto b = read_file<uint16_t>(dir + "/bias.bf16", size_t(N));
             HIP(hipMalloc(&db, b.size() * 2));
             HIP(hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice));
@@ -326,6 +331,21 @@ static int gpu_test(const std::string &dir) {
             write_file(dir + "/next.u8", qh);
             write_file(dir + "/next_scales.f32", qsh);
             for (void *p : {dr, dq, dqs}) (void)hipFree(p);
+        } else if (dense_epilogue) {
+            // ops::linear with a dense output and an epilogue that is no
+            // prepared finish (none was prepared): the GEMM, then
+            // pointwise(output, output, e) (ops/linear.cpp:68-82).
+            auto r = read_file<uint16_t>(dir + "/residual.bf16", size_t(M) * N);
+            void *dr;
+            HIP(hipMalloc(&dr, r.size() * 2));
+            HIP(hipMemcpy(dr, r.data(), r.size() * 2, hipMemcpyHostToDevice));
+            ops::Epilogue e;
+            e.activation = static_cast<ops::Activation>(dense_act);
+            if (dense_residual) e.residual = TensorView(dr, M, N, Type::BF16, 0, 0);
+            layer.apply(TensorView(dx, M, K, Type::BF16, 0, 0), TensorView(dy, M, N, Type::BF16, 0, 0),
+                        layer.bias_, e, scratch);
+            HIP(hipStreamSynchronize(stream));
+            (void)hipFree(dr);
         } else if (finish) {
             // ops::linear with a bias + activation epilogue (fused finish)
             ops::Epilogue e;

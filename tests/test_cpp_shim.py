@@ -123,6 +123,38 @@ def test_linear_finish_end_to_end(dev, orc, tmp_path, act):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("activation,use_residual", [(3, 0), (1, 1), (5, 1), (0, 1)])
+def test_linear_dense_epilogue_end_to_end(dev, orc, tmp_path, activation, use_residual):
+    """ops::linear with a dense output and an epilogue that is no prepared
+    finish (SiLU, or a residual, with no finish prepared): the GEMM, then the
+    dense pointwise pass in place, as the reference falls back
+    (ops/linear.cpp:68-82). Against the oracle GEMM and the oracle epilogue
+    of its stored result."""
+    M, N, K = 32, 512, 1024
+    xb = synthetic.activations(M, K, seed=activation + 9)
+    wb = synthetic.weights(N, K, seed=activation + 9)
+    rng = np.random.default_rng(activation)
+    bias = synthetic.f32_to_bf16_bits(rng.standard_normal(N) * 0.1)
+    residual = synthetic.f32_to_bf16_bits(rng.standard_normal((M, N)))
+    for name, a in (("x", xb), ("w", wb), ("bias", bias), ("residual", residual)):
+        a.tofile(tmp_path / f"{name}.bf16")
+    (tmp_path / "shape.txt").write_text(f"{M} {N} {K} int8\n")
+    (tmp_path / "dense.txt").write_text(f"{activation} {use_residual}\n")
+    print(f"test_shim gpu dense epilogue act={activation} residual={use_residual}", flush=True)
+    r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    y = np.fromfile(tmp_path / "y.bf16", np.uint16).reshape(M, N)
+    wq, sw = orc.quantize_rows(wb, I8)
+    xq, sx = orc.quantize_rows(xb, I8)
+    plain = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw, order=0)
+    _, _, want, _ = orc.pointwise_quantize(plain, I8, bias=bias,
+                                           residual=residual if use_residual else None,
+                                           activation=activation)
+    assert np.array_equal(y, want)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("activation,use_residual", [(1, 0), (5, 0), (3, 1), (6, 0)])
 def test_linear_quantized_output_end_to_end(dev, orc, tmp_path, activation, use_residual):
     """ops::linear with a quantized output (ops/linear.cpp:35-78): a bias +

@@ -201,3 +201,43 @@ def test_sequence_producers_in_a_graph(dev, orc):
         assert np.array_equal(ps.cpu().numpy(), s)
         yo, _, _, _, _ = orc.norm_linear(xsb, wq_np, sw_np, I8)
         assert np.array_equal(bits(y), yo)
+
+
+@pytest.mark.parametrize("dtype,src_type", [(torch.bfloat16, BF16), (torch.float16, F16)])
+@pytest.mark.parametrize("cols", [9, 2048, 6144, 16391, 20480])
+def test_pointwise_dense(dev, orc, dtype, src_type, cols):
+    """qlin_pointwise (the reference's ops::pointwise, sequence_pointwise.cu:
+    281-287): the epilogue's rows, bit-exact against the oracle's retained
+    rows, into a new output and in place, with the raw rows, held in
+    registers and streamed (past 16384 columns)."""
+    from breeze_tts_cpp_amd import qlinear
+    x_rows, repeat, rps, valid = 4, 2, 4, 3
+    rows = x_rows * repeat
+    g = torch.Generator().manual_seed(cols * 5 + src_type)
+    x, b = mk(g, dtype, x_rows, cols, sc=2.0), mk(g, dtype, cols, sc=0.3)
+    gate, cond = mk(g, dtype, 2, cols, sc=0.2, off=1.0), mk(g, dtype, 1, cols, sc=0.5)
+    res = mk(g, dtype, 3, cols)
+    idx = np.array([0, 1, 2, -1, 2, 1, 0, -5], np.int32)
+    cases = [dict(activation=a) for a in (0, 2, 3, 5)] + [
+        dict(bias=b, gate=gate, condition=cond, residual=res, residual_index=idx, value_scale=0.75,
+             residual_scale=1.5, output_scale=0.5, activation=5, rows_per_sequence=rps,
+             valid_rows_per_sequence=valid, input_repeat=repeat),
+        dict(bias=b, residual=mk(g, dtype, x_rows, cols), activation=3)]
+    for case in cases:
+        tag = {k: v for k, v in case.items() if not isinstance(v, np.ndarray)}
+        print(f"pointwise dense dtype={dtype} cols={cols} {tag}", flush=True)
+        _, _, out, raw = orc.pointwise_quantize(x, I8, src_type=src_type, raw=True, **case)
+        dev_args = {k: (torch.from_numpy(v).to(dev) if k == "residual_index" else
+                        dev16(v, dtype, dev)) if isinstance(v, np.ndarray) else v
+                    for k, v in case.items()}
+        raw_d = torch.empty(out.shape, dtype=dtype, device=dev)
+        ep = qlinear.epilogue(raw=raw_d, **dev_args)
+        y = qlinear.pointwise(dev16(x, dtype, dev), ep)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y), out)
+        assert np.array_equal(bits(raw_d), raw)
+        if case.get("input_repeat", 1) == 1:
+            xd = dev16(x, dtype, dev)
+            qlinear.pointwise(xd, qlinear.epilogue(**dev_args), out=xd)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(xd), out)
