@@ -304,9 +304,27 @@ def main():
         "roofline": roofline,
     }
 
+    gpu_prefill_qkv = None
     if not args.no_prefill:
         progress("prefill M=4096")
-        result["prefill"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args)
+        detail = bench_prefill(torch, qlinear, synthetic, dev, stream, args)
+        # the metric's prefill half as flat scalars, the per-projection rows
+        # under prefill_detail
+        result["prefill"] = {"M": M_PREFILL}
+        for mode, leg in detail.items():
+            unit = "TOPS" if mode.endswith("int8") else "TFLOPS"
+            result["prefill"][f"{mode}_{unit}"] = leg["TOPS"]
+            result["prefill"][f"{mode}_frac_mfma"] = leg["frac_mfma"]
+        result["prefill_detail"] = detail
+        g = detail["int8"]["projections"]["gate_up"]
+        gpu_prefill_qkv = detail["int8"]["projections"]["qkv"]["TOPS"]
+        achieved = g["TOPS"]
+        result["roofline_mfma"] = {
+            "bound": "mfma", "kernel": f"tiled_gemm INT8 gate_up M={M_PREFILL}",
+            "achieved": achieved, "peak": I8_PEAK_TOPS, "unit": "TOPS",
+            "frac": round(achieved / I8_PEAK_TOPS, 4), "us_per_launch": g["us"],
+            "ops_per_launch": 2 * M_PREFILL * g["N"] * g["K"],
+            "traffic": measured_prefill_traffic("INT8 gate_up")}
         progress("prefill M=1024")
         result["prefill_m1024"] = bench_prefill(torch, qlinear, synthetic, dev, stream, args,
                                                 M=1024)
@@ -315,7 +333,7 @@ def main():
 
     if not args.no_cpu:
         progress("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(args, value)
+        result["cpu_baseline"] = cpu_baseline(args, value, gpu_prefill_qkv)
 
     print(json.dumps(result), flush=True)
 
@@ -420,6 +438,24 @@ def measured_traffic(name):
                 found = None
             break
     return found
+
+
+def measured_prefill_traffic(label):
+    """HBM bytes per launch (scaled FETCH_SIZE + WRITE_SIZE) of the prefill
+    GEMM labelled `label` ("INT8 gate_up", ...) in the committed counter
+    summary profiles/mfma_util_prefill.md (its last two columns); None when
+    the summary has no such row."""
+    path = os.path.join(ROOT, "profiles", "mfma_util_prefill.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0] == label:
+            try:
+                return int(cells[-2].replace(",", "")) + int(cells[-1].replace(",", ""))
+            except ValueError:
+                return None
+    return None
 
 
 def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projections):
@@ -616,37 +652,63 @@ def bench_producers(torch, qlinear, synthetic, dev, stream, args):
     return out
 
 
-def cpu_baseline(args, gpu_value):
-    """The oracle's multithreaded C restatement of quant + INT8 GEMM + dequant
-    (oracle/qlinear_oracle.c, orc_cpu_qlinear) on one layer's four projections
-    at M=32: a bounded sample of the step (1 of 16 layers), repeated for about
-    12 s; the median rep is reported."""
+def cpu_baseline(args, gpu_value, gpu_prefill=None):
+    """The oracle's multithreaded C restatement of quant + GEMM + dequant
+    (oracle/qlinear_oracle.c, orc_cpu_qlinear; the x86-64-v4 build on an
+    AVX-512 host) timed on bounded samples of the BASELINE configs, about
+    20 s in all, median rep of each:
+    - INT8 per-token, one layer's four projections at M=32 (1 of the step's
+      16 layers; this is `value`, in the step's GB/s of algorithmic bytes);
+    - FP8 and group_int8 (H128 rotation, K128 groups) one layer at M=32, GB/s;
+    - INT8 prefill: the qkv projection at M=4096, TOPS."""
     from breeze_tts_cpp_amd import synthetic
     from oracle import oracle
 
-    threads = args.cpu_threads or (os.cpu_count() or 1)
-    jobs = []
-    total_bytes = 0
-    for name, (N, K) in synthetic.PROJECTIONS.items():
-        wq, sw = oracle.quantize_rows(synthetic.weights(N, K, seed=1000), oracle.I8)
-        xb = synthetic.activations(M_DECODE, K, seed=0)
-        jobs.append((xb, wq, sw))
-        total_bytes += gemm_bytes(M_DECODE, N, K) + quant_bytes(M_DECODE, K)
-    oracle.cpu_qlinear(*jobs[0], oracle.I8, threads=threads)  # warm-up
-    times = []
-    # About 10-12 s of CPU work: reps until 12 s have passed (at most 1000).
-    t_end = time.time() + 12.0
-    while len(times) < 5 or (time.time() < t_end and len(times) < 1000):
-        t0 = time.perf_counter()
-        for xb, wq, sw in jobs:
-            oracle.cpu_qlinear(xb, wq, sw, oracle.I8, threads=threads)
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    gbs = total_bytes / t / 1e9
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    _, isa = oracle.cpu_lib()
+
+    def timed(jobs, seconds):
+        for job in jobs[:1]:
+            oracle.cpu_qlinear(*job, threads=threads, fast=True)  # warm-up
+        times = []
+        t_end = time.time() + seconds
+        while len(times) < 3 or (time.time() < t_end and len(times) < 1000):
+            t0 = time.perf_counter()
+            for job in jobs:
+                oracle.cpu_qlinear(*job, threads=threads, fast=True)
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)), len(times)
+
+    def layer(fmt, group):
+        jobs, total = [], 0
+        for name, (N, K) in synthetic.PROJECTIONS.items():
+            wq, sw = oracle.quantize_rows(synthetic.weights(N, K, seed=1000), fmt, group=group,
+                                          rotation=group)
+            jobs.append((synthetic.activations(M_DECODE, K, seed=0), wq, sw, fmt, group, group))
+            total += gemm_bytes(M_DECODE, N, K, group) + quant_bytes(M_DECODE, K, group)
+        return jobs, total
+
+    out = {}
+    jobs, total = layer(oracle.I8, 0)
+    t, reps = timed(jobs, 8.0)
+    gbs = total / t / 1e9
+    sample = [f"INT8 one layer (4 projections, M={M_DECODE}) of the {LAYERS}-layer step, "
+              f"median of {reps} reps"]
+    for mode, fmt, group in (("fp8", oracle.FP8, 0), ("group_int8", oracle.I8, 128)):
+        jobs, total = layer(fmt, group)
+        t, reps = timed(jobs, 4.0)
+        out[f"{mode}_GBps"] = round(total / t / 1e9, 2)
+        sample.append(f"{mode} one layer M={M_DECODE} ({reps} reps)")
+    N, K = synthetic.PROJECTIONS["qkv"]
+    wq, sw = oracle.quantize_rows(synthetic.weights(N, K, seed=1000), oracle.I8)
+    t, reps = timed([(synthetic.activations(M_PREFILL, K, seed=0), wq, sw, oracle.I8, 0, 0)], 6.0)
+    out["prefill_int8_qkv_TOPS"] = round(2 * M_PREFILL * N * K / t / 1e12, 3)
+    sample.append(f"INT8 qkv M={M_PREFILL} ({reps} reps)")
+    ratio = f"; GPU/CPU = {round(gpu_value / gbs, 1)}x (decode step)"
+    if gpu_prefill:
+        ratio += f", {round(gpu_prefill / out['prefill_int8_qkv_TOPS'], 1)}x (INT8 prefill)"
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"one layer (4 INT8 projections, M={M_DECODE}) of the {LAYERS}-layer "
-                      f"step, median of {len(times)} reps; GPU/CPU = "
-                      f"{round(gpu_value / gbs, 1)}x"}
+            "isa": isa, **out, "sample": "; ".join(sample) + ratio}
 
 
 if __name__ == "__main__":

@@ -241,9 +241,39 @@ def gemm_grouped_ideal(xq, sx, wq, sw, fmt: int, input_group: int, weight_group:
     return y
 
 
+_cpu_lib = None
+
+
+def host_has_avx512() -> bool:
+    """The x86-64-v4 feature set (AVX-512 F/BW/CD/DQ/VL) on this host."""
+    try:
+        flags = next(l for l in open("/proc/cpuinfo") if l.startswith("flags")).split()
+    except (OSError, StopIteration):
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"))
+
+
+def cpu_lib():
+    """The library the CPU baseline times: liboracle_v4.so (the same source
+    built for x86-64-v4) on an AVX-512 host, else liboracle.so."""
+    global _cpu_lib
+    if _cpu_lib is None:
+        v4 = os.path.join(_HERE, "liboracle_v4.so")
+        if host_has_avx512() and os.path.exists(v4):
+            L = ctypes.CDLL(v4)
+            P, i = ctypes.c_void_p, ctypes.c_int
+            L.orc_cpu_qlinear.restype = i
+            L.orc_cpu_qlinear.argtypes = [P, i, i, i, i, P, P, i, i, i, i, P, P, P, i]
+            _cpu_lib = (L, "x86-64-v4")
+        else:
+            _cpu_lib = (lib(), "x86-64-v3")
+    return _cpu_lib
+
+
 def cpu_qlinear(x_bits, wq, sw, fmt: int, group: int = 0, rotation: int = 0,
-                threads: int = 1, out_type: int = BF16):
-    """The whole per-call path on the CPU (quantize X, GEMM, dequant)."""
+                threads: int = 1, out_type: int = BF16, fast: bool = False):
+    """The whole per-call path on the CPU (quantize X, GEMM, dequant). fast:
+    the build for this host's widest vector ISA (cpu_lib), same results."""
     x_bits = np.ascontiguousarray(x_bits, np.uint16)
     wq = np.ascontiguousarray(wq, np.uint8)
     sw = np.ascontiguousarray(sw, np.float32)
@@ -253,8 +283,9 @@ def cpu_qlinear(x_bits, wq, sw, fmt: int, group: int = 0, rotation: int = 0,
     xq = np.zeros((M, K), np.uint8)
     groups = (K + group - 1) // group if group else 1
     sx = np.zeros((groups * M,), np.float32)
-    lib().orc_cpu_qlinear(_p(x_bits), BF16, M, N, K, _p(wq), _p(sw), fmt, group, rotation,
-                          out_type, _p(y), _p(xq), _p(sx), threads)
+    L = cpu_lib()[0] if fast else lib()
+    L.orc_cpu_qlinear(_p(x_bits), BF16, M, N, K, _p(wq), _p(sw), fmt, group, rotation,
+                      out_type, _p(y), _p(xq), _p(sx), threads)
     return y
 
 

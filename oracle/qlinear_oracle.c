@@ -803,9 +803,13 @@ typedef struct {
 static void *gemm_job(void *arg) {
     job_t *j = (job_t *)arg;
     int M = j->M, N = j->N, K = j->K, G = j->group;
+    /* Blocks of 32 token rows stay cache-resident while the thread's weight
+     * rows stream past them; every output is still one dot product in K
+     * order. */
+    for (int mb = 0; mb < M; mb += 32)
     for (int n = j->n0; n < j->n1; ++n) {
         const uint8_t *b = j->wq + (size_t)n * K;
-        for (int m = 0; m < M; ++m) {
+        for (int m = mb; m < M && m < mb + 32; ++m) {
             const uint8_t *a = j->xq + (size_t)m * K;
             float v;
             if (j->fmt == T_I8 && !G) {

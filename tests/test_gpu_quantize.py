@@ -134,7 +134,7 @@ def test_zero_rows_and_extremes(dev, orc):
     bits = synthetic.activations(6, 2048, seed=9)
     bits[0] = 0
     bits[1, :] = synthetic.f32_to_bf16_bits(np.float32(1e-30))  # amax/127 below FLT_MIN? no: > tiny
-    bits[2, 5] = synthetic.f32_to_bf16_bits(np.float32(3.0e38))
+    bits[2, 5] = synthetic.f32_to_bf16_bits(np.float32(3.0e38)).item()
     for fmt in (I8, FP8):
         for group, rotation in ((0, 0), (0, 128), (128, 0), (128, 128)):
             q, s = run(dev, bits, fmt, group=group, rotation=rotation)

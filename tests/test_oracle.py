@@ -317,20 +317,32 @@ def test_grouped_matches_ideal_and_splits(orc):
     del rng
 
 
-def test_cpu_baseline_equals_oracle_pipeline(orc):
-    M, N, K = 8, 64, 512
+@pytest.mark.parametrize("fast", [False, True])
+@pytest.mark.parametrize("M", [8, 70])
+def test_cpu_baseline_equals_oracle_pipeline(orc, M, fast):
+    """The timed CPU baseline (both builds; M = 70 spans three 32-row blocks)
+    equals the oracle pipeline: INT8, group_int8, FP8 (the per-channel FP8
+    dot sums decoded products in K order in fp32, as orc_gemm_grouped does
+    for one group spanning K)."""
+    N, K = 64, 512
     bits_x = synthetic.activations(M, K, seed=17)
     bits_w = synthetic.weights(N, K, seed=17)
     wq, sw = orc.quantize_rows(bits_w, I8)
-    y = orc.cpu_qlinear(bits_x, wq, sw, I8, threads=3)
+    y = orc.cpu_qlinear(bits_x, wq, sw, I8, threads=3, fast=fast)
     xq, sx = orc.quantize_rows(bits_x, I8)
     ref = orc.epilogue_i8(orc.gemm_i8_acc(xq, wq), sx, sw, order=0)
     assert np.array_equal(y, ref)
     wq, sw = orc.quantize_rows(bits_w, I8, group=128, rotation=128)
-    y = orc.cpu_qlinear(bits_x, wq, sw, I8, group=128, rotation=128, threads=2)
+    y = orc.cpu_qlinear(bits_x, wq, sw, I8, group=128, rotation=128, threads=2, fast=fast)
     xq, sx = orc.quantize_rows(bits_x, I8, group=128, rotation=128)
     ref, _ = orc.gemm_grouped(xq, sx, wq, sw, I8, 128, 128)
     assert np.array_equal(y, ref)
+    wq, sw = orc.quantize_rows(bits_w, FP8)
+    y = orc.cpu_qlinear(bits_x, wq, sw, FP8, threads=4, fast=fast)
+    xq, sx = orc.quantize_rows(bits_x, FP8)
+    ideal = orc.gemm_fp8_ideal(xq, sx, wq, sw)
+    got = synthetic.bf16_bits_to_f32(y).astype(np.float64)
+    assert np.linalg.norm(got - ideal) / np.linalg.norm(ideal) <= 1e-2
 
 
 # ---------------------------------------------------------------- evaluation orders
