@@ -246,9 +246,6 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
             return fail(QLIN_ERR_UNSUPPORTED,
                         "skinny path splits (%d) must be in 1..ceil(K/256) = %d", p.splits,
                         blocks_k);
-        const bool small_group = (input_group && input_group < 128) || (weight_group && weight_group < 128);
-        if (small_group && p.splits != 1)
-            return fail(QLIN_ERR_UNSUPPORTED, "K groups of 32/64 have no split-K skinny variant");
         if (p.staged < 0 || p.staged > 2)
             return fail(QLIN_ERR_UNSUPPORTED, "skinny staged must be 0, 1 or 2");
         // Token tiles run along the grid's z dimension (at most 65535).
@@ -412,8 +409,6 @@ int gemm_impl(const qlin_path *path, const void *x, const float *sx, const void 
     if (packed && !(path && path->kind)) p.staged = 0;
     int status = check_path(p, rows, N, K, fmt, input_group, weight_group);
     if (status) return status;
-    if (packed && ((input_group && input_group < 128) || (weight_group && weight_group < 128)))
-        return fail(QLIN_ERR_UNSUPPORTED, "packed weights support K groups of 128 only");
     qlin::GemmArgs a{static_cast<const uint8_t *>(x),
                      sx,
                      static_cast<const uint8_t *>(w),

@@ -1131,9 +1131,9 @@ int launch_slab(const GemmArgs &a, dim3 grid, int span, int staged, hipStream_t 
     return 0;
 }
 
-template <int Fmt, int MT, int NF, bool Grouped, int NB>
+template <int Fmt, int MT, int NF, bool Grouped, int NB, int GS = 128>
 int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
-    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, true>), grid,
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, false, NB, true, 0, GS>), grid,
                        dim3(64 * kWaves), 0, stream, QLIN_SKINNY_ARGS);
     return 0;
 }
@@ -1142,9 +1142,6 @@ int launch_packed(const GemmArgs &a, dim3 grid, int span, hipStream_t stream) {
 // row-major, unsplit paths only).
 template <int Fmt, int MT, int NF, bool Grouped, int GS = 128>
 int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
-    // 32/64 groups: row-major weights and no split only (checked first, so
-    // the packed and split-K launches below run with GS == 128).
-    if (GS != 128 && (a.packed || p.splits != 1)) return -4;
     if (p.waves != kWaves) return -4;
     const int span = span_of(a.K, p.splits);
     if (a.packed) {
@@ -1157,10 +1154,10 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         constexpr int kMaxNB = 10 / (NF + MT) > 4 ? 4 : (10 / (NF + MT) < 1 ? 1 : 10 / (NF + MT));
         const int nb = span / kBlockK < kMaxNB ? span / kBlockK : kMaxNB;
         switch (nb) {
-        case 1: return launch_packed<Fmt, MT, NF, Grouped, 1>(a, grid, span, stream);
-        case 2: if constexpr (kMaxNB >= 2) return launch_packed<Fmt, MT, NF, Grouped, 2>(a, grid, span, stream); break;
-        case 3: if constexpr (kMaxNB >= 3) return launch_packed<Fmt, MT, NF, Grouped, 3>(a, grid, span, stream); break;
-        case 4: if constexpr (kMaxNB >= 4) return launch_packed<Fmt, MT, NF, Grouped, 4>(a, grid, span, stream); break;
+        case 1: return launch_packed<Fmt, MT, NF, Grouped, 1, GS>(a, grid, span, stream);
+        case 2: if constexpr (kMaxNB >= 2) return launch_packed<Fmt, MT, NF, Grouped, 2, GS>(a, grid, span, stream); break;
+        case 3: if constexpr (kMaxNB >= 3) return launch_packed<Fmt, MT, NF, Grouped, 3, GS>(a, grid, span, stream); break;
+        case 4: if constexpr (kMaxNB >= 4) return launch_packed<Fmt, MT, NF, Grouped, 4, GS>(a, grid, span, stream); break;
         default: break;
         }
         return -4;
@@ -1185,7 +1182,8 @@ int launch_variant(const GemmArgs &a, const GemmPath &p, hipStream_t stream) {
         return 0;
     }
     if (p.staged) return -4;
-    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, true>), grid, block, 0, stream,
+    hipLaunchKernelGGL((skinny_gemm<Fmt, MT, NF, kWaves, Grouped, true, 0, false, 0, GS>), grid,
+                       block, 0, stream,
                        a.x, a.sx, a.w, a.sw, a.y, a.workspace, a.M, a.N, a.K, span,
                        a.input_group, a.weight_group, a.bias, a.act, int(a.out_type == F16), a.fq);
     const size_t quads = (size_t(a.M) * a.N) / 4;

@@ -135,8 +135,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     static_assert(ROWS % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "stage rows per instruction");
     static_assert(!kScaleDma || (BN * 4 <= 1024 && BM * 4 <= 1024 && NW >= 2),
                   "one scale instruction per operand");
-    static_assert(GS == 128 || (Grouped && BK == 128 && !PackedW && (GS == 32 || GS == 64)),
-                  "K groups of 32 / 64 use 128-byte stages of row-major weights");
+    static_assert(GS == 128 || (Grouped && BK == 128 && (GS == 32 || GS == 64)),
+                  "K groups of 32 / 64 use 128-byte stages");
     // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
     constexpr bool kMF32 = Fmt == FP8 && !Grouped && BK == 64;
@@ -1157,15 +1157,8 @@ int launch_shape(const GemmArgs &a, hipStream_t stream) {
     hipLaunchKernelGGL((tiled_gemm<Fmt, WN, WM, WTN, WTM, BK, STAGES, Grouped, KF, Out, PW, GS>), \
                        grid, block, lds, stream, a.x, a.sx, a.w, a.sw, a.y, a.M, a.N, a.K,      \
                        tiles_m, tiles_n, a.input_group, a.weight_group, a.bias, a.act)
-    if constexpr (GS < 128) {
-        // Small K groups: row-major weights only.
-        if (a.packed) return -4;
-        if (a.K % BK == 0) QLIN_TILED(true, false);
-        else QLIN_TILED(false, false);
-    } else {
-        if (a.K % BK == 0) { if (a.packed) QLIN_TILED(true, true); else QLIN_TILED(true, false); }
-        else { if (a.packed) QLIN_TILED(false, true); else QLIN_TILED(false, false); }
-    }
+    if (a.K % BK == 0) { if (a.packed) QLIN_TILED(true, true); else QLIN_TILED(true, false); }
+    else { if (a.packed) QLIN_TILED(false, true); else QLIN_TILED(false, false); }
 #undef QLIN_TILED
     return 0;
 }

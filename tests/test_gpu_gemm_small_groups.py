@@ -89,13 +89,14 @@ def test_small_groups_prefill_projection(dev, orc, fmt, ig, wg):
 
 
 def test_small_groups_unsupported_forms(dev, orc):
-    """Split-K skinny paths and four-wave tiled paths decline 32/64 groups."""
+    """Four-wave tiled paths decline 32/64 groups (split-K skinny paths take
+    them, test_small_groups_split_and_packed)."""
     from breeze_tts_cpp_amd import qlinear
     M, N, K = 8, 64, 1024
     xq, sx = orc.quantize_rows(synthetic.activations(M, K, seed=1), I8, group=32)
     wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=1), I8, group=32)
     args = [torch.from_numpy(a).to(dev) for a in (xq, sx, wq, sw)]
-    for path in (qlinear.Path(1, 16, 16, 2, 8, 0), qlinear.Path(2, 128, 128, 1, 1, 0)):
+    for path in (qlinear.Path(2, 128, 128, 1, 1, 0),):
         with pytest.raises(qlinear.QLinearError):
             qlinear.gemm(*args, I8, input_group=32, weight_group=32, path=path,
                          workspace=torch.empty(1 << 20, dtype=torch.uint8, device=dev))
@@ -135,3 +136,67 @@ def test_staged_ragged_k(dev, orc, fmt, group, M, K):
                  else orc.gemm_fp8_ideal(xq, sx, wq, sw))
         f = synthetic.bf16_bits_to_f32(got).astype(np.float64)
         assert np.linalg.norm(f - ideal) / np.linalg.norm(ideal) <= 1e-2
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("ig,wg", [(32, 32), (64, 128), (0, 64), (32, 0)])
+@pytest.mark.parametrize("M,N,K", [(8, 256, 2048), (32, 512, 6144), (5, 48, 1536)])
+def test_small_groups_split_and_packed(dev, orc, fmt, ig, wg, M, N, K):
+    """K groups of 32 / 64 on the decode kernel's grid split-K (2 and 3
+    splits: wave ranges of each split summed in order, then fp32 partials
+    carrying their outer scales summed in split order, as the reference's
+    split grouped GEMM and quant_split_reduce_scale do, quant_grouped.cu:
+    171-239, quant_reduce.cuh:9-19) and on packed weights: INT8 bit-exact
+    against the oracle over the same partition, FP8 within rel-L2 1e-2."""
+    from breeze_tts_cpp_amd import qlinear
+    print(f"small groups split/packed fmt={fmt} ig={ig} wg={wg} M={M} N={N} K={K}", flush=True)
+    xq, sx = quantize(orc, synthetic.activations(M, K, seed=M + ig + 3), fmt, ig)
+    wq, sw = quantize(orc, synthetic.weights(N, K, seed=N + wg + 3), fmt, wg)
+    xd, sxd = torch.from_numpy(xq).to(dev), torch.from_numpy(sx).to(dev)
+    wd, swd = torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev)
+    runs = []
+    for splits in (2, 3):
+        p = qlinear.Path(qlinear.KIND_SKINNY, 16 * -(-min(M, 32) // 16), 16, splits, 8, 0)
+        runs.append((p, False))
+    runs.append((qlinear.plan(M, N, K, fmt, ig, wg), True))
+    for p, packed in runs:
+        if packed:
+            w_in = qlinear.pack_weights(wd)
+            path = qlinear.Path(p.kind, p.tokens, p.channels, p.splits, p.waves, 0)
+        else:
+            w_in, path = wd, p
+        print(f"  path {path} packed={packed}", flush=True)
+        y = qlinear.gemm(xd, sxd, w_in, swd, fmt, input_group=ig, weight_group=wg, path=path)
+        torch.cuda.synchronize()
+        got = bits(y)
+        if fmt == I8:
+            part = qlinear.grouped_partition(path, K, fmt, ig, wg, packed=packed)
+            ref, _ = orc.gemm_grouped(xq, sx, wq, sw, fmt, ig, wg, *part)
+            assert np.array_equal(got, ref), f"{path}: {np.count_nonzero(got != ref)} mismatches"
+        else:
+            ideal = orc.gemm_grouped_ideal(xq, sx, wq, sw, fmt, ig, wg)
+            f = synthetic.bf16_bits_to_f32(got).astype(np.float64)
+            assert np.linalg.norm(f - ideal) / np.linalg.norm(ideal) <= 1e-2, path
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+@pytest.mark.parametrize("ig,wg", [(32, 32), (64, 64), (128, 32)])
+def test_small_groups_packed_prefill(dev, orc, fmt, ig, wg):
+    """The prefill kernel's small-group tiles on packed weights: identical to
+    the row-major weights (both sum all of K in one range)."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N, K = 300, 256, 2048
+    print(f"small groups packed prefill fmt={fmt} ig={ig} wg={wg}", flush=True)
+    xq, sx = quantize(orc, synthetic.activations(M, K, seed=ig + wg), fmt, ig)
+    wq, sw = quantize(orc, synthetic.weights(N, K, seed=ig * wg), fmt, wg)
+    xd, sxd = torch.from_numpy(xq).to(dev), torch.from_numpy(sx).to(dev)
+    wd, swd = torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev)
+    packed = qlinear.pack_weights(wd)
+    paths = [qlinear.Path(qlinear.KIND_TILED, 128, 128, 1, 8, 0)]
+    if fmt == I8:
+        paths.append(qlinear.Path(qlinear.KIND_TILED, 128, 256, 1, 8, 0))
+    for p in paths:
+        y_row = qlinear.gemm(xd, sxd, wd, swd, fmt, input_group=ig, weight_group=wg, path=p)
+        y_pk = qlinear.gemm(xd, sxd, packed, swd, fmt, input_group=ig, weight_group=wg, path=p)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y_pk), bits(y_row)), p
