@@ -71,6 +71,12 @@ int qlin_linear_noalloc(const qlin_path *path, const void *x, int ld, int src_ty
                         qlin_stream_t stream) {
     if (rows < 1 || N < 1 || K < 1)
         return qlin::set_error(QLIN_ERR_INVALID, "qlin_linear_noalloc: invalid shape");
+    // The group sizes qlin_linear accepts, checked before they size the
+    // scratch layout.
+    auto valid_group = [](int g) { return g == 0 || g == 32 || g == 64 || g == 128; };
+    if (!valid_group(input_group) || !valid_group(weight_group))
+        return qlin::set_error(QLIN_ERR_INVALID,
+                               "qlin_linear_noalloc: quantization group must be 0, 32, 64 or 128");
     // Layout: codes [rows, K] | scales [groups, rows] | split-K partials,
     // each 256-byte aligned.
     const size_t groups = input_group ? (size_t(K) + input_group - 1) / input_group : 1;

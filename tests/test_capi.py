@@ -299,13 +299,24 @@ def test_noalloc_scratch_limit():
     rc = L.qlin_linear_noalloc(None, FAKE, 16384, BF16, FAKE, FAKE, FAKE, 4096, 16, 16384, I8,
                                BF16, 0, 0, 0, None)
     assert rc == -3 and b"fixed" in L.qlin_last_error()
+    # an invalid group is rejected as qlin_linear rejects it, before it sizes
+    # the scratch layout
+    for ig, wg in ((-1, 0), (96, 128), (128, -128)):
+        rc = L.qlin_linear_noalloc(None, FAKE, 2048, BF16, FAKE, FAKE, FAKE, 16, 2048, 2048, I8,
+                                   BF16, ig, wg, 0, None)
+        assert rc == -1 and b"group" in L.qlin_last_error(), (ig, wg)
 
 
-def test_stream_read_validation():
-    """The streaming-read ceiling kernel rejects unaligned or ragged buffers
-    before launching."""
-    L = qlinear.load()
-    assert L.qlin_stream_read(FAKE + 8, 1 << 20, None, None) == -1
-    assert L.qlin_stream_read(FAKE, (1 << 20) + 4, None, None) == -1
-    assert L.qlin_stream_read(FAKE, 0, None, None) == -1
-    assert L.qlin_stream_read(None, 1 << 20, None, None) == -1
+def test_measure_library():
+    """The streaming-read measurement kernel lives in its own library
+    (include/qlin_measure.h), outside the quantized linear ABI, and rejects
+    unaligned or ragged buffers before launching."""
+    from breeze_tts_cpp_amd import measure
+    text = open(os.path.join(ROOT, "include", "qlin_measure.h")).read()
+    assert sorted(set(re.findall(r"\b(qlm_[a-z_]+)\s*\(", text))) == ["qlm_stream_read"]
+    assert not hasattr(qlinear.load(), "qlin_stream_read")
+    L = measure.load()
+    assert L.qlm_stream_read(FAKE + 8, 1 << 20, None, None) == -1
+    assert L.qlm_stream_read(FAKE, (1 << 20) + 4, None, None) == -1
+    assert L.qlm_stream_read(FAKE, 0, None, None) == -1
+    assert L.qlm_stream_read(None, 1 << 20, None, None) == -1

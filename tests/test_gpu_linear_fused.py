@@ -254,3 +254,49 @@ def test_fused_group_linear_special_rows(dev, orc, src):
         for rotation in (0, 128):
             print(f"fused group special rows src={src} fmt={fmt} rot={rotation}", flush=True)
             run_group_pair(dev, orc, xb, fmt, N, K, rotation, src=src, oracle=False)
+
+
+@pytest.mark.parametrize("case", ["y_aliases_x", "sx_in_x_row_tail", "xq_in_x_allocation"])
+def test_fused_linear_aliasing_falls_back(dev, orc, case):
+    """A fused-eligible decode linear (M = 16, N = K = 2048) whose output or
+    scratch overlaps x's span (rows * ld elements) takes the two-launch form,
+    which reads all of x before anything is written: y in place over x; the
+    scales in the unused tail of x's first strided row (ld = 2K); the codes
+    starting in the unused tail of x's last strided row and running on into
+    the rest of x's allocation. Output bits equal quantizer + GEMM on a copy
+    of x."""
+    from breeze_tts_cpp_amd import qlinear
+    M, N, K = 16, 2048, 2048
+    assert fused_eligible(qlinear.plan(M, N, K, I8), M, N, K)
+    print(f"aliasing {case}", flush=True)
+    xb = synthetic.activations(M, K, seed=77)
+    wq, sw = orc.quantize_rows(synthetic.weights(N, K, seed=78), I8)
+    wq_d, sw_d = torch.from_numpy(wq).to(dev), torch.from_numpy(sw).to(dev)
+    x_ref = dev16(xb, torch.bfloat16, dev)
+    xq_ref, sx_ref = qlinear.row_quantize(x_ref, I8)
+    y_ref = qlinear.gemm(xq_ref, sx_ref, wq_d, sw_d, I8)
+    xq = torch.empty((M, K), dtype=torch.uint8, device=dev)
+    sx = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if case == "y_aliases_x":
+        buf = x_ref.clone()
+        ld, x_ptr, xq_ptr, sx_ptr, y_ptr = K, buf.data_ptr(), xq.data_ptr(), sx.data_ptr(), buf.data_ptr()
+    else:
+        # rows of 2K bf16 (ld = 2K): columns [K, 2K) of each row are unused;
+        # 4 extra rows hold the rest of a codes block that starts in the
+        # last row's tail
+        buf = torch.zeros((M + 4, 2 * K), dtype=torch.bfloat16, device=dev)
+        buf[:M, :K] = x_ref
+        ld, x_ptr, y_ptr = 2 * K, buf.data_ptr(), y.data_ptr()
+        row_bytes = 2 * K * 2
+        if case == "sx_in_x_row_tail":
+            xq_ptr, sx_ptr = xq.data_ptr(), buf.data_ptr() + K * 2
+        else:
+            xq_ptr, sx_ptr = buf.data_ptr() + (M - 1) * row_bytes + K * 2, sx.data_ptr()
+            assert (M - 1) * row_bytes + K * 2 + M * K <= buf.numel() * 2
+    L = qlinear.load()
+    rc = L.qlin_linear(None, x_ptr, ld, BF16, xq_ptr, sx_ptr, wq_d.data_ptr(), sw_d.data_ptr(),
+                       y_ptr, M, N, K, I8, BF16, 0, 0, 0, None, 0, None)
+    assert rc == 0, L.qlin_last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(buf if case == "y_aliases_x" else y), bits(y_ref))
