@@ -344,6 +344,7 @@ def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
     graph replayed `reps` times; microseconds per launch. Also the GEMM warm
     (one weight copy, cache-resident) and the streaming-read ceiling over the
     same copies."""
+    from breeze_tts_cpp_amd import measure
     rot = 128 if group else 0
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -398,7 +399,7 @@ def decode_sweep(torch, qlinear, synthetic, dev, stream, fmt, group, M, reps):
                                       for _ in range(16)], 16)
         # the streaming-read ceiling: the same weight copies read once each
         # by the plain 16-byte-load kernel (qlin_stream_read), same replay
-        us_stream = time_graph(lambda: [qlinear.stream_read(wc, stream=stream) for wc in ws],
+        us_stream = time_graph(lambda: [measure.stream_read(wc, stream=stream) for wc in ws],
                                len(ws))
         b = gemm_bytes(M, N, K, group)
         rows[name] = {"N": N, "K": K, "us_per_launch": round(us, 3), "bytes": b,
@@ -464,6 +465,7 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
     copies of each projection's weight bytes (two passes), 5 rounds of each projection's
     16-layer decode linear (qlin_linear, fused at M=32), then one M=4096 INT8,
     FP8, group_int8 and group_fp8 GEMM per projection."""
+    from breeze_tts_cpp_amd import measure
     src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -478,7 +480,7 @@ def profile_run(torch, qlinear, synthetic, dev, stream, layers, inputs, projecti
         # back from the caches; the second is the measurement
         for _ in range(2):
             for buf in copies:
-                qlinear.stream_read(buf, stream=stream)
+                measure.stream_read(buf, stream=stream)
             torch.cuda.synchronize()
         del copies
     for name, (N, K) in projections:

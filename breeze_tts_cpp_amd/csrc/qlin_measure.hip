@@ -1,12 +1,15 @@
-// qlin_stream_read: the streaming-read ceiling that the decode GEMMs are
-// measured against. No counterpart in the reference: a measurement helper
-// for bench.py. It reads `bytes` of device memory once with 16-byte non-temporal loads
-// (512 workgroups of 512 threads, 4 loads in flight per lane, each workgroup
-// a contiguous share), xor-reduces what it read and stores to `sink` only on
-// an impossible value, so nothing but the reads reach memory.
+// qlm_stream_read (include/qlin_measure.h): the streaming-read ceiling that
+// the decode GEMMs are measured against, in a library of its own so that it
+// stays out of the quantized linear ABI. No counterpart in the reference. It
+// reads `bytes` of device memory once with 16-byte non-temporal loads (512
+// workgroups of 512 threads, 4 loads in flight per lane, each workgroup a
+// contiguous share), xor-reduces what it read and stores to `sink` only on an
+// impossible value, so nothing but the reads reach memory.
 #include <hip/hip_runtime.h>
 
-#include "qlin_internal.hpp"
+#include <cstdint>
+
+#include "../../include/qlin_measure.h"
 
 namespace {
 
@@ -24,7 +27,7 @@ __global__ __launch_bounds__(kThreads) void stream_read(const uint4 *__restrict_
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const long j = i + long(u) * kThreads;
-                        v[u] = uint4{0, 0, 0, 0};
+            v[u] = uint4{0, 0, 0, 0};
             if (j < last) {
                 const i32x4 t = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(src + j));
                 v[u] = uint4{unsigned(t[0]), unsigned(t[1]), unsigned(t[2]), unsigned(t[3])};
@@ -38,19 +41,14 @@ __global__ __launch_bounds__(kThreads) void stream_read(const uint4 *__restrict_
 
 }  // namespace
 
-extern "C" int qlin_stream_read(const void *src, size_t bytes, unsigned *sink,
-                                qlin_stream_t stream) {
-    if (!src || bytes == 0 || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
-        return qlin::set_error(QLIN_ERR_INVALID,
-                               "qlin_stream_read: src must be 16-byte aligned, bytes a nonzero "
-                               "multiple of 16");
+extern "C" int qlm_stream_read(const void *src, size_t bytes, unsigned *sink,
+                               qlm_stream_t stream) {
+    if (!src || bytes == 0 || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16) return -1;
     const long total = long(bytes / 16);
     const long per_wg = (total + kWorkgroups - 1) / kWorkgroups;
     const int wgs = int((total + per_wg - 1) / per_wg);
     hipLaunchKernelGGL(stream_read, dim3(wgs), dim3(kThreads), 0,
                        reinterpret_cast<hipStream_t>(stream), static_cast<const uint4 *>(src),
                        per_wg, total, sink);
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? QLIN_OK
-                           : qlin::set_error(QLIN_ERR_HIP, "qlin_stream_read: launch failed");
+    return hipGetLastError() == hipSuccess ? 0 : -5;
 }

@@ -74,8 +74,7 @@ EXPORTS = ("qlin_version", "qlin_last_error", "qlin_row_quantize", "qlin_plan",
            "qlin_quantized_gated", "qlin_packed_weight_bytes", "qlin_pack_weights",
            "qlin_gemm_packed", "qlin_linear_packed", "qlin_gemm_finish", "qlin_norm_linear",
            "qlin_norm_fusion_init", "qlin_epilogue_init", "qlin_layer_norm_quantize",
-           "qlin_pointwise_quantize", "qlin_pointwise", "qlin_linear_noalloc", "qlin_noalloc_scratch_bytes",
-           "qlin_stream_read")
+           "qlin_pointwise_quantize", "qlin_pointwise", "qlin_linear_noalloc", "qlin_noalloc_scratch_bytes")
 
 
 def load():
@@ -105,8 +104,6 @@ def load():
                                       i, i, i, P]
     L.qlin_noalloc_scratch_bytes.restype = sz
     L.qlin_noalloc_scratch_bytes.argtypes = []
-    L.qlin_stream_read.restype = i
-    L.qlin_stream_read.argtypes = [P, sz, P, P]
     L.qlin_linear.argtypes = [ctypes.POINTER(qlin_path), P, i, i, P, P, P, P, P, i, i, i, i, i,
                               i, i, i, P, sz, P]
     L.qlin_quantized_norm.restype = i
@@ -525,11 +522,3 @@ def linear_noalloc(x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, fmt: int
                                       fmt, _TYPES[out.dtype], group, group, rotation,
                                       _stream(stream)))
     return out
-
-
-def stream_read(buf: torch.Tensor, stream=None) -> None:
-    """The streaming-read ceiling kernel (qlin_stream_read): reads every byte
-    of the contiguous device tensor `buf` once (its size a multiple of 16)."""
-    assert buf.is_contiguous()
-    _check(load().qlin_stream_read(buf.data_ptr(), buf.numel() * buf.element_size(), None,
-                                   _stream(stream)))

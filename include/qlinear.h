@@ -32,8 +32,6 @@
  *                       <- no counterpart in the reference: qlin_linear with its
  *                          scratch in a fixed library-owned device array, for callers
  *                          that cannot allocate
- *   qlin_stream_read    <- no counterpart in the reference: the streaming-read
- *                          ceiling the decode GEMMs are measured against
  *
  * Operand layouts (reference core/quantization.h:24-49):
  *   x  int8/e4m3 [rows, K] dense          sx f32 [rows] or [ceil(K/ig), rows]
@@ -349,15 +347,6 @@ int qlin_linear_noalloc(const qlin_path *path, const void *x, int ld, int src_ty
                         const void *w, const float *sw, void *y, int rows, int N, int K, int fmt,
                         int out_type, int input_group, int weight_group, int rotation,
                         qlin_stream_t stream);
-
-/* Streaming-read ceiling (measurement helper; no counterpart in the
- * reference). Reads `bytes` (a nonzero multiple of 16) at 16-byte aligned
- * `src` once with 16-byte loads, 512 workgroups of 512 threads; writes
- * nothing except, never in practice, to `sink` (NULL, or room for 512
- * unsigned values: a workgroup stores its xor only if it equals one fixed
- * constant, which keeps the loads live). bench.py times it over the decode
- * weight sizes as the ceiling for the decode GEMMs. */
-int qlin_stream_read(const void *src, size_t bytes, unsigned *sink, qlin_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -97,14 +97,14 @@ def test_stream_read_ceiling_kernel(dev):
     the sink stays untouched and the buffer unchanged, for sizes that are not
     a multiple of its 512-workgroup split (a tail workgroup with fewer
     16-byte rows) and for the decode weight sizes."""
-    from breeze_tts_cpp_amd import qlinear
-    L = qlinear.load()
+    from breeze_tts_cpp_amd import measure
+    L = measure.load()
     for nbytes in (16, 16 * 1000 + 16, 2048 * 2048, 12288 * 2048):
         print(f"stream_read bytes={nbytes}", flush=True)
         buf = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev)
         ref = buf.clone()
         sink = torch.full((1024,), 7, dtype=torch.int32, device=dev)
-        assert L.qlin_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), None) == 0
+        assert L.qlm_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), None) == 0
         torch.cuda.synchronize()
         assert torch.equal(buf, ref)
         assert bool((sink == 7).all())
