@@ -229,9 +229,6 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
 
 int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_group,
                int weight_group) {
-    (void)rows;
-    (void)N;
-    (void)fmt;
     if (p.kind == QLIN_KIND_SKINNY) {
         if (p.tokens != 16 && p.tokens != 32 && p.tokens != 64)
             return fail(QLIN_ERR_UNSUPPORTED, "skinny path tokens must be 16/32/64 (got %d)",
@@ -269,6 +266,13 @@ int check_path(const qlin_path &p, int rows, int N, int K, int fmt, int input_gr
         return ok();
     }
     if (p.kind == QLIN_KIND_TILED) {
+        // No 512-channel tile: a register-streamed 512x128 INT8 kernel (four
+        // 128x128 waves, weights global -> registers, tokens through LDS)
+        // measured slower than the planned tiles and faulted the GPU under
+        // graph replay with its cause unfound, so it is not built.
+        if (p.channels == 512 || p.tokens == 512)
+            return fail(QLIN_ERR_UNSUPPORTED,
+                        "tiled 512-channel path is disabled (register-streamed kernel not built)");
         if (!((p.channels == 256 && (p.tokens == 256 || p.tokens == 128)) ||
               (p.channels == 128 && (p.tokens == 128 || p.tokens == 64))))
             return fail(QLIN_ERR_UNSUPPORTED,

@@ -90,6 +90,10 @@ def test_gemm_validation():
     assert call(M=256, path=qlinear.Path(T, 64, 128, 1, 4), ig=32, wg=32) == -4
     assert call(M=256, path=qlinear.Path(T, 128, 128, 1, 1), ig=32, wg=32) == -4  # small groups: 8 waves
     assert call(M=256, fmt=FP8, path=qlinear.Path(T, 128, 256, 1, 8), ig=64, wg=64) == -4  # FP8: 128x128
+    # the 512x128 register-streamed path is disabled (not built)
+    assert call(M=256, path=qlinear.Path(T, 128, 512, 1, 4)) == -4
+    assert b"disabled" in L.qlin_last_error()
+    assert call(M=256, path=qlinear.Path(T, 512, 128, 1, 4)) == -4
     # grid limits are checked before any launch: token tiles on the skinny
     # grid's z dimension (<= 65535), macro tiles on the tiled grid's x (< 2^31)
     assert call(M=1 << 23, N=64, K=256, path=qlinear.Path(qlinear.KIND_SKINNY, 64, 16, 1, 8)) == -4
