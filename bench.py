@@ -140,6 +140,10 @@ def parse():
                     help="short run for rocprofv3 counter passes: a 64 MiB device copy "
                          "(calibrates FETCH_SIZE/WRITE_SIZE), then the decode GEMM graphs "
                          "and one prefill GEMM per format; prints no JSON")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only the M=4096 comparison with the vendor library's GEMMs "
+                         "(hipBLASLt through torch._int_mm / torch._scaled_mm) on the same "
+                         "quantized operands; prints one JSON line")
     return ap.parse_args()
 
 
@@ -157,6 +161,10 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream()
     I8, FP8 = qlinear.I8, qlinear.FP8
+    if args.vendor:
+        print(json.dumps({"vendor_compare": vendor_compare(torch, qlinear, synthetic, dev,
+                                                           stream)}), flush=True)
+        return
     projections = list(synthetic.PROJECTIONS.items())
 
     def bf16_dev(bits):
@@ -573,6 +581,78 @@ def bench_prefill(torch, qlinear, synthetic, dev, stream, args, M=M_PREFILL):
         peak = I8_PEAK_TOPS if fmt == qlinear.I8 else FP8_PEAK_TFLOPS
         out[fmt_name] = {"TOPS": round(tops, 1), "frac_mfma": round(tops / peak, 4),
                          "peak": peak, "projections": rows}
+    return out
+
+
+def vendor_compare(torch, qlinear, synthetic, dev, stream, M=M_PREFILL):
+    """The vendor library's GEMMs on this build's quantized operands (the same
+    synthetic activations and weights as the prefill legs), timed beside the
+    planned qlin GEMM the same way (graphs of 10 calls, warm-up, 5
+    interleaved rounds, medians): INT8 torch._int_mm (int8 x int8 -> int32,
+    no dequant epilogue, so it does less work than qlin's bf16 output) and FP8
+    torch._scaled_mm with row-wise scales and bf16 output (the same contract
+    as qlin's FP8 GEMM). Both run on hipBLASLt on this image."""
+    import statistics
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps, rounds = 10, 5
+    out = {}
+    for fmt_name, fmt in (("int8", qlinear.I8), ("fp8", qlinear.FP8)):
+        rows, legs = {}, {}
+        for name, (N, K) in synthetic.PROJECTIONS.items():
+            x = torch.from_numpy(synthetic.activations(M, K, seed=1).view(np.int16)).view(
+                torch.bfloat16).to(dev)
+            w = torch.from_numpy(synthetic.weights(N, K, seed=1).view(np.int16)).view(
+                torch.bfloat16).to(dev)
+            with torch.cuda.stream(stream):
+                xq, sx = qlinear.row_quantize(x, fmt, stream=stream)
+                wq, sw = qlinear.row_quantize(w, fmt, stream=stream)
+                y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            torch.cuda.synchronize()
+            if fmt == qlinear.I8:
+                a8, b8 = xq.view(torch.int8), wq.view(torch.int8)
+                vendor = lambda a8=a8, b8=b8: torch._int_mm(a8, b8.t())
+            else:
+                a8, b8 = xq.view(torch.float8_e4m3fn), wq.view(torch.float8_e4m3fn)
+                sa, sb = sx.view(M, 1), sw.view(1, N)
+                vendor = lambda a8=a8, b8=b8, sa=sa, sb=sb: torch._scaled_mm(
+                    a8, b8.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+            ours = lambda xq=xq, sx=sx, wq=wq, sw=sw, y=y: qlinear.gemm(
+                xq, sx, wq, sw, fmt, out=y, stream=stream)
+            for leg, fn in (("vendor", vendor), ("qlin", ours)):
+                with torch.cuda.stream(stream):
+                    fn()
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    for _ in range(reps):
+                        fn()
+                legs[(name, leg)] = {"graph": g, "ops": 2 * M * N * K, "us": [],
+                                     "keep": (xq, sx, wq, sw, y)}
+        torch.cuda.synchronize()
+        for _ in range(30):
+            for leg in legs.values():
+                leg["graph"].replay()
+        torch.cuda.synchronize()
+        for r in range(rounds):
+            for key in (list(legs) if r % 2 == 0 else list(reversed(legs))):
+                with torch.cuda.stream(stream):
+                    start.record(stream)
+                    legs[key]["graph"].replay()
+                    end.record(stream)
+                torch.cuda.synchronize()
+                legs[key]["us"].append(start.elapsed_time(end) * 1e3 / reps)
+        totals = {"vendor": [0, 0.0], "qlin": [0, 0.0]}
+        for (name, leg), v in legs.items():
+            us = statistics.median(v["us"])
+            rows.setdefault(name, {})[leg + "_us"] = round(us, 2)
+            totals[leg][0] += v["ops"]
+            totals[leg][1] += us
+        out[fmt_name] = {k: round(o / (u * 1e-6) / 1e12, 1) for k, (o, u) in totals.items()}
+        out[fmt_name]["unit"] = "TOPS" if fmt == qlinear.I8 else "TFLOPS"
+        out[fmt_name]["projections"] = rows
+        del legs
+    out["vendor_ops"] = {"int8": "torch._int_mm, int32 output (no dequant epilogue)",
+                         "fp8": "torch._scaled_mm, row-wise fp32 scales, bf16 output"}
     return out
 
 

@@ -161,16 +161,18 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     // at M = 1024 and 4096, per-channel and K128 groups, realistic data).
     // A grid is run in rounds of 256 workgroups (one per CU); `full` says its
     // last round is at least 90% occupied.
-    //  - INT8 per-channel, all with eight waves: 256x256 (128x64 waves) when
+    //  - INT8 per-channel, all with eight waves: 256x256 (128x64 waves, two
+    //    double-buffered 128-byte K stages) when
     //    it has >= 192 tiles (qkv/gate_up at 4096, gate_up at 1024); else
     //    256x128 (128x32 waves, 128-byte K stages) for >= 256 tiles in full
     //    rounds: down at 4096 54 us against 68 us on 128x128; else 128x128
     //    (64x32 waves): qkv
     //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
-    //  - FP8 per-channel: 256x256 with eight 128x64 waves (32x32x64 MFMA)
-    //    when it has >= 256 tiles (gate_up at 4096 114 us against 116 us
-    //    with four 128x128 waves); else 256x128 (eight 128x32 waves,
-    //    16x16x128 MFMA over 128-byte stages) for >= 256 tiles in full
+    //  - FP8 per-channel: 256x256 with eight 128x64 waves (32x32x64 MFMA,
+    //    two double-buffered 128-byte K stages) when it has >= 256 tiles
+    //    (gate_up at 4096 91 us; 114 us with 64-byte stages against 116 us
+    //    with four 128x128 waves); else 256x128 (eight 128x32 waves, the same
+    //    pipeline) for >= 256 tiles in full
     //    rounds: o_proj at 4096 27.7 us against 30.2 us with four 128x64
     //    waves on 32x32x64 and 30.4 on 128x128; else 128x128 with eight 64x32 waves on
     //    the 16x16x128 MFMA over 128-byte K stages: down at 1024 35.5 us

@@ -140,6 +140,11 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
     // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
     constexpr bool kMF32 = Fmt == FP8 && !Grouped && BK == 64;
+    // FP8 per-channel on double-buffered 128-byte stages: 32x32x64 tiles as
+    // well (16-register accumulators, which the compiler keeps in place; its
+    // 16x16x128 form rotates them through copies and spills at 256x256).
+    constexpr bool kDB32 = Fmt == FP8 && !Grouped && BK == 128 && STAGES == 2;
+    constexpr bool kAcc32 = kMF32 || kDB32;
     // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
     // exactly 64, the FP8 16x16x128 pipeline 128; K groups are 128 wide (two
     // INT8 stages or one FP8 stage).
@@ -252,9 +257,9 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         wait_vmcnt<(INSTS + (kScaleDma ? 1 : 0)) * S>();
     };
 
-    Acc acc[(Grouped || kMF32) ? 1 : WTN][(Grouped || kMF32) ? 1 : WTM];
-    f32x16 acc32[kMF32 ? WTN / 2 : 1][kMF32 ? WTM / 2 : 1];
-    if constexpr (kMF32) {
+    Acc acc[(Grouped || kAcc32) ? 1 : WTN][(Grouped || kAcc32) ? 1 : WTM];
+    f32x16 acc32[kAcc32 ? WTN / 2 : 1][kAcc32 ? WTM / 2 : 1];
+    if constexpr (kAcc32) {
 #pragma unroll
         for (int i = 0; i < WTN / 2; ++i)
 #pragma unroll
@@ -263,7 +268,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                 for (int e = 0; e < 16; ++e) acc32[i][j][e] = 0.f;
     }
     float facc[Grouped ? WTN : 1][Grouped ? WTM : 1][4];
-    if constexpr (!Grouped && !kMF32) {
+    if constexpr (!Grouped && !kAcc32) {
 #pragma unroll
         for (int i = 0; i < WTN; ++i)
 #pragma unroll
@@ -374,6 +379,132 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             step(s + 1, a1, b1, a0, b0);
         }
         if (s < stages) step(s, a0, b0, a1, b1);
+    } else if constexpr (kDB32) {
+        // The double-buffered pipeline below on 32x32x64 FP8 tiles: lane l
+        // holds row l % 32 of a 32-row block and, for 64-K step h of the
+        // stage, K bytes [64h + 32*(l/32), +32).
+        const int r32 = lane & 31, g32 = lane >> 5;
+        const int a_r0 = wave_n * 16 * WTN + r32, b_r0 = BN + wave_m * 16 * WTM + r32;
+        const int a_sw = swizzle<BK>(a_r0), b_sw = swizzle<BK>(b_r0);
+        constexpr int NA = WTN / 2, NBF = WTM / 2;
+        auto rd = [&](const uint8_t *p, int h, int sw) {
+            const int c = 4 * h + 2 * g32;
+            const i32x4 lo = *reinterpret_cast<const i32x4 *>(p + ((c ^ sw) * 16));
+            const i32x4 hi = *reinterpret_cast<const i32x4 *>(p + (((c + 1) ^ sw) * 16));
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        auto read_b = [&](int st, i32x8 (&bb)[NBF][2]) {
+            const uint8_t *pb = lds + (st % 2) * STAGE_BYTES + b_r0 * BK;
+#pragma unroll
+            for (int j = 0; j < NBF; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) bb[j][h] = rd(pb + j * 32 * BK, h, b_sw);
+        };
+        auto read_a = [&](int st, int i, i32x8 (&a)[2]) {
+            const uint8_t *pa = lds + (st % 2) * STAGE_BYTES + (a_r0 + i * 32) * BK;
+            a[0] = rd(pa, 0, a_sw);
+            a[1] = rd(pa, 1, a_sw);
+        };
+        auto row = [&](int i, const i32x8 (&a)[2], const i32x8 (&bb)[NBF][2]) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < NBF; ++j)
+                    acc32[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        a[h], bb[j][h], acc32[i][j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        };
+        // One set of token fragments: the next stage's are read into it
+        // after this stage's last MFMAs have issued (their reads of the
+        // registers happen at issue), under the MFMAs still executing.
+        auto step = [&](int s, i32x8 (&bb)[NBF][2], i32x8 (&a)[2]) {
+#pragma unroll
+            for (int i = 0; i + 1 < NA; ++i) {
+                i32x8 an[2];
+                read_a(s, i + 1, an);
+                row(i, a, bb);
+                a[0] = an[0];
+                a[1] = an[1];
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            row(NA - 1, a, bb);
+            wait_vmcnt<0>();
+            lds_barrier();
+            if (s + 2 < stages) issue(s + 2, (s + 2) * BK);
+            read_b(s + 1, bb);
+            read_a(s + 1, 0, a);
+        };
+        i32x8 b0[NBF][2], a0[2];
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (1 < stages) issue(1, BK);
+        read_b(0, b0);
+        read_a(0, 0, a0);
+        for (int s = 0; s < stages; ++s) step(s, b0, a0);
+    } else if constexpr (!Grouped && STAGES == 2) {
+        // Two 128-byte stages, double-buffered (a 256x256 tile's 64 KB stages
+        // fit the LDS twice). The DMA of stage s+1 is issued once every wave
+        // has read stage s-1, and has the MFMAs of a whole stage to land. A
+        // step reads its weight fragments one 16-row block ahead of that
+        // block's MFMAs, so a wave holds the token fragments of two stages but
+        // only two weight fragments: i32x8 fragments (FP8: one 16x16x128 MFMA
+        // per tile and stage, INT8: two 16x16x64) at two waves per SIMD.
+        static_assert(BK == 128, "double-buffered 128-byte stages");
+        const int a_off = a_row0 * BK, b_off = b_row0 * BK;
+        const int a_c0 = (quad ^ swizzle<BK>(a_row0)) * 16;
+        const int a_c1 = ((4 + quad) ^ swizzle<BK>(a_row0)) * 16;
+        const int b_c0 = (quad ^ swizzle<BK>(b_row0)) * 16;
+        const int b_c1 = ((4 + quad) ^ swizzle<BK>(b_row0)) * 16;
+        auto rd = [&](const uint8_t *p, int c0, int c1) {
+            const i32x4 lo = *reinterpret_cast<const i32x4 *>(p + c0);
+            const i32x4 hi = *reinterpret_cast<const i32x4 *>(p + c1);
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        auto read_b = [&](int st, i32x8 (&bb)[WTM]) {
+            const uint8_t *pb = lds + (st % 2) * STAGE_BYTES + b_off;
+#pragma unroll
+            for (int j = 0; j < WTM; ++j) bb[j] = rd(pb + j * 16 * BK, b_c0, b_c1);
+        };
+        auto read_a = [&](int st, int i) {
+            return rd(lds + (st % 2) * STAGE_BYTES + a_off + i * 16 * BK, a_c0, a_c1);
+        };
+        auto row = [&](int i, const i32x8 &a, const i32x8 (&bb)[WTM]) {
+#pragma unroll
+            for (int j = 0; j < WTM; ++j) MMA::run(acc[i][j], a, bb[j]);
+        };
+        // Step s: weight blocks 0..WTN-2 (each reading the next block first);
+        // wait for stage s+1 and barrier (every wave's reads of stage s are
+        // complete: its slot takes stage s+2); read stage s+1's token
+        // fragments and first weight block (unconditional: after the last
+        // stage they read a slot whose values go unused); the last block.
+        auto step = [&](int s, const i32x8 (&bb)[WTM], i32x8 a, i32x8 (&nb)[WTM], i32x8 &na) {
+#pragma unroll
+            for (int i = 0; i + 1 < WTN; ++i) {
+                const i32x8 an = read_a(s, i + 1);
+                row(i, a, bb);
+                a = an;
+                // Keeps the next block's reads from being hoisted (all of a
+                // stage's weight fragments at once do not fit the registers).
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            wait_vmcnt<0>();
+            lds_barrier();
+            if (s + 2 < stages) issue(s + 2, (s + 2) * BK);
+            read_b(s + 1, nb);
+            na = read_a(s + 1, 0);
+            row(WTN - 1, a, bb);
+        };
+        i32x8 b0[WTM], b1[WTM], a0;
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (1 < stages) issue(1, BK);
+        read_b(0, b0);
+        a0 = read_a(0, 0);
+        int s = 0;
+        for (; s + 1 < stages; s += 2) {
+            step(s, b0, a0, b1, a0);
+            step(s + 1, b1, a0, b0, a0);
+        }
+        if (s < stages) step(s, b0, a0, b1, a0);
     } else if constexpr (!Grouped) {
         // Software pipeline, one stage per step (INT8: BK = 64, one 64-K
         // MFMA per tile, or BK = 128, two; FP8: BK = 128, one 128-K MFMA).
@@ -808,7 +939,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         *reinterpret_cast<uint2 *>(wbuf + m_l * ROWB + (((byte >> 4) ^ (m_l % CH)) << 4) +
                                    (byte & 15)) = packed;
     };
-    if constexpr (kMF32) {
+    if constexpr (kAcc32) {
         // 32x32 tile: lane l, register 4b+e holds C[n = 8b + 4*(l/32) + e][m = l % 32].
 #pragma unroll
         for (int j = 0; j < WTM / 2; ++j) {
@@ -1216,8 +1347,10 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
             return launch_wide<Fmt, 2, 1, 3, Out>(a, s);
+        // 256x256: eight 128x64 waves on two double-buffered 128-byte K
+        // stages (gate_up at 4096 87 us against 95 us on four 64-byte stages).
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
         // 128x128: eight waves of 64x32 (waves 8) or four of 64x64 (waves 1).
@@ -1233,17 +1366,21 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, false, Out>(a, s);
         return -4;
     } else {
-        // 256x128 with eight waves of 128x32 on the 16x16x128 MFMA over
-        // 128-byte K stages (down at 4096 54 us against 60 us for one
-        // workgroup of four 128x64 waves on 32x32x64).
+        // 256x128 with eight waves of 128x32 on two double-buffered 128-byte
+        // K stages, 32x32x64 MFMAs (down at 4096 46.2 us against 47.9 us on
+        // three stages of 16x16x128, and 60 us for one workgroup of four
+        // 128x64 waves).
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 2, 128, 2, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
             return launch_wide<Fmt, 2, 1, 3, Out>(a, s);
+        // 256x256: eight 128x64 waves of 32x32x64 MFMAs on two double-buffered
+        // 128-byte K stages (gate_up at 4096 91 us against 103 us on four
+        // 64-byte stages).
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 4, 64, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
         // 128x128: eight waves of 64x32 on the 16x16x128 FP8 MFMA over
