@@ -169,9 +169,10 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    (64x32 waves): qkv
     //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
     //  - FP8 per-channel: 256x256 with eight 128x64 waves (32x32x64 MFMA,
-    //    two double-buffered 128-byte K stages) when it has >= 256 tiles
+    //    two double-buffered 128-byte K stages) when it has >= 192 tiles
     //    (gate_up at 4096 91 us; 114 us with 64-byte stages against 116 us
-    //    with four 128x128 waves); else 256x128 (eight 128x32 waves, the same
+    //    with four 128x128 waves; gate_up at 1024 29.3 us against 33.2 us on
+    //    128x128); else 256x128 (eight 128x32 waves, the same
     //    pipeline) for >= 256 tiles in full
     //    rounds: o_proj at 4096 27.7 us against 30.2 us with four 128x64
     //    waves on 32x32x64 and 30.4 on 128x128; else 128x128 with eight 64x32 waves on
@@ -200,7 +201,7 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
         if (tiles_256 >= 192) p.channels = p.tokens = 256;
         else if (tiles_256x128 >= 256 && full) p.channels = 256;
     } else if (!grouped) {
-        if (tiles_256 >= 256) {
+        if (tiles_256 >= 192) {
             p.channels = p.tokens = 256;
             p.waves = 8;
         } else if (tiles_256x128 >= 256 && full) {
