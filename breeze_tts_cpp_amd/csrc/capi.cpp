@@ -168,9 +168,9 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     //    rounds: down at 4096 54 us against 68 us on 128x128; else 128x128
     //    (64x32 waves): qkv
     //    at 1024 14.4 us against 19.1 us with four 64x64 waves.
-    //  - FP8 per-channel: 256x256 with eight 128x64 waves (32x32x64 MFMA,
+    //  - FP8 per-channel: 256x256 with eight 128x64 waves (16x16x128 MFMA,
     //    two double-buffered 128-byte K stages) when it has >= 192 tiles
-    //    (gate_up at 4096 91 us; 114 us with 64-byte stages against 116 us
+    //    (gate_up at 4096 90 us; 114 us with 64-byte stages against 116 us
     //    with four 128x128 waves; gate_up at 1024 29.3 us against 33.2 us on
     //    128x128); else 256x128 (eight 128x32 waves, the same
     //    pipeline) for >= 256 tiles in full

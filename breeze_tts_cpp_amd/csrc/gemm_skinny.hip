@@ -11,7 +11,8 @@
 // contiguous bytes per load) straight into MFMA A-fragment registers; the
 // tokens are the MFMA B side (zero-padded to 16*MT). INT8 uses
 // v_mfma_i32_16x16x64_i8 (exact int32), FP8 e4m3 uses
-// v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales. The waves of a
+// v_mfma_f32_16x16x128_f8f6f4 (zero scale operands to the f8f6f4 builtin,
+// for which the compiler emits the unscaled instruction). The waves of a
 // workgroup split K and reduce through LDS; optionally the grid splits K
 // further into workspace partials that a second kernel reduces in split order.
 //
@@ -66,14 +67,13 @@ template <> struct Mfma<I8> {
 template <> struct Mfma<FP8> {
     using Acc = f32x4;
     using Scalar = float;
-    // Two 64-K pieces -> one 128-K MFMA (format 0 = e4m3 for A and B, unit
-    // E8M0 scales 0x7f).
+    // Two 64-K pieces -> one 128-K MFMA (format 0 = e4m3 for A and B; zero
+    // scale operands select the unscaled instruction).
     __device__ static void run(Acc &c, const i32x4 &a0, const i32x4 &a1, const i32x4 &b0,
                                const i32x4 &b1) {
         i32x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
         i32x8 b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0,
-                                                             0x7f7f7f7f);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
     }
 };
 

@@ -9,7 +9,11 @@
 // Work decomposition: one workgroup per macro tile of BN weight rows x BM
 // tokens; WN x WM wave64s, each owning a (16*WTN) x (16*WTM) sub-tile of
 // 16x16 MFMA tiles (INT8: v_mfma_i32_16x16x64_i8, exact int32; FP8:
-// v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales).
+// v_mfma_f32_16x16x128_f8f6f4, the plain e4m3 product with fp32
+// accumulation: the f8f6f4 builtins get zero scale operands, for which the
+// compiler emits the unscaled instruction. With unit E8M0 scales (0x7f) it
+// keeps the scaled form, whose scale operand occupies a VGPR: FP8 prefill
+// measured 7% slower that way, and its 256x256 double-buffered tile spilled).
 //
 // Operand staging: K advances in BK-byte stages through a STAGES-deep LDS
 // ring filled by buffer_load ... lds (global -> LDS without registers), so
@@ -57,9 +61,9 @@ template <> struct TileMma<I8> {
 };
 template <> struct TileMma<FP8> {
     using Acc = f32x4;
+    // Zero scale operands: the unscaled v_mfma_f32_16x16x128_f8f6f4.
     __device__ static void run(Acc &c, const i32x8 &a, const i32x8 &b) {
-        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0,
-                                                             0x7f7f7f7f);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
     }
 };
 
@@ -137,14 +141,10 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
                   "one scale instruction per operand");
     static_assert(GS == 128 || (Grouped && BK == 128 && (GS == 32 || GS == 64)),
                   "K groups of 32 / 64 use 128-byte stages");
-    // FP8 per-channel uses v_mfma_scale_f32_32x32x64_f8f6f4 (32-byte
+    // FP8 per-channel on 64-byte stages uses v_mfma_f32_32x32x64_f8f6f4 (32-byte
     // fragments cover 32 rows x 64 K, half the registers of 16x16x128 per K).
     constexpr bool kMF32 = Fmt == FP8 && !Grouped && BK == 64;
-    // FP8 per-channel on double-buffered 128-byte stages: 32x32x64 tiles as
-    // well (16-register accumulators, which the compiler keeps in place; its
-    // 16x16x128 form rotates them through copies and spills at 256x256).
-    constexpr bool kDB32 = Fmt == FP8 && !Grouped && BK == 128 && STAGES == 2;
-    constexpr bool kAcc32 = kMF32 || kDB32;
+    constexpr bool kAcc32 = kMF32;
     // K bytes per stage: the INT8 16x16x64 and FP8 32x32x64 pipelines consume
     // exactly 64, the FP8 16x16x128 pipeline 128; K groups are 128 wide (two
     // INT8 stages or one FP8 stage).
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 #pragma unroll
                 for (int j = 0; j < NBF; ++j)
                     acc32[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a[i], bb[j], acc32[i][j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+                        a[i], bb[j], acc32[i][j], 0, 0, 0, 0, 0, 0);
         };
         constexpr int kEarly = NA / 4 > 0 ? NA / 4 : 1;
         auto step = [&](int s, const i32x8 (&a)[NA], const i32x8 (&bb)[NBF], i32x8 (&na)[NA],
@@ -379,67 +379,6 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             step(s + 1, a1, b1, a0, b0);
         }
         if (s < stages) step(s, a0, b0, a1, b1);
-    } else if constexpr (kDB32) {
-        // The double-buffered pipeline below on 32x32x64 FP8 tiles: lane l
-        // holds row l % 32 of a 32-row block and, for 64-K step h of the
-        // stage, K bytes [64h + 32*(l/32), +32).
-        const int r32 = lane & 31, g32 = lane >> 5;
-        const int a_r0 = wave_n * 16 * WTN + r32, b_r0 = BN + wave_m * 16 * WTM + r32;
-        const int a_sw = swizzle<BK>(a_r0), b_sw = swizzle<BK>(b_r0);
-        constexpr int NA = WTN / 2, NBF = WTM / 2;
-        auto rd = [&](const uint8_t *p, int h, int sw) {
-            const int c = 4 * h + 2 * g32;
-            const i32x4 lo = *reinterpret_cast<const i32x4 *>(p + ((c ^ sw) * 16));
-            const i32x4 hi = *reinterpret_cast<const i32x4 *>(p + (((c + 1) ^ sw) * 16));
-            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        };
-        auto read_b = [&](int st, i32x8 (&bb)[NBF][2]) {
-            const uint8_t *pb = lds + (st % 2) * STAGE_BYTES + b_r0 * BK;
-#pragma unroll
-            for (int j = 0; j < NBF; ++j)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) bb[j][h] = rd(pb + j * 32 * BK, h, b_sw);
-        };
-        auto read_a = [&](int st, int i, i32x8 (&a)[2]) {
-            const uint8_t *pa = lds + (st % 2) * STAGE_BYTES + (a_r0 + i * 32) * BK;
-            a[0] = rd(pa, 0, a_sw);
-            a[1] = rd(pa, 1, a_sw);
-        };
-        auto row = [&](int i, const i32x8 (&a)[2], const i32x8 (&bb)[NBF][2]) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int j = 0; j < NBF; ++j)
-                    acc32[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a[h], bb[j][h], acc32[i][j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-        };
-        // One set of token fragments: the next stage's are read into it
-        // after this stage's last MFMAs have issued (their reads of the
-        // registers happen at issue), under the MFMAs still executing.
-        auto step = [&](int s, i32x8 (&bb)[NBF][2], i32x8 (&a)[2]) {
-#pragma unroll
-            for (int i = 0; i + 1 < NA; ++i) {
-                i32x8 an[2];
-                read_a(s, i + 1, an);
-                row(i, a, bb);
-                a[0] = an[0];
-                a[1] = an[1];
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            row(NA - 1, a, bb);
-            wait_vmcnt<0>();
-            lds_barrier();
-            if (s + 2 < stages) issue(s + 2, (s + 2) * BK);
-            read_b(s + 1, bb);
-            read_a(s + 1, 0, a);
-        };
-        i32x8 b0[NBF][2], a0[2];
-        wait_vmcnt<0>();
-        lds_barrier();
-        if (1 < stages) issue(1, BK);
-        read_b(0, b0);
-        read_a(0, 0, a0);
-        for (int s = 0; s < stages; ++s) step(s, b0, a0);
     } else if constexpr (!Grouped && STAGES == 2) {
         // Two 128-byte stages, double-buffered (a 256x256 tile's 64 KB stages
         // fit the LDS twice). The DMA of stage s+1 is issued once every wave
@@ -1084,7 +1023,7 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
 }
 
 // Per-channel GEMM on 32x32 MFMA tiles with 128x128 wave tiles
-// (INT8: v_mfma_i32_32x32x32_i8; FP8: v_mfma_scale_f32_32x32x64_f8f6f4),
+// (INT8: v_mfma_i32_32x32x32_i8; FP8: v_mfma_f32_32x32x64_f8f6f4),
 // WN x WM wave64s, one wave per SIMD. LDS traffic per MFMA op is what bounds
 // the 128x64-wave kernel above on gfx950 (~128 B/clk per CU for ds_read_b128
 // plus the global->LDS writes): a 128x128 wave tile reads (128+128)*64 bytes
@@ -1256,7 +1195,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void wide_gemm(
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j0 + j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        fa[i], fb[j], acc[i][j0 + j], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+                        fa[i], fb[j], acc[i][j0 + j], 0, 0, 0, 0, 0, 0);
         };
         // Stage s uses A fragments fa (read during stage s-1); the next
         // stage's go to the other set, so that the loop, unrolled by two,
@@ -1450,18 +1389,17 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
         return -4;
     } else {
         // 256x128 with eight waves of 128x32 on two double-buffered 128-byte
-        // K stages, 32x32x64 MFMAs (down at 4096 46.2 us against 47.9 us on
-        // three stages of 16x16x128, and 60 us for one workgroup of four
-        // 128x64 waves).
+        // K stages (down at 4096 45.5 us against 48.0 us on three stages, and
+        // 60 us for one workgroup of four 128x64 waves).
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 2, 128, 2, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
             return launch_wide<Fmt, 2, 1, 3, Out>(a, s);
-        // 256x256: eight 128x64 waves of 32x32x64 MFMAs on two double-buffered
-        // 128-byte K stages (gate_up at 4096 91 us against 103 us on four
-        // 64-byte stages).
+        // 256x256: eight 128x64 waves on two double-buffered 128-byte K stages
+        // (gate_up at 4096 90 us against 103 us on four 64-byte stages of
+        // 32x32x64 MFMAs).
         if (p.channels == 256 && p.tokens == 256 && p.waves == 8)
             return launch_shape<Fmt, 2, 4, 8, 4, 128, 2, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128)
