@@ -905,9 +905,15 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         // stage's slot (read before the barrier: the next step's DMA refills
         // the slot); then the ring wait, barrier and the next stage's
         // fragment reads.
-        auto step = [&](int s, const Frag (&a)[WTN], const Frag (&bb)[WTM], Frag (&na)[WTN],
-                        Frag (&nb)[WTM]) {
-            const bool first = s % SPG == 0, last = s % SPG == SPG - 1 || s + 1 == stages;
+        // first_ / last_: 1 or 0 when the caller knows whether stage s opens
+        // or closes its group (the main loop), 2 to decide at run time. A
+        // known first stage starts its MFMAs from an inline zero accumulator
+        // instead of zeroing the partials with moves.
+        auto step = [&](int s, auto first_, auto last_, const Frag (&a)[WTN],
+                        const Frag (&bb)[WTM], Frag (&na)[WTN], Frag (&nb)[WTM]) {
+            constexpr int FC = decltype(first_)::value, LC = decltype(last_)::value;
+            const bool first = FC == 2 ? s % SPG == 0 : FC == 1;
+            const bool last = LC == 2 ? (s % SPG == SPG - 1 || s + 1 == stages) : LC == 1;
             if (s + STAGES - 1 < stages) issue(s + STAGES - 1, (s + STAGES - 1) * BK);
 #pragma unroll
             for (int i = 0; i < WTN; ++i)
@@ -923,6 +929,16 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             // i32x8 fragments: unconditional, as in the per-channel pipeline.
             if (BK == 128 || s + 1 < stages) read(s + 1, na, nb);
         };
+        using C0 = std::integral_constant<int, 0>;
+        using C1 = std::integral_constant<int, 1>;
+        using C2 = std::integral_constant<int, 2>;
+        // In the loop s is even: with two stages per group, stage s opens
+        // and stage s+1 closes a group; with one, every stage does both.
+        using F0 = C1;
+        using L0 = std::conditional_t<SPG == 1, C1, C0>;
+        using F1 = std::conditional_t<SPG == 1, C1, C0>;
+        using L1 = C1;
+        static_assert(SPG == 1 || SPG == 2, "stages per K group");
         Frag a0[WTN], b0[WTM], a1[WTN], b1[WTM];
         if (stages >= STAGES - 1) wait_ring(std::integral_constant<int, STAGES - 2>{});
         else wait_vmcnt<0>();
@@ -930,10 +946,10 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
         read(0, a0, b0);
         int s = 0;
         for (; s + 1 < stages; s += 2) {
-            step(s, a0, b0, a1, b1);
-            step(s + 1, a1, b1, a0, b0);
+            step(s, F0{}, L0{}, a0, b0, a1, b1);
+            step(s + 1, F1{}, L1{}, a1, b1, a0, b0);
         }
-        if (s < stages) step(s, a0, b0, a1, b1);
+        if (s < stages) step(s, C2{}, C2{}, a0, b0, a1, b1);
       }
     }
 
