@@ -354,3 +354,32 @@ def test_staged_skinny_variants(dev, orc, fmt, grouped):
             else:
                 ideal = orc.gemm_fp8_ideal(xq, sx, wq, sw)
                 assert rel_l2(bits_to_f32(y), ideal) <= FP8_REL_L2
+
+
+@pytest.mark.parametrize("fmt", [I8, FP8])
+def test_prefill_graph_replay(dev, orc, fmt):
+    """The planned prefill GEMMs (256x256 and 256x128 double-buffered tiles)
+    captured in a HIP graph: every one of several replays, with eager work
+    and synchronizations between them, reproduces the eager output bit for
+    bit."""
+    from breeze_tts_cpp_amd import qlinear
+    M = 1024
+    stream = torch.cuda.Stream()
+    for N, K in ((12288, 2048), (2048, 6144)):
+        print(f"prefill graph replay fmt={fmt} M={M} N={N} K={K}", flush=True)
+        xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=N + 3)
+        args = (dev_u8(xq, dev), dev_f32(sx, dev), dev_u8(wq, dev), dev_f32(sw, dev), fmt)
+        ref = qlinear.gemm(*args)
+        y = torch.empty_like(ref)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            qlinear.gemm(*args, out=y, stream=stream)
+        for r in range(3):
+            y.fill_(0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"replay {r}"
+            qlinear.gemm(*args)  # eager work between replays
+        del g
