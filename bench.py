@@ -151,7 +151,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized linear path has no multi-GPU "
-              "component in this build (see DESIGN.md for how it would shard).", file=sys.stderr)
+              "component in this build; --gpus N with N > 1 is not supported.", file=sys.stderr)
         sys.exit(2)
     import torch
 
