@@ -198,8 +198,13 @@ qlin_path choose(int rows, int N, int K, int fmt, int input_group, int weight_gr
     p.tokens = 128;
     if (!grouped && fmt == QLIN_I8) {
         p.waves = 8;
+        // 256x256 from 192 tiles. Below that, 256x128 only for long K: the
+        // double-buffered 128x128 tile, two workgroups per CU, overlaps one
+        // workgroup's prologue and epilogue with the other's MFMAs, which
+        // pays while K is short (o_proj at M = 4096: 18.8 us against 19.7 us
+        // on 256x128; down, K = 6144, keeps 256x128: 45.6 us against 48.3).
         if (tiles_256 >= 192) p.channels = p.tokens = 256;
-        else if (tiles_256x128 >= 256 && full) p.channels = 256;
+        else if (tiles_256x128 >= 256 && full && K > 2048) p.channels = 256;
     } else if (!grouped) {
         if (tiles_256 >= 192) {
             p.channels = p.tokens = 256;

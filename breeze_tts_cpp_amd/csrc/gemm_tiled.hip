@@ -1376,11 +1376,13 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, true, Out>(a, s);
         return -4;
     } else if constexpr (Fmt == I8) {
-        // 256x128 with eight waves of 128x32 over 128-byte K stages (two
+        // 256x128 with eight waves of 64x64 over 128-byte K stages (two
         // MFMAs per tile and stage, half the barriers of 64-byte stages:
-        // down at 4096 54 us against 59 us, o_proj 28 against 29).
+        // down at 4096 54 us against 59 us, o_proj 28 against 29). A 64x64
+        // wave reads 16 KB of fragments per stage where a 128x32 wave reads
+        // 20 KB: down at 4096 46.8 us against 47.8 us.
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 2, 128, 3, false, Out>(a, s);
+            return launch_shape<Fmt, 4, 2, 4, 4, 128, 3, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)
@@ -1407,11 +1409,12 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 4, 4, 1, 128, 4, false, Out>(a, s);
         return -4;
     } else {
-        // 256x128 with eight waves of 128x32 on two double-buffered 128-byte
+        // 256x128 with eight waves of 64x64 on two double-buffered 128-byte
         // K stages (down at 4096 45.5 us against 48.0 us on three stages, and
-        // 60 us for one workgroup of four 128x64 waves).
+        // 60 us for one workgroup of four 128x64 waves; 64x64 waves against
+        // 128x32: o_proj 18.9 us against 19.2 us).
         if (p.channels == 256 && p.tokens == 128 && p.waves == 8)
-            return launch_shape<Fmt, 2, 4, 8, 2, 128, 2, false, Out>(a, s);
+            return launch_shape<Fmt, 4, 2, 4, 4, 128, 2, false, Out>(a, s);
         if (p.channels == 256 && p.tokens == 256 && p.waves == 4)
             return launch_wide<Fmt, 2, 2, 4, Out>(a, s);
         if (p.channels == 256 && p.tokens == 128 && p.waves == 2)

@@ -110,8 +110,10 @@ def test_prefill_plan_rules():
     def tile(M, name, fmt, g=0):
         p = qlinear.plan(M, *shapes[name], fmt, g, g)
         return (p.channels, p.tokens, p.waves)
+    # INT8: 256x256 from 192 tiles, 256x128 for long K, else the 128x128 tile
+    assert tile(4096, "gate_up", I8) == (256, 256, 8) and tile(4096, "down", I8) == (256, 128, 8)
     assert tile(4096, "qkv", I8) == (256, 256, 8) and tile(1024, "gate_up", I8) == (256, 256, 8)
-    assert tile(4096, "o_proj", I8) == (256, 128, 8) and tile(1024, "qkv", I8) == (128, 128, 8)
+    assert tile(4096, "o_proj", I8) == (128, 128, 8) and tile(1024, "qkv", I8) == (128, 128, 8)
     assert tile(4096, "gate_up", FP8) == (256, 256, 8) and tile(4096, "down", FP8) == (256, 128, 8)
     assert tile(1024, "gate_up", FP8) == (256, 256, 8)   # 192 tiles, as INT8
     assert tile(4096, "qkv", I8, 128) == (256, 128, 8) and tile(4096, "qkv", FP8, 128) == (256, 128, 8)
