@@ -65,8 +65,15 @@ __global__ __launch_bounds__(kThreads) void residual_rms_quantize(
     float sum = 0.f;
 #pragma unroll
     for (int p = 0; p < 4; ++p) sum += v[0][2 * p] * v[0][2 * p] + v[0][2 * p + 1] * v[0][2 * p + 1];
-#pragma unroll
-    for (int d = 16; d; d /= 2) sum += __shfl_down(sum, d, 32);
+    // The 32-lane shuffle-down tree (lane i adds lane i + d, d = 16 .. 1),
+    // exact in lane 0 of each group, where it is read: the lanes whose values
+    // reach it are below d at step d, so their partner i ^ d is i + d and the
+    // exchange runs on DPP and row swaps instead of LDS.
+    sum += lane_xor<16>(sum);
+    sum += lane_xor<8>(sum);
+    sum += lane_xor<4>(sum);
+    sum += lane_xor<2>(sum);
+    sum += lane_xor<1>(sum);
     __shared__ float partial[kThreads / 32];
     if ((threadIdx.x & 31) == 0) partial[threadIdx.x / 32] = sum;
     __syncthreads();

@@ -50,14 +50,17 @@ namespace {
 // cub::BlockReduce<float, 256>::Sum with the warp-reductions algorithm
 // (CUDA 13 CUB): each 32-lane group adds lane i + s into lane i for s = 1,
 // 2, 4, 8, 16 (when i + s < 32), then the eight group totals are added in
-// group order. Every thread returns the same total.
+// group order. Every thread returns the same total. The lane exchange is
+// lane ^ s (DPP and row swaps, no LDS round trip): every lane whose value
+// reaches the group's lane 0 is a multiple of 2s at step s, whose partner
+// i ^ s is i + s, so lane 0 adds the same operands in the same order.
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
     const int l32 = threadIdx.x & 31;
-#pragma unroll
-    for (int s = 1; s < 32; s *= 2) {
-        const float o = __shfl_down(v, s, 32);
-        if (l32 + s < 32) v += o;
-    }
+    v += lane_xor<1>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<8>(v);
+    v += lane_xor<16>(v);
     if (l32 == 0) red[threadIdx.x >> 5] = v;
     __syncthreads();
     float total = red[0];
@@ -74,6 +77,27 @@ __device__ __forceinline__ float block_max_256(float v, float *red) {
     const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     return r;
+}
+
+// A 32-lane group's shuffle-down tree (lane i adds lane i + d for d = 16,
+// 8, 4, 2, 1), exact in lane 0 of the group: the lanes whose values reach
+// it are below d at step d, where the partner i ^ d is i + d, so the lane
+// exchange needs no LDS round trip. Other lanes hold other sums.
+__device__ __forceinline__ float sum32_down(float v) {
+    v += lane_xor<16>(v);
+    v += lane_xor<8>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<1>(v);
+    return v;
+}
+__device__ __forceinline__ int sum32_down(int v) {
+    v += __float_as_int(lane_xor<16>(__int_as_float(v)));
+    v += __float_as_int(lane_xor<8>(__int_as_float(v)));
+    v += __float_as_int(lane_xor<4>(__int_as_float(v)));
+    v += __float_as_int(lane_xor<2>(__int_as_float(v)));
+    v += __float_as_int(lane_xor<1>(__int_as_float(v)));
+    return v;
 }
 
 // Exact e4m3fn decode (OCP; 0x7f / 0xff NaN).
@@ -642,8 +666,7 @@ __global__ __launch_bounds__(256) void norm_project(
         for (int c = l32 * 4; c < k; c += 128)
             acc = __builtin_amdgcn_sdot4(*reinterpret_cast<const int *>(act8 + c),
                                          *reinterpret_cast<const int *>(wr + c), acc, false);
-#pragma unroll
-        for (int d = 16; d; d /= 2) acc += __shfl_down(acc, d, 32);
+        acc = sum32_down(acc);
         result = (float(acc) * sw[channel]) * step;
     } else {
         float acc = 0.f;
@@ -654,8 +677,7 @@ __global__ __launch_bounds__(256) void norm_project(
                 acc = __builtin_fmaf(to_float(act16[c + e], T{}), decode_fp8((wq >> (8 * e)) & 0xffu),
                                      acc);
         }
-#pragma unroll
-        for (int d = 16; d; d /= 2) acc += __shfl_down(acc, d, 32);
+        acc = sum32_down(acc);
         result = (acc * sw[channel]) * step;
     }
     if (l32 == 0) {
