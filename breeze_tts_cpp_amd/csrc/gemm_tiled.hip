@@ -1432,8 +1432,14 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
             return launch_shape<Fmt, 2, 2, 8, 4, 64, 4, false, Out>(a, s);
         // 128x128: eight waves of 64x32 on the 16x16x128 FP8 MFMA over
         // 128-byte K stages (waves 8), or four 64x64 waves of 32x32x64 (1).
-        if (p.channels == 128 && p.tokens == 128 && p.waves == 8)
+        // Up to K = 2048 two double-buffered stages, two workgroups per CU
+        // (o_proj at 4096 17.8 us against 18.3 us on 256x128, qkv at 1024
+        // 11.7 us against 12.0 us on four stages); beyond, four stages (down
+        // at 1024 on 128x128: 23.5 us, against 32.5 us double-buffered).
+        if (p.channels == 128 && p.tokens == 128 && p.waves == 8) {
+            if (a.K <= 2048) return launch_shape<Fmt, 2, 4, 4, 2, 128, 2, false, Out>(a, s);
             return launch_shape<Fmt, 2, 4, 4, 2, 128, 4, false, Out>(a, s);
+        }
         if (p.channels == 128 && p.tokens == 128)
             return launch_shape<Fmt, 2, 2, 4, 4, 64, 4, false, Out>(a, s);
         // 128x64: four waves of 64x32 (32x32x64 MFMA) or eight of 32x32

@@ -116,6 +116,7 @@ def test_prefill_plan_rules():
     assert tile(4096, "o_proj", I8) == (128, 128, 8) and tile(1024, "qkv", I8) == (128, 128, 8)
     assert tile(4096, "gate_up", FP8) == (256, 256, 8) and tile(4096, "down", FP8) == (256, 128, 8)
     assert tile(1024, "gate_up", FP8) == (256, 256, 8)   # 192 tiles, as INT8
+    assert tile(4096, "o_proj", FP8) == (128, 128, 8)    # K <= 2048: the 128x128 tile, as INT8
     assert tile(4096, "qkv", I8, 128) == (256, 128, 8) and tile(4096, "qkv", FP8, 128) == (256, 128, 8)
     assert tile(1024, "gate_up", I8, 128) == (128, 128, 8) and tile(1024, "gate_up", FP8, 128) == (128, 128, 8)
     assert tile(4096, "qkv", I8, 32) == (256, 128, 8) and tile(4096, "qkv", FP8, 64) == (128, 128, 8)

@@ -245,9 +245,11 @@ def _tiled_paths(grouped=False, fmt=I8):
 
 
 @pytest.mark.parametrize("fmt", [I8, FP8])
-@pytest.mark.parametrize("M,N,K", [(200, 144, 336), (300, 272, 1024), (130, 512, 2048)])
+@pytest.mark.parametrize("M,N,K", [(200, 144, 336), (300, 272, 1024), (130, 512, 2048),
+                                   (150, 208, 2112)])
 def test_tiled_variants_ragged(dev, orc, fmt, M, N, K):
-    """Every macro-tile shape on ragged M/N edges and K not a multiple of 128."""
+    """Every macro-tile shape on ragged M/N edges and K not a multiple of 128
+    (K above 2048 takes the FP8 128x128 tile's four-stage form)."""
     xq, sx, wq, sw = operands(orc, M, N, K, fmt, seed=M + N + K)
     ideal = None if fmt == I8 else orc.gemm_fp8_ideal(xq, sx, wq, sw)
     for p in _tiled_paths(fmt=fmt):
