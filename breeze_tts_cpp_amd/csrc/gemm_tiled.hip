@@ -594,10 +594,12 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
             }
         }
     } else if constexpr (Fmt == FP8 && WTN * WTM > 8) {
-        // FP8 K groups on 128x32 waves: one 128-K group per stage,
-        // stage-synchronous (the software-pipelined form below needs a second
-        // set of i32x8 fragments that these waves have no registers for: it
-        // spilled and ran slower). Stages wait for themselves; the group
+        // FP8 K groups on wave tiles of more than 8 MFMA tiles (the 256x128
+        // tile's 64x64 waves): one 128-K group per stage, stage-synchronous
+        // (the software-pipelined form below needs a second set of i32x8
+        // fragments that these waves have no registers for: it spilled and
+        // ran slower; so did a double-buffered form reading weight fragments
+        // a block ahead, 42-45 VGPRs). Stages wait for themselves; the group
         // scales are the stage slot's scale rows.
         for (int s = 0; s < stages; ++s) {
             // Stage s has landed once at most the newer stages are outstanding.
@@ -683,83 +685,8 @@ __global__ __launch_bounds__(64 * WN * WM) void tiled_gemm(
       // rescale). Larger wave tiles have no registers for the second bank
       // (it spilled on 256x128) and apply each group at its last stage.
       constexpr bool kTwoBanks = WTN * WTM <= 8 && SPG == 2;
-      if constexpr (STAGES == 2) {
-        // Two double-buffered 128-byte stages, one K group each (the
-        // per-channel double-buffered pipeline): weight fragments read one
-        // 16-row block ahead of that block's MFMAs, the group's partials from
-        // zero, the group applied from the stage slot's scale rows before the
-        // barrier that lets the next DMA refill the slot.
-        static_assert(BK == kGroupK, "one K group per double-buffered stage");
-        // Partials of two weight blocks: block i's group is applied after
-        // block i+1's MFMAs have issued, so only two blocks' partials are
-        // live and the rescale spreads between the MFMAs.
-        Acc part[2][WTM];
-        auto rd = [&](const uint8_t *p, int c0, int c1) { return frag(p, c0, c1); };
-        auto read_b = [&](int st, Frag (&bb)[WTM]) {
-            const uint8_t *pb = lds + (st % 2) * STAGE_BYTES + b_off;
-#pragma unroll
-            for (int j = 0; j < WTM; ++j) bb[j] = rd(pb + j * 16 * BK, b_c0, b_c1);
-        };
-        auto read_a = [&](int st, int i) {
-            return rd(lds + (st % 2) * STAGE_BYTES + a_off + i * 16 * BK, a_c0, a_c1);
-        };
-        auto row = [&](int i, const Frag &a, const Frag (&bb)[WTM]) {
-#pragma unroll
-            for (int j = 0; j < WTM; ++j) {
-                part[i % 2][j] = Acc{0, 0, 0, 0};
-                MMA::run(part[i % 2][j], a, bb[j]);
-            }
-        };
-        // Group of stage st for block i: facc = fmaf(p, sx_g * sw_g, facc)
-        // with the scale rows of the stage's slot.
-        auto apply_row = [&](int st, int i, const float (&xg)[WTM]) {
-            const float *slot =
-                reinterpret_cast<const float *>(lds + (st % 2) * STAGE_BYTES + ROWS * BK);
-            const f32x4 wg =
-                *reinterpret_cast<const f32x4 *>(slot + wave_n * 16 * WTN + i * 16 + quad * 4);
-#pragma unroll
-            for (int j = 0; j < WTM; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    facc[i][j][r] =
-                        __builtin_fmaf(float(part[i % 2][j][r]), xg[j] * wg[r], facc[i][j][r]);
-        };
-        auto step = [&](int s, const Frag (&bb)[WTM], Frag a, Frag (&nb)[WTM], Frag &na) {
-            const float *slot =
-                reinterpret_cast<const float *>(lds + (s % 2) * STAGE_BYTES + ROWS * BK);
-            float xg[WTM];
-#pragma unroll
-            for (int j = 0; j < WTM; ++j)
-                xg[j] = slot[256 + wave_m * 16 * WTM + j * 16 + row16];
-#pragma unroll
-            for (int i = 0; i < WTN; ++i) {
-                Frag an;
-                if (i + 1 < WTN) an = read_a(s, i + 1);
-                row(i, a, bb);
-                if (i > 0) apply_row(s, i - 1, xg);
-                if (i + 1 < WTN) a = an;
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            apply_row(s, WTN - 1, xg);
-            wait_vmcnt<0>();
-            lds_barrier();
-            if (s + 2 < stages) issue(s + 2, (s + 2) * BK);
-            read_b(s + 1, nb);
-            na = read_a(s + 1, 0);
-        };
-        Frag b0[WTM], b1[WTM], a0;
-        wait_vmcnt<0>();
-        lds_barrier();
-        if (1 < stages) issue(1, BK);
-        read_b(0, b0);
-        a0 = read_a(0, 0);
-        int s = 0;
-        for (; s + 1 < stages; s += 2) {
-            step(s, b0, a0, b1, a0);
-            step(s + 1, b1, a0, b0, a0);
-        }
-        if (s < stages) step(s, b0, a0, b1, a0);
-      } else if constexpr (kTwoBanks) {
+      static_assert(STAGES >= 3, "the K-group software pipeline keeps a stage in flight");
+      if constexpr (kTwoBanks) {
         Acc pp[2][WTN][WTM];
         float xg[WTM];
         f32x4 wg[WTN];
@@ -1353,8 +1280,9 @@ int dispatch_shape(const GemmArgs &a, const GemmPath &p, hipStream_t s) {
         // 128-byte stages, and the 4-wave 128x64 tile runs two accumulator
         // banks.
         constexpr int GBK = Fmt == I8 ? 64 : 128;
-        // 256x128, eight 64x64 waves: FP8 on two double-buffered 128-byte
-        // stages (group_fp8 at 4096 1.44 against 1.41 PFLOPS on three); INT8
+        // 256x128, eight 64x64 waves: FP8 on two 128-byte stages in the
+        // stage-synchronous loop (group_fp8 at 4096 1.44 against 1.41 PFLOPS
+        // on three); INT8
         // on four 64-byte stages (on 128-byte stages it spills). 64x64 waves
         // read fewer fragment bytes than 128x32 waves: gate_up at 4096
         // INT8 161 us against 165 us, FP8 134 us against 138 us.
